@@ -1,0 +1,221 @@
+/*
+ * osh_hip.h -- C ABI of libosh_hip.so, the MI355X (gfx950) backend for
+ * OnnxSharp's dense-contraction operators: Conv (+ fused Relu/SiLU),
+ * MatMul with a fused column bias, and DynamicQuantizeMatMul.
+ *
+ * One P/Invoke surface: device, memory, copies, streams/events, one-time
+ * weight packing, operator launches and operator-level shape logic.  Plain
+ * pointers and sizes only.  Every entry point returns an osh_status (0 = OK,
+ * negative = error) and leaves a message for osh_last_error() on the calling
+ * thread.  Launch entry points are asynchronous on the given stream (NULL =
+ * the device's default stream); pointers named d_* are device memory.
+ *
+ * Reference citations are relative to the OnnxSharp source tree.
+ */
+#ifndef OSH_HIP_H
+#define OSH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(_WIN32)
+#define OSH_API __declspec(dllexport)
+#else
+#define OSH_API __attribute__((visibility("default")))
+#endif
+
+typedef int osh_status;
+enum {
+    OSH_OK = 0,
+    OSH_E_INVALID = -1,     /* bad argument or shape (reference: OnnxSharpException) */
+    OSH_E_UNSUPPORTED = -2, /* shape/attribute the backend does not take (reference: NotSupportedException;
+                               an emitter refusing an op, src/OnnxSharp.Vulkan/VkOpRegistry.cs:168-180) */
+    OSH_E_DEVICE = -3,      /* HIP runtime error (reference: VkDeviceLostException) */
+    OSH_E_NOMEM = -4        /* device allocation failed */
+};
+
+typedef void *osh_stream; /* hipStream_t */
+typedef void *osh_event;  /* hipEvent_t */
+
+/* Fused activation of a Conv, UnaryOpKind subset that
+ * GraphFusion.FuseActivationIntoProducer moves into a producer
+ * (src/OnnxSharp/Core/GraphFusion.cs:1713-1718). */
+enum { OSH_ACT_NONE = 0, OSH_ACT_RELU = 1, OSH_ACT_SILU = 2 };
+
+/* ONNX auto_pad (src/OnnxSharp/Ops/DnnOps.cs:69-89). */
+enum { OSH_PAD_NOTSET = 0, OSH_PAD_SAME_UPPER = 1, OSH_PAD_SAME_LOWER = 2, OSH_PAD_VALID = 3 };
+
+/* ------------------------------------------------------------------ errors */
+
+/* Message of the last failing call on this thread ("" if none). */
+OSH_API const char *osh_last_error(void);
+
+/* ------------------------------------------------------------------ device */
+
+typedef struct osh_device_info {
+    char name[64];
+    char arch[32];          /* e.g. "gfx950" */
+    int compute_units;
+    int clock_khz;
+    size_t total_mem;
+    size_t lds_per_block;
+} osh_device_info;
+
+/* Select device `dev` for the calling thread and report it (info may be NULL).
+ * Replaces VkDevice creation (src/OnnxSharp.Vulkan/VkDevice.cs:9-120). */
+OSH_API osh_status osh_init(int dev, osh_device_info *info);
+OSH_API osh_status osh_device_count(int *count);
+OSH_API osh_status osh_device_synchronize(void);
+
+/* ------------------------------------------------------------------ memory */
+
+/* Device buffers: the C# side pools them by (kind, bytes) as VkBufferPool does
+ * (src/OnnxSharp.Vulkan/VkBufferPool.cs:20-190). */
+OSH_API osh_status osh_malloc(void **d_ptr, size_t bytes);
+OSH_API osh_status osh_free(void *d_ptr);
+/* Pinned host staging (hipHostMalloc; replaces VkSegment staging buffers,
+ * src/OnnxSharp.Vulkan/VkSegment.cs:370,462). */
+OSH_API osh_status osh_host_alloc(void **h_ptr, size_t bytes);
+OSH_API osh_status osh_host_free(void *h_ptr);
+
+/* ------------------------------------------------------------------ copies */
+
+OSH_API osh_status osh_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes, osh_stream s);
+OSH_API osh_status osh_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes, osh_stream s);
+OSH_API osh_status osh_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes, osh_stream s);
+/* Byte fill by a kernel (safe inside captured graphs). */
+OSH_API osh_status osh_memset_d8(void *d_dst, int value, size_t bytes, osh_stream s);
+
+/* --------------------------------------------------------- streams / events */
+
+OSH_API osh_status osh_stream_create(osh_stream *s);
+OSH_API osh_status osh_stream_destroy(osh_stream s);
+/* One sync per segment, as VkSegment.Execute waits one fence
+ * (src/OnnxSharp.Vulkan/VkSegment.cs:598-599). */
+OSH_API osh_status osh_stream_sync(osh_stream s);
+OSH_API osh_status osh_event_create(osh_event *e);
+OSH_API osh_status osh_event_destroy(osh_event e);
+OSH_API osh_status osh_event_record(osh_event e, osh_stream s);
+OSH_API osh_status osh_event_elapsed_ms(osh_event start, osh_event stop, float *ms);
+
+/* ------------------------------------------------------------ Conv (A1-A8) */
+
+/* Conv attributes as ConvLayer reads them (src/OnnxSharp/Ops/DnnOps.cs:116-132):
+ * an absent list has n_* = 0. */
+typedef struct osh_conv_attrs {
+    int group;
+    int auto_pad;            /* OSH_PAD_* */
+    int n_kernel_shape, kernel_shape[2];
+    int n_strides, strides[2];
+    int n_pads, pads[4];
+    int n_dilations, dilations[2];
+} osh_conv_attrs;
+
+/* Resolved 2-D conv launch (the fields of Conv2DParams,
+ * src/OnnxSharp.Vulkan/VkConv.cs:24-51). */
+typedef struct osh_conv_params {
+    int n, c, h, w;          /* input NCHW */
+    int m, kh, kw, group;    /* weight OIHW: [m, c/group, kh, kw] */
+    int sh, sw, dh, dw;      /* strides, dilations */
+    int pt, pl, pb, pr;      /* pads (top, left, bottom, right) */
+    int oh, ow;              /* output spatial size */
+} osh_conv_params;
+
+/* ConvLayer.GetMemoryShapes (src/OnnxSharp/Ops/DnnOps.cs:134-201): output
+ * dims of a 4-D (NCHW) input.  Keeps the reference's rule that the shape uses
+ * the begin pad as the end pad unless more than 2*spatial pads are given. */
+OSH_API osh_status osh_conv_infer_shape(const osh_conv_attrs *attrs, const int64_t x_dims[4],
+                                        const int64_t w_dims[4], int64_t y_dims[4]);
+
+/* ConvLayer.Resolve + output shape (src/OnnxSharp/Ops/DnnOps.cs:379-409). */
+OSH_API osh_status osh_conv_resolve(const osh_conv_attrs *attrs, const int64_t x_dims[4],
+                                    const int64_t w_dims[4], osh_conv_params *out);
+
+/* Bytes of the packed weight buffer osh_conv_pack_weights writes for p. */
+OSH_API osh_status osh_conv_packed_weight_bytes(const osh_conv_params *p, size_t *bytes);
+
+/* One-time weight packing on the device (replaces NchwcConv.PackWeights,
+ * src/OnnxSharp/Kernels/NchwcConv.cs:247-274, and PackedConv.PackWeights,
+ * src/OnnxSharp/Kernels/PackedConv.cs:155-182).  d_w is OIHW f32. */
+OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *d_w, void *d_packed,
+                                         osh_stream s);
+
+/* Conv forward, NCHW f32 in and out, bias (length m) optional, fused
+ * activation act (ConvLayer.Forward, src/OnnxSharp/Ops/DnnOps.cs:411-500).
+ * d_wpacked is the output of osh_conv_pack_weights for the same p. */
+OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,
+                                  const float *d_bias, int act, float *d_y, osh_stream s);
+
+/* ------------------------------------------------- MatMul + bias (A9, A10) */
+
+/* C[m,n] (row stride ldc) = A[m,k] (lda) * B[k,n] (ldb)
+ *   + col_bias[j] (MatMulLayer's FusedBias, src/OnnxSharp/Ops/DnnOps.cs:2817,3009-3022)
+ *   or + row_bias[i] (Conv-style per-row bias, GemmKernel.Multiply's `bias`),
+ * column bias taking precedence as in GemmKernel.cs:1113-1152; then act.
+ * With col_scale: C = col_scale[j] * (A*B) + col_bias[j] in one fmaf
+ * (GemmKernel.cs:1210-1241).  Any pointer except A, B, C may be NULL.
+ * Replaces GemmKernel.Multiply / MultiplyPacked
+ * (src/OnnxSharp/Tensors/GemmKernel.cs:131-269,675-852). */
+OSH_API osh_status osh_gemm_f32(int m, int n, int k, const float *d_a, int lda, const float *d_b, int ldb,
+                                const float *d_col_bias, const float *d_row_bias, const float *d_col_scale,
+                                int act, float *d_c, int ldc, osh_stream s);
+
+/* Batched form of the same (MatMulLayer broadcast with per-batch strides,
+ * GemmKernel.MultiplyBatched, src/OnnxSharp/Tensors/GemmKernel.cs:284-405);
+ * stride 0 broadcasts an operand. */
+OSH_API osh_status osh_gemm_f32_batched(int batch, int m, int n, int k, const float *d_a, int lda,
+                                        int64_t stride_a, const float *d_b, int ldb, int64_t stride_b,
+                                        const float *d_col_bias, int act, float *d_c, int ldc,
+                                        int64_t stride_c, osh_stream s);
+
+/* MatMulLayer.GetMemoryShapes numpy broadcast (src/OnnxSharp/Ops/DnnOps.cs:2789-2900):
+ * output dims of A (rank ra) x B (rank rb); returns the output rank in *ry. */
+OSH_API osh_status osh_matmul_infer_shape(const int64_t *a_dims, int ra, const int64_t *b_dims, int rb,
+                                          int64_t *y_dims, int *ry);
+
+/* ------------------------------------------- DynamicQuantizeMatMul (A13-A15) */
+
+/* Bytes of the packed int8 weight buffer and of the scratch buffer that
+ * osh_dqmm_u8s8 needs for (m, k, n). */
+OSH_API osh_status osh_dqmm_packed_weight_bytes(int k, int n, size_t *bytes);
+OSH_API osh_status osh_dqmm_scratch_bytes(int m, int k, size_t *bytes);
+
+/* One-time packing of W [k,n] (int8 when w_signed, else uint8) minus its zero
+ * point(s) (n_wzp = 0: none, 1: per-tensor, n: per-column) into the
+ * MFMA-ready layout, with per-column sums.  Fails with OSH_E_UNSUPPORTED if
+ * (w - w_zp) leaves [-128, 127].  (Int8F32Gemm.WidenWeights + GemmKernel.Pack,
+ * src/OnnxSharp/Ops/QuantizedMatMulOps.cs:261-277.) */
+OSH_API osh_status osh_dqmm_pack_weights(int k, int n, const void *d_w, int w_signed, const int32_t *h_wzp,
+                                         int n_wzp, void *d_packed, osh_stream s);
+
+/* DynamicQuantizeMatMulLayer.Forward (src/OnnxSharp/Ops/QuantizedMatMulOps.cs:115-201):
+ *   per-tensor u8 quantization of A [m,k] (min/max including 0, NaN skipped;
+ *   scale = (max-min)/255, zp = clamp(rne(-min/scale)); q = clamp(rne(x*(1/scale))+zp)),
+ *   int32 accumulation of (q - zp)(w - w_zp), then
+ *   out[i,j] = fmaf(acc, scale * w_scale[j], bias[j]).
+ * w_scale has n_wscale = 1 or n entries; bias may be NULL; d_acc (m*n int32)
+ * may be NULL, else receives the exact accumulators; d_qparams (may be NULL)
+ * receives {scale as float bits, zp}.  d_scratch has osh_dqmm_scratch_bytes. */
+OSH_API osh_status osh_dqmm_u8s8(int m, int k, int n, const float *d_a, const void *d_wpacked,
+                                 const float *d_wscale, int n_wscale, const float *d_bias, float *d_out,
+                                 int32_t *d_acc, int32_t *d_qparams, void *d_scratch, osh_stream s);
+
+/* DynamicQuantizeLinear (src/OnnxSharp/Ops/QuantOps.cs:166-227) on the device:
+ * q (u8, n values), scale and zero point into d_qparams {scale bits, zp}. */
+OSH_API osh_status osh_dynamic_quantize_linear(int64_t n, const float *d_x, uint8_t *d_q, int32_t *d_qparams,
+                                               void *d_scratch, osh_stream s);
+
+/* ------------------------------------------------------ elementwise helpers */
+
+/* In-place activation pass (TensorOps.ElementWiseUnary, src/OnnxSharp/Tensors/TensorOps.cs:267-300). */
+OSH_API osh_status osh_activation_f32(int64_t n, const float *d_x, int act, float *d_y, osh_stream s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OSH_HIP_H */

@@ -1,0 +1,258 @@
+// osh_conv.hip -- Conv entry points of the C ABI: shape logic of ConvLayer
+// (src/OnnxSharp/Ops/DnnOps.cs:53-89,134-201,379-409) and the kernel choice
+// of ConvLayer.Forward (DnnOps.cs:411-500), re-planned for gfx950:
+//
+//   depthwise (group == C == M)         -> dw_conv_kernel (direct, ky -> kx FMA chain)
+//   1x1 / stride 1 / pad 0 / dil 1      -> MFMA GEMM over NCHW (W[M,C] x X[C,H*W])
+//   3x3 / pad 1 / dil 1 / stride 1 or 2 -> MFMA implicit GEMM on an LDS halo tile
+//   everything else                     -> MFMA implicit GEMM with an im2col gather
+//
+// Bias and the fused activation (Relu / SiLU, GraphFusion.cs:1713-1718) are
+// applied in registers before the single store.
+#include <cstring>
+
+#include "osh_conv3x3.h"
+#include "osh_igemm.h"
+#include "osh_launch.h"
+
+using namespace osh;
+
+namespace osh {
+
+// DnnOps.cs:53-67 (ceil_mode is false for Conv).
+static int spatial_out(int input, int kernel, int stride, int dilation, int pad_begin, int pad_end) {
+    int effective = (kernel - 1) * dilation + 1;
+    int numerator = input + pad_begin + pad_end - effective;
+    return numerator / stride + 1;  // C# integer division truncates toward zero, as C does
+}
+
+// DnnOps.cs:69-89.
+static void auto_pad(int mode, int input, int kernel, int stride, int dilation, int *begin, int *end) {
+    int effective = (kernel - 1) * dilation + 1;
+    int output = (input + stride - 1) / stride;  // ceil(input / stride) for positive sizes
+    if (mode == OSH_PAD_SAME_UPPER || mode == OSH_PAD_SAME_LOWER) {
+        int total = (output - 1) * stride + effective - input;
+        if (total < 0) total = 0;
+        int b = mode == OSH_PAD_SAME_UPPER ? total / 2 : total - total / 2;
+        *begin = b;
+        *end = total - b;
+    } else {  // VALID
+        *begin = 0;
+        *end = 0;
+    }
+}
+
+static osh_status check_attrs(const osh_conv_attrs *at, const int64_t x[4], const int64_t w[4]) {
+    if (!at || !x || !w) return fail(OSH_E_INVALID, "Conv: NULL argument");
+    if (at->n_kernel_shape < 0 || at->n_kernel_shape > 2 || at->n_strides < 0 || at->n_strides > 2 ||
+        at->n_dilations < 0 || at->n_dilations > 2 || at->n_pads < 0 || at->n_pads > 4)
+        return fail(OSH_E_INVALID, "Conv: attribute list length out of range for a 2-D conv");
+    if (at->auto_pad < OSH_PAD_NOTSET || at->auto_pad > OSH_PAD_VALID)
+        return fail(OSH_E_INVALID, "Conv: unknown auto_pad %d", at->auto_pad);
+    for (int i = 0; i < 4; i++)
+        if (x[i] <= 0 || w[i] <= 0 || x[i] > (1 << 30) || w[i] > (1 << 30))
+            return fail(OSH_E_INVALID, "Conv: non-positive or oversized dimension");
+    long long channels = x[1];
+    if (at->group <= 0 || channels % at->group != 0)
+        return fail(OSH_E_INVALID, "Conv: channels %lld not divisible by group %d", channels, at->group);
+    if (w[1] != channels / at->group)
+        return fail(OSH_E_INVALID, "Conv: weight in-channels %lld != %lld", (long long)w[1], channels / at->group);
+    if (w[0] % at->group != 0)
+        return fail(OSH_E_INVALID, "Conv: output channels %lld not divisible by group %d", (long long)w[0],
+                    at->group);
+    for (int i = 0; i < at->n_strides; i++)
+        if (at->strides[i] <= 0) return fail(OSH_E_INVALID, "Conv: stride must be positive");
+    for (int i = 0; i < at->n_dilations; i++)
+        if (at->dilations[i] <= 0) return fail(OSH_E_INVALID, "Conv: dilation must be positive");
+    for (int i = 0; i < at->n_pads; i++)
+        if (at->pads[i] < 0) return fail(OSH_E_UNSUPPORTED, "Conv: negative pads are not supported");
+    return OSH_OK;
+}
+
+// ---------------------------------------------------------------- depthwise
+
+template <int ACT>
+__global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const float *__restrict__ x,
+                                                      const float *__restrict__ w, const float *__restrict__ bias,
+                                                      float *__restrict__ y) {
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long total = (long long)p.n * p.m * p.oh * p.ow;
+    if (idx >= total) return;
+    int ox = (int)(idx % p.ow);
+    long long t = idx / p.ow;
+    int oy = (int)(t % p.oh);
+    t /= p.oh;
+    int c = (int)(t % p.m);
+    int n = (int)(t / p.m);
+    const float *xc = x + ((long long)n * p.c + c) * p.h * p.w;
+    const float *wc = w + (long long)c * p.kh * p.kw;
+    float acc = bias ? bias[c] : 0.f;
+    for (int ky = 0; ky < p.kh; ky++) {
+        int iy = oy * p.sh - p.pt + ky * p.dh;
+        if ((unsigned)iy >= (unsigned)p.h) continue;
+        for (int kx = 0; kx < p.kw; kx++) {
+            int ix = ox * p.sw - p.pl + kx * p.dw;
+            if ((unsigned)ix >= (unsigned)p.w) continue;
+            acc = __builtin_fmaf(wc[ky * p.kw + kx], xc[(long long)iy * p.w + ix], acc);
+        }
+    }
+    y[idx] = activate<ACT>(acc);
+}
+
+enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3 };
+
+static ConvAlgo select_algo(const osh_conv_params *p) {
+    if (p->group == p->c && p->group == p->m && p->group > 1) return ALGO_DEPTHWISE;
+    if (p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 && p->oh == p->h &&
+        p->ow == p->w)
+        return ALGO_POINTWISE;
+    if (conv3x3_eligible(p)) return ALGO_DIRECT3X3;
+    return ALGO_IM2COL;
+}
+
+static osh_status check_params(const osh_conv_params *p) {
+    if (!p) return fail(OSH_E_INVALID, "Conv: params is NULL");
+    if (p->n <= 0 || p->c <= 0 || p->h <= 0 || p->w <= 0 || p->m <= 0 || p->kh <= 0 || p->kw <= 0 ||
+        p->group <= 0 || p->sh <= 0 || p->sw <= 0 || p->dh <= 0 || p->dw <= 0 || p->oh <= 0 || p->ow <= 0)
+        return fail(OSH_E_INVALID, "Conv: non-positive size in params");
+    if (p->pt < 0 || p->pl < 0) return fail(OSH_E_UNSUPPORTED, "Conv: negative pads are not supported");
+    if (p->c % p->group != 0 || p->m % p->group != 0)
+        return fail(OSH_E_INVALID, "Conv: channels not divisible by group");
+    long long cpg = p->c / p->group;
+    if (cpg * p->kh * p->kw > (1LL << 30) || (long long)p->oh * p->ow > (1LL << 30) ||
+        (long long)p->n * p->group > 65535)
+        return fail(OSH_E_UNSUPPORTED, "Conv: problem exceeds the launch limits");
+    return OSH_OK;
+}
+
+}  // namespace osh
+
+extern "C" {
+
+OSH_API osh_status osh_conv_infer_shape(const osh_conv_attrs *at, const int64_t x[4], const int64_t w[4],
+                                        int64_t y[4]) {
+    osh_status st = check_attrs(at, x, w);
+    if (st != OSH_OK) return st;
+    if (!y) return fail(OSH_E_INVALID, "Conv: y_dims is NULL");
+    const int spatial = 2;
+    y[0] = x[0];
+    y[1] = w[0];
+    for (int i = 0; i < spatial; i++) {
+        int kernel = at->n_kernel_shape > i ? at->kernel_shape[i] : (int)w[2 + i];
+        int stride = at->n_strides > i ? at->strides[i] : 1;
+        int dilation = at->n_dilations > i ? at->dilations[i] : 1;
+        int pad_begin = at->n_pads > i ? at->pads[i] : 0;
+        // DnnOps.cs:174-175: the end pad is read only when more than 2*spatial pads are given,
+        // so a 4-entry pads list makes the shape use the begin pad twice.
+        int pad_end = at->n_pads > 2 * spatial ? at->pads[spatial + i] : pad_begin;
+        if (at->auto_pad != OSH_PAD_NOTSET) auto_pad(at->auto_pad, (int)x[2 + i], kernel, stride, dilation, &pad_begin, &pad_end);
+        int o = spatial_out((int)x[2 + i], kernel, stride, dilation, pad_begin, pad_end);
+        if (o <= 0) return fail(OSH_E_INVALID, "Conv: output spatial size %d is not positive", o);
+        y[2 + i] = o;
+    }
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_conv_resolve(const osh_conv_attrs *at, const int64_t x[4], const int64_t w[4],
+                                    osh_conv_params *p) {
+    if (!p) return fail(OSH_E_INVALID, "Conv: out is NULL");
+    int64_t y[4];
+    osh_status st = osh_conv_infer_shape(at, x, w, y);
+    if (st != OSH_OK) return st;
+    const int spatial = 2;
+    int strides[2], dil[2], pads[4];
+    for (int i = 0; i < spatial; i++) {
+        int kernel = at->n_kernel_shape > i ? at->kernel_shape[i] : (int)w[2 + i];
+        strides[i] = at->n_strides > i ? at->strides[i] : 1;
+        dil[i] = at->n_dilations > i ? at->dilations[i] : 1;
+        if (at->auto_pad != OSH_PAD_NOTSET) {
+            auto_pad(at->auto_pad, (int)x[2 + i], kernel, strides[i], dil[i], &pads[i], &pads[spatial + i]);
+        } else {
+            pads[i] = at->n_pads > i ? at->pads[i] : 0;
+            pads[spatial + i] = at->n_pads > spatial + i ? at->pads[spatial + i] : pads[i];
+        }
+    }
+    memset(p, 0, sizeof(*p));
+    p->n = (int)x[0]; p->c = (int)x[1]; p->h = (int)x[2]; p->w = (int)x[3];
+    // The kernels take their taps from the weight tensor (as ConvLayer's CPU kernels do).
+    p->m = (int)w[0]; p->kh = (int)w[2]; p->kw = (int)w[3]; p->group = at->group;
+    p->sh = strides[0]; p->sw = strides[1]; p->dh = dil[0]; p->dw = dil[1];
+    p->pt = pads[0]; p->pl = pads[1]; p->pb = pads[2]; p->pr = pads[3];
+    p->oh = (int)y[2]; p->ow = (int)y[3];
+    return check_params(p);
+}
+
+OSH_API osh_status osh_conv_packed_weight_bytes(const osh_conv_params *p, size_t *bytes) {
+    osh_status st = check_params(p);
+    if (st != OSH_OK) return st;
+    if (!bytes) return fail(OSH_E_INVALID, "bytes is NULL");
+    size_t oihw = (size_t)p->m * (p->c / p->group) * p->kh * p->kw * sizeof(float);
+    *bytes = select_algo(p) == ALGO_DIRECT3X3 ? conv3x3_packed_bytes(p) : oihw;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *d_w, void *d_packed,
+                                         osh_stream s) {
+    osh_status st = check_params(p);
+    if (st != OSH_OK) return st;
+    if (!d_w || !d_packed) return fail(OSH_E_INVALID, "Conv pack: NULL pointer");
+    if (select_algo(p) == ALGO_DIRECT3X3) return conv3x3_pack(p, d_w, d_packed, to_stream(s));
+    size_t oihw = (size_t)p->m * (p->c / p->group) * p->kh * p->kw * sizeof(float);
+    OSH_HIP_CHECK(hipMemcpyAsync(d_packed, d_w, oihw, hipMemcpyDeviceToDevice, to_stream(s)));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,
+                                  const float *d_bias, int act, float *d_y, osh_stream s) {
+    osh_status st = check_params(p);
+    if (st != OSH_OK) return st;
+    if (!d_x || !d_wpacked || !d_y) return fail(OSH_E_INVALID, "Conv: NULL tensor pointer");
+    if (act < OSH_ACT_NONE || act > OSH_ACT_SILU) return fail(OSH_E_INVALID, "Conv: unknown activation %d", act);
+    hipStream_t stream = to_stream(s);
+    const float *w = static_cast<const float *>(d_wpacked);
+    const int cpg = p->c / p->group, opg = p->m / p->group;
+    const long long in_hw = (long long)p->h * p->w, out_hw = (long long)p->oh * p->ow;
+
+    switch (select_algo(p)) {
+    case ALGO_DEPTHWISE: {
+        long long total = (long long)p->n * p->m * out_hw;
+        dim3 grid((unsigned)((total + 255) / 256));
+        OSH_DISPATCH_ACT(act, ACT,
+                         hipLaunchKernelGGL(dw_conv_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, w, d_bias, d_y));
+        OSH_LAUNCH_CHECK("dw_conv_kernel");
+        return OSH_OK;
+    }
+    case ALGO_DIRECT3X3:
+        return conv3x3_launch(p, d_x, w, d_bias, act, d_y, stream);
+    case ALGO_POINTWISE:
+    case ALGO_IM2COL: {
+        const bool pw = select_algo(p) == ALGO_POINTWISE;
+        IgemmArgs a{};
+        a.M = opg;
+        a.N = (int)out_hw;
+        a.K = cpg * p->kh * p->kw;
+        a.A = w;
+        a.lda = a.K;
+        a.strideA = 0;
+        a.strideA_in = (long long)opg * a.K;
+        a.B = d_x;
+        a.ldb = (int)in_hw;
+        a.strideB = (long long)p->c * in_hw;
+        a.strideB_in = (long long)cpg * in_hw;
+        a.C = d_y;
+        a.ldc = (int)out_hw;
+        a.strideC = (long long)p->m * out_hw;
+        a.strideC_in = (long long)opg * out_hw;
+        a.row_bias = d_bias;
+        a.bias_stride = opg;
+        a.zdiv = p->group;
+        a.H = p->h; a.W = p->w; a.KH = p->kh; a.KW = p->kw;
+        a.sh = p->sh; a.sw = p->sw; a.dh = p->dh; a.dw = p->dw;
+        a.pt = p->pt; a.pl = p->pl; a.OW = p->ow;
+        return launch_igemm(a, p->n * p->group, pw ? B_DENSE : B_IM2COL, act, stream);
+    }
+    }
+    return fail(OSH_E_INVALID, "Conv: no kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,406 @@
+// osh_dqmm.hip -- DynamicQuantizeMatMul and DynamicQuantizeLinear on gfx950.
+//
+// Reference: DynamicQuantizeMatMulLayer.Forward (src/OnnxSharp/Ops/QuantizedMatMulOps.cs:115-201),
+// Quantizer.MinMax (src/OnnxSharp/Tensors/Quantization.cs:109-181), QuantizeAndWiden
+// (QuantizedMatMulOps.cs:280-335) and the zero-point identity of PackedInt8Weights
+// (src/OnnxSharp/Kernels/Int8Gemm.cs:66-70).
+//
+// Pipeline (three launches, all on the caller's stream):
+//   1. dqmm_minmax_kernel   grid-stride min/max of A (0 included, NaN skipped) into per-block
+//                           partials.
+//   2. dqmm_quantize_kernel every block reduces the partials to scale = (max-min)/255 (1 if
+//                           not > 0), zp = clamp(rne(-min/scale)), inv = 1/scale -- single IEEE
+//                           ops, no contraction -- then q = clamp(rne(x*inv) + zp, 0, 255); stores
+//                           a'' = q - 128 as s8 in the MFMA operand layout, the per-row sums of
+//                           a'', and a per-row flag for x*inv = NaN (the reference's q is then
+//                           NaN and its whole output row is NaN).
+//   3. dqmm_gemm_kernel     v_mfma_i32_32x32x32_i8 over a'' x w'' (both s8), then the exact
+//                           integer correction
+//                             acc = sum a''w'' + off_j*rowsum_i + alpha*colsum_j + K*alpha*off_j
+//                           with alpha = 128 - zp and w' = w'' + off_j (w'' is the raw s8
+//                           weight, or w - 128 for u8 weights; off_j = (u8 ? 128 : 0) - w_zp_j),
+//                           which equals sum (q - zp)(w - w_zp) exactly; then
+//                           out = fmaf((float)acc, scale * w_scale[j], bias[j]).
+//
+// Operand layout (both operands): fragment f = (tile, kstep) holds 64 lanes x 16 bytes;
+// lane l carries row/column (l & 31) of the tile and k = kstep*32 + 16*(l >> 5) + byte.
+// A and B use the same k assignment, so the MFMA pairs matching k regardless of the
+// hardware's internal k order.
+#include "osh_common.h"
+
+using namespace osh;
+
+namespace osh {
+
+constexpr int DQ_MINMAX_BLOCKS = 256;
+constexpr int DQ_THREADS = 256;
+
+struct DqScratch {  // layout of the caller's scratch buffer
+    float partial_min[DQ_MINMAX_BLOCKS];
+    float partial_max[DQ_MINMAX_BLOCKS];
+    int zp;
+    float scale;
+    float inv;
+    int pad[61];
+    // followed by: int rowsum[mpad]; int rownan[mpad]; int8 a_packed[mpad * kpad]
+};
+
+__host__ __device__ static inline int pad32(int v) { return (v + 31) & ~31; }
+
+static size_t scratch_bytes(int m, int k) {
+    return sizeof(DqScratch) + (size_t)pad32(m) * 8 + (size_t)pad32(m) * pad32(k);
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = __builtin_fminf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Block-level min/max of (lo, hi) into thread 0's return values.
+__device__ void block_minmax(float &lo, float &hi) {
+    __shared__ float smin[DQ_THREADS / 64], smax[DQ_THREADS / 64];
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        smin[w] = lo;
+        smax[w] = hi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < DQ_THREADS / 64; i++) {
+            lo = __builtin_fminf(lo, smin[i]);
+            hi = __builtin_fmaxf(hi, smax[i]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(DQ_THREADS) void dqmm_minmax_kernel(const float *__restrict__ a, long long n,
+                                                                  DqScratch *__restrict__ sc, int *__restrict__ rowsum,
+                                                                  int rows) {
+    float lo = 0.f, hi = 0.f;  // 0 is always inside the range (Quantization.cs:115-116)
+    long long stride = (long long)gridDim.x * blockDim.x;
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    // 16-byte loads when the base is aligned (all callers pass tensor bases)
+    long long n4 = (reinterpret_cast<uintptr_t>(a) & 15) == 0 ? n / 4 : 0;
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    for (long long j = i; j < n4; j += stride) {
+        float4 v = a4[j];
+        // NaN lanes are skipped (compare-false keeps the running value)
+        lo = v.x < lo ? v.x : lo; hi = v.x > hi ? v.x : hi;
+        lo = v.y < lo ? v.y : lo; hi = v.y > hi ? v.y : hi;
+        lo = v.z < lo ? v.z : lo; hi = v.z > hi ? v.z : hi;
+        lo = v.w < lo ? v.w : lo; hi = v.w > hi ? v.w : hi;
+    }
+    for (long long j = n4 * 4 + i; j < n; j += stride) {
+        float v = a[j];
+        lo = v < lo ? v : lo;
+        hi = v > hi ? v : hi;
+    }
+    for (long long j = i; j < 2 * (long long)rows; j += stride) rowsum[j] = 0;  // rowsum and rownan
+    block_minmax(lo, hi);
+    if (threadIdx.x == 0) {
+        sc->partial_min[blockIdx.x] = lo;
+        sc->partial_max[blockIdx.x] = hi;
+    }
+}
+
+// Every consumer block reduces the per-block partials itself (a few hundred
+// floats from L2), so no grid-wide counter is needed and the scratch needs no
+// initialisation.  Block 0 publishes the parameters for later launches.
+__device__ void dq_params(DqScratch *__restrict__ sc, int nparts, int *__restrict__ qparams, float &inv_out,
+                          int &zp_out) {
+    __shared__ float s_inv;
+    __shared__ int s_zp;
+    float lo = 0.f, hi = 0.f;
+    for (int b = threadIdx.x; b < nparts; b += blockDim.x) {
+        lo = __builtin_fminf(lo, sc->partial_min[b]);
+        hi = __builtin_fmaxf(hi, sc->partial_max[b]);
+    }
+    block_minmax(lo, hi);
+    if (threadIdx.x == 0) {
+        // QuantizedMatMulOps.cs:151-155
+        float scale = (hi - lo) / 255.0f;
+        if (!(scale > 0.0f)) scale = 1.0f;
+        float zf = __builtin_rintf(-lo / scale);
+        int zp = (int)zf;
+        zp = zp < 0 ? 0 : (zp > 255 ? 255 : zp);
+        float inv = 1.0f / scale;  // QuantizeAndWiden multiplies by the reciprocal (QuantizedMatMulOps.cs:282)
+        s_inv = inv;
+        s_zp = zp;
+        if (blockIdx.x == 0) {
+            sc->scale = scale;
+            sc->zp = zp;
+            sc->inv = inv;
+            if (qparams) {
+                qparams[0] = __float_as_int(scale);
+                qparams[1] = zp;
+            }
+        }
+    }
+    __syncthreads();
+    inv_out = s_inv;
+    zp_out = s_zp;
+}
+
+// q = clamp(rne(x * inv) + zp, 0, 255) as QuantizeAndWiden computes it in float.
+// A NaN product yields 0 here; callers flag it (the reference's q is NaN then).
+__device__ __forceinline__ int quantize_one(float x, float inv, float zpf) {
+    float q = __builtin_rintf(x * inv) + zpf;
+    q = __builtin_fminf(255.0f, __builtin_fmaxf(0.0f, q));
+    return (int)q;
+}
+
+// One thread per (row, 16-wide k segment): writes one 16-byte operand slot.
+__global__ __launch_bounds__(DQ_THREADS) void dqmm_quantize_kernel(const float *__restrict__ a, int m, int k,
+                                                                    DqScratch *__restrict__ sc, int nparts,
+                                                                    int *__restrict__ qparams,
+                                                                    int *__restrict__ rowsum,
+                                                                    int8_t *__restrict__ apk) {
+    float inv;
+    int zp;
+    dq_params(sc, nparts, qparams, inv, zp);
+    const float zpf = (float)zp;
+    const int kpad = pad32(k), segs = kpad / 16;
+    long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long total = (long long)pad32(m) * segs;
+    if (t >= total) return;
+    int row = (int)(t / segs), seg = (int)(t % segs);
+    int vals[16];
+    int sum = 0;
+    bool nan = false;
+    const float *src = a + (long long)row * k + seg * 16;
+#pragma unroll
+    for (int b = 0; b < 16; b++) {
+        int kk = seg * 16 + b;
+        int v = 0;  // padding rows/columns carry a'' = 0
+        if (row < m && kk < k) {
+            float x = src[b];
+            nan |= !(x * inv == x * inv);
+            v = quantize_one(x, inv, zpf) - 128;
+            sum += v;
+        }
+        vals[b] = v;
+    }
+    i32x4 packed;
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+        packed[w] = (vals[4 * w] & 0xff) | ((vals[4 * w + 1] & 0xff) << 8) | ((vals[4 * w + 2] & 0xff) << 16) |
+                    ((vals[4 * w + 3] & 0xff) << 24);
+    // fragment (row/32, seg/2), lane = (row & 31) + 32 * (seg & 1)
+    long long frag = (long long)(row >> 5) * (kpad / 32) + (seg >> 1);
+    int lane = (row & 31) + 32 * (seg & 1);
+    reinterpret_cast<i32x4 *>(apk)[frag * 64 + lane] = packed;
+    if (row < m && sum != 0) atomicAdd(&rowsum[row], sum);
+    if (row < m && nan) atomicOr(&rowsum[pad32(m) + row], 1);
+}
+
+// DynamicQuantizeLinear output: u8 q in the input's own layout.
+__global__ __launch_bounds__(DQ_THREADS) void dql_quantize_kernel(const float *__restrict__ x, long long n,
+                                                                   DqScratch *__restrict__ sc, int nparts,
+                                                                   int *__restrict__ qparams,
+                                                                   uint8_t *__restrict__ q) {
+    float inv;
+    int zp;
+    dq_params(sc, nparts, qparams, inv, zp);
+    const float zpf = (float)zp;
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long stride = (long long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) q[i] = (uint8_t)quantize_one(x[i], inv, zpf);
+}
+
+// Packed weight buffer: int8 fragments [npad/32][kpad/32][64][16], then int colsum[npad],
+// then int off[npad].
+static size_t packed_w_bytes(int k, int n) { return (size_t)pad32(n) * pad32(k) + (size_t)pad32(n) * 8; }
+
+__global__ void dqmm_pack_kernel(int k, int n, const void *__restrict__ w, int w_signed,
+                                 const int *__restrict__ wzp, int n_wzp, int8_t *__restrict__ out,
+                                 int *__restrict__ colsum, int *__restrict__ off) {
+    // one thread per column
+    int j = blockIdx.x * blockDim.x + threadIdx.x;
+    int npad = pad32(n), kpad = pad32(k);
+    if (j >= npad) return;
+    int zp = (j < n && n_wzp > 0) ? (n_wzp == 1 ? wzp[0] : wzp[j]) : 0;
+    int o = (w_signed ? 0 : 128) - zp;
+    int s = 0;
+    for (int kk = 0; kk < kpad; kk++) {
+        int v = 0;
+        if (j < n && kk < k) {
+            long long idx = (long long)kk * n + j;
+            v = w_signed ? (int)reinterpret_cast<const int8_t *>(w)[idx]
+                         : (int)reinterpret_cast<const uint8_t *>(w)[idx] - 128;
+            s += v;
+        }
+        long long frag = (long long)(j >> 5) * (kpad / 32) + (kk >> 5);
+        int lane = (j & 31) + 32 * ((kk >> 4) & 1);
+        out[(frag * 64 + lane) * 16 + (kk & 15)] = (int8_t)v;
+    }
+    colsum[j] = s;
+    off[j] = j < n ? o : 0;
+}
+
+// Wave tile 32 x 32, 4 waves per block as 2 x 2 -> 64 x 64 outputs per block.
+__global__ __launch_bounds__(256) void dqmm_gemm_kernel(int m, int k, int n, const int8_t *__restrict__ apk,
+                                                        const int8_t *__restrict__ wpk,
+                                                        const int *__restrict__ colsum, const int *__restrict__ off,
+                                                        const int *__restrict__ rowsum,
+                                                        const DqScratch *__restrict__ sc,
+                                                        const float *__restrict__ wscale, int n_wscale,
+                                                        const float *__restrict__ bias, float *__restrict__ out,
+                                                        int *__restrict__ acc_out) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int mt = blockIdx.y * 2 + (wave >> 1);
+    const int nt = blockIdx.x * 2 + (wave & 1);
+    const int kpad = pad32(k), ks = kpad / 32;
+    if (mt * 32 >= pad32(m) || nt * 32 >= pad32(n)) return;
+    const i32x4 *A = reinterpret_cast<const i32x4 *>(apk) + (long long)mt * ks * 64 + lane;
+    const i32x4 *B = reinterpret_cast<const i32x4 *>(wpk) + (long long)nt * ks * 64 + lane;
+    i32x16 acc = {};
+    int s = 0;
+    for (; s + 4 <= ks; s += 4) {
+        i32x4 a0 = A[(s + 0) * 64], a1 = A[(s + 1) * 64], a2 = A[(s + 2) * 64], a3 = A[(s + 3) * 64];
+        i32x4 b0 = B[(s + 0) * 64], b1 = B[(s + 1) * 64], b2 = B[(s + 2) * 64], b3 = B[(s + 3) * 64];
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a2, b2, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a3, b3, acc, 0, 0, 0);
+    }
+    for (; s < ks; s++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[s * 64], B[s * 64], acc, 0, 0, 0);
+
+    const int j = nt * 32 + (lane & 31);
+    const int mpad = pad32(m);
+    if (j >= n) return;
+    // two's-complement wrap-around is exact as long as the final sum fits in int32
+    const unsigned alpha = (unsigned)(128 - sc->zp);
+    const unsigned offj = (unsigned)off[j];
+    const unsigned colterm = alpha * (unsigned)colsum[j] + (unsigned)k * alpha * offj;
+    const float comb = sc->scale * (n_wscale == 1 ? wscale[0] : wscale[j]);  // CombinedScale, :203-221
+    const float b = bias ? bias[j] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        int i = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (i < m) {
+            int v = (int)((unsigned)acc[r] + offj * (unsigned)rowsum[i] + colterm);
+            if (acc_out) acc_out[(long long)i * n + j] = v;
+            float o = __builtin_fmaf((float)v, comb, b);
+            if (rowsum[mpad + i]) o = __builtin_nanf("");
+            out[(long long)i * n + j] = o;
+        }
+    }
+}
+
+static osh_status run_minmax(const float *a, long long count, DqScratch *sc, int *rowsum, int rows, int *nparts,
+                             hipStream_t st) {
+    long long blocks = (count / 4 + DQ_THREADS - 1) / DQ_THREADS;
+    if (blocks < 1) blocks = 1;
+    if (blocks > DQ_MINMAX_BLOCKS) blocks = DQ_MINMAX_BLOCKS;
+    hipLaunchKernelGGL(dqmm_minmax_kernel, dim3((unsigned)blocks), dim3(DQ_THREADS), 0, st, a, count, sc, rowsum,
+                       rows);
+    *nparts = (int)blocks;
+    OSH_LAUNCH_CHECK("dqmm_minmax_kernel");
+    return OSH_OK;
+}
+
+}  // namespace osh
+
+extern "C" {
+
+OSH_API osh_status osh_dqmm_packed_weight_bytes(int k, int n, size_t *bytes) {
+    if (k <= 0 || n <= 0 || !bytes) return fail(OSH_E_INVALID, "DQM: bad size");
+    *bytes = packed_w_bytes(k, n);
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_dqmm_scratch_bytes(int m, int k, size_t *bytes) {
+    if (m < 0 || k <= 0 || !bytes) return fail(OSH_E_INVALID, "DQM: bad size");
+    *bytes = scratch_bytes(m, k);
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_dqmm_pack_weights(int k, int n, const void *d_w, int w_signed, const int32_t *h_wzp,
+                                         int n_wzp, void *d_packed, osh_stream s) {
+    if (k <= 0 || n <= 0 || !d_w || !d_packed) return fail(OSH_E_INVALID, "DQM pack: bad argument");
+    if (n_wzp != 0 && n_wzp != 1 && n_wzp != n)
+        return fail(OSH_E_INVALID, "DQM pack: w_zero_point has %d entries (need 1 or %d)", n_wzp, n);
+    if (n_wzp > 0 && !h_wzp) return fail(OSH_E_INVALID, "DQM pack: w_zero_point is NULL");
+    if ((long long)k * 255 * 255 > 2147483647LL)
+        return fail(OSH_E_UNSUPPORTED, "DQM: K=%d can overflow the int32 accumulator", k);
+    for (int i = 0; i < n_wzp; i++)
+        if (h_wzp[i] < -32768 || h_wzp[i] > 32767)
+            return fail(OSH_E_UNSUPPORTED, "DQM pack: weight zero point %d out of range", h_wzp[i]);
+    hipStream_t st = to_stream(s);
+    int *d_zp = nullptr;
+    if (n_wzp > 0) {
+        OSH_HIP_CHECK(hipMalloc((void **)&d_zp, sizeof(int) * n_wzp));
+        hipError_t e = hipMemcpyAsync(d_zp, h_wzp, sizeof(int) * n_wzp, hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) {
+            (void)hipFree(d_zp);
+            return fail(OSH_E_DEVICE, "DQM pack: copy of zero points failed: %s", hipGetErrorString(e));
+        }
+    }
+    int8_t *frag = static_cast<int8_t *>(d_packed);
+    int *colsum = reinterpret_cast<int *>(frag + (size_t)pad32(n) * pad32(k));
+    int *off = colsum + pad32(n);
+    hipLaunchKernelGGL(dqmm_pack_kernel, dim3((pad32(n) + 63) / 64), dim3(64), 0, st, k, n, d_w, w_signed, d_zp,
+                       n_wzp, frag, colsum, off);
+    hipError_t le = hipGetLastError();
+    hipError_t se = hipStreamSynchronize(st);
+    if (d_zp) (void)hipFree(d_zp);
+    if (le != hipSuccess) return fail(OSH_E_DEVICE, "dqmm_pack_kernel launch failed: %s", hipGetErrorString(le));
+    if (se != hipSuccess) return fail(OSH_E_DEVICE, "DQM pack failed: %s", hipGetErrorString(se));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_dqmm_u8s8(int m, int k, int n, const float *d_a, const void *d_wpacked,
+                                 const float *d_wscale, int n_wscale, const float *d_bias, float *d_out,
+                                 int32_t *d_acc, int32_t *d_qparams, void *d_scratch, osh_stream s) {
+    if (m < 0 || k <= 0 || n <= 0) return fail(OSH_E_INVALID, "DQM: bad size m=%d k=%d n=%d", m, k, n);
+    if (m == 0) return OSH_OK;
+    if (!d_a || !d_wpacked || !d_wscale || !d_out || !d_scratch) return fail(OSH_E_INVALID, "DQM: NULL pointer");
+    if (n_wscale != 1 && n_wscale != n) return fail(OSH_E_INVALID, "DQM: w_scale has %d entries", n_wscale);
+    if ((long long)k * 255 * 255 > 2147483647LL)
+        return fail(OSH_E_UNSUPPORTED, "DQM: K=%d can overflow the int32 accumulator", k);
+    if (pad32(m) / 32 > 2 * 65535) return fail(OSH_E_UNSUPPORTED, "DQM: m too large");
+    hipStream_t st = to_stream(s);
+    DqScratch *sc = static_cast<DqScratch *>(d_scratch);
+    int *rowsum = reinterpret_cast<int *>(sc + 1);
+    int8_t *apk = reinterpret_cast<int8_t *>(rowsum + 2 * pad32(m));
+    int nparts = 0;
+    osh_status r = run_minmax(d_a, (long long)m * k, sc, rowsum, pad32(m), &nparts, st);
+    if (r != OSH_OK) return r;
+    long long qthreads = (long long)pad32(m) * (pad32(k) / 16);
+    hipLaunchKernelGGL(dqmm_quantize_kernel, dim3((unsigned)((qthreads + DQ_THREADS - 1) / DQ_THREADS)),
+                       dim3(DQ_THREADS), 0, st, d_a, m, k, sc, nparts, (int *)d_qparams, rowsum, apk);
+    OSH_LAUNCH_CHECK("dqmm_quantize_kernel");
+    const int8_t *frag = static_cast<const int8_t *>(d_wpacked);
+    const int *colsum = reinterpret_cast<const int *>(frag + (size_t)pad32(n) * pad32(k));
+    const int *off = colsum + pad32(n);
+    dim3 grid((pad32(n) / 32 + 1) / 2, (pad32(m) / 32 + 1) / 2);
+    hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
+                       d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
+    OSH_LAUNCH_CHECK("dqmm_gemm_kernel");
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_dynamic_quantize_linear(int64_t n, const float *d_x, uint8_t *d_q, int32_t *d_qparams,
+                                               void *d_scratch, osh_stream s) {
+    if (n <= 0 || !d_x || !d_q || !d_scratch) return fail(OSH_E_INVALID, "DQL: bad argument");
+    hipStream_t st = to_stream(s);
+    DqScratch *sc = static_cast<DqScratch *>(d_scratch);
+    int *rowsum = reinterpret_cast<int *>(sc + 1);
+    int nparts = 0;
+    osh_status r = run_minmax(d_x, n, sc, rowsum, 0, &nparts, st);
+    if (r != OSH_OK) return r;
+    long long blocks = (n + DQ_THREADS - 1) / DQ_THREADS;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(dql_quantize_kernel, dim3((unsigned)blocks), dim3(DQ_THREADS), 0, st, d_x, n, sc, nparts,
+                       (int *)d_qparams, d_q);
+    OSH_LAUNCH_CHECK("dql_quantize_kernel");
+    return OSH_OK;
+}
+
+}  // extern "C"

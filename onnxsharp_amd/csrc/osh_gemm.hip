@@ -1,0 +1,128 @@
+// osh_gemm.hip -- MatMul (+ fused column bias) entry points of the C ABI.
+//
+// Replaces GemmKernel.Multiply / MultiplyPacked / MultiplyBatched
+// (src/OnnxSharp/Tensors/GemmKernel.cs:131-269,284-405,675-852) and the shape
+// rules of MatMulLayer (src/OnnxSharp/Ops/DnnOps.cs:2789-3103).
+#include <algorithm>
+
+#include "osh_igemm.h"
+#include "osh_launch.h"
+
+using namespace osh;
+
+namespace osh {
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+osh_status launch_igemm(const IgemmArgs &a, int zcount, int bmode, int act, hipStream_t st) {
+    if (a.M <= 0 || a.N <= 0 || zcount <= 0) return OSH_OK;
+    const bool vec_a = a.K % 4 == 0 && a.lda % 4 == 0 && aligned16(a.A) && a.strideA % 4 == 0 &&
+                       a.strideA_in % 4 == 0;
+    const bool vec_b = bmode == B_DENSE && a.ldb % 4 == 0 && aligned16(a.B) && a.strideB % 4 == 0 &&
+                       a.strideB_in % 4 == 0;
+    // Small-M problems (conv with few output channels) take a 32-row tile.
+    const bool small_m = a.M <= 32;
+    dim3 block(256);
+#define OSH_IG_LAUNCH(BM, BN, WM, WN, BMODE, VA, VB)                                                   \
+    do {                                                                                              \
+        dim3 grid(ceil_div(a.N, BN), ceil_div(a.M, BM), zcount);                                      \
+        OSH_DISPATCH_ACT(act, ACT,                                                                    \
+            hipLaunchKernelGGL((igemm_f32_kernel<BM, BN, WM, WN, BMODE, VA, VB, ACT>), grid, block, 0, \
+                               st, a));                                                               \
+    } while (0)
+#define OSH_IG_SHAPE(BMODE, VA, VB)                                \
+    do {                                                          \
+        if (small_m) OSH_IG_LAUNCH(32, 128, 1, 4, BMODE, VA, VB); \
+        else OSH_IG_LAUNCH(64, 64, 2, 2, BMODE, VA, VB);          \
+    } while (0)
+    if (bmode == B_IM2COL) {
+        if (vec_a) OSH_IG_SHAPE(B_IM2COL, true, false);
+        else OSH_IG_SHAPE(B_IM2COL, false, false);
+    } else {
+        if (vec_a && vec_b) OSH_IG_SHAPE(B_DENSE, true, true);
+        else if (vec_a) OSH_IG_SHAPE(B_DENSE, true, false);
+        else if (vec_b) OSH_IG_SHAPE(B_DENSE, false, true);
+        else OSH_IG_SHAPE(B_DENSE, false, false);
+    }
+#undef OSH_IG_SHAPE
+#undef OSH_IG_LAUNCH
+    OSH_LAUNCH_CHECK("igemm_f32_kernel");
+    return OSH_OK;
+}
+
+}  // namespace osh
+
+extern "C" {
+
+OSH_API osh_status osh_gemm_f32_batched(int batch, int m, int n, int k, const float *d_a, int lda,
+                                        int64_t stride_a, const float *d_b, int ldb, int64_t stride_b,
+                                        const float *d_col_bias, int act, float *d_c, int ldc,
+                                        int64_t stride_c, osh_stream s) {
+    if (batch < 0 || m < 0 || n < 0 || k < 0) return fail(OSH_E_INVALID, "negative GEMM size");
+    if (batch == 0 || m == 0 || n == 0) return OSH_OK;
+    if (!d_a || !d_b || !d_c) return fail(OSH_E_INVALID, "A, B and C must be non-NULL");
+    if (lda < k || ldb < n || ldc < n) return fail(OSH_E_INVALID, "leading dimension smaller than the row");
+    if (batch > 65535) return fail(OSH_E_UNSUPPORTED, "batch %d exceeds the grid limit", batch);
+    IgemmArgs a{};
+    a.M = m; a.N = n; a.K = k;
+    a.A = d_a; a.lda = lda; a.strideA = stride_a;
+    a.B = d_b; a.ldb = ldb; a.strideB = stride_b;
+    a.C = d_c; a.ldc = ldc; a.strideC = stride_c;
+    a.col_bias = d_col_bias;
+    a.zdiv = 1;
+    return launch_igemm(a, batch, B_DENSE, act, to_stream(s));
+}
+
+OSH_API osh_status osh_gemm_f32(int m, int n, int k, const float *d_a, int lda, const float *d_b, int ldb,
+                                const float *d_col_bias, const float *d_row_bias, const float *d_col_scale,
+                                int act, float *d_c, int ldc, osh_stream s) {
+    if (m < 0 || n < 0 || k < 0) return fail(OSH_E_INVALID, "negative GEMM size");
+    if (m == 0 || n == 0) return OSH_OK;
+    if (!d_a || !d_b || !d_c) return fail(OSH_E_INVALID, "A, B and C must be non-NULL");
+    if (lda < k || ldb < n || ldc < n) return fail(OSH_E_INVALID, "leading dimension smaller than the row");
+    IgemmArgs a{};
+    a.M = m; a.N = n; a.K = k;
+    a.A = d_a; a.lda = lda;
+    a.B = d_b; a.ldb = ldb;
+    a.C = d_c; a.ldc = ldc;
+    a.col_bias = d_col_bias;
+    a.row_bias = d_row_bias;
+    a.col_scale = d_col_scale;
+    a.zdiv = 1;
+    return launch_igemm(a, 1, B_DENSE, act, to_stream(s));
+}
+
+// MatMul numpy broadcast (MatMulLayer.GetMemoryShapes, src/OnnxSharp/Ops/DnnOps.cs:2840-2900):
+// rank-1 operands are promoted ([k] -> [1,k] for A, [k] -> [k,1] for B) and the
+// promoted axis is dropped from the output; batch axes align right and take
+// the larger extent.
+OSH_API osh_status osh_matmul_infer_shape(const int64_t *a_dims, int ra, const int64_t *b_dims, int rb,
+                                          int64_t *y_dims, int *ry) {
+    if (!a_dims || !b_dims || !y_dims || !ry) return fail(OSH_E_INVALID, "NULL argument");
+    if (ra < 1 || rb < 1 || ra > 8 || rb > 8) return fail(OSH_E_INVALID, "MatMul rank out of range");
+    int64_t A[8], B[8];
+    int na = ra, nb = rb;
+    for (int i = 0; i < ra; i++) A[i] = a_dims[i];
+    for (int i = 0; i < rb; i++) B[i] = b_dims[i];
+    bool a1 = ra == 1, b1 = rb == 1;
+    if (a1) { A[1] = A[0]; A[0] = 1; na = 2; }
+    if (b1) { B[1] = 1; nb = 2; }
+    int64_t m = A[na - 2], k = A[na - 1], k2 = B[nb - 2], n = B[nb - 1];
+    if (k != k2) return fail(OSH_E_INVALID, "MatMul: K mismatch (%lld vs %lld)", (long long)k, (long long)k2);
+    int batch_rank = std::max(na, nb) - 2;
+    int out = 0;
+    for (int i = 0; i < batch_rank; i++) {
+        int ia = i - (batch_rank - (na - 2)), ib = i - (batch_rank - (nb - 2));
+        int64_t da = ia >= 0 ? A[ia] : 1, db = ib >= 0 ? B[ib] : 1;
+        if (da != db && da != 1 && db != 1)
+            return fail(OSH_E_INVALID, "MatMul: batch dims %lld and %lld do not broadcast", (long long)da,
+                        (long long)db);
+        y_dims[out++] = std::max(da, db);
+    }
+    if (!a1) y_dims[out++] = m;
+    if (!b1) y_dims[out++] = n;
+    *ry = out;
+    return OSH_OK;
+}
+
+}  // extern "C"

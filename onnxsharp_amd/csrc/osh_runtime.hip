@@ -1,0 +1,175 @@
+// osh_runtime.hip -- device, memory, copies, streams, events and errors of
+// the C ABI (include/osh_hip.h).  Replaces the Vulkan runtime layer of the
+// reference backend (src/OnnxSharp.Vulkan/VkDevice.cs, VkBufferPool.cs,
+// VkSegment.cs) with plain HIP calls.
+#include <cstdarg>
+#include <cstring>
+
+#include "osh_common.h"
+
+namespace osh {
+
+static thread_local char g_err[512] = "";
+
+osh_status fail(osh_status code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+void clear_error() { g_err[0] = 0; }
+
+const char *last_error() { return g_err; }
+
+__global__ void fill_u8_kernel(uint8_t *__restrict__ p, uint8_t v, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) p[i] = v;
+}
+
+}  // namespace osh
+
+using namespace osh;
+
+extern "C" {
+
+OSH_API const char *osh_last_error(void) { return osh::last_error(); }
+
+OSH_API osh_status osh_device_count(int *count) {
+    if (!count) return fail(OSH_E_INVALID, "count is NULL");
+    OSH_HIP_CHECK(hipGetDeviceCount(count));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_init(int dev, osh_device_info *info) {
+    int n = 0;
+    OSH_HIP_CHECK(hipGetDeviceCount(&n));
+    if (dev < 0 || dev >= n) return fail(OSH_E_INVALID, "device %d out of range (%d devices)", dev, n);
+    OSH_HIP_CHECK(hipSetDevice(dev));
+    if (info) {
+        hipDeviceProp_t p;
+        OSH_HIP_CHECK(hipGetDeviceProperties(&p, dev));
+        memset(info, 0, sizeof(*info));
+        strncpy(info->name, p.name, sizeof(info->name) - 1);
+        strncpy(info->arch, p.gcnArchName, sizeof(info->arch) - 1);
+        info->compute_units = p.multiProcessorCount;
+        info->clock_khz = p.clockRate;
+        info->total_mem = p.totalGlobalMem;
+        info->lds_per_block = p.sharedMemPerBlock;
+        if (strncmp(info->arch, "gfx950", 6) != 0)
+            return fail(OSH_E_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only", dev,
+                        info->arch);
+    }
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_device_synchronize(void) {
+    OSH_HIP_CHECK(hipDeviceSynchronize());
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_malloc(void **d_ptr, size_t bytes) {
+    if (!d_ptr) return fail(OSH_E_INVALID, "d_ptr is NULL");
+    *d_ptr = nullptr;
+    if (bytes == 0) return OSH_OK;
+    hipError_t e = hipMalloc(d_ptr, bytes);
+    if (e != hipSuccess) return fail(OSH_E_NOMEM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_free(void *d_ptr) {
+    if (d_ptr) OSH_HIP_CHECK(hipFree(d_ptr));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_host_alloc(void **h_ptr, size_t bytes) {
+    if (!h_ptr) return fail(OSH_E_INVALID, "h_ptr is NULL");
+    *h_ptr = nullptr;
+    if (bytes == 0) return OSH_OK;
+    hipError_t e = hipHostMalloc(h_ptr, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) return fail(OSH_E_NOMEM, "hipHostMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_host_free(void *h_ptr) {
+    if (h_ptr) OSH_HIP_CHECK(hipHostFree(h_ptr));
+    return OSH_OK;
+}
+
+static osh_status copy(void *dst, const void *src, size_t bytes, hipMemcpyKind kind, osh_stream s) {
+    if (bytes == 0) return OSH_OK;
+    if (!dst || !src) return fail(OSH_E_INVALID, "NULL pointer in copy of %zu bytes", bytes);
+    OSH_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, kind, to_stream(s)));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes, osh_stream s) {
+    return copy(d_dst, h_src, bytes, hipMemcpyHostToDevice, s);
+}
+
+OSH_API osh_status osh_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes, osh_stream s) {
+    return copy(h_dst, d_src, bytes, hipMemcpyDeviceToHost, s);
+}
+
+OSH_API osh_status osh_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes, osh_stream s) {
+    return copy(d_dst, d_src, bytes, hipMemcpyDeviceToDevice, s);
+}
+
+OSH_API osh_status osh_memset_d8(void *d_dst, int value, size_t bytes, osh_stream s) {
+    if (bytes == 0) return OSH_OK;
+    if (!d_dst) return fail(OSH_E_INVALID, "d_dst is NULL");
+    size_t blocks = (bytes + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(fill_u8_kernel, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), (uint8_t *)d_dst,
+                       (uint8_t)value, bytes);
+    OSH_LAUNCH_CHECK("fill_u8_kernel");
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_stream_create(osh_stream *s) {
+    if (!s) return fail(OSH_E_INVALID, "s is NULL");
+    hipStream_t st;
+    OSH_HIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    *s = st;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_stream_destroy(osh_stream s) {
+    if (s) OSH_HIP_CHECK(hipStreamDestroy(to_stream(s)));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_stream_sync(osh_stream s) {
+    OSH_HIP_CHECK(hipStreamSynchronize(to_stream(s)));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_event_create(osh_event *e) {
+    if (!e) return fail(OSH_E_INVALID, "e is NULL");
+    hipEvent_t ev;
+    OSH_HIP_CHECK(hipEventCreate(&ev));
+    *e = ev;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_event_destroy(osh_event e) {
+    if (e) OSH_HIP_CHECK(hipEventDestroy(reinterpret_cast<hipEvent_t>(e)));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_event_record(osh_event e, osh_stream s) {
+    if (!e) return fail(OSH_E_INVALID, "e is NULL");
+    OSH_HIP_CHECK(hipEventRecord(reinterpret_cast<hipEvent_t>(e), to_stream(s)));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_event_elapsed_ms(osh_event start, osh_event stop, float *ms) {
+    if (!start || !stop || !ms) return fail(OSH_E_INVALID, "NULL argument");
+    OSH_HIP_CHECK(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)));
+    OSH_HIP_CHECK(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)));
+    return OSH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,255 @@
+"""Operator layers over the HIP backend, mirroring OnnxSharp's own layers.
+
+Names, attribute meaning and errors follow the reference operators (paths
+relative to the OnnxSharp source tree):
+
+  ConvLayer                    src/OnnxSharp/Ops/DnnOps.cs:101-501
+  MatMulLayer (+ FusedBias)    src/OnnxSharp/Ops/DnnOps.cs:2789-3103
+  DynamicQuantizeMatMulLayer   src/OnnxSharp/Ops/QuantizedMatMulOps.cs:28-376
+  DynamicQuantizeLinearLayer   src/OnnxSharp/Ops/QuantOps.cs:166-227
+
+Shape inference, pad resolution and kernel choice run inside libosh_hip.so
+(C++); this module only moves torch device pointers across the C ABI.  Tensors
+are device tensors (torch on ROCm is used for device memory and streams).
+Shape errors raise OshError (the reference raises OnnxSharpException); shapes
+the backend does not take raise OshUnsupported (an emitter refusing an op).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence
+
+import torch
+
+from . import native as N
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _need_f32(name: str, t: torch.Tensor) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32, got {t.dtype}")
+    return t.contiguous()
+
+
+class ConvLayer:
+    """2-D Conv with an optional fused activation ("Relu" / "Silu").
+
+    Attributes follow ONNX Conv as ConvLayer reads them: an attribute that is
+    not given stays empty (kernel_shape then comes from the weights)."""
+
+    def __init__(self, group: int = 1, kernel_shape: Sequence[int] = (), strides: Sequence[int] = (),
+                 pads: Sequence[int] = (), dilations: Sequence[int] = (), auto_pad: str = "NOTSET",
+                 fused_activation: Optional[str] = None, name: str = "conv"):
+        if auto_pad not in N.AUTO_PAD:
+            raise ValueError(f"Conv '{name}': unknown auto_pad {auto_pad!r}")
+        if fused_activation not in N.ACTIVATIONS:
+            raise ValueError(f"Conv '{name}': activation {fused_activation!r} cannot be fused")
+        self.name = name
+        self.fused_activation = fused_activation
+        a = N.ConvAttrs()
+        a.group = int(group)
+        a.auto_pad = N.AUTO_PAD[auto_pad]
+        for field, count, vals, cap in (("kernel_shape", "n_kernel_shape", kernel_shape, 2),
+                                        ("strides", "n_strides", strides, 2), ("pads", "n_pads", pads, 4),
+                                        ("dilations", "n_dilations", dilations, 2)):
+            vals = list(vals)
+            if len(vals) > cap:
+                raise N.OshUnsupported(N.OSH_E_UNSUPPORTED, f"Conv '{name}': only 2-D convolution is implemented")
+            setattr(a, count, len(vals))
+            arr = getattr(a, field)
+            for i, v in enumerate(vals):
+                arr[i] = int(v)
+        self.attrs = a
+        self._packed = None  # (key, params, buffer)
+
+    # -- shape logic (C++ side of the library)
+    def get_memory_shapes(self, x_shape: Sequence[int], w_shape: Sequence[int]) -> tuple:
+        if len(x_shape) != 4 or len(w_shape) != 4:
+            raise N.OshUnsupported(N.OSH_E_UNSUPPORTED,
+                                   f"Conv '{self.name}': only 2D convolution (NCHW) is implemented")
+        y = N.dims64([0, 0, 0, 0])
+        N.call("osh_conv_infer_shape", C.byref(self.attrs), N.dims64(x_shape), N.dims64(w_shape), y)
+        return tuple(int(v) for v in y)
+
+    def resolve(self, x_shape: Sequence[int], w_shape: Sequence[int]) -> N.ConvParams:
+        self.get_memory_shapes(x_shape, w_shape)
+        p = N.ConvParams()
+        N.call("osh_conv_resolve", C.byref(self.attrs), N.dims64(x_shape), N.dims64(w_shape), C.byref(p))
+        return p
+
+    # -- one-time weight packing (PrepackWeights)
+    def prepack_weights(self, x_shape: Sequence[int], w: torch.Tensor):
+        w = _need_f32("weight", w)
+        p = self.resolve(x_shape, tuple(w.shape))
+        nbytes = C.c_size_t()
+        N.call("osh_conv_packed_weight_bytes", C.byref(p), C.byref(nbytes))
+        buf = torch.empty(max(1, nbytes.value), dtype=torch.uint8, device=w.device)
+        N.call("osh_conv_pack_weights", C.byref(p), _ptr(w), _ptr(buf), C.c_void_p(_stream()))
+        self._packed = ((w.data_ptr(), tuple(w.shape), tuple(x_shape), w._version), p, buf)
+        return p, buf
+
+    def forward(self, x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        x = _need_f32("input", x)
+        key = (w.data_ptr(), tuple(w.shape), tuple(x.shape), w._version)
+        if self._packed is None or self._packed[0] != key:
+            self.prepack_weights(tuple(x.shape), w)
+        _, p, buf = self._packed
+        y_shape = (p.n, p.m, p.oh, p.ow)
+        if bias is not None:
+            bias = _need_f32("bias", bias)
+            if bias.numel() < p.m:
+                raise N.OshError(N.OSH_E_INVALID, f"Conv '{self.name}': bias has {bias.numel()} values, {p.m} needed")
+        if out is None:
+            out = torch.empty(y_shape, dtype=torch.float32, device=x.device)
+        elif tuple(out.shape) != y_shape or not out.is_contiguous():
+            raise ValueError(f"Conv '{self.name}': output must be a contiguous {y_shape} tensor")
+        N.call("osh_conv2d_f32", C.byref(p), _ptr(x), _ptr(buf), _ptr(bias), N.ACTIVATIONS[self.fused_activation],
+               _ptr(out), C.c_void_p(_stream()))
+        return out
+
+
+class MatMulLayer:
+    """numpy-broadcast MatMul with an optional fused column bias (FusedBias)."""
+
+    def __init__(self, fused_bias: Optional[torch.Tensor] = None, name: str = "matmul"):
+        self.fused_bias = fused_bias
+        self.name = name
+
+    def get_memory_shapes(self, a_shape: Sequence[int], b_shape: Sequence[int]) -> tuple:
+        y = N.dims64([0] * 8)
+        ry = C.c_int()
+        N.call("osh_matmul_infer_shape", N.dims64(a_shape), len(a_shape), N.dims64(b_shape), len(b_shape), y,
+               C.byref(ry))
+        return tuple(int(y[i]) for i in range(ry.value))
+
+    def forward(self, a: torch.Tensor, b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        a = _need_f32("A", a)
+        b = _need_f32("B", b)
+        y_shape = self.get_memory_shapes(tuple(a.shape), tuple(b.shape))
+        bias = self.fused_bias
+        if out is None:
+            out = torch.empty(y_shape, dtype=torch.float32, device=a.device)
+        a2 = a.reshape(1, -1) if a.dim() == 1 else a
+        b2 = b.reshape(-1, 1) if b.dim() == 1 else b
+        m, k = a2.shape[-2], a2.shape[-1]
+        n = b2.shape[-1]
+        if bias is not None:
+            bias = _need_f32("bias", bias)
+            if bias.numel() != n:
+                raise N.OshError(N.OSH_E_INVALID, f"MatMul '{self.name}': fused bias has {bias.numel()} values, {n} needed")
+        stream = C.c_void_p(_stream())
+        if b2.dim() == 2:
+            # all batch rows share B: one GEMM over batch*m rows (DnnOps.cs:2975-3034)
+            rows = a2.numel() // k
+            N.call("osh_gemm_f32", rows, n, k, _ptr(a2), k, _ptr(b2), n, _ptr(bias), None, None, N.ACT_NONE,
+                   _ptr(out), n, stream)
+            return out
+        # general broadcast: expand batch dims, one strided batched GEMM
+        batch_shape = y_shape[:-2] if (a.dim() > 1 and b.dim() > 1) else y_shape[:-1]
+        ab = a2.expand(*batch_shape, m, k) if a2.dim() > 2 or batch_shape else a2
+        bb = b2.expand(*batch_shape, k, n)
+        ab = ab.reshape(-1, m, k)
+        bb = bb.reshape(-1, k, n)
+        sa = ab.stride(0) if ab.shape[0] > 1 else 0
+        sb = bb.stride(0) if bb.shape[0] > 1 else 0
+        if ab.stride(1) != k or ab.stride(2) != 1:
+            ab = ab.contiguous()
+            sa = m * k
+        if bb.stride(1) != n or bb.stride(2) != 1:
+            bb = bb.contiguous()
+            sb = k * n
+        batch = max(ab.shape[0], bb.shape[0])
+        N.call("osh_gemm_f32_batched", batch, m, n, k, _ptr(ab), k, sa, _ptr(bb), n, sb, _ptr(bias), N.ACT_NONE,
+               _ptr(out), n, m * n, stream)
+        return out
+
+
+class DynamicQuantizeMatMulLayer:
+    """DynamicQuantizeMatMul with inputs [A, W, w_zero_point, w_scale, bias] (the reference's order)."""
+
+    def __init__(self, name: str = "dqmm"):
+        self.name = name
+        self._packed = None
+        self._scratch = None
+
+    @staticmethod
+    def get_memory_shapes(a_shape: Sequence[int], w_shape: Sequence[int]) -> tuple:
+        if len(w_shape) != 2:
+            raise N.OshError(N.OSH_E_INVALID, f"DynamicQuantizeMatMul: weight must be 2-D, got {tuple(w_shape)}")
+        if a_shape[-1] != w_shape[0]:
+            raise N.OshError(N.OSH_E_INVALID, f"DynamicQuantizeMatMul: K mismatch ({tuple(a_shape)} x {tuple(w_shape)})")
+        return tuple(a_shape[:-1]) + (int(w_shape[1]),)
+
+    def prepack_weights(self, w: torch.Tensor, w_zero_point=None):
+        if w.dtype not in (torch.int8, torch.uint8) or w.dim() != 2 or not w.is_cuda:
+            raise N.OshError(N.OSH_E_INVALID, "DynamicQuantizeMatMul: W must be a 2-D int8/uint8 device tensor")
+        w = w.contiguous()
+        k, n = w.shape
+        zps = [] if w_zero_point is None else [int(v) for v in torch.as_tensor(w_zero_point).reshape(-1).tolist()]
+        zarr = (C.c_int32 * max(1, len(zps)))(*zps)
+        nbytes = C.c_size_t()
+        N.call("osh_dqmm_packed_weight_bytes", k, n, C.byref(nbytes))
+        buf = torch.empty(nbytes.value, dtype=torch.uint8, device=w.device)
+        N.call("osh_dqmm_pack_weights", k, n, _ptr(w), 1 if w.dtype == torch.int8 else 0, zarr, len(zps), _ptr(buf),
+               C.c_void_p(_stream()))
+        self._packed = ((w.data_ptr(), tuple(w.shape), w._version, tuple(zps)), buf)
+        return buf
+
+    def forward(self, a: torch.Tensor, w: torch.Tensor, w_zero_point=None, w_scale: Optional[torch.Tensor] = None,
+                bias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                acc_out: Optional[torch.Tensor] = None, qparams_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        a = _need_f32("A", a)
+        y_shape = self.get_memory_shapes(tuple(a.shape), tuple(w.shape))
+        k, n = w.shape
+        m = a.numel() // k
+        zps = () if w_zero_point is None else tuple(int(v) for v in torch.as_tensor(w_zero_point).reshape(-1).tolist())
+        key = (w.data_ptr(), tuple(w.shape), w._version, zps)
+        if self._packed is None or self._packed[0] != key:
+            self.prepack_weights(w, w_zero_point)
+        wbuf = self._packed[1]
+        if w_scale is None:
+            w_scale = torch.ones(1, dtype=torch.float32, device=a.device)
+        w_scale = _need_f32("w_scale", w_scale)
+        if bias is not None:
+            bias = _need_f32("bias", bias)
+        sbytes = C.c_size_t()
+        N.call("osh_dqmm_scratch_bytes", m, k, C.byref(sbytes))
+        if self._scratch is None or self._scratch.numel() < sbytes.value:
+            self._scratch = torch.empty(sbytes.value, dtype=torch.uint8, device=a.device)
+        if out is None:
+            out = torch.empty(y_shape, dtype=torch.float32, device=a.device)
+        N.call("osh_dqmm_u8s8", m, k, n, _ptr(a), _ptr(wbuf), _ptr(w_scale), w_scale.numel(), _ptr(bias), _ptr(out),
+               _ptr(acc_out), _ptr(qparams_out), _ptr(self._scratch), C.c_void_p(_stream()))
+        return out
+
+
+class DynamicQuantizeLinearLayer:
+    """DynamicQuantizeLinear: (q u8, scale, zero point)."""
+
+    def __init__(self, name: str = "dql"):
+        self.name = name
+        self._scratch = None
+
+    def forward(self, x: torch.Tensor):
+        x = _need_f32("x", x)
+        sbytes = C.c_size_t()
+        N.call("osh_dqmm_scratch_bytes", 0, 1, C.byref(sbytes))
+        if self._scratch is None or self._scratch.numel() < sbytes.value:
+            self._scratch = torch.empty(sbytes.value, dtype=torch.uint8, device=x.device)
+        q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+        qp = torch.empty(2, dtype=torch.int32, device=x.device)
+        N.call("osh_dynamic_quantize_linear", x.numel(), _ptr(x), _ptr(q), _ptr(qp), _ptr(self._scratch),
+               C.c_void_p(_stream()))
+        qh = qp.cpu()
+        scale = qh[0:1].view(torch.float32).item()
+        return q, scale, int(qh[1].item())

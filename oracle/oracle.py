@@ -1,0 +1,254 @@
+"""numpy front end of the CPU oracle (oracle/osh_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker, never as the thing
+measured or shipped.  Each function names the reference routine it restates
+(paths relative to the OnnxSharp source tree).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "build", "liboracle.so")
+_lib = None
+
+ORDER_IM2COL = 0  # ic -> ky -> kx (ConvKernels.Im2Col / PackedConv / Pointwise / FirstConv)
+ORDER_NCHWC = 1  # icb -> ky -> kx -> lane16 (NchwcConv.Row, AVX-512 hosts)
+
+_fp = C.POINTER(C.c_float)
+_dp = C.POINTER(C.c_double)
+_ip = C.POINTER(C.c_int)
+_i32p = C.POINTER(C.c_int32)
+_u8p = C.POINTER(C.c_uint8)
+_vp = C.c_void_p
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        l = C.CDLL(_LIB_PATH)
+        if not l.orc_cpu_ok():
+            raise RuntimeError("oracle build needs an AVX2+FMA host")
+        l.orc_gemm_f32.argtypes = [C.c_int, C.c_int, C.c_int, _fp, C.c_int, _fp, C.c_int, _fp, _fp, _fp,
+                                   _fp, C.c_int, C.c_int]
+        l.orc_gemm_f64.argtypes = [C.c_int, C.c_int, C.c_int, _fp, _fp, _fp, _fp, _dp]
+        l.orc_conv2d_f32.argtypes = [C.c_int] + [C.c_int] * 16 + [_fp, _fp, _fp, _fp]
+        l.orc_conv2d_f32.restype = C.c_int
+        l.orc_conv2d_f64.argtypes = [C.c_int] * 16 + [_fp, _fp, _fp, _dp]
+        l.orc_conv_dw_f32.argtypes = [C.c_int] * 14 + [_fp, _fp, _fp, _fp]
+        l.orc_winograd_f23.argtypes = [C.c_int] * 5 + [_fp, _fp, _fp, _fp]
+        for f in (l.orc_exp_ref, l.orc_silu_ref, l.orc_silu_scalar, l.orc_relu):
+            f.argtypes = [C.c_long, _fp, _fp]
+        l.orc_minmax.argtypes = [C.c_long, _fp, _fp, _fp]
+        l.orc_dql_params.argtypes = [C.c_float, C.c_float, _fp, _ip]
+        l.orc_quantize_u8.argtypes = [C.c_long, _fp, C.c_float, C.c_int, _u8p]
+        l.orc_dynamic_quantize_linear.argtypes = [C.c_long, _fp, _u8p, _fp, _ip]
+        l.orc_dqmm.argtypes = [C.c_int, C.c_int, C.c_int, _fp, _vp, C.c_int, _ip, C.c_int, _fp, C.c_int, _fp,
+                               _fp, _i32p, _fp, C.c_int, _fp, _ip]
+        l.orc_matmul_integer.argtypes = [C.c_int, C.c_int, C.c_int, _u8p, C.c_int, _vp, C.c_int, _ip, C.c_int,
+                                         _i32p]
+        l.orc_set_threads.argtypes = [C.c_int]
+        _lib = l
+    return _lib
+
+
+def set_threads(t: int) -> None:
+    lib().orc_set_threads(int(t))
+
+
+def _f(a):
+    return None if a is None else a.ctypes.data_as(_fp)
+
+
+def _c32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------- GEMM
+
+def gemm_f32(a, b, row_bias=None, col_bias=None, col_scale=None, fused=True):
+    """GemmKernel.Multiply / MultiplyPacked (GemmKernel.cs:1070-1241): FMA chain from the bias."""
+    a, b = _c32(a), _c32(b)
+    row_bias, col_bias, col_scale = _c32(row_bias), _c32(col_bias), _c32(col_scale)
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    c = np.empty((m, n), np.float32)
+    lib().orc_gemm_f32(m, k, n, _f(a), k, _f(b), n, _f(row_bias), _f(col_bias), _f(col_scale), _f(c), n,
+                       1 if fused else 0)
+    return c
+
+
+def gemm_f64(a, b, col_bias=None, row_bias=None):
+    """Double-precision naive product (GemmKernelTests' naive loop)."""
+    a, b = _c32(a), _c32(b)
+    col_bias, row_bias = _c32(col_bias), _c32(row_bias)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float64)
+    lib().orc_gemm_f64(m, k, n, _f(a), _f(b), _f(col_bias), _f(row_bias), c.ctypes.data_as(_dp))
+    return c
+
+
+# ---------------------------------------------------------------- conv
+
+def conv2d_f32(x, w, bias, strides, pads, dilations, group, out_hw, order=ORDER_IM2COL):
+    """NCHW conv, reference accumulation order `order`; pads are the begin pads (top, left)."""
+    x, w, bias = _c32(x), _c32(w), _c32(bias)
+    N, Cc, H, W = x.shape
+    M, _, KH, KW = w.shape
+    OH, OW = out_hw
+    y = np.empty((N, M, OH, OW), np.float32)
+    rc = lib().orc_conv2d_f32(order, N, Cc, H, W, M, KH, KW, group, strides[0], strides[1], dilations[0],
+                              dilations[1], pads[0], pads[1], OH, OW, _f(x), _f(w), _f(bias), _f(y))
+    if rc != 0:
+        raise ValueError("NCHWc order needs C/group % 16 == 0")
+    return y
+
+
+def conv2d_f64(x, w, bias, strides, pads, dilations, group, out_hw):
+    """Textbook direct conv in double (ConvKernels.Direct semantics)."""
+    x, w, bias = _c32(x), _c32(w), _c32(bias)
+    N, Cc, H, W = x.shape
+    M, _, KH, KW = w.shape
+    OH, OW = out_hw
+    y = np.empty((N, M, OH, OW), np.float64)
+    lib().orc_conv2d_f64(N, Cc, H, W, M, KH, KW, group, strides[0], strides[1], dilations[0], dilations[1],
+                         pads[0], pads[1], OH, OW, _f(x), _f(w), _f(bias), y.ctypes.data_as(_dp))
+    return y
+
+
+def conv_dw_f32(x, w, bias, strides, pads, dilations, out_hw):
+    """DepthwiseConv (group == C == M)."""
+    x, w, bias = _c32(x), _c32(w), _c32(bias)
+    N, Cc, H, W = x.shape
+    KH, KW = w.shape[2], w.shape[3]
+    OH, OW = out_hw
+    y = np.empty((N, Cc, OH, OW), np.float32)
+    lib().orc_conv_dw_f32(N, Cc, H, W, KH, KW, strides[0], strides[1], dilations[0], dilations[1], pads[0],
+                          pads[1], OH, OW, _f(x), _f(w), _f(bias), _f(y))
+    return y
+
+
+def winograd_f23(x, w, bias):
+    """Winograd F(2x2,3x3), stride 1, pad 1 (Winograd.cs)."""
+    x, w, bias = _c32(x), _c32(w), _c32(bias)
+    N, Cc, H, W = x.shape
+    M = w.shape[0]
+    y = np.empty((N, M, H, W), np.float32)
+    lib().orc_winograd_f23(N, Cc, H, W, M, _f(x), _f(w), _f(bias), _f(y))
+    return y
+
+
+# ---------------------------------------------------------------- activations
+
+def _unary(fn, x):
+    x = _c32(x)
+    y = np.empty_like(x)
+    fn(x.size, _f(x), _f(y))
+    return y
+
+
+def exp_ref(x):
+    """VectorMath.Exp polynomial."""
+    return _unary(lib().orc_exp_ref, x)
+
+
+def silu_ref(x):
+    """VectorMath.Silu vector path."""
+    return _unary(lib().orc_silu_ref, x)
+
+
+def silu_scalar(x):
+    """TensorOps scalar SiLU tail (C library expf in place of MathF.Exp)."""
+    return _unary(lib().orc_silu_scalar, x)
+
+
+def relu(x):
+    return _unary(lib().orc_relu, x)
+
+
+# ---------------------------------------------------------------- int8
+
+def minmax(x):
+    x = _c32(x)
+    mn, mx = C.c_float(), C.c_float()
+    lib().orc_minmax(x.size, _f(x), C.byref(mn), C.byref(mx))
+    return mn.value, mx.value
+
+
+def dql_params(mn, mx):
+    s, z = C.c_float(), C.c_int()
+    lib().orc_dql_params(mn, mx, C.byref(s), C.byref(z))
+    return np.float32(s.value), z.value
+
+
+def quantize_u8(x, scale, zp):
+    x = _c32(x)
+    q = np.empty(x.shape, np.uint8)
+    lib().orc_quantize_u8(x.size, _f(x), float(scale), int(zp), q.ctypes.data_as(_u8p))
+    return q
+
+
+def dynamic_quantize_linear(x):
+    x = _c32(x)
+    q = np.empty(x.shape, np.uint8)
+    s, z = C.c_float(), C.c_int()
+    lib().orc_dynamic_quantize_linear(x.size, _f(x), q.ctypes.data_as(_u8p), C.byref(s), C.byref(z))
+    return q, np.float32(s.value), z.value
+
+
+def _zp_arr(zp):
+    if zp is None:
+        return None, 0
+    z = np.ascontiguousarray(np.atleast_1d(zp), dtype=np.int32)
+    return z, z.size
+
+
+def dqmm(a, w, w_zp=None, w_scale=None, bias=None, fused=True):
+    """DynamicQuantizeMatMul [A, W, w_zp, w_scale, bias] (QuantizedMatMulOps.cs:115-201).
+
+    Returns (out f32, acc int32 exact, acc f32 reference chain, scale, zp)."""
+    a = _c32(a)
+    m, k = a.reshape(-1, a.shape[-1]).shape
+    w = np.ascontiguousarray(w)
+    assert w.dtype in (np.int8, np.uint8) and w.shape[0] == k
+    n = w.shape[1]
+    z, nz = _zp_arr(w_zp)
+    ws = None if w_scale is None else np.ascontiguousarray(np.atleast_1d(w_scale), np.float32)
+    bias = _c32(bias)
+    out = np.empty((m, n), np.float32)
+    acc = np.empty((m, n), np.int32)
+    accf = np.empty((m, n), np.float32)
+    s, zz = C.c_float(), C.c_int()
+    lib().orc_dqmm(m, k, n, _f(a), w.ctypes.data, 1 if w.dtype == np.int8 else 0,
+                   None if z is None else z.ctypes.data_as(_ip), nz, _f(ws), 0 if ws is None else ws.size,
+                   _f(bias), _f(out), acc.ctypes.data_as(_i32p), _f(accf), 1 if fused else 0, C.byref(s),
+                   C.byref(zz))
+    return out, acc, accf, np.float32(s.value), zz.value
+
+
+def matmul_integer(a, b, a_zp=0, b_zp=None):
+    """MatMulInteger (Int8Gemm.MultiplyIntegerScalar): exact int32."""
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b)
+    m, k = a.shape
+    n = b.shape[1]
+    z, nz = _zp_arr(b_zp)
+    c = np.empty((m, n), np.int32)
+    lib().orc_matmul_integer(m, k, n, a.ctypes.data_as(_u8p), int(a_zp), b.ctypes.data,
+                             1 if b.dtype == np.int8 else 0, None if z is None else z.ctypes.data_as(_ip), nz,
+                             c.ctypes.data_as(_i32p))
+    return c

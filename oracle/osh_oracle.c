@@ -1,0 +1,602 @@
+/*
+ * osh_oracle.c -- CPU restatement of OnnxSharp's dense-contraction arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * library in onnxsharp_amd/csrc: tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py are the only callers.  Nothing in the product
+ * path links or calls it.
+ *
+ * Every function restates the arithmetic of the C# reference (paths below are
+ * relative to the OnnxSharp source tree) in the same per-element operation
+ * order, so that where the reference is a single FMA chain the restatement is
+ * bit-exact, and elsewhere the difference is a documented rounding choice.
+ *
+ *   orc_gemm_f32        src/OnnxSharp/Tensors/GemmKernel.cs:1070-1241 (MR12/6/4 micro-kernels:
+ *                       accumulator starts at the bias, k-ascending fmaf chain, fused
+ *                       column-scale epilogue fmaf(acc, scale, bias)); unfused tails
+ *                       GemmKernel.cs:1594-1608,1645-1690
+ *   orc_conv2d_f32      order ORC_ORDER_IM2COL: ConvKernels.cs:554-563 + GemmKernel.cs:1156-1207
+ *                       (ic -> ky -> kx fmaf chain from the bias; also PackedConv.cs:420-440,
+ *                       Pointwise ConvKernels.cs:464-514, FirstConv.cs:351-420)
+ *                       order ORC_ORDER_NCHWC: NchwcConv.cs:533-605 (icb -> ky -> kx -> lane16)
+ *   orc_conv2d_f64      ConvKernels.cs:656-754 (textbook direct conv, in double)
+ *   orc_conv_dw_f32     DepthwiseConv.cs:95-185 (bias, then ky -> kx fmaf)
+ *   orc_winograd_f23    Winograd.cs:125-166 (G g G^T), :414-443 (B^T d B), :234-258 (16 GEMMs),
+ *                       :497-513 (A^T M A + bias)
+ *   orc_exp_ref         VectorMath.cs:21-43 (clamp, Cody-Waite 2-term split, degree-6 Horner)
+ *   orc_silu_ref        VectorMath.cs:70-77 (x * (1 / (1 + exp(-x))))
+ *   orc_minmax          Quantization.cs:109-181 (0 always included, NaN skipped)
+ *   orc_dql_params      QuantizedMatMulOps.cs:151-155
+ *   orc_quantize_u8     QuantizedMatMulOps.cs:280-335, Quantization.cs:68-103
+ *   orc_dqmm            QuantizedMatMulOps.cs:115-201 (+ Int8F32Gemm.cs:124-174 weight widening)
+ *   orc_matmul_integer  Int8Gemm.cs:212-236 (int64 sum of (a - a_zp)(b - b_zp[col]))
+ *
+ * Build: see oracle/Makefile (gcc, -O3 -ffp-contract=off; fmaf is explicit).
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORC_API __attribute__((visibility("default")))
+#define HOT
+
+/* ------------------------------------------------------------------ threads */
+
+static int g_threads = 1;
+
+/* The build uses -mavx2 -mfma (fmaf then vectorises along the output row);
+ * the loader checks this before the first call. */
+ORC_API int orc_cpu_ok(void)
+{
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+}
+
+ORC_API void orc_set_threads(int t) { g_threads = t < 1 ? 1 : t; }
+ORC_API int orc_get_threads(void) { return g_threads; }
+
+typedef void (*range_fn)(void *ctx, long begin, long end);
+
+typedef struct {
+    range_fn fn;
+    void *ctx;
+    long begin, end;
+} job_t;
+
+static void *job_main(void *p)
+{
+    job_t *j = (job_t *)p;
+    j->fn(j->ctx, j->begin, j->end);
+    return NULL;
+}
+
+/* Split [0, n) into contiguous chunks over g_threads threads.  Each output
+ * element is computed by exactly one thread with the same per-element order,
+ * so the result does not depend on the thread count. */
+static void parallel_for(long n, range_fn fn, void *ctx)
+{
+    int t = g_threads;
+    if (t <= 1 || n < 2) {
+        fn(ctx, 0, n);
+        return;
+    }
+    if (t > n) t = (int)n;
+    pthread_t th[256];
+    job_t jobs[256];
+    if (t > 256) t = 256;
+    long base = n / t, rem = n % t, at = 0;
+    for (int i = 0; i < t; i++) {
+        long len = base + (i < rem ? 1 : 0);
+        jobs[i].fn = fn;
+        jobs[i].ctx = ctx;
+        jobs[i].begin = at;
+        jobs[i].end = at + len;
+        at += len;
+    }
+    for (int i = 1; i < t; i++) pthread_create(&th[i], NULL, job_main, &jobs[i]);
+    job_main(&jobs[0]);
+    for (int i = 1; i < t; i++) pthread_join(th[i], NULL);
+}
+
+/* --------------------------------------------------------------------- GEMM */
+
+typedef struct {
+    int m, k, n, lda, ldb, ldc, fused;
+    const float *a, *b, *row_bias, *col_bias, *col_scale;
+    float *c;
+} gemm_ctx;
+
+/* One row: acc[j] = init; acc[j] = fmaf(a[i,t], b[t,j], acc[j]) for t ascending.
+ * Init follows Multiply12Rows (GemmKernel.cs:1113-1152): column scale present
+ * -> 0; else column bias -> col_bias[j]; else row bias -> row_bias[i]; else 0. */
+HOT static void gemm_rows(void *p, long r0, long r1)
+{
+    gemm_ctx *g = (gemm_ctx *)p;
+    const int k = g->k, n = g->n;
+    for (long i = r0; i < r1; i++) {
+        float *acc = g->c + i * (long)g->ldc;
+        const float *arow = g->a + i * (long)g->lda;
+        if (g->col_scale)
+            for (int j = 0; j < n; j++) acc[j] = 0.0f;
+        else if (g->col_bias)
+            for (int j = 0; j < n; j++) acc[j] = g->col_bias[j];
+        else {
+            float rb = g->row_bias ? g->row_bias[i] : 0.0f;
+            for (int j = 0; j < n; j++) acc[j] = rb;
+        }
+        for (int t = 0; t < k; t++) {
+            const float av = arow[t];
+            const float *brow = g->b + (long)t * g->ldb;
+            for (int j = 0; j < n; j++) acc[j] = fmaf(av, brow[j], acc[j]);
+        }
+        if (g->col_scale) {
+            for (int j = 0; j < n; j++) {
+                float bb = g->col_bias ? g->col_bias[j] : 0.0f;
+                acc[j] = g->fused ? fmaf(acc[j], g->col_scale[j], bb)
+                                  : (g->col_bias ? acc[j] * g->col_scale[j] + bb
+                                                 : acc[j] * g->col_scale[j]);
+            }
+        }
+    }
+}
+
+/* C[m,n] (ldc) = A[m,k] (lda) * B[k,n] (ldb) with the reference's bias and
+ * column-scale epilogue.  fused=1 is the micro-kernel epilogue (one fmaf),
+ * fused=0 the ScaleColumns tail (multiply, then add). */
+ORC_API void orc_gemm_f32(int m, int k, int n, const float *a, int lda, const float *b, int ldb,
+                          const float *row_bias, const float *col_bias, const float *col_scale,
+                          float *c, int ldc, int fused)
+{
+    gemm_ctx g = {m, k, n, lda, ldb, ldc, fused, a, b, row_bias, col_bias, col_scale, c};
+    parallel_for(m, gemm_rows, &g);
+}
+
+/* Double-precision naive product (the reference tests' "naive" oracle,
+ * tests/OnnxSharp.Tests/GemmKernelTests.cs:174-180,205-214). */
+ORC_API void orc_gemm_f64(int m, int k, int n, const float *a, const float *b, const float *col_bias,
+                          const float *row_bias, double *c)
+{
+    for (int i = 0; i < m; i++)
+        for (int j = 0; j < n; j++) {
+            double s = col_bias ? col_bias[j] : (row_bias ? row_bias[i] : 0.0);
+            for (int t = 0; t < k; t++) s += (double)a[(long)i * k + t] * b[(long)t * n + j];
+            c[(long)i * n + j] = s;
+        }
+}
+
+/* --------------------------------------------------------------------- conv */
+
+enum { ORC_ORDER_IM2COL = 0, ORC_ORDER_NCHWC = 1 };
+
+typedef struct {
+    int N, C, H, W, M, KH, KW, group, sh, sw, dh, dw, pt, pl, OH, OW;
+} conv_shape;
+
+typedef struct {
+    conv_shape s;
+    int order, Hp, Wp;
+    const float *xpad; /* [N][C][Hp][Wp], zero halo */
+    const float *w, *bias;
+    float *y;
+} conv_ctx;
+
+/* Zero-padded copy of the input so that every tap reads a value (padding
+ * positions read 0, as the reference's im2col / blocked buffers do). */
+static float *pad_input(const conv_shape *s, const float *x, int *Hp_out, int *Wp_out)
+{
+    long needH = (long)(s->OH - 1) * s->sh + (long)(s->KH - 1) * s->dh + 1;
+    long needW = (long)(s->OW - 1) * s->sw + (long)(s->KW - 1) * s->dw + 1;
+    long Hp = s->pt + s->H, Wp = s->pl + s->W;
+    if (needH > Hp) Hp = needH;
+    if (needW > Wp) Wp = needW;
+    float *xp = (float *)calloc((size_t)s->N * s->C * Hp * Wp, sizeof(float));
+    for (long nc = 0; nc < (long)s->N * s->C; nc++)
+        for (int yy = 0; yy < s->H; yy++)
+            memcpy(xp + (nc * Hp + yy + s->pt) * Wp + s->pl, x + (nc * s->H + yy) * (long)s->W,
+                   sizeof(float) * s->W);
+    *Hp_out = (int)Hp;
+    *Wp_out = (int)Wp;
+    return xp;
+}
+
+HOT static void conv_planes(void *p, long t0, long t1)
+{
+    conv_ctx *cx = (conv_ctx *)p;
+    const conv_shape *s = &cx->s;
+    const int cpg = s->C / s->group, opg = s->M / s->group;
+    const int OW = s->OW;
+    float *acc = (float *)malloc(sizeof(float) * OW);
+    float *xv = (float *)malloc(sizeof(float) * OW);
+    for (long t = t0; t < t1; t++) { /* t = (n * M + oc) * OH + oy */
+        int oy = (int)(t % s->OH);
+        long nm = t / s->OH;
+        int oc = (int)(nm % s->M), n = (int)(nm / s->M);
+        int g = oc / opg;
+        float b0 = cx->bias ? cx->bias[oc] : 0.0f;
+        for (int ox = 0; ox < OW; ox++) acc[ox] = b0;
+        const float *wo = cx->w + (long)oc * cpg * s->KH * s->KW;
+        if (cx->order == ORC_ORDER_NCHWC) {
+            for (int ib = 0; ib < cpg / 16; ib++)
+                for (int ky = 0; ky < s->KH; ky++)
+                    for (int kx = 0; kx < s->KW; kx++)
+                        for (int lane = 0; lane < 16; lane++) {
+                            int ic = ib * 16 + lane;
+                            float wv = wo[((long)ic * s->KH + ky) * s->KW + kx];
+                            const float *row = cx->xpad +
+                                (((long)n * s->C + g * cpg + ic) * cx->Hp + (long)oy * s->sh + (long)ky * s->dh) * cx->Wp +
+                                (long)kx * s->dw;
+                            for (int ox = 0; ox < OW; ox++) xv[ox] = row[(long)ox * s->sw];
+                            for (int ox = 0; ox < OW; ox++) acc[ox] = fmaf(xv[ox], wv, acc[ox]);
+                        }
+        } else {
+            for (int ic = 0; ic < cpg; ic++)
+                for (int ky = 0; ky < s->KH; ky++)
+                    for (int kx = 0; kx < s->KW; kx++) {
+                        float wv = wo[((long)ic * s->KH + ky) * s->KW + kx];
+                        const float *row = cx->xpad +
+                            (((long)n * s->C + g * cpg + ic) * cx->Hp + (long)oy * s->sh + (long)ky * s->dh) * cx->Wp +
+                            (long)kx * s->dw;
+                        if (s->sw == 1)
+                            for (int ox = 0; ox < OW; ox++) acc[ox] = fmaf(wv, row[ox], acc[ox]);
+                        else {
+                            for (int ox = 0; ox < OW; ox++) xv[ox] = row[(long)ox * s->sw];
+                            for (int ox = 0; ox < OW; ox++) acc[ox] = fmaf(wv, xv[ox], acc[ox]);
+                        }
+                    }
+        }
+        memcpy(cx->y + t * (long)OW, acc, sizeof(float) * OW);
+    }
+    free(acc);
+    free(xv);
+}
+
+/* NCHW conv with explicit begin pads; the output size is given (the caller
+ * resolved it as ConvLayer.GetMemoryShapes does).  Returns -1 if the NCHWc
+ * order is asked for a shape it does not cover (C/group not a multiple of 16). */
+ORC_API int orc_conv2d_f32(int order, int N, int C, int H, int W, int M, int KH, int KW, int group, int sh,
+                           int sw, int dh, int dw, int pt, int pl, int OH, int OW, const float *x,
+                           const float *w, const float *bias, float *y)
+{
+    conv_shape s = {N, C, H, W, M, KH, KW, group, sh, sw, dh, dw, pt, pl, OH, OW};
+    if (order == ORC_ORDER_NCHWC && (C / group) % 16 != 0) return -1;
+    conv_ctx cx;
+    cx.s = s;
+    cx.order = order;
+    float *xp = pad_input(&s, x, &cx.Hp, &cx.Wp);
+    cx.xpad = xp;
+    cx.w = w;
+    cx.bias = bias;
+    cx.y = y;
+    parallel_for((long)N * M * OH, conv_planes, &cx);
+    free(xp);
+    return 0;
+}
+
+/* Textbook direct conv in double (ConvKernels.Direct semantics). */
+ORC_API void orc_conv2d_f64(int N, int C, int H, int W, int M, int KH, int KW, int group, int sh, int sw,
+                            int dh, int dw, int pt, int pl, int OH, int OW, const float *x, const float *w,
+                            const float *bias, double *y)
+{
+    int cpg = C / group, opg = M / group;
+    for (int n = 0; n < N; n++)
+        for (int oc = 0; oc < M; oc++) {
+            int g = oc / opg;
+            for (int oy = 0; oy < OH; oy++)
+                for (int ox = 0; ox < OW; ox++) {
+                    double s = bias ? bias[oc] : 0.0;
+                    for (int ic = 0; ic < cpg; ic++)
+                        for (int ky = 0; ky < KH; ky++) {
+                            int iy = oy * sh - pt + ky * dh;
+                            if (iy < 0 || iy >= H) continue;
+                            for (int kx = 0; kx < KW; kx++) {
+                                int ix = ox * sw - pl + kx * dw;
+                                if (ix < 0 || ix >= W) continue;
+                                s += (double)x[(((long)n * C + g * cpg + ic) * H + iy) * W + ix] *
+                                     w[(((long)oc * cpg + ic) * KH + ky) * KW + kx];
+                            }
+                        }
+                    y[(((long)n * M + oc) * OH + oy) * OW + ox] = s;
+                }
+        }
+}
+
+/* Depthwise conv (group == C == M, one input channel per group): the
+ * accumulator starts at the bias and runs ky -> kx with fmaf (the reference's
+ * vector path; its stride>1 path is unfused, a rounding-only difference). */
+ORC_API void orc_conv_dw_f32(int N, int C, int H, int W, int KH, int KW, int sh, int sw, int dh, int dw,
+                             int pt, int pl, int OH, int OW, const float *x, const float *w,
+                             const float *bias, float *y)
+{
+    for (int n = 0; n < N; n++)
+        for (int c = 0; c < C; c++)
+            for (int oy = 0; oy < OH; oy++)
+                for (int ox = 0; ox < OW; ox++) {
+                    float acc = bias ? bias[c] : 0.0f;
+                    for (int ky = 0; ky < KH; ky++) {
+                        int iy = oy * sh - pt + ky * dh;
+                        if (iy < 0 || iy >= H) continue;
+                        for (int kx = 0; kx < KW; kx++) {
+                            int ix = ox * sw - pl + kx * dw;
+                            if (ix < 0 || ix >= W) continue;
+                            acc = fmaf(w[((long)c * KH + ky) * KW + kx],
+                                       x[(((long)n * C + c) * H + iy) * W + ix], acc);
+                        }
+                    }
+                    y[(((long)n * C + c) * OH + oy) * OW + ox] = acc;
+                }
+}
+
+/* Winograd F(2x2, 3x3), stride 1, pad 1 (Winograd.cs).  Output size == input size. */
+ORC_API void orc_winograd_f23(int N, int C, int H, int W, int M, const float *x, const float *w,
+                              const float *bias, float *y)
+{
+    int tilesY = (H + 1) / 2, tilesX = (W + 1) / 2, tiles = tilesY * tilesX;
+    float *U = (float *)malloc(sizeof(float) * 16 * (size_t)M * C);
+    float *V = (float *)malloc(sizeof(float) * 16 * (size_t)C * tiles);
+    float *Mc = (float *)malloc(sizeof(float) * 16 * (size_t)M * tiles);
+    for (int oc = 0; oc < M; oc++)
+        for (int ic = 0; ic < C; ic++) {
+            const float *g = w + ((long)oc * C + ic) * 9;
+            float s[12], u[16];
+            for (int j = 0; j < 3; j++) {
+                float g0 = g[j], g1 = g[3 + j], g2 = g[6 + j];
+                s[j] = g0;
+                s[3 + j] = (g0 + g1 + g2) * 0.5f;
+                s[6 + j] = (g0 - g1 + g2) * 0.5f;
+                s[9 + j] = g2;
+            }
+            for (int i = 0; i < 4; i++) {
+                float a = s[i * 3], b = s[i * 3 + 1], c = s[i * 3 + 2];
+                u[i * 4] = a;
+                u[i * 4 + 1] = (a + b + c) * 0.5f;
+                u[i * 4 + 2] = (a - b + c) * 0.5f;
+                u[i * 4 + 3] = c;
+            }
+            for (int comp = 0; comp < 16; comp++) U[(long)comp * M * C + (long)oc * C + ic] = u[comp];
+        }
+    for (int n = 0; n < N; n++) {
+        const float *xn = x + (long)n * C * H * W;
+        for (int c = 0; c < C; c++)
+            for (int ty = 0; ty < tilesY; ty++)
+                for (int tx = 0; tx < tilesX; tx++) {
+                    float d[16], t[16];
+                    int y0 = ty * 2 - 1, x0 = tx * 2 - 1;
+                    for (int i = 0; i < 4; i++)
+                        for (int j = 0; j < 4; j++) {
+                            int yy = y0 + i, xx = x0 + j;
+                            d[i * 4 + j] = (yy >= 0 && yy < H && xx >= 0 && xx < W)
+                                               ? xn[((long)c * H + yy) * W + xx] : 0.0f;
+                        }
+                    for (int j = 0; j < 4; j++) {
+                        float d0 = d[j], d1 = d[4 + j], d2 = d[8 + j], d3 = d[12 + j];
+                        t[j] = d0 - d2;
+                        t[4 + j] = d1 + d2;
+                        t[8 + j] = d2 - d1;
+                        t[12 + j] = d1 - d3;
+                    }
+                    long tile = (long)ty * tilesX + tx;
+                    for (int i = 0; i < 4; i++) {
+                        float a = t[i * 4], b = t[i * 4 + 1], c2 = t[i * 4 + 2], d3 = t[i * 4 + 3];
+                        V[((long)(i * 4) * C + c) * tiles + tile] = a - c2;
+                        V[((long)(i * 4 + 1) * C + c) * tiles + tile] = b + c2;
+                        V[((long)(i * 4 + 2) * C + c) * tiles + tile] = c2 - b;
+                        V[((long)(i * 4 + 3) * C + c) * tiles + tile] = b - d3;
+                    }
+                }
+        for (int comp = 0; comp < 16; comp++)
+            orc_gemm_f32(M, C, tiles, U + (long)comp * M * C, C, V + (long)comp * C * tiles, tiles, NULL, NULL,
+                         NULL, Mc + (long)comp * M * tiles, tiles, 1);
+        for (int oc = 0; oc < M; oc++) {
+            float b = bias ? bias[oc] : 0.0f;
+            for (int ty = 0; ty < tilesY; ty++)
+                for (int tx = 0; tx < tilesX; tx++) {
+                    long tile = (long)ty * tilesX + tx;
+                    float t[8];
+                    for (int j = 0; j < 4; j++) {
+                        float m0 = Mc[((long)j * M + oc) * tiles + tile];
+                        float m1 = Mc[((long)(4 + j) * M + oc) * tiles + tile];
+                        float m2 = Mc[((long)(8 + j) * M + oc) * tiles + tile];
+                        float m3 = Mc[((long)(12 + j) * M + oc) * tiles + tile];
+                        t[j] = m0 + m1 + m2;
+                        t[4 + j] = m1 - m2 - m3;
+                    }
+                    float y00 = t[0] + t[1] + t[2] + b;
+                    float y01 = t[1] - t[2] - t[3] + b;
+                    float y10 = t[4] + t[5] + t[6] + b;
+                    float y11 = t[5] - t[6] - t[7] + b;
+                    int oy = ty * 2, ox = tx * 2;
+                    float *yc = y + ((long)n * M + oc) * H * W;
+                    if (oy < H) {
+                        if (ox < W) yc[(long)oy * W + ox] = y00;
+                        if (ox + 1 < W) yc[(long)oy * W + ox + 1] = y01;
+                    }
+                    if (oy + 1 < H) {
+                        if (ox < W) yc[(long)(oy + 1) * W + ox] = y10;
+                        if (ox + 1 < W) yc[(long)(oy + 1) * W + ox + 1] = y11;
+                    }
+                }
+        }
+    }
+    free(U);
+    free(V);
+    free(Mc);
+}
+
+/* --------------------------------------------------------------- activations */
+
+/* exp polynomial of the reference vector path (VectorMath.Exp). */
+static float exp_ref(float x)
+{
+    x = fminf(fmaxf(x, -87.3f), 88.7f);
+    float n = nearbyintf(x * 1.4426950408889634f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.4286067653e-6f, r);
+    float p = 1.0f / 720.0f;
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int32_t bits = ((int32_t)n + 127) << 23;
+    float two_n;
+    memcpy(&two_n, &bits, 4);
+    return p * two_n;
+}
+
+ORC_API void orc_exp_ref(long n, const float *x, float *y)
+{
+    for (long i = 0; i < n; i++) y[i] = exp_ref(x[i]);
+}
+
+/* SiLU of the vector path: x * (1 / (1 + exp(x * -1))). */
+ORC_API void orc_silu_ref(long n, const float *x, float *y)
+{
+    for (long i = 0; i < n; i++) {
+        float v = x[i];
+        float e = exp_ref(v * -1.0f);
+        y[i] = v * (1.0f / (1.0f + e));
+    }
+}
+
+/* SiLU of the scalar tail (MathF.Exp; here the C library's expf, whose last
+ * bit is not pinned against .NET). */
+ORC_API void orc_silu_scalar(long n, const float *x, float *y)
+{
+    for (long i = 0; i < n; i++) y[i] = x[i] * (1.0f / (1.0f + expf(-x[i])));
+}
+
+ORC_API void orc_relu(long n, const float *x, float *y)
+{
+    for (long i = 0; i < n; i++) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+
+/* ------------------------------------------------------------------ int8 DQM */
+
+ORC_API void orc_minmax(long n, const float *x, float *mn, float *mx)
+{
+    float lo = 0.0f, hi = 0.0f;
+    for (long i = 0; i < n; i++) {
+        float v = x[i];
+        if (isnan(v)) continue;
+        if (v < lo) lo = v;
+        if (v > hi) hi = v;
+    }
+    *mn = lo;
+    *mx = hi;
+}
+
+ORC_API void orc_dql_params(float mn, float mx, float *scale, int *zp)
+{
+    float s = (mx - mn) / 255.0f;
+    if (!(s > 0.0f)) s = 1.0f;
+    float z = nearbyintf(-mn / s);
+    int zi = (int)z;
+    if (zi < 0) zi = 0;
+    if (zi > 255) zi = 255;
+    *scale = s;
+    *zp = zi;
+}
+
+static inline float quant1(float x, float inv, float zpf)
+{
+    float q = nearbyintf(x * inv) + zpf;
+    return fminf(255.0f, fmaxf(0.0f, q));
+}
+
+ORC_API void orc_quantize_u8(long n, const float *x, float scale, int zp, uint8_t *q)
+{
+    float inv = 1.0f / scale, zpf = (float)zp;
+    for (long i = 0; i < n; i++) q[i] = (uint8_t)quant1(x[i], inv, zpf);
+}
+
+/* DynamicQuantizeLinear (QuantOps.cs:166-227): q, scale, zero point. */
+ORC_API void orc_dynamic_quantize_linear(long n, const float *x, uint8_t *q, float *scale, int *zp)
+{
+    float mn, mx;
+    orc_minmax(n, x, &mn, &mx);
+    orc_dql_params(mn, mx, scale, zp);
+    orc_quantize_u8(n, x, *scale, *zp, q);
+}
+
+static inline int wval(const void *w, int w_signed, long idx)
+{
+    return w_signed ? (int)((const int8_t *)w)[idx] : (int)((const uint8_t *)w)[idx];
+}
+
+typedef struct {
+    int m, k, n, w_signed, n_wzp, n_wscale, fused, zp;
+    const uint8_t *q;
+    const void *w;
+    const int *wzp;
+    const float *wscale, *bias;
+    float scale;
+    float *out;
+    int32_t *acc;
+    float *acc_f32;
+} dqmm_ctx;
+
+static void dqmm_rows(void *p, long r0, long r1)
+{
+    dqmm_ctx *d = (dqmm_ctx *)p;
+    for (long i = r0; i < r1; i++)
+        for (int j = 0; j < d->n; j++) {
+            int zpw = d->wzp ? (d->n_wzp == 1 ? d->wzp[0] : d->wzp[j]) : 0;
+            int64_t s = 0;
+            float sf = 0.0f;
+            for (int t = 0; t < d->k; t++) {
+                int qa = (int)d->q[i * (long)d->k + t] - d->zp;
+                int qw = wval(d->w, d->w_signed, (long)t * d->n + j) - zpw;
+                s += (int64_t)qa * qw;
+                sf = fmaf((float)qa, (float)qw, sf);
+            }
+            if (d->acc) d->acc[i * (long)d->n + j] = (int32_t)s;
+            if (d->acc_f32) d->acc_f32[i * (long)d->n + j] = sf;
+            float ws = d->wscale ? (d->n_wscale == 1 ? d->wscale[0] : d->wscale[j]) : 1.0f;
+            float comb = d->scale * ws;
+            float b = d->bias ? d->bias[j] : 0.0f;
+            /* The reference epilogue consumes its FP32 accumulator. */
+            float acc = sf;
+            d->out[i * (long)d->n + j] = d->fused ? fmaf(acc, comb, b)
+                                                  : (d->bias ? acc * comb + b : acc * comb);
+        }
+}
+
+/* DynamicQuantizeMatMul with inputs [A, W, w_zp, w_scale, bias]:
+ *   per-tensor u8 quantization of A, (q - zp)(w - w_zp) summed (exact int64
+ *   into acc_i32; the reference's FP32 fmaf chain into acc_f32), then
+ *   out = fmaf(acc_f32, a_scale * w_scale[j], bias[j]) (fused=1) or the
+ *   unfused tail form (fused=0).  scale/zp are returned.  */
+ORC_API void orc_dqmm(int m, int k, int n, const float *a, const void *w, int w_signed, const int *wzp,
+                      int n_wzp, const float *wscale, int n_wscale, const float *bias, float *out,
+                      int32_t *acc_i32, float *acc_f32, int fused, float *scale_out, int *zp_out)
+{
+    float mn, mx, scale;
+    int zp;
+    orc_minmax((long)m * k, a, &mn, &mx);
+    orc_dql_params(mn, mx, &scale, &zp);
+    uint8_t *q = (uint8_t *)malloc((size_t)m * k);
+    orc_quantize_u8((long)m * k, a, scale, zp, q);
+    dqmm_ctx d = {m, k, n, w_signed, n_wzp, n_wscale, fused, zp, q, w, wzp, wscale, bias, scale,
+                  out, acc_i32, acc_f32};
+    parallel_for(m, dqmm_rows, &d);
+    free(q);
+    if (scale_out) *scale_out = scale;
+    if (zp_out) *zp_out = zp;
+}
+
+/* MatMulInteger: int64 sum of (a - a_zp)(b - b_zp[col]) (Int8Gemm.MultiplyIntegerScalar). */
+ORC_API void orc_matmul_integer(int m, int k, int n, const uint8_t *a, int a_zp, const void *b, int b_signed,
+                                const int *b_zp, int n_bzp, int32_t *c)
+{
+    for (int i = 0; i < m; i++)
+        for (int j = 0; j < n; j++) {
+            int zp = b_zp ? (n_bzp == 1 ? b_zp[0] : b_zp[j]) : 0;
+            int64_t s = 0;
+            for (int t = 0; t < k; t++)
+                s += (int64_t)((int)a[(long)i * k + t] - a_zp) * (wval(b, b_signed, (long)t * n + j) - zp);
+            c[(long)i * n + j] = (int32_t)s;
+        }
+}

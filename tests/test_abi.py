@@ -1,0 +1,133 @@
+"""CPU tests of the C ABI: the library loads, exports every declared symbol,
+and its host-side operator logic (shape inference, pad resolution, errors)
+follows the reference.  No kernel is launched here."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from onnxsharp_amd import native as N
+from onnxsharp_amd.layers import ConvLayer, MatMulLayer, DynamicQuantizeMatMulLayer
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "osh_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"OSH_API\s+[\w\s\*]+?\b(osh_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    for must in ("osh_init", "osh_malloc", "osh_memcpy_h2d", "osh_conv2d_f32", "osh_gemm_f32", "osh_dqmm_u8s8",
+                 "osh_last_error"):
+        assert must in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    for s in declared_symbols():
+        assert hasattr(lib, s), s
+    assert set(declared_symbols()) == set(N.EXPORTED)
+
+
+def test_last_error_reports_invalid_arguments():
+    st = N.lib().osh_gemm_f32(-1, 1, 1, None, 1, None, 1, None, None, None, 0, None, 1, None)
+    assert st == N.OSH_E_INVALID
+    assert "negative" in N.last_error()
+
+
+# ------------------------------------------------------------ Conv shape logic
+
+@pytest.mark.parametrize("attrs,x,w,y", [
+    (dict(pads=[1, 1, 1, 1]), (1, 64, 160, 160), (64, 64, 3, 3), (1, 64, 160, 160)),
+    (dict(strides=[2, 2], pads=[1, 1, 1, 1]), (1, 128, 80, 80), (256, 128, 3, 3), (1, 256, 40, 40)),
+    (dict(), (1, 256, 80, 80), (128, 256, 1, 1), (1, 128, 80, 80)),
+    (dict(auto_pad="SAME_UPPER", strides=[2, 2]), (1, 1, 9, 11), (1, 1, 3, 3), (1, 1, 5, 6)),
+    (dict(auto_pad="VALID"), (2, 4, 9, 9), (8, 4, 3, 3), (2, 8, 7, 7)),
+    (dict(dilations=[2, 2], pads=[2, 2, 2, 2]), (1, 4, 11, 11), (5, 4, 3, 3), (1, 5, 11, 11)),
+    (dict(group=2, strides=[1, 2], pads=[0, 1, 0, 1]), (2, 8, 9, 7), (6, 4, 3, 3), (2, 6, 7, 4)),
+    (dict(kernel_shape=[3, 3], strides=[2, 2], pads=[1, 1, 1, 1]), (1, 3, 640, 640), (16, 3, 3, 3), (1, 16, 320, 320)),
+])
+def test_conv_get_memory_shapes(attrs, x, w, y):
+    assert ConvLayer(**attrs).get_memory_shapes(x, w) == y
+
+
+def test_conv_end_pads_follow_the_reference_shape_rule():
+    # DnnOps.cs:174-175 reads the end pad only when more than 2*spatial pads are given, so
+    # [0, 0, 1, 1] infers the shape as if the pads were [0, 0, 0, 0].
+    assert ConvLayer(pads=[0, 0, 1, 1]).get_memory_shapes((1, 1, 8, 8), (1, 1, 3, 3)) == (1, 1, 6, 6)
+    p = ConvLayer(pads=[0, 0, 1, 1]).resolve((1, 1, 8, 8), (1, 1, 3, 3))
+    assert (p.pt, p.pl, p.pb, p.pr, p.oh, p.ow) == (0, 0, 1, 1, 6, 6)
+
+
+def test_conv_same_upper_equals_explicit_pads():
+    # PadConv1DTests.Conv2DSameUpperWithoutKernelShape
+    a = ConvLayer(auto_pad="SAME_UPPER", strides=[2, 2]).resolve((1, 1, 9, 11), (1, 1, 3, 3))
+    b = ConvLayer(pads=[1, 1, 1, 1], strides=[2, 2]).resolve((1, 1, 9, 11), (1, 1, 3, 3))
+    assert (a.pt, a.pl, a.oh, a.ow) == (b.pt, b.pl, b.oh, b.ow) == (1, 1, 5, 6)
+
+
+def test_conv_same_lower_puts_the_odd_pad_first():
+    p = ConvLayer(auto_pad="SAME_LOWER", strides=[2, 2]).resolve((1, 1, 10, 10), (1, 1, 4, 4))
+    assert (p.pt, p.pb) == (1, 1) and (p.oh, p.ow) == (5, 5)
+    p = ConvLayer(auto_pad="SAME_LOWER").resolve((1, 1, 10, 10), (1, 1, 4, 4))
+    assert (p.pt, p.pb) == (2, 1)
+    p = ConvLayer(auto_pad="SAME_UPPER").resolve((1, 1, 10, 10), (1, 1, 4, 4))
+    assert (p.pt, p.pb) == (1, 2)
+
+
+@pytest.mark.parametrize("attrs,x,w,msg", [
+    (dict(group=3), (1, 8, 5, 5), (8, 8, 3, 3), "divisible"),
+    (dict(), (1, 8, 5, 5), (8, 4, 3, 3), "in-channels"),
+    (dict(), (1, 8, 2, 2), (8, 8, 5, 5), "not positive"),
+])
+def test_conv_shape_errors(attrs, x, w, msg):
+    with pytest.raises(N.OshError, match=msg):
+        ConvLayer(**attrs).get_memory_shapes(x, w)
+
+
+def test_conv_rejects_non_2d():
+    with pytest.raises(N.OshUnsupported):
+        ConvLayer().get_memory_shapes((1, 8, 5), (8, 8, 3))
+    with pytest.raises(N.OshUnsupported):
+        ConvLayer(strides=[1, 1, 1])
+
+
+# ------------------------------------------------------------ MatMul shape logic
+
+@pytest.mark.parametrize("a,b,y", [
+    ((1024, 768), (768, 768), (1024, 768)),
+    ((2, 3, 4), (4, 5), (2, 3, 5)),
+    ((4,), (4, 5), (5,)),
+    ((3, 4), (4,), (3,)),
+    ((4,), (4,), ()),
+    ((2, 1, 3, 4), (5, 4, 6), (2, 5, 3, 6)),
+])
+def test_matmul_get_memory_shapes(a, b, y):
+    assert MatMulLayer().get_memory_shapes(a, b) == y
+
+
+def test_matmul_shape_errors():
+    with pytest.raises(N.OshError, match="K mismatch"):
+        MatMulLayer().get_memory_shapes((3, 4), (5, 6))
+    with pytest.raises(N.OshError, match="broadcast"):
+        MatMulLayer().get_memory_shapes((2, 3, 4), (3, 4, 5))
+
+
+def test_dqmm_shapes():
+    assert DynamicQuantizeMatMulLayer.get_memory_shapes((4, 512, 512), (512, 2048)) == (4, 512, 2048)
+    with pytest.raises(N.OshError):
+        DynamicQuantizeMatMulLayer.get_memory_shapes((4, 512), (256, 2048))
+
+
+def test_size_queries():
+    s = C.c_size_t()
+    N.call("osh_dqmm_packed_weight_bytes", 512, 2048, C.byref(s))
+    assert s.value == 512 * 2048 + 2048 * 8
+    N.call("osh_dqmm_scratch_bytes", 512, 512, C.byref(s))
+    assert s.value >= 512 * 512
+    p = ConvLayer(pads=[1, 1, 1, 1]).resolve((1, 64, 160, 160), (64, 64, 3, 3))
+    N.call("osh_conv_packed_weight_bytes", C.byref(p), C.byref(s))
+    assert s.value == 64 * 64 * 9 * 4

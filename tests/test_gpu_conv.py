@@ -1,0 +1,93 @@
+"""GPU parity: Conv (+ bias + fused Relu/SiLU) through osh_conv2d_f32 against
+the oracle's restatements of the reference kernels, in both accumulation
+orders the reference uses (NCHWc on AVX-512 hosts, im2col/panel on AVX2)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import assert_fp32_close, fp32_violations
+from onnxsharp_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(x, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def run_conv(cuda, x, w, b, act=None, **attrs):
+    from onnxsharp_amd.layers import ConvLayer
+    layer = ConvLayer(fused_activation=act, **attrs)
+    y = layer.forward(_t(x, cuda), _t(w, cuda), None if b is None else _t(b, cuda))
+    return y.cpu().numpy(), layer.resolve(x.shape, w.shape)
+
+
+def oracle_conv(oracle, x, w, b, p, act, order=None):
+    o = oracle.ORDER_NCHWC if order is None and (p.c // p.group) % 16 == 0 and p.group == 1 else (order or 0)
+    y = oracle.conv2d_f32(x, w, b, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), p.group, (p.oh, p.ow), order=o)
+    if act == "Silu":
+        y = oracle.silu_ref(y)
+    elif act == "Relu":
+        y = oracle.relu(y)
+    return y
+
+
+# (name, x shape, w shape, attrs, act)
+CASES = [
+    ("c2_3x3s1_64to64_160", (1, 64, 160, 160), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1]), "Silu"),
+    ("c3a_1x1_256to128_80", (1, 256, 80, 80), (128, 256, 1, 1), dict(), "Silu"),
+    ("c3b_3x3s2_128to256_80", (1, 128, 80, 80), (256, 128, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), "Silu"),
+    ("yolo_stem_3to16_s2", (1, 3, 64, 64), (16, 3, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), "Silu"),
+    ("3x3s1_small_spatial_20", (1, 64, 20, 20), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1]), "Silu"),
+    ("3x3s1_odd_33x45", (1, 24, 33, 45), (40, 24, 3, 3), dict(pads=[1, 1, 1, 1]), "Relu"),
+    ("3x3s2_odd_41x37", (1, 16, 41, 37), (72, 16, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), None),
+    ("1x1_no_bias_batch2", (2, 40, 17, 19), (24, 40, 1, 1), dict(), None),
+    ("grouped_2", (2, 8, 9, 7), (6, 4, 3, 3), dict(group=2, strides=[1, 2], pads=[0, 1, 0, 1]), "Silu"),
+    ("dilated_5x5", (1, 5, 23, 21), (7, 5, 5, 5), dict(pads=[4, 4, 4, 4], dilations=[2, 2]), None),
+    ("depthwise_3x3", (1, 32, 20, 20), (32, 1, 3, 3), dict(group=32, pads=[1, 1, 1, 1]), None),
+    ("depthwise_3x3_s2", (1, 24, 19, 18), (24, 1, 3, 3), dict(group=24, strides=[2, 2], pads=[1, 1, 1, 1]), "Silu"),
+    ("same_upper_s2", (1, 1, 9, 11), (1, 1, 3, 3), dict(auto_pad="SAME_UPPER", strides=[2, 2]), None),
+    ("valid_1x3", (1, 6, 10, 12), (4, 6, 1, 3), dict(auto_pad="VALID"), None),
+]
+
+
+@pytest.mark.parametrize("name,xs,ws,attrs,act", CASES, ids=[c[0] for c in CASES])
+def test_conv_parity(cuda, oracle, name, xs, ws, attrs, act):
+    print(f"conv {name} x={xs} w={ws} {attrs} act={act}", flush=True)
+    seed = sum(xs) * 7 + sum(ws)
+    x = synth.uniform(seed, xs)
+    w = synth.normal(seed + 1, ws, 0, 0.05)
+    b = None if "no_bias" in name else synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    y, p = run_conv(cuda, x, w, b, act, **attrs)
+    ref = oracle_conv(oracle, x, w, b, p, act)
+    nbad, dmax = fp32_violations(y, ref)
+    print(f"  max|d|={dmax:.3e} violations={nbad}", flush=True)
+    assert_fp32_close(y, ref, name)
+    # also within the bar of the other ISA order
+    alt = oracle_conv(oracle, x, w, b, p, act, order=oracle.ORDER_IM2COL)
+    assert_fp32_close(y, alt, name + " (im2col order)")
+
+
+def test_conv_known_answer_same_upper(cuda):
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "known_answers.json")))["conv_same_upper_s2"]
+    x = np.arange(1, 100, dtype=np.float32).reshape(1, 1, 9, 11)
+    w = np.ones((1, 1, 3, 3), np.float32)
+    ya, _ = run_conv(cuda, x, w, None, auto_pad="SAME_UPPER", strides=[2, 2])
+    yb, _ = run_conv(cuda, x, w, None, pads=[1, 1, 1, 1], strides=[2, 2])
+    assert ya.shape == tuple(g["out_shape"])
+    assert (ya[0, 0] == np.array(g["y"], np.float32)).all()
+    assert (ya == yb).all()
+
+
+def test_conv_silu_epilogue_bit_exact_on_bias_only_input(cuda, oracle):
+    # zero input: the conv output is exactly the bias, so the fused SiLU must equal
+    # VectorMath.Silu of the bias bit for bit
+    x = np.zeros((1, 64, 40, 40), np.float32)
+    w = synth.normal(5, (64, 64, 3, 3), 0, 0.05)
+    b = synth.normal(6, (64,), 0, 3.0)
+    y, _ = run_conv(cuda, x, w, b, "Silu", pads=[1, 1, 1, 1])
+    expect = oracle.silu_ref(b)
+    assert (y[0] == expect[:, None, None]).all()

@@ -1,0 +1,114 @@
+"""GPU parity: DynamicQuantizeMatMul / DynamicQuantizeLinear.  int32
+accumulators and quantization parameters are bit-exact; the FP32 output is
+bit-exact against the fused epilogue fmaf(acc, scale * w_scale, bias)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from onnxsharp_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(x, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def run_dqmm(cuda, a, w, wzp, ws, bias):
+    import torch
+    from onnxsharp_amd.layers import DynamicQuantizeMatMulLayer
+    m = a.size // a.shape[-1]
+    n = w.shape[1]
+    acc = torch.empty((m, n), dtype=torch.int32, device=cuda)
+    qp = torch.empty(2, dtype=torch.int32, device=cuda)
+    layer = DynamicQuantizeMatMulLayer()
+    out = layer.forward(_t(a, cuda), _t(w, cuda), wzp, None if ws is None else _t(np.atleast_1d(ws), cuda),
+                        None if bias is None else _t(bias, cuda), acc_out=acc, qparams_out=qp)
+    q = qp.cpu().numpy()
+    return out.cpu().numpy(), acc.cpu().numpy(), np.float32(q[0:1].view(np.float32)[0]), int(q[1])
+
+
+@pytest.mark.parametrize("m,k,n,wdt,zp_kind", [
+    (512, 512, 2048, np.int8, None),       # encoder-FFN workload
+    (4, 13, 11, np.int8, None),
+    (33, 100, 70, np.uint8, "tensor"),
+    (17, 64, 40, np.uint8, "column"),
+    (5, 1280, 32, np.int8, "column"),      # Int8Tests.F32SubstituteExactAtLongK shape
+    (1, 7, 3, np.int8, "tensor"),
+])
+def test_dqmm_parity(cuda, oracle, m, k, n, wdt, zp_kind):
+    print(f"dqmm m={m} k={k} n={n} w={wdt.__name__} zp={zp_kind}", flush=True)
+    a = synth.normal(m + k, (m, k))
+    lo, hi = (-127, 127) if wdt == np.int8 else (0, 255)
+    w = synth.randint(m + n, (k, n), lo, hi, wdt)
+    base = 0 if wdt == np.int8 else 128
+    wzp = None if zp_kind is None else (
+        np.array([base + 3], np.int32) if zp_kind == "tensor" else synth.randint(n, (n,), -20, 20, np.int32) + base)
+    ws = synth.uniform(k + n, (n,), 0.001, 0.02)
+    bias = synth.normal(m + k + n, (n,), 0, 0.01)
+    out, acc, s, z = run_dqmm(cuda, a, w, wzp, ws, bias)
+    eo, eacc, eaccf, es, ez = oracle.dqmm(a, w, wzp, ws, bias, fused=True)
+    assert (s, z) == (es, ez), "quantization parameters"
+    assert np.array_equal(acc, eacc), f"int32 accumulators differ at {np.argwhere(acc != eacc)[:5]}"
+    assert np.array_equal(eaccf, eacc.astype(np.float32))  # the reference's FP32 chain is exact here
+    assert np.array_equal(out, eo), "fused dequant epilogue"
+    # the reference's unfused tail rows (acc*s + b) are within one rounding
+    eu = oracle.dqmm(a, w, wzp, ws, bias, fused=False)[0]
+    assert np.abs(out - eu).max() <= 1e-6 * max(1.0, np.abs(eu).max())
+
+
+def test_dqmm_scalar_scale_no_bias_and_edge_values(cuda, oracle):
+    a = np.concatenate([synth.normal(1, (6, 40)), np.zeros((1, 40), np.float32)]).astype(np.float32)
+    a[2, 5] = 0.0
+    a[3, :] = 7.25  # a constant positive row
+    w = synth.randint(2, (40, 9), -128, 127, np.int8)
+    out, acc, s, z = run_dqmm(cuda, a, w, None, np.float32(0.05), None)
+    eo, eacc, _, es, ez = oracle.dqmm(a, w, None, np.float32(0.05), None)
+    assert (s, z) == (es, ez)
+    assert np.array_equal(acc, eacc)
+    assert np.array_equal(out, eo)
+
+
+def test_dqmm_all_zero_input_uses_unit_scale(cuda, oracle):
+    a = np.zeros((3, 16), np.float32)
+    w = synth.randint(3, (16, 5), -127, 127, np.int8)
+    out, acc, s, z = run_dqmm(cuda, a, w, None, np.float32(1.0), None)
+    assert (s, z) == (np.float32(1.0), 0)
+    assert (acc == 0).all() and (out == 0).all()
+
+
+def test_dqmm_nan_row_propagates(cuda, oracle):
+    a = synth.normal(4, (4, 32))
+    a[1, 3] = np.nan
+    w = synth.randint(5, (32, 6), -127, 127, np.int8)
+    out, acc, s, z = run_dqmm(cuda, a, w, None, np.float32(0.5), None)
+    # Quantizer.MinMax skips NaN, so the parameters come from the other values
+    es, ez = oracle.dql_params(*oracle.minmax(a))
+    assert (s, z) == (es, ez)
+    assert np.isnan(out[1]).all() and np.isfinite(np.delete(out, 1, axis=0)).all()
+    good = np.delete(np.arange(4), 1)
+    _, eacc, _, _, _ = oracle.dqmm(a[good], w, None, np.float32(0.5), None)
+    # rows without NaN quantize with the same global parameters
+    q = oracle.quantize_u8(a[good], es, ez)
+    assert np.array_equal(acc[good], (q.astype(np.int64) - ez) @ w.astype(np.int64))
+
+
+def test_dynamic_quantize_linear_known_answer(cuda):
+    from onnxsharp_amd.layers import DynamicQuantizeLinearLayer
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "known_answers.json")))["dynamic_quantize_linear"]
+    q, s, z = DynamicQuantizeLinearLayer().forward(_t(np.array(g["x"], np.float32), cuda))
+    assert np.float32(s) == np.float32(3) / np.float32(255)
+    assert z == g["zero_point"]
+    assert q.cpu().numpy().tolist() == g["q"]
+
+
+def test_dynamic_quantize_linear_matches_oracle(cuda, oracle):
+    from onnxsharp_amd.layers import DynamicQuantizeLinearLayer
+    x = synth.normal(9, (1000003,), 0.3, 2.0)
+    q, s, z = DynamicQuantizeLinearLayer().forward(_t(x, cuda))
+    eq, es, ez = oracle.dynamic_quantize_linear(x)
+    assert (np.float32(s), z) == (es, ez)
+    assert np.array_equal(q.cpu().numpy(), eq)

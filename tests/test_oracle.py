@@ -1,0 +1,267 @@
+"""CPU tests that pin the oracle (oracle/osh_oracle.c) before it is trusted.
+
+Each check is chosen so that a plausible slip in the restatement (a dropped
+term, a transposed operand, a wrong rounding mode or order) fails it:
+known answers from the reference's own tests, closed forms in float64,
+brute force on small inputs, and invariants of the integer algebra.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from onnxsharp_amd import synth
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "known_answers.json")))
+
+
+# ----------------------------------------------------------- known answers
+
+def test_dynamic_quantize_linear_known_answer(oracle):
+    g = GOLD["dynamic_quantize_linear"]
+    q, s, z = oracle.dynamic_quantize_linear(np.array(g["x"], np.float32))
+    assert s == np.float32(3) / np.float32(255)
+    assert z == g["zero_point"]
+    assert q.tolist() == g["q"]
+
+
+def test_matmul_integer_known_answer(oracle):
+    g = GOLD["matmul_integer"]
+    c = oracle.matmul_integer(np.array(g["a"], np.uint8), np.array(g["b"], np.uint8))
+    assert c.tolist() == g["c"]
+
+
+def test_quantize_u8_known_answer(oracle):
+    g = GOLD["quantize_u8"]
+    q = oracle.quantize_u8(np.array(g["x"], np.float32), g["scale"], g["zero_point"])
+    assert q.tolist() == g["q"]
+
+
+def test_conv_same_upper_window_sums(oracle):
+    g = GOLD["conv_same_upper_s2"]
+    x = np.arange(1, 100, dtype=np.float32).reshape(1, 1, 9, 11)
+    w = np.ones((1, 1, 3, 3), np.float32)
+    y = oracle.conv2d_f32(x, w, None, (2, 2), (1, 1), (1, 1), 1, (5, 6))
+    xp = np.pad(x[0, 0].astype(np.int64), 1)
+    brute = np.array([[xp[2 * i:2 * i + 3, 2 * j:2 * j + 3].sum() for j in range(6)] for i in range(5)])
+    assert (brute == np.array(g["y"])).all()
+    assert (y[0, 0] == brute).all()
+
+
+# ----------------------------------------------------------- GEMM
+
+@pytest.mark.parametrize("m,k,n", [(257, 64, 257), (64, 64, 64), (5, 17, 33), (17, 1, 257), (1, 257, 64),
+                                   (96, 320, 1280)])
+def test_gemm_chain_matches_float64(oracle, m, k, n):
+    # GemmKernelTests.Check: |d| / max(1, |x|) <= 1e-4 against a double-precision naive product
+    rng = np.random.default_rng(m * 31 + k * 7 + n)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    cb = rng.uniform(-1, 1, n).astype(np.float32)
+    c = oracle.gemm_f32(a, b, col_bias=cb)
+    ref = oracle.gemm_f64(a, b, col_bias=cb)
+    assert (np.abs(c - ref) / np.maximum(1.0, np.abs(ref))).max() <= 1e-4
+    assert np.allclose(ref, a.astype(np.float64) @ b.astype(np.float64) + cb, rtol=1e-12, atol=1e-9)
+
+
+def test_gemm_chain_is_sequential_fma(oracle):
+    # one output by hand: acc = bias; acc = fma(a_t, b_t, acc) for t ascending
+    rng = np.random.default_rng(1)
+    a = rng.uniform(-1, 1, (3, 50)).astype(np.float32)
+    b = rng.uniform(-1, 1, (50, 4)).astype(np.float32)
+    cb = rng.uniform(-1, 1, 4).astype(np.float32)
+    c = oracle.gemm_f32(a, b, col_bias=cb)
+    for i in range(3):
+        for j in range(4):
+            acc = np.float32(cb[j])
+            for t in range(50):
+                # float64 product of two float32 is exact; adding it in float64 and rounding once is an fma
+                acc = np.float32(np.float64(acc) + np.float64(a[i, t]) * np.float64(b[t, j]))
+            assert c[i, j] == acc
+
+
+def test_gemm_row_bias_and_column_scale(oracle):
+    rng = np.random.default_rng(2)
+    a = rng.uniform(-1, 1, (7, 33)).astype(np.float32)
+    b = rng.uniform(-1, 1, (33, 45)).astype(np.float32)
+    rb = rng.uniform(-1, 1, 7).astype(np.float32)
+    cs = rng.uniform(1e-4, 1e-2, 45).astype(np.float32)
+    cb = rng.uniform(-1, 1, 45).astype(np.float32)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.abs(oracle.gemm_f32(a, b, row_bias=rb) - (ref + rb[:, None])).max() < 1e-4
+    fused = oracle.gemm_f32(a, b, col_bias=cb, col_scale=cs)
+    plain = oracle.gemm_f32(a, b)
+    # GemmKernelTests.PackedScaleBiasMatchesEpilogue: fused epilogue == GEMM then *scale + bias
+    exp = plain.astype(np.float64) * cs + cb
+    assert (np.abs(fused - exp) / np.maximum(1, np.abs(exp))).max() <= 1e-5
+    unf = oracle.gemm_f32(a, b, col_bias=cb, col_scale=cs, fused=False)
+    assert (unf == (plain * cs + cb).astype(np.float32)).all()
+
+
+# ----------------------------------------------------------- conv
+
+CONV_CASES = [
+    # (N, C, H, W, M, KH, KW, group, strides, pads(t,l), dil, out)
+    (1, 16, 12, 13, 8, 3, 3, 1, (1, 1), (1, 1), (1, 1), (12, 13)),
+    (1, 32, 10, 10, 16, 3, 3, 1, (2, 2), (1, 1), (1, 1), (5, 5)),
+    (2, 8, 9, 7, 6, 3, 3, 2, (1, 2), (0, 1), (1, 1), (7, 4)),
+    (1, 4, 11, 11, 5, 3, 3, 1, (1, 1), (2, 2), (2, 2), (11, 11)),
+    (1, 3, 17, 17, 16, 3, 3, 1, (2, 2), (1, 1), (1, 1), (9, 9)),
+    (1, 24, 6, 6, 12, 1, 1, 1, (1, 1), (0, 0), (1, 1), (6, 6)),
+    (1, 5, 8, 9, 7, 5, 5, 1, (1, 1), (2, 2), (1, 1), (8, 9)),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv_orders_match_direct(oracle, case):
+    N_, Cc, H, W, M, KH, KW, g, s, p, d, o = case
+    x = synth.uniform(11, (N_, Cc, H, W))
+    w = synth.normal(12, (M, Cc // g, KH, KW), 0, 0.05)
+    b = synth.normal(13, (M,), 0, 0.01)
+    ref = oracle.conv2d_f64(x, w, b, s, p, d, g, o)
+    # independent float64 conv by explicit zero padding + einsum over windows
+    xp = np.zeros((N_, Cc, H + 2 * p[0] + KH * d[0], W + 2 * p[1] + KW * d[1]))
+    xp[:, :, p[0]:p[0] + H, p[1]:p[1] + W] = x
+    ind = np.zeros((N_, M) + o)
+    for oc in range(M):
+        gi = oc // (M // g)
+        for ky in range(KH):
+            for kx in range(KW):
+                win = xp[:, gi * (Cc // g):(gi + 1) * (Cc // g),
+                         ky * d[0]: ky * d[0] + o[0] * s[0]: s[0], kx * d[1]: kx * d[1] + o[1] * s[1]: s[1]]
+                ind[:, oc] += np.einsum("nchw,c->nhw", win[:, :, :o[0], :o[1]], w[oc, :, ky, kx])
+        ind[:, oc] += b[oc]
+    assert np.allclose(ref, ind, rtol=0, atol=1e-9)
+    y = oracle.conv2d_f32(x, w, b, s, p, d, g, o, order=oracle.ORDER_IM2COL)
+    assert np.abs(y - ref).max() <= 1e-5
+    if (Cc // g) % 16 == 0:
+        yn = oracle.conv2d_f32(x, w, b, s, p, d, g, o, order=oracle.ORDER_NCHWC)
+        assert np.abs(yn - ref).max() <= 1e-5
+
+
+def test_nchwc_order_differs_from_im2col_order_only_by_rounding(oracle):
+    # the two ISA orders are different FMA chains: same value to rounding, not bit-equal in general
+    x = synth.uniform(21, (1, 32, 20, 20))
+    w = synth.normal(22, (32, 32, 3, 3), 0, 0.05)
+    b = synth.normal(23, (32,), 0, 0.01)
+    a = oracle.conv2d_f32(x, w, b, (1, 1), (1, 1), (1, 1), 1, (20, 20), order=oracle.ORDER_IM2COL)
+    c = oracle.conv2d_f32(x, w, b, (1, 1), (1, 1), (1, 1), 1, (20, 20), order=oracle.ORDER_NCHWC)
+    assert not np.array_equal(a, c)
+    assert np.abs(a - c).max() < 1e-5
+
+
+def test_depthwise_matches_grouped_direct(oracle):
+    x = synth.uniform(31, (1, 12, 15, 14))
+    w = synth.normal(32, (12, 1, 3, 3), 0, 0.05)
+    b = synth.normal(33, (12,), 0, 0.01)
+    for s in ((1, 1), (2, 2)):
+        o = ((15 + 2 - 3) // s[0] + 1, (14 + 2 - 3) // s[1] + 1)
+        ref = oracle.conv2d_f64(x, w, b, s, (1, 1), (1, 1), 12, o)
+        y = oracle.conv_dw_f32(x, w, b, s, (1, 1), (1, 1), o)
+        assert np.abs(y - ref).max() <= 1e-6
+
+
+@pytest.mark.parametrize("hw", [(6, 6), (13, 9), (20, 20)])
+def test_winograd_matches_direct(oracle, hw):
+    x = synth.uniform(41, (1, 8, *hw))
+    w = synth.normal(42, (9, 8, 3, 3), 0, 0.05)
+    b = synth.normal(43, (9,), 0, 0.01)
+    ref = oracle.conv2d_f64(x, w, b, (1, 1), (1, 1), (1, 1), 1, hw)
+    y = oracle.winograd_f23(x, w, b)
+    assert np.abs(y - ref).max() <= 1e-5
+
+
+# ----------------------------------------------------------- activations
+
+def test_exp_polynomial_accuracy(oracle):
+    x = np.linspace(-87.0, 88.0, 200001, dtype=np.float32)
+    e = oracle.exp_ref(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    assert (np.abs(e - ref) / ref).max() < 4e-7  # VectorMath.cs:20 claims ~1e-7 relative
+    # clamping: beyond the range the polynomial saturates at the clamp values
+    big = oracle.exp_ref(np.array([200.0, -200.0], np.float32))
+    assert big[0] == oracle.exp_ref(np.array([88.7], np.float32))[0]
+    assert big[1] == oracle.exp_ref(np.array([-87.3], np.float32))[0]
+
+
+def test_silu_matches_float64(oracle):
+    x = synth.uniform(51, (100000,), -20, 20)
+    y = oracle.silu_ref(x).astype(np.float64)
+    xd = x.astype(np.float64)
+    ref = xd / (1.0 + np.exp(-xd))
+    assert (np.abs(y - ref) <= 1e-6 * np.maximum(1, np.abs(ref))).all()
+    assert oracle.silu_ref(np.array([0.0], np.float32))[0] == 0.0
+    s = oracle.silu_scalar(x).astype(np.float64)
+    assert np.abs(s - ref).max() < 1e-5
+
+
+def test_relu(oracle):
+    x = np.array([-1, -0.0, 0, 2.5, np.nan], np.float32)
+    assert oracle.relu(x).tolist() == [0.0, 0.0, 0.0, 2.5, 0.0]
+
+
+# ----------------------------------------------------------- int8
+
+def test_minmax_includes_zero_and_skips_nan(oracle):
+    assert oracle.minmax(np.array([1, 2, 3], np.float32)) == (0.0, 3.0)
+    assert oracle.minmax(np.array([-4, np.nan, -1], np.float32)) == (-4.0, 0.0)
+    x = synth.normal(61, (4097,))
+    assert oracle.minmax(x) == (min(0.0, float(x.min())), max(0.0, float(x.max())))
+
+
+def test_dql_params_follow_the_formula(oracle):
+    for mn, mx in [(-1.0, 2.0), (0.0, 0.0), (-3.3, 0.0), (0.0, 7.1), (-0.37, 0.91)]:
+        s, z = oracle.dql_params(mn, mx)
+        es = np.float32(np.float32(mx) - np.float32(mn)) / np.float32(255)
+        if not es > 0:
+            es = np.float32(1)
+        assert s == es
+        assert z == int(np.clip(np.rint(np.float32(-np.float32(mn)) / es), 0, 255))
+
+
+def test_quantize_rounds_half_to_even(oracle):
+    q = oracle.quantize_u8(np.array([0.25, 0.75, 1.25, -0.25, -0.75], np.float32), 0.5, 10)
+    assert q.tolist() == [10, 12, 12, 10, 8]
+
+
+def test_dqmm_accumulators_are_exact_integers(oracle):
+    m, k, n = 64, 512, 96
+    a = synth.normal(71, (m, k))
+    w = synth.randint(72, (k, n), -127, 127, np.int8)
+    ws = synth.uniform(73, (n,), 0.001, 0.02)
+    bias = synth.normal(74, (n,), 0, 0.01)
+    out, acc, accf, s, z = oracle.dqmm(a, w, None, ws, bias)
+    q, s2, z2 = oracle.dynamic_quantize_linear(a)
+    assert (s, z) == (s2, z2)
+    brute = (q.astype(np.int64) - z) @ w.astype(np.int64)
+    assert (acc == brute).all()
+    # the reference's FP32 chain is exact here (|partial sums| < 2^24), so it equals the integer
+    assert (accf == acc.astype(np.float32)).all()
+    comb = (s * ws).astype(np.float32)
+    expect = (acc.astype(np.float64) * comb.astype(np.float64) + bias)
+    assert np.abs(out - expect).max() <= 1e-5 * np.abs(expect).max()
+
+
+def test_dqmm_weight_zero_points_and_u8_weights(oracle):
+    m, k, n = 9, 40, 13
+    a = synth.normal(81, (m, k))
+    for wdt, lo, hi in ((np.uint8, 0, 255), (np.int8, -128, 127)):
+        w = synth.randint(82, (k, n), lo, hi, wdt)
+        zp = synth.randint(83, (n,), -20, 20, np.int32) + (128 if wdt == np.uint8 else 0)
+        out, acc, accf, s, z = oracle.dqmm(a, w, zp, np.float32(0.01), None)
+        q, _, _ = oracle.dynamic_quantize_linear(a)
+        brute = (q.astype(np.int64) - z) @ (w.astype(np.int64) - zp[None, :])
+        assert (acc == brute).all()
+        mi = oracle.matmul_integer(q, w, z, zp)
+        assert (mi == brute).all()
+
+
+def test_planted_mistake_is_caught(oracle):
+    # a transposed weight (a plausible layout slip) must fail the float64 comparison used above
+    x = synth.uniform(91, (1, 4, 7, 7))
+    w = synth.normal(92, (4, 4, 3, 3), 0, 0.05)
+    ref = oracle.conv2d_f64(x, w, None, (1, 1), (1, 1), (1, 1), 1, (7, 7))
+    bad = oracle.conv2d_f32(x, np.ascontiguousarray(w.transpose(0, 1, 3, 2)), None, (1, 1), (1, 1), (1, 1), 1, (7, 7))
+    assert np.abs(bad - ref).max() > 1e-3
