@@ -1,0 +1,335 @@
+"""Benchmark of the dense-contraction hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+
+A step is one launch of the hot path on resident synthetic inputs.  The
+default workload is the 3x3 stride-1 pad-1 Conv + bias + fused SiLU on
+X[1,64,160,160] U(0,1), W[64,64,3,3] N(0,0.05), b[64] N(0,0.01) (the shape the
+reference publishes a CPU number for).  Other workloads (--config):
+  c1   MatMul + Add(bias) fused: A[1024,768] x B[768,768] + bias[768], U(-1,1)
+  c3a  1x1 conv 256->128 @ 80x80 + bias + SiLU
+  c3b  3x3 stride-2 conv 128->256, 80x80 -> 40x40 + bias + SiLU
+  c5   int8 DynamicQuantizeMatMul A f32[512,512] N(0,1), W s8[512,2048], per-column scales, bias
+
+Prints ONE JSON line.  `value` is whole-job TFLOP/s (TOP/s for c5) from HIP
+events on the launch stream over exactly K back-to-back steps; `roofline`
+prices the dominant kernel against the MI355X peak; `cpu_baseline` times the
+CPU oracle (a restatement of the reference's CPU kernels) on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK = {"fp32_mfma_tflops": 157.3, "int8_tops": 5000.0, "hbm_gbs": 8000.0}
+METRIC = "conv/GEMM TFLOP/s + % MI355X MFMA peak; ms/frame YOLO11n-shape 640²"
+
+
+def host_info() -> dict:
+    info = {"model": "", "flags": [], "logical_cpus": os.cpu_count()}
+    try:
+        txt = open("/proc/cpuinfo").read()
+        for line in txt.splitlines():
+            if line.startswith("model name") and not info["model"]:
+                info["model"] = line.split(":", 1)[1].strip()
+            if line.startswith("flags"):
+                fl = set(line.split(":", 1)[1].split())
+                info["flags"] = sorted(f for f in ("avx2", "fma", "avx512f", "avx512vl", "avx512_vnni", "avx_vnni")
+                                       if f in fl)
+                break
+        cores = {(l.split(":")[1].strip()) for l in txt.splitlines() if l.startswith("core id")}
+        sockets = {(l.split(":")[1].strip()) for l in txt.splitlines() if l.startswith("physical id")}
+        info["physical_cores"] = max(1, len(cores)) * max(1, len(sockets))
+    except OSError:
+        pass
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    return info
+
+
+class Workload:
+    name = ""
+    flops = 0.0        # algorithmic flops (or int ops) per step
+    bytes = 0.0        # algorithmic HBM bytes per step (each tensor read or written once)
+    bound = "mfma"
+    peak = PEAK["fp32_mfma_tflops"]
+    dtype = "f32"
+    kernel = ""
+    config: dict = {}
+
+    def step(self):
+        raise NotImplementedError
+
+    def cpu_step(self, oracle):
+        raise NotImplementedError
+
+
+def _t(x, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+class ConvWorkload(Workload):
+    def __init__(self, dev, name, xs, ws, stride, act, kernel, seed):
+        import torch
+        from onnxsharp_amd import native as N, synth
+        from onnxsharp_amd.layers import ConvLayer
+        self.name = name
+        self.kernel = kernel
+        k = ws[2]
+        pad = (k - 1) // 2
+        self.layer = ConvLayer(strides=[stride, stride], pads=[pad] * 4, fused_activation=act)
+        self.x_np = synth.uniform(seed, xs)
+        self.w_np = synth.normal(seed + 1, ws, 0.0, 0.05)
+        self.b_np = synth.normal(seed + 2, (ws[0],), 0.0, 0.01)
+        self.x, self.w, self.b = _t(self.x_np, dev), _t(self.w_np, dev), _t(self.b_np, dev)
+        p, buf = self.layer.prepack_weights(xs, self.w)
+        self.p, self.wbuf = p, buf
+        self.y = torch.empty((p.n, p.m, p.oh, p.ow), dtype=torch.float32, device=dev)
+        self.flops = 2.0 * p.n * p.m * (p.c // p.group) * p.kh * p.kw * p.oh * p.ow
+        self.bytes = 4.0 * (self.x.numel() + self.w.numel() + self.b.numel() + self.y.numel())
+        self.act = N.ACTIVATIONS[act]
+        self.fn = N.lib().osh_conv2d_f32
+        self.args = (C.byref(p), C.c_void_p(self.x.data_ptr()), C.c_void_p(buf.data_ptr()),
+                     C.c_void_p(self.b.data_ptr()), self.act, C.c_void_p(self.y.data_ptr()))
+        self.config = {"workload": f"conv{k}x{k} s{stride} p{pad} {xs[1]}->{ws[0]} @{xs[2]}x{xs[3]} + bias"
+                                   + (f" + {act}" if act else ""),
+                       "x": list(xs), "w": list(ws), "stride": stride, "pads": [pad] * 4,
+                       "inputs": "x U(0,1), w N(0,0.05), b N(0,0.01), splitmix64 seeds "
+                                 f"{seed},{seed + 1},{seed + 2}"}
+
+    def step(self, stream):
+        st = self.fn(*self.args, stream)
+        if st != 0:
+            from onnxsharp_amd import native as N
+            N.check(st)
+
+    def cpu_step(self, oracle):
+        p = self.p
+        y = oracle.conv2d_f32(self.x_np, self.w_np, self.b_np, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), p.group,
+                              (p.oh, p.ow), order=oracle.ORDER_IM2COL)
+        return oracle.silu_ref(y)
+
+
+class GemmWorkload(Workload):
+    def __init__(self, dev):
+        import torch
+        from onnxsharp_amd import native as N, synth
+        self.name = "c1"
+        self.kernel = "igemm_f32_kernel"
+        m, k, n = 1024, 768, 768
+        self.a_np = synth.uniform(101, (m, k), -1, 1)
+        self.b_np = synth.uniform(102, (k, n), -1, 1)
+        self.bias_np = synth.uniform(103, (n,), -1, 1)
+        self.a, self.b, self.bias = _t(self.a_np, dev), _t(self.b_np, dev), _t(self.bias_np, dev)
+        self.c = torch.empty((m, n), dtype=torch.float32, device=dev)
+        self.flops = 2.0 * m * n * k
+        self.bytes = 4.0 * (m * k + k * n + n + m * n)
+        self.fn = N.lib().osh_gemm_f32
+        self.args = (m, n, k, C.c_void_p(self.a.data_ptr()), k, C.c_void_p(self.b.data_ptr()), n,
+                     C.c_void_p(self.bias.data_ptr()), None, None, N.ACT_NONE, C.c_void_p(self.c.data_ptr()), n)
+        self.config = {"workload": "MatMul+Add(bias) fused, A[1024x768] . B[768x768] + bias[768]",
+                       "inputs": "U(-1,1), splitmix64 seeds 101,102,103"}
+
+    def step(self, stream):
+        st = self.fn(*self.args, stream)
+        if st != 0:
+            from onnxsharp_amd import native as N
+            N.check(st)
+
+    def cpu_step(self, oracle):
+        return oracle.gemm_f32(self.a_np, self.b_np, col_bias=self.bias_np)
+
+
+class DqmmWorkload(Workload):
+    def __init__(self, dev):
+        import torch
+        from onnxsharp_amd import native as N, synth
+        from onnxsharp_amd.layers import DynamicQuantizeMatMulLayer
+        self.name = "c5"
+        self.kernel = "dqmm_gemm_kernel"
+        self.dtype = "int8"
+        self.bound = "hbm"
+        m, k, n = 512, 512, 2048
+        self.a_np = synth.normal(201, (m, k))
+        self.w_np = synth.randint(202, (k, n), -127, 127, np.int8)
+        self.ws_np = synth.uniform(203, (n,), 0.001, 0.02)
+        self.bias_np = synth.normal(204, (n,), 0, 0.01)
+        self.a, self.w = _t(self.a_np, dev), _t(self.w_np, dev)
+        self.ws, self.bias = _t(self.ws_np, dev), _t(self.bias_np, dev)
+        self.layer = DynamicQuantizeMatMulLayer()
+        self.out = self.layer.forward(self.a, self.w, None, self.ws, self.bias)  # packs W, sizes scratch
+        self.flops = 2.0 * m * n * k
+        self.bytes = 4.0 * m * k + k * n + 4.0 * m * n + 8.0 * n
+        self.fn = N.lib().osh_dqmm_u8s8
+        self.args = (m, k, n, C.c_void_p(self.a.data_ptr()), C.c_void_p(self.layer._packed[1].data_ptr()),
+                     C.c_void_p(self.ws.data_ptr()), n, C.c_void_p(self.bias.data_ptr()),
+                     C.c_void_p(self.out.data_ptr()), None, None, C.c_void_p(self.layer._scratch.data_ptr()))
+        self.config = {"workload": "int8 DynamicQuantizeMatMul A f32[512x512] -> u8, W s8[512x2048], "
+                                   "per-column scales, bias",
+                       "inputs": "A N(0,1), W uniform{-127..127}, w_scale U(0.001,0.02), bias N(0,0.01), "
+                                 "splitmix64 seeds 201-204"}
+
+    def step(self, stream):
+        st = self.fn(*self.args, stream)
+        if st != 0:
+            from onnxsharp_amd import native as N
+            N.check(st)
+
+    def cpu_step(self, oracle):
+        return oracle.dqmm(self.a_np, self.w_np, None, self.ws_np, self.bias_np)[0]
+
+
+def make_workload(name, dev):
+    if name == "c2":
+        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "conv3x3_kernel", 1)
+    if name == "c3a":
+        return ConvWorkload(dev, "c3a", (1, 256, 80, 80), (128, 256, 1, 1), 1, "Silu", "igemm_f32_kernel", 11)
+    if name == "c3b":
+        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "conv3x3_kernel", 21)
+    if name == "c1":
+        return GemmWorkload(dev)
+    if name == "c5":
+        return DqmmWorkload(dev)
+    raise SystemExit(f"unknown --config {name}")
+
+
+def time_gpu(wl, steps, warmup):
+    import torch
+    from onnxsharp_amd import native as N
+    stream = torch.cuda.current_stream().cuda_stream
+    sp = C.c_void_p(stream)
+    for _ in range(warmup):
+        wl.step(sp)
+    torch.cuda.synchronize()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    N.call("osh_event_create", C.byref(e0))
+    N.call("osh_event_create", C.byref(e1))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    N.call("osh_event_record", e0, sp)
+    for _ in range(steps):
+        wl.step(sp)
+    N.call("osh_event_record", e1, sp)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = C.c_float()
+    N.call("osh_event_elapsed_ms", e0, e1, C.byref(ms))
+    N.call("osh_event_destroy", e0)
+    N.call("osh_event_destroy", e1)
+    return ms.value, wall
+
+
+def cpu_baseline(wl, threads, budget_s):
+    from oracle import oracle
+    oracle.set_threads(threads)
+    wl.cpu_step(oracle)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        wl.cpu_step(oracle)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return wl.flops * n / el / 1e12, n, el
+
+
+def read_traffic(kernel, name):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    try:
+        d = json.load(open(path))
+        return d.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU (every box here has one MI355X); "
+              f"--gpus {args.gpus} is not supported. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from onnxsharp_amd import native as N
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    info = N.DeviceInfo()
+    N.call("osh_init", 0, C.byref(info))
+    dev = torch.device("cuda", 0)
+
+    wl = make_workload(args.config, dev)
+    ms, wall = time_gpu(wl, args.steps, args.warmup)
+    ms_step = ms / args.steps
+    tflops = wl.flops / (ms_step * 1e-3) / 1e12
+    if wl.bound == "hbm":
+        achieved = wl.bytes / (ms_step * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm_gbs"], "unit": "GB/s",
+                "frac": round(achieved / PEAK["hbm_gbs"], 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
+                "frac": round(tflops / PEAK["fp32_mfma_tflops"], 4)}
+    roof["traffic"] = read_traffic(wl.kernel, wl.name)
+    roof["kernel"] = wl.kernel
+    roof["algorithmic_per_launch"] = {"flops": wl.flops, "bytes": wl.bytes}
+
+    cpu = None
+    if not args.no_cpu:
+        hi = host_info()
+        v4, n4, el4 = cpu_baseline(wl, 4, args.cpu_seconds)
+        unit = "TOP/s" if wl.dtype == "int8" else "TFLOP/s"
+        cpu = {"value": round(v4, 5), "unit": unit, "cores": 4, "kind": "port",
+               "sample": f"{n4} full steps of the same workload in {el4:.1f} s (oracle, 4 threads)",
+               "host": hi}
+        allc = hi.get("affinity_cpus") or hi.get("physical_cores") or 4
+        allc = int(min(allc, hi.get("physical_cores", allc), 16))
+        if allc != 4:
+            va, na, ela = cpu_baseline(wl, allc, args.cpu_seconds / 2)
+            cpu["all_cores"] = {"value": round(va, 5), "cores": allc,
+                                "sample": f"{na} steps in {ela:.1f} s"}
+
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TOP/s" if wl.dtype == "int8" else "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl.dtype,
+        "data": "synthetic",
+        "config": wl.config,
+        "frac_of_mfma_peak": round(tflops / (PEAK["int8_tops"] if wl.dtype == "int8" else PEAK["fp32_mfma_tflops"]), 4),
+        "wall_s": round(wall, 4),
+        "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.compute_units},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

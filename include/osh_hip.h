@@ -71,6 +71,16 @@ OSH_API osh_status osh_init(int dev, osh_device_info *info);
 OSH_API osh_status osh_device_count(int *count);
 OSH_API osh_status osh_device_synchronize(void);
 
+/* Backend options (the reference reads its kernel switches from ONNXSHARP_*
+ * environment variables, e.g. src/OnnxSharp/Kernels/NchwcConv.cs:39-40).
+ *   "exact_silu": 0 (default) = fused SiLU epilogues use exp2/rcp (relative
+ *                 difference to the reference polynomial < 2e-6);
+ *                 1 = the reference polynomial and IEEE division bit for bit
+ *                 (src/OnnxSharp/Tensors/VectorMath.cs:21-77).  Initial value
+ *                 from ONNXSHARP_HIP_EXACT_SILU. */
+OSH_API osh_status osh_config_set(const char *key, int value);
+OSH_API osh_status osh_config_get(const char *key, int *value);
+
 /* ------------------------------------------------------------------ memory */
 
 /* Device buffers: the C# side pools them by (kind, bytes) as VkBufferPool does

@@ -21,8 +21,11 @@ LIB = os.path.join(HERE, "libosh_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+
 CFLAGS = [
     f"--offload-arch={ARCH}",
+    "-I", INCLUDE,
     "-O3",
     "-std=c++17",
     "-fPIC",

@@ -4,7 +4,11 @@
 //
 //   depthwise (group == C == M)         -> dw_conv_kernel (direct, ky -> kx FMA chain)
 //   1x1 / stride 1 / pad 0 / dil 1      -> MFMA GEMM over NCHW (W[M,C] x X[C,H*W])
-//   3x3 / pad 1 / dil 1 / stride 1 or 2 -> MFMA implicit GEMM on an LDS halo tile
+//   3x3 / pad 1 / dil 1 / stride 1, C = 16, 32, 64, OW % 8 == 0
+//                                       -> wave-independent MFMA kernel (osh_conv3x3_wi.h)
+//   3x3 / pad 1 / dil 1 / stride 1 or 2, C = 16..128 (C % 16 == 0), OW % 4 == 0
+//                                       -> weight-stationary MFMA kernel (osh_conv3x3_ws.h)
+//   other 3x3 / pad 1 / dil 1 / s 1, 2  -> MFMA implicit GEMM on an LDS halo tile (osh_conv3x3.h)
 //   everything else                     -> MFMA implicit GEMM with an im2col gather
 //
 // Bias and the fused activation (Relu / SiLU, GraphFusion.cs:1713-1718) are
@@ -12,6 +16,8 @@
 #include <cstring>
 
 #include "osh_conv3x3.h"
+#include "osh_conv3x3_wi.h"
+#include "osh_conv3x3_ws.h"
 #include "osh_igemm.h"
 #include "osh_launch.h"
 
@@ -99,13 +105,15 @@ __global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const f
     y[idx] = activate<ACT>(acc);
 }
 
-enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3 };
+enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3, ALGO_WS3X3 = 4, ALGO_WI3X3 = 5 };
 
 static ConvAlgo select_algo(const osh_conv_params *p) {
     if (p->group == p->c && p->group == p->m && p->group > 1) return ALGO_DEPTHWISE;
     if (p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 && p->oh == p->h &&
         p->ow == p->w)
         return ALGO_POINTWISE;
+    if (conv3x3_wi_eligible(p)) return ALGO_WI3X3;
+    if (conv3x3_ws_eligible(p)) return ALGO_WS3X3;
     if (conv3x3_eligible(p)) return ALGO_DIRECT3X3;
     return ALGO_IM2COL;
 }
@@ -187,7 +195,12 @@ OSH_API osh_status osh_conv_packed_weight_bytes(const osh_conv_params *p, size_t
     if (st != OSH_OK) return st;
     if (!bytes) return fail(OSH_E_INVALID, "bytes is NULL");
     size_t oihw = (size_t)p->m * (p->c / p->group) * p->kh * p->kw * sizeof(float);
-    *bytes = select_algo(p) == ALGO_DIRECT3X3 ? conv3x3_packed_bytes(p) : oihw;
+    switch (select_algo(p)) {
+    case ALGO_WI3X3: *bytes = conv3x3_wi_packed_bytes(p); break;
+    case ALGO_WS3X3: *bytes = conv3x3_ws_packed_bytes(p); break;
+    case ALGO_DIRECT3X3: *bytes = conv3x3_packed_bytes(p); break;
+    default: *bytes = oihw;
+    }
     return OSH_OK;
 }
 
@@ -196,6 +209,8 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
     osh_status st = check_params(p);
     if (st != OSH_OK) return st;
     if (!d_w || !d_packed) return fail(OSH_E_INVALID, "Conv pack: NULL pointer");
+    if (select_algo(p) == ALGO_WI3X3) return conv3x3_wi_pack(p, d_w, d_packed, to_stream(s));
+    if (select_algo(p) == ALGO_WS3X3) return conv3x3_ws_pack(p, d_w, d_packed, to_stream(s));
     if (select_algo(p) == ALGO_DIRECT3X3) return conv3x3_pack(p, d_w, d_packed, to_stream(s));
     size_t oihw = (size_t)p->m * (p->c / p->group) * p->kh * p->kw * sizeof(float);
     OSH_HIP_CHECK(hipMemcpyAsync(d_packed, d_w, oihw, hipMemcpyDeviceToDevice, to_stream(s)));
@@ -222,6 +237,10 @@ OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, co
         OSH_LAUNCH_CHECK("dw_conv_kernel");
         return OSH_OK;
     }
+    case ALGO_WI3X3:
+        return conv3x3_wi_launch(p, d_x, w, d_bias, act, d_y, stream, device_cus());
+    case ALGO_WS3X3:
+        return conv3x3_ws_launch(p, d_x, w, d_bias, act, d_y, stream);
     case ALGO_DIRECT3X3:
         return conv3x3_launch(p, d_x, w, d_bias, act, d_y, stream);
     case ALGO_POINTWISE:

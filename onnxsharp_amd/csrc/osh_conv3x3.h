@@ -6,14 +6,19 @@
 // accumulators per row group) and through PackedConv / Im2Col elsewhere.  Here
 // a workgroup owns 64 output channels x TH output rows x 32 output columns.
 // Per chunk of CI input channels it stages
-//   - the input halo patch  [CI][(TH-1)*S+3][31*S+3]  (zero outside the image;
-//     for S = 2 each row is stored even columns first, then odd columns, so the
-//     stride-2 taps read consecutive LDS words), and
-//   - the packed weights    [9 taps][CI][64 oc]        (one contiguous block),
-// and every wave issues v_mfma_f32_32x32x2f32 with A = weights (oc x ic pair)
-// and B = patch (ic pair x 32 pixels of one output row).  The accumulation
-// order per output is: bias, then chunk -> tap (ky, kx) -> input-channel pair,
-// i.e. the NchwcConv order (icb -> ky -> kx -> lane) with 8-channel blocks.
+//   - the input halo patch  [(TH-1)*S+3 rows][2][31*S+3 cols][4]  (zero outside
+//     the image; channel ci lives at [ci / 4][..][ci % 4]; for S = 2 each row is
+//     stored even columns first, then odd columns, so the stride-2 taps of 32
+//     neighbouring pixels are consecutive), and
+//   - the packed weights    [9 taps][2][64 oc][4]                 (one contiguous
+//     block, same channel split),
+// so a lane fetches the operands of four k-steps with one ds_read_b128 each.
+// Every wave issues v_mfma_f32_32x32x2f32 with A = weights (32 oc x channel
+// pair) and B = patch (channel pair x 32 pixels of one output row); the next
+// tap's operands are loaded while the current tap's four MFMAs run.  The
+// accumulation order per output is: bias, then chunk of 8 channels -> tap
+// (ky, kx) -> channel pairs (s, s + 4), an NchwcConv-like order
+// (icb -> ky -> kx -> lane) with 8-channel blocks.
 #pragma once
 
 #include "osh_common.h"
@@ -33,15 +38,18 @@ inline size_t conv3x3_packed_bytes(const osh_conv_params *p) {
     return mt * chunks * 9 * C3_CI * C3_BM * sizeof(float);
 }
 
-// packed[mt][chunk][tap][ci][64] = w[mt*64 + oc][chunk*CI + ci][tap] (0 beyond M or C).
+// packed[mt][chunk][tap][ci / 4][oc 64][ci % 4] = w[mt*64 + oc][chunk*CI + ci][tap] (0 beyond M or C).
 __global__ void conv3x3_pack_kernel(int M, int C, const float *__restrict__ w, float *__restrict__ out,
                                     long long total) {
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    int oc = (int)(i % C3_BM);
-    long long t = i / C3_BM;
-    int ci = (int)(t % C3_CI);
-    t /= C3_CI;
+    int c4 = (int)(i % 4);
+    long long t = i / 4;
+    int oc = (int)(t % C3_BM);
+    t /= C3_BM;
+    int chi = (int)(t % 2);
+    t /= 2;
+    int ci = chi * 4 + c4;
     int tap = (int)(t % 9);
     t /= 9;
     int chunks = (C + C3_CI - 1) / C3_CI;
@@ -65,6 +73,7 @@ __global__ __launch_bounds__(TH * 2 * 64) void conv3x3_kernel(osh_conv_params p,
                                                              const float *__restrict__ bias,
                                                              float *__restrict__ y) {
     constexpr int CI = C3_CI;
+    static_assert(CI == 8, "the operand layout splits a chunk into two groups of four channels");
     constexpr int NW = TH * 2;             // waves: (row, oc half)
     constexpr int THREADS = NW * 64;
     constexpr int PR = (TH - 1) * S + 3;   // patch rows
@@ -76,15 +85,16 @@ __global__ __launch_bounds__(TH * 2 * 64) void conv3x3_kernel(osh_conv_params p,
     constexpr int WE4 = 9 * CI * C3_BM / 4;  // weight float4 per chunk
     constexpr int W_PER = (WE4 + THREADS - 1) / THREADS;
 
-    __shared__ __align__(16) float Xs[2][CI][PR][PITCH];
-    __shared__ __align__(16) float Ws[2][9][CI][C3_BM];
+    __shared__ __align__(16) float Xs[2][PR][2][PITCH][4];
+    __shared__ __align__(16) float Ws[2][9][2][C3_BM][4];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wrow = wave >> 1, whalf = wave & 1;
     const int ox0 = blockIdx.x * 32;
     const int oy0 = blockIdx.y * TH;
-    const int mt = blockIdx.z % ((p.m + C3_BM - 1) / C3_BM);
-    const int n = blockIdx.z / ((p.m + C3_BM - 1) / C3_BM);
+    const int mtiles = (p.m + C3_BM - 1) / C3_BM;
+    const int mt = blockIdx.z % mtiles;
+    const int n = blockIdx.z / mtiles;
     const int chunks = (p.c + CI - 1) / CI;
     const int H = p.h, W = p.w;
     const float *__restrict__ xn = x + (long long)n * p.c * H * W;
@@ -127,10 +137,10 @@ __global__ __launch_bounds__(TH * 2 * 64) void conv3x3_kernel(osh_conv_params p,
                 int r = (e / PC) % PR;
                 int col = e % PC;
                 int sc = S == 1 ? col : ((col & 1) ? HALF + (col >> 1) : (col >> 1));
-                Xs[buf][ci][r][sc] = rp[i];
+                Xs[buf][r][ci >> 2][sc][ci & 3] = rp[i];
             }
         }
-        float4 *wdst = reinterpret_cast<float4 *>(&Ws[buf][0][0][0]);
+        float4 *wdst = reinterpret_cast<float4 *>(&Ws[buf][0][0][0][0]);
 #pragma unroll
         for (int i = 0; i < W_PER; i++) {
             int e = tid + i * THREADS;
@@ -148,26 +158,34 @@ __global__ __launch_bounds__(TH * 2 * 64) void conv3x3_kernel(osh_conv_params p,
         acc[r] = (bias && oc < p.m) ? bias[oc] : 0.f;
     }
 
+    // stored column of pixel l32 for tap kx
+    auto scol = [&](int kx) { return S == 1 ? l32 + kx : (kx == 1 ? HALF + l32 : l32 + (kx >> 1)); };
+
     load_chunk(0);
     store_chunk(0);
     __syncthreads();
     for (int ch = 0; ch < chunks; ch++) {
         const int buf = ch & 1;
         if (ch + 1 < chunks) load_chunk(ch + 1);
+        const float4 *wa = reinterpret_cast<const float4 *>(&Ws[buf][0][lhi][whalf * 32 + l32][0]);
+        constexpr int WTAP4 = 2 * C3_BM;  // float4 stride between taps
+        float4 a = wa[0];
+        float4 b = *reinterpret_cast<const float4 *>(&Xs[buf][wrow * S][lhi][scol(0)][0]);
 #pragma unroll
-        for (int ky = 0; ky < 3; ky++) {
-            const int prow = wrow * S + ky;
-#pragma unroll
-            for (int kx = 0; kx < 3; kx++) {
-                // stored column of pixel l32 for tap kx
-                const int scol = S == 1 ? l32 + kx : (kx == 1 ? HALF + l32 : l32 + (kx >> 1));
-#pragma unroll
-                for (int s2 = 0; s2 < CI / 2; s2++) {
-                    const int ci = 2 * s2 + lhi;
-                    float a = Ws[buf][ky * 3 + kx][ci][whalf * 32 + l32];
-                    float b = Xs[buf][ci][prow][scol];
-                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
-                }
+        for (int tap = 0; tap < 9; tap++) {
+            float4 an, bn;
+            if (tap < 8) {
+                const int ky = (tap + 1) / 3, kx = (tap + 1) % 3;
+                an = wa[(tap + 1) * WTAP4];
+                bn = *reinterpret_cast<const float4 *>(&Xs[buf][wrow * S + ky][lhi][scol(kx)][0]);
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+            if (tap < 8) {
+                a = an;
+                b = bn;
             }
         }
         if (ch + 1 < chunks) store_chunk(buf ^ 1);

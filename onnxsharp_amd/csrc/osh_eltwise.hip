@@ -27,9 +27,24 @@ OSH_API osh_status osh_activation_f32(int64_t n, const float *d_x, int act, floa
     if (!d_x || !d_y) return fail(OSH_E_INVALID, "NULL pointer");
     long long blocks = (n + 255) / 256;
     if (blocks > 8192) blocks = 8192;
-    OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL(activation_kernel<ACT>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s),
-                                        d_x, d_y, (long long)n));
+    // the standalone pass is TensorOps.ElementWiseUnary itself: always the reference SiLU
+    const int a = act == OSH_ACT_SILU ? ACT_SILU_EXACT : act;
+    switch (a) {
+    case OSH_ACT_NONE:
+        hipLaunchKernelGGL(activation_kernel<OSH_ACT_NONE>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
+                           d_y, (long long)n);
+        break;
+    case OSH_ACT_RELU:
+        hipLaunchKernelGGL(activation_kernel<OSH_ACT_RELU>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
+                           d_y, (long long)n);
+        break;
+    case ACT_SILU_EXACT:
+        hipLaunchKernelGGL(activation_kernel<ACT_SILU_EXACT>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
+                           d_y, (long long)n);
+        break;
+    default:
+        return fail(OSH_E_INVALID, "unknown activation %d", act);
+    }
     OSH_LAUNCH_CHECK("activation_kernel");
     return OSH_OK;
 }

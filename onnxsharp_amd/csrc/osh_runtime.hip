@@ -3,6 +3,7 @@
 // reference backend (src/OnnxSharp.Vulkan/VkDevice.cs, VkBufferPool.cs,
 // VkSegment.cs) with plain HIP calls.
 #include <cstdarg>
+#include <cstdlib>
 #include <cstring>
 
 #include "osh_common.h"
@@ -23,6 +24,16 @@ void clear_error() { g_err[0] = 0; }
 
 const char *last_error() { return g_err; }
 
+static int g_exact_silu = -1;  // -1: read ONNXSHARP_HIP_EXACT_SILU on first use
+
+bool exact_silu() {
+    if (g_exact_silu < 0) {
+        const char *e = getenv("ONNXSHARP_HIP_EXACT_SILU");
+        g_exact_silu = (e && atoi(e) != 0) ? 1 : 0;
+    }
+    return g_exact_silu == 1;
+}
+
 __global__ void fill_u8_kernel(uint8_t *__restrict__ p, uint8_t v, size_t n) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -36,6 +47,24 @@ using namespace osh;
 extern "C" {
 
 OSH_API const char *osh_last_error(void) { return osh::last_error(); }
+
+OSH_API osh_status osh_config_set(const char *key, int value) {
+    if (!key) return fail(OSH_E_INVALID, "key is NULL");
+    if (strcmp(key, "exact_silu") == 0) {
+        g_exact_silu = value != 0;
+        return OSH_OK;
+    }
+    return fail(OSH_E_INVALID, "unknown option '%s'", key);
+}
+
+OSH_API osh_status osh_config_get(const char *key, int *value) {
+    if (!key || !value) return fail(OSH_E_INVALID, "NULL argument");
+    if (strcmp(key, "exact_silu") == 0) {
+        *value = exact_silu() ? 1 : 0;
+        return OSH_OK;
+    }
+    return fail(OSH_E_INVALID, "unknown option '%s'", key);
+}
 
 OSH_API osh_status osh_device_count(int *count) {
     if (!count) return fail(OSH_E_INVALID, "count is NULL");

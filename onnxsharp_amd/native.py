@@ -62,6 +62,8 @@ _SIGS = {
     "osh_init": ([_i, C.POINTER(DeviceInfo)], _i),
     "osh_device_count": ([C.POINTER(C.c_int)], _i),
     "osh_device_synchronize": ([], _i),
+    "osh_config_set": ([C.c_char_p, _i], _i),
+    "osh_config_get": ([C.c_char_p, C.POINTER(C.c_int)], _i),
     "osh_malloc": ([C.POINTER(_vp), _sz], _i),
     "osh_free": ([_vp], _i),
     "osh_host_alloc": ([C.POINTER(_vp), _sz], _i),

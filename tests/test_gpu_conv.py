@@ -1,6 +1,7 @@
 """GPU parity: Conv (+ bias + fused Relu/SiLU) through osh_conv2d_f32 against
 the oracle's restatements of the reference kernels, in both accumulation
 orders the reference uses (NCHWc on AVX-512 hosts, im2col/panel on AVX2)."""
+import ctypes as C
 import json
 import os
 
@@ -42,6 +43,10 @@ CASES = [
     ("c3b_3x3s2_128to256_80", (1, 128, 80, 80), (256, 128, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), "Silu"),
     ("yolo_stem_3to16_s2", (1, 3, 64, 64), (16, 3, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), "Silu"),
     ("3x3s1_small_spatial_20", (1, 64, 20, 20), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1]), "Silu"),
+    ("3x3s1_c32_m40_partial_tiles", (1, 32, 18, 24), (40, 32, 3, 3), dict(pads=[1, 1, 1, 1]), "Silu"),
+    ("3x3s1_c16_batch2", (2, 16, 12, 16), (16, 16, 3, 3), dict(pads=[1, 1, 1, 1]), "Relu"),
+    ("3x3s1_c64_m96_80", (1, 64, 40, 80), (96, 64, 3, 3), dict(pads=[1, 1, 1, 1]), None),
+    ("3x3s2_c64_m64_40", (1, 64, 80, 80), (64, 64, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), "Silu"),
     ("3x3s1_odd_33x45", (1, 24, 33, 45), (40, 24, 3, 3), dict(pads=[1, 1, 1, 1]), "Relu"),
     ("3x3s2_odd_41x37", (1, 16, 41, 37), (72, 16, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), None),
     ("1x1_no_bias_batch2", (2, 40, 17, 19), (24, 40, 1, 1), dict(), None),
@@ -82,12 +87,24 @@ def test_conv_known_answer_same_upper(cuda):
     assert (ya == yb).all()
 
 
-def test_conv_silu_epilogue_bit_exact_on_bias_only_input(cuda, oracle):
-    # zero input: the conv output is exactly the bias, so the fused SiLU must equal
-    # VectorMath.Silu of the bias bit for bit
+def test_conv_silu_epilogue_on_bias_only_input(cuda, oracle):
+    # zero input: the conv output is exactly the bias, so the fused SiLU can be
+    # compared on its own.  exact_silu=1 must reproduce VectorMath.Silu bit for
+    # bit; the default exp2/rcp epilogue must stay within 2e-6 of it.
+    from onnxsharp_amd import native as N
     x = np.zeros((1, 64, 40, 40), np.float32)
     w = synth.normal(5, (64, 64, 3, 3), 0, 0.05)
     b = synth.normal(6, (64,), 0, 3.0)
-    y, _ = run_conv(cuda, x, w, b, "Silu", pads=[1, 1, 1, 1])
-    expect = oracle.silu_ref(b)
-    assert (y[0] == expect[:, None, None]).all()
+    expect = oracle.silu_ref(b)[:, None, None]
+    old = C.c_int()
+    N.call("osh_config_get", b"exact_silu", C.byref(old))
+    try:
+        N.call("osh_config_set", b"exact_silu", 1)
+        y, _ = run_conv(cuda, x, w, b, "Silu", pads=[1, 1, 1, 1])
+        assert (y[0] == expect).all()
+        N.call("osh_config_set", b"exact_silu", 0)
+        y, _ = run_conv(cuda, x, w, b, "Silu", pads=[1, 1, 1, 1])
+        rel = np.abs(y[0] - expect) / np.maximum(np.abs(expect), 1e-30)
+        assert rel.max() < 2e-6
+    finally:
+        N.call("osh_config_set", b"exact_silu", old.value)
