@@ -10,6 +10,7 @@ reference publishes a CPU number for).  Other workloads (--config):
   c3a  1x1 conv 256->128 @ 80x80 + bias + SiLU
   c3b  3x3 stride-2 conv 128->256, 80x80 -> 40x40 + bias + SiLU
   c5   int8 DynamicQuantizeMatMul A f32[512,512] N(0,1), W s8[512,2048], per-column scales, bias
+  copy 64 MiB device-to-device copy (osh_memcpy_d2d): calibrates the HBM byte counters
 
 Prints ONE JSON line.  `value` is whole-job TFLOP/s (TOP/s for c5) from HIP
 events on the launch stream over exactly K back-to-back steps; `roofline`
@@ -191,17 +192,45 @@ class DqmmWorkload(Workload):
         return oracle.dqmm(self.a_np, self.w_np, None, self.ws_np, self.bias_np)[0]
 
 
+class CopyWorkload(Workload):
+    """Plain 64 MiB device copy: its FETCH_SIZE / WRITE_SIZE counter readings
+    calibrate the per-dispatch HBM traffic of the other workloads."""
+
+    def __init__(self, dev):
+        import torch
+        from onnxsharp_amd import native as N
+        self.name = "copy"
+        self.kernel = "__amd_rocclr_copyBuffer"
+        self.bound = "hbm"
+        self.nbytes = 64 << 20
+        self.src = torch.ones(self.nbytes // 4, dtype=torch.float32, device=dev)
+        self.dst = torch.empty_like(self.src)
+        self.flops = 0.0
+        self.bytes = 2.0 * self.nbytes
+        self.fn = N.lib().osh_memcpy_d2d
+        self.args = (C.c_void_p(self.dst.data_ptr()), C.c_void_p(self.src.data_ptr()), self.nbytes)
+        self.config = {"workload": "device-to-device copy of 64 MiB (counter calibration)"}
+
+    def step(self, stream):
+        st = self.fn(*self.args, stream)
+        if st != 0:
+            from onnxsharp_amd import native as N
+            N.check(st)
+
+
 def make_workload(name, dev):
     if name == "c2":
-        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "conv3x3_kernel", 1)
+        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "conv3x3_wi_kernel", 1)
     if name == "c3a":
         return ConvWorkload(dev, "c3a", (1, 256, 80, 80), (128, 256, 1, 1), 1, "Silu", "igemm_f32_kernel", 11)
     if name == "c3b":
-        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "conv3x3_kernel", 21)
+        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "conv3x3_ws_kernel", 21)
     if name == "c1":
         return GemmWorkload(dev)
     if name == "c5":
         return DqmmWorkload(dev)
+    if name == "copy":
+        return CopyWorkload(dev)
     raise SystemExit(f"unknown --config {name}")
 
 
@@ -282,6 +311,11 @@ def main():
     ms, wall = time_gpu(wl, args.steps, args.warmup)
     ms_step = ms / args.steps
     tflops = wl.flops / (ms_step * 1e-3) / 1e12
+    if wl.name == "copy":
+        gbs = wl.bytes / (ms_step * 1e-3) / 1e9
+        print(json.dumps({"metric": "device copy GB/s", "value": round(gbs, 1), "unit": "GB/s",
+                          "ms_per_step": round(ms_step, 5), "bytes_per_step": wl.bytes}), flush=True)
+        return
     if wl.bound == "hbm":
         achieved = wl.bytes / (ms_step * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm_gbs"], "unit": "GB/s",
