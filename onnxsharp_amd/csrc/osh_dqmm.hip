@@ -34,6 +34,7 @@ namespace osh {
 
 constexpr int DQ_MINMAX_BLOCKS = 256;
 constexpr int DQ_THREADS = 256;
+constexpr int DQ_KC = 8;  // k-steps of 32 per GEMM load chunk
 
 struct DqScratch {  // layout of the caller's scratch buffer
     float partial_min[DQ_MINMAX_BLOCKS];
@@ -80,8 +81,7 @@ __device__ void block_minmax(float &lo, float &hi) {
 }
 
 __global__ __launch_bounds__(DQ_THREADS) void dqmm_minmax_kernel(const float *__restrict__ a, long long n,
-                                                                  DqScratch *__restrict__ sc, int *__restrict__ rowsum,
-                                                                  int rows) {
+                                                                  DqScratch *__restrict__ sc) {
     float lo = 0.f, hi = 0.f;  // 0 is always inside the range (Quantization.cs:115-116)
     long long stride = (long long)gridDim.x * blockDim.x;
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -101,7 +101,6 @@ __global__ __launch_bounds__(DQ_THREADS) void dqmm_minmax_kernel(const float *__
         lo = v < lo ? v : lo;
         hi = v > hi ? v : hi;
     }
-    for (long long j = i; j < 2 * (long long)rows; j += stride) rowsum[j] = 0;  // rowsum and rownan
     block_minmax(lo, hi);
     if (threadIdx.x == 0) {
         sc->partial_min[blockIdx.x] = lo;
@@ -155,48 +154,83 @@ __device__ __forceinline__ int quantize_one(float x, float inv, float zpf) {
     return (int)q;
 }
 
-// One thread per (row, 16-wide k segment): writes one 16-byte operand slot.
+// One wave per row of A (padded rows write zeros): each lane quantizes 4
+// consecutive k per step (one 16-byte load, one 4-byte store into the lane's
+// operand slot), and the row sum of a'' and the NaN flag are wave reductions,
+// so the kernel needs no atomics and no zeroed scratch.
+struct Quad {
+    float v[4];
+};
+
+// x[kk .. kk+3] of one row (zeros past k or for padding rows).
+__device__ __forceinline__ Quad load_quad(const float *__restrict__ src, int kk, int k, bool live, bool vec) {
+    Quad q = {{0.f, 0.f, 0.f, 0.f}};
+    if (live && kk < k) {
+        if (vec) {
+            float4 v = *reinterpret_cast<const float4 *>(src + kk);
+            q.v[0] = v.x; q.v[1] = v.y; q.v[2] = v.z; q.v[3] = v.w;
+        } else {
+#pragma unroll
+            for (int b = 0; b < 4; b++) q.v[b] = kk + b < k ? src[kk + b] : 0.f;
+        }
+    }
+    return q;
+}
+
+constexpr int DQ_QPRE = 4;  // row chunks of 256 loaded before the parameter reduction
+
 __global__ __launch_bounds__(DQ_THREADS) void dqmm_quantize_kernel(const float *__restrict__ a, int m, int k,
                                                                     DqScratch *__restrict__ sc, int nparts,
                                                                     int *__restrict__ qparams,
                                                                     int *__restrict__ rowsum,
                                                                     int8_t *__restrict__ apk) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (DQ_THREADS / 64) + (threadIdx.x >> 6);
+    const int kpad = pad32(k), mpad = pad32(m);
+    const bool live = row < m;
+    const float *src = a + (long long)(live ? row : 0) * k;
+    const bool vec = (k & 3) == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+    // The first chunks of the row are in flight while the block reduces the
+    // min/max partials.
+    Quad pre[DQ_QPRE];
+#pragma unroll
+    for (int c = 0; c < DQ_QPRE; c++) pre[c] = load_quad(src, 4 * lane + 256 * c, k, live, vec);
     float inv;
     int zp;
     dq_params(sc, nparts, qparams, inv, zp);
+    if (row >= mpad) return;
     const float zpf = (float)zp;
-    const int kpad = pad32(k), segs = kpad / 16;
-    long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    long long total = (long long)pad32(m) * segs;
-    if (t >= total) return;
-    int row = (int)(t / segs), seg = (int)(t % segs);
-    int vals[16];
+    int *dst = reinterpret_cast<int *>(apk) + (long long)(row >> 5) * (kpad / 32) * 256 + (row & 31) * 4;
     int sum = 0;
     bool nan = false;
-    const float *src = a + (long long)row * k + seg * 16;
+    auto emit = [&](const Quad &x, int kk) {
+        unsigned packed = 0;
 #pragma unroll
-    for (int b = 0; b < 16; b++) {
-        int kk = seg * 16 + b;
-        int v = 0;  // padding rows/columns carry a'' = 0
-        if (row < m && kk < k) {
-            float x = src[b];
-            nan |= !(x * inv == x * inv);
-            v = quantize_one(x, inv, zpf) - 128;
-            sum += v;
+        for (int b = 0; b < 4; b++) {
+            int v = 0;  // padding rows/columns carry a'' = 0
+            if (live && kk + b < k) {
+                float p = x.v[b] * inv;
+                nan |= !(p == p);
+                v = quantize_one(x.v[b], inv, zpf) - 128;
+                sum += v;
+            }
+            packed |= (unsigned)(v & 0xff) << (8 * b);
         }
-        vals[b] = v;
-    }
-    i32x4 packed;
+        // fragment (row/32, kk/32); lane slot (row & 31) + 32 * ((kk >> 4) & 1); byte kk & 15
+        dst[(kk >> 5) * 256 + ((kk >> 4) & 1) * 128 + ((kk & 15) >> 2)] = (int)packed;
+    };
 #pragma unroll
-    for (int w = 0; w < 4; w++)
-        packed[w] = (vals[4 * w] & 0xff) | ((vals[4 * w + 1] & 0xff) << 8) | ((vals[4 * w + 2] & 0xff) << 16) |
-                    ((vals[4 * w + 3] & 0xff) << 24);
-    // fragment (row/32, seg/2), lane = (row & 31) + 32 * (seg & 1)
-    long long frag = (long long)(row >> 5) * (kpad / 32) + (seg >> 1);
-    int lane = (row & 31) + 32 * (seg & 1);
-    reinterpret_cast<i32x4 *>(apk)[frag * 64 + lane] = packed;
-    if (row < m && sum != 0) atomicAdd(&rowsum[row], sum);
-    if (row < m && nan) atomicOr(&rowsum[pad32(m) + row], 1);
+    for (int c = 0; c < DQ_QPRE; c++) {
+        const int kk = 4 * lane + 256 * c;
+        if (kk < kpad) emit(pre[c], kk);
+    }
+    for (int kk = 4 * lane + 256 * DQ_QPRE; kk < kpad; kk += 256) emit(load_quad(src, kk, k, live, vec), kk);
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    const bool any_nan = __any(nan);
+    if (lane == 0) {
+        rowsum[row] = sum;
+        rowsum[mpad + row] = any_nan ? 1 : 0;
+    }
 }
 
 // DynamicQuantizeLinear output: u8 q in the input's own layout.
@@ -259,47 +293,85 @@ __global__ __launch_bounds__(256) void dqmm_gemm_kernel(int m, int k, int n, con
     if (mt * 32 >= pad32(m) || nt * 32 >= pad32(n)) return;
     const i32x4 *A = reinterpret_cast<const i32x4 *>(apk) + (long long)mt * ks * 64 + lane;
     const i32x4 *B = reinterpret_cast<const i32x4 *>(wpk) + (long long)nt * ks * 64 + lane;
-    i32x16 acc = {};
-    int s = 0;
-    for (; s + 4 <= ks; s += 4) {
-        i32x4 a0 = A[(s + 0) * 64], a1 = A[(s + 1) * 64], a2 = A[(s + 2) * 64], a3 = A[(s + 3) * 64];
-        i32x4 b0 = B[(s + 0) * 64], b1 = B[(s + 1) * 64], b2 = B[(s + 2) * 64], b3 = B[(s + 3) * 64];
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a2, b2, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a3, b3, acc, 0, 0, 0);
-    }
-    for (; s < ks; s++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[s * 64], B[s * 64], acc, 0, 0, 0);
-
+    // Epilogue operands are loaded before the k loop so their latency overlaps it.
+    // The lane's 16 rows are 4 runs of 4 consecutive rows: their row sums and
+    // NaN flags are 8 int4 loads (rows are padded to mpad, columns to npad).
     const int j = nt * 32 + (lane & 31);
     const int mpad = pad32(m);
-    if (j >= n) return;
-    // two's-complement wrap-around is exact as long as the final sum fits in int32
-    const unsigned alpha = (unsigned)(128 - sc->zp);
+    int4 rs[4], rn[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int i0 = mt * 32 + 8 * g + 4 * (lane >> 5);
+        rs[g] = *reinterpret_cast<const int4 *>(rowsum + i0);
+        rn[g] = *reinterpret_cast<const int4 *>(rowsum + mpad + i0);
+    }
+    // two's-complement wrap-around below is exact as long as the final sum fits in int32
     const unsigned offj = (unsigned)off[j];
-    const unsigned colterm = alpha * (unsigned)colsum[j] + (unsigned)k * alpha * offj;
-    const float comb = sc->scale * (n_wscale == 1 ? wscale[0] : wscale[j]);  // CombinedScale, :203-221
-    const float b = bias ? bias[j] : 0.0f;
+    const int csum = colsum[j];
+    const float ws = j < n ? (n_wscale == 1 ? wscale[0] : wscale[j]) : 0.0f;
+    const float bj = (bias && j < n) ? bias[j] : 0.0f;
+    const int azp = sc->zp;
+    const float ascale = sc->scale;
+    // k in chunks of DQ_KC steps: the next chunk's 2*DQ_KC loads are in flight
+    // while the current chunk's MFMAs run.
+    i32x16 acc = {};
+    i32x4 a[DQ_KC], b[DQ_KC];
+    const int full = ks / DQ_KC;
+    if (full > 0) {
+#pragma unroll
+        for (int t = 0; t < DQ_KC; t++) {
+            a[t] = A[t * 64];
+            b[t] = B[t * 64];
+        }
+    }
+    for (int c = 0; c < full; c++) {
+        i32x4 na[DQ_KC], nb[DQ_KC];
+        const bool more = c + 1 < full;
+        if (more) {
+#pragma unroll
+            for (int t = 0; t < DQ_KC; t++) {
+                na[t] = A[((c + 1) * DQ_KC + t) * 64];
+                nb[t] = B[((c + 1) * DQ_KC + t) * 64];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < DQ_KC; t++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[t], b[t], acc, 0, 0, 0);
+        if (more) {
+#pragma unroll
+            for (int t = 0; t < DQ_KC; t++) {
+                a[t] = na[t];
+                b[t] = nb[t];
+            }
+        }
+    }
+    for (int s = full * DQ_KC; s < ks; s++)
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[s * 64], B[s * 64], acc, 0, 0, 0);
+
+    if (j >= n) return;
+    const unsigned alpha = (unsigned)(128 - azp);
+    const unsigned colterm = alpha * (unsigned)csum + (unsigned)k * alpha * offj;
+    const float comb = ascale * ws;  // CombinedScale, QuantizedMatMulOps.cs:203-221
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        int i = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int i = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int4 s4 = rs[r >> 2], n4 = rn[r >> 2];
+        const int rsum = (r & 3) == 0 ? s4.x : (r & 3) == 1 ? s4.y : (r & 3) == 2 ? s4.z : s4.w;
+        const int rnan = (r & 3) == 0 ? n4.x : (r & 3) == 1 ? n4.y : (r & 3) == 2 ? n4.z : n4.w;
         if (i < m) {
-            int v = (int)((unsigned)acc[r] + offj * (unsigned)rowsum[i] + colterm);
+            int v = (int)((unsigned)acc[r] + offj * (unsigned)rsum + colterm);
             if (acc_out) acc_out[(long long)i * n + j] = v;
-            float o = __builtin_fmaf((float)v, comb, b);
-            if (rowsum[mpad + i]) o = __builtin_nanf("");
+            float o = __builtin_fmaf((float)v, comb, bj);
+            if (rnan) o = __builtin_nanf("");
             out[(long long)i * n + j] = o;
         }
     }
 }
 
-static osh_status run_minmax(const float *a, long long count, DqScratch *sc, int *rowsum, int rows, int *nparts,
-                             hipStream_t st) {
+static osh_status run_minmax(const float *a, long long count, DqScratch *sc, int *nparts, hipStream_t st) {
     long long blocks = (count / 4 + DQ_THREADS - 1) / DQ_THREADS;
     if (blocks < 1) blocks = 1;
     if (blocks > DQ_MINMAX_BLOCKS) blocks = DQ_MINMAX_BLOCKS;
-    hipLaunchKernelGGL(dqmm_minmax_kernel, dim3((unsigned)blocks), dim3(DQ_THREADS), 0, st, a, count, sc, rowsum,
-                       rows);
+    hipLaunchKernelGGL(dqmm_minmax_kernel, dim3((unsigned)blocks), dim3(DQ_THREADS), 0, st, a, count, sc);
     *nparts = (int)blocks;
     OSH_LAUNCH_CHECK("dqmm_minmax_kernel");
     return OSH_OK;
@@ -370,10 +442,10 @@ OSH_API osh_status osh_dqmm_u8s8(int m, int k, int n, const float *d_a, const vo
     int *rowsum = reinterpret_cast<int *>(sc + 1);
     int8_t *apk = reinterpret_cast<int8_t *>(rowsum + 2 * pad32(m));
     int nparts = 0;
-    osh_status r = run_minmax(d_a, (long long)m * k, sc, rowsum, pad32(m), &nparts, st);
+    osh_status r = run_minmax(d_a, (long long)m * k, sc, &nparts, st);
     if (r != OSH_OK) return r;
-    long long qthreads = (long long)pad32(m) * (pad32(k) / 16);
-    hipLaunchKernelGGL(dqmm_quantize_kernel, dim3((unsigned)((qthreads + DQ_THREADS - 1) / DQ_THREADS)),
+    const int rows_per_block = DQ_THREADS / 64;
+    hipLaunchKernelGGL(dqmm_quantize_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
                        dim3(DQ_THREADS), 0, st, d_a, m, k, sc, nparts, (int *)d_qparams, rowsum, apk);
     OSH_LAUNCH_CHECK("dqmm_quantize_kernel");
     const int8_t *frag = static_cast<const int8_t *>(d_wpacked);
@@ -391,9 +463,8 @@ OSH_API osh_status osh_dynamic_quantize_linear(int64_t n, const float *d_x, uint
     if (n <= 0 || !d_x || !d_q || !d_scratch) return fail(OSH_E_INVALID, "DQL: bad argument");
     hipStream_t st = to_stream(s);
     DqScratch *sc = static_cast<DqScratch *>(d_scratch);
-    int *rowsum = reinterpret_cast<int *>(sc + 1);
     int nparts = 0;
-    osh_status r = run_minmax(d_x, n, sc, rowsum, 0, &nparts, st);
+    osh_status r = run_minmax(d_x, n, sc, &nparts, st);
     if (r != OSH_OK) return r;
     long long blocks = (n + DQ_THREADS - 1) / DQ_THREADS;
     if (blocks > 4096) blocks = 4096;
