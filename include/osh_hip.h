@@ -77,7 +77,13 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 difference to the reference polynomial < 2e-6);
  *                 1 = the reference polynomial and IEEE division bit for bit
  *                 (src/OnnxSharp/Tensors/VectorMath.cs:21-77).  Initial value
- *                 from ONNXSHARP_HIP_EXACT_SILU. */
+ *                 from ONNXSHARP_HIP_EXACT_SILU.
+ *   "gemm_variant": -1 (default) = dense GEMMs (MatMul, 1x1 conv) pick their
+ *                 wave tile from the problem size; 0..N-1 forces one tile
+ *                 where the operands allow it (tuning and tests); -2 = always
+ *                 use the LDS-staged GEMM tile.  Every choice sums k in the
+ *                 same order.  Initial value from ONNXSHARP_HIP_GEMM_VARIANT.
+ *   "gemm_variants" (get only): N, the number of wave tiles. */
 OSH_API osh_status osh_config_set(const char *key, int value);
 OSH_API osh_status osh_config_get(const char *key, int *value);
 

@@ -100,6 +100,23 @@ __device__ __forceinline__ float activate(float x) {
 
 bool exact_silu();
 
+// Compute units of the current device (256 on MI355X).
+inline int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+// Forced gemm16 wave tile (-1 = automatic, -2 = LDS-staged tile only) and
+// the number of wave tiles.
+int gemm_variant();
+int gemm16_variant_count();
+
 // Dispatch a runtime activation code to a template instantiation of a fused epilogue.
 #define OSH_DISPATCH_ACT(act, ACT, ...)                      \
     switch (act) {                                           \

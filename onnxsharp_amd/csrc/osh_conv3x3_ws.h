@@ -255,17 +255,6 @@ __global__ __launch_bounds__(KS * 64) void conv3x3_ws_kernel(osh_conv_params p, 
     }
 }
 
-inline int device_cus() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-    }
-    return cus;
-}
-
 // Workgroups per CU of the persistent grid (ONNXSHARP_HIP_WS_WGS_PER_CU, default 2;
 // the knob follows the reference's ONNXSHARP_* environment switches).
 inline int ws_wgs_per_cu() {

@@ -5,6 +5,7 @@
 // rules of MatMulLayer (src/OnnxSharp/Ops/DnnOps.cs:2789-3103).
 #include <algorithm>
 
+#include "osh_gemm16.h"
 #include "osh_igemm.h"
 #include "osh_launch.h"
 
@@ -14,8 +15,106 @@ namespace osh {
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Wave tiles of gemm16_kernel: (16*TM) x (16*BV*TN) outputs per wave.
+struct G16Variant {
+    int tm, tn, bv, kc;
+};
+static const G16Variant kG16[] = {
+    {1, 1, 1, 32},  // 0: 16 x 16, 32-k chunks
+    {1, 1, 2, 32},  // 1: 16 x 32, 32-k chunks
+    {1, 1, 3, 32},  // 2: 16 x 48, 32-k chunks
+    {1, 1, 4, 32},  // 3: 16 x 64, 32-k chunks
+    {2, 1, 2, 32},  // 4: 32 x 32, 32-k chunks
+    {2, 1, 3, 32},  // 5: 32 x 48, 32-k chunks
+    {2, 1, 4, 32},  // 6: 32 x 64, 32-k chunks
+    {1, 1, 3, 64},  // 7: 16 x 48, 64-k chunks
+    {1, 1, 4, 64},  // 8: 16 x 64, 64-k chunks
+    {1, 1, 1, 64},  // 9: 16 x 16, 64-k chunks
+    {1, 1, 2, 64},  // 10: 16 x 32, 64-k chunks
+};
+constexpr int kG16Count = sizeof(kG16) / sizeof(kG16[0]);
+
+}  // namespace osh
+
+int osh::gemm16_variant_count() { return kG16Count; }
+
+namespace osh {
+
+static bool aligned_to(const void *p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+// Operand constraints of a wave tile (see osh_gemm16.h): 16-byte A rows,
+// BV-wide B loads and C stores on BV-aligned rows, N a multiple of BV, and
+// 32-bit buffer offsets.
+static bool g16_fits(const IgemmArgs &a, const G16Variant &v) {
+    const int bv = v.bv;
+    const int al = bv == 3 ? 1 : bv;  // 12-byte accesses need 4-byte alignment only
+    if (a.K < 1 || a.N < bv || a.N % bv) return false;
+    if (a.lda % 4 || !aligned_to(a.A, 16) || a.strideA % 4 || a.strideA_in % 4) return false;
+    if (a.ldb % al || !aligned_to(a.B, 4 * al) || a.strideB % al || a.strideB_in % al) return false;
+    if (a.ldc % al || !aligned_to(a.C, 4 * al) || a.strideC % al || a.strideC_in % al) return false;
+    if (((long long)(a.M - 1) * a.lda + a.K) * 4 >= (1LL << 31)) return false;
+    if (((long long)(a.K - 1) * a.ldb + a.N) * 4 >= (1LL << 31)) return false;
+    return true;
+}
+
+// Predicted cost: rounds of waves over the SIMDs times the MFMAs of one wave
+// tile, inflated by the operand traffic per MFMA (TN B loads and about TM/2
+// A loads feed TM*TN*BV MFMAs per k4 step).
+static double g16_cost(const IgemmArgs &a, int zcount, const G16Variant &v, int cus) {
+    const long long waves = (long long)ceil_div(a.M, 16 * v.tm) * ceil_div(a.N, 16 * v.bv * v.tn) * zcount;
+    const long long rounds = (waves + 4LL * cus - 1) / (4LL * cus);
+    const double u = (double)v.tm * v.tn * v.bv;
+    return rounds * u * ceil_div(a.K, 4) * (1.0 + 0.5 * (v.tn + 0.5 * v.tm) / u);
+}
+
+template <int TM, int TN, int BV, int KC>
+static osh_status g16_launch(const IgemmArgs &a, int zcount, int act, hipStream_t st) {
+    const int tiles_m = ceil_div(a.M, 16 * TM), tiles_n = ceil_div(a.N, 16 * BV * TN);
+    const long long blocks = (long long)ceil_div(tiles_m, 4) * tiles_n;
+    if (blocks > 0x7fffffffLL) return fail(OSH_E_UNSUPPORTED, "GEMM grid too large");
+    dim3 grid((unsigned)blocks, zcount);
+    OSH_DISPATCH_ACT(act, ACT,
+                     hipLaunchKernelGGL((gemm16_kernel<TM, TN, BV, KC, ACT>), grid, dim3(256), 0, st, a, tiles_m));
+    OSH_LAUNCH_CHECK("gemm16_kernel");
+    return OSH_OK;
+}
+
+// Returns true when a gemm16 tile took the problem (*status = its launch status).
+static bool launch_gemm16(const IgemmArgs &a, int zcount, int act, hipStream_t st, osh_status *status) {
+    const int forced = gemm_variant();
+    if (forced == -2 || zcount > 65535) return false;
+    int best = -1;
+    if (forced >= 0) {
+        if (forced < kG16Count && g16_fits(a, kG16[forced])) best = forced;
+    } else {
+        const int cus = device_cus();
+        double bc = 0;
+        for (int i = 0; i < kG16Count; i++) {
+            if (!g16_fits(a, kG16[i])) continue;
+            const double c = g16_cost(a, zcount, kG16[i], cus);
+            if (best < 0 || c < bc) best = i, bc = c;
+        }
+    }
+    switch (best) {
+    case 0: *status = g16_launch<1, 1, 1, 32>(a, zcount, act, st); return true;
+    case 1: *status = g16_launch<1, 1, 2, 32>(a, zcount, act, st); return true;
+    case 2: *status = g16_launch<1, 1, 3, 32>(a, zcount, act, st); return true;
+    case 3: *status = g16_launch<1, 1, 4, 32>(a, zcount, act, st); return true;
+    case 4: *status = g16_launch<2, 1, 2, 32>(a, zcount, act, st); return true;
+    case 5: *status = g16_launch<2, 1, 3, 32>(a, zcount, act, st); return true;
+    case 6: *status = g16_launch<2, 1, 4, 32>(a, zcount, act, st); return true;
+    case 7: *status = g16_launch<1, 1, 3, 64>(a, zcount, act, st); return true;
+    case 8: *status = g16_launch<1, 1, 4, 64>(a, zcount, act, st); return true;
+    case 9: *status = g16_launch<1, 1, 1, 64>(a, zcount, act, st); return true;
+    case 10: *status = g16_launch<1, 1, 2, 64>(a, zcount, act, st); return true;
+    default: return false;
+    }
+}
+
 osh_status launch_igemm(const IgemmArgs &a, int zcount, int bmode, int act, hipStream_t st) {
     if (a.M <= 0 || a.N <= 0 || zcount <= 0) return OSH_OK;
+    osh_status g16_status = OSH_OK;
+    if (bmode == B_DENSE && launch_gemm16(a, zcount, act, st, &g16_status)) return g16_status;
     const bool vec_a = a.K % 4 == 0 && a.lda % 4 == 0 && aligned16(a.A) && a.strideA % 4 == 0 &&
                        a.strideA_in % 4 == 0;
     const bool vec_b = bmode == B_DENSE && a.ldb % 4 == 0 && aligned16(a.B) && a.strideB % 4 == 0 &&

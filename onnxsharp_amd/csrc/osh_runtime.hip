@@ -25,6 +25,7 @@ void clear_error() { g_err[0] = 0; }
 const char *last_error() { return g_err; }
 
 static int g_exact_silu = -1;  // -1: read ONNXSHARP_HIP_EXACT_SILU on first use
+static int g_gemm_variant = -3;  // -3: read ONNXSHARP_HIP_GEMM_VARIANT on first use
 
 bool exact_silu() {
     if (g_exact_silu < 0) {
@@ -32,6 +33,14 @@ bool exact_silu() {
         g_exact_silu = (e && atoi(e) != 0) ? 1 : 0;
     }
     return g_exact_silu == 1;
+}
+
+int gemm_variant() {
+    if (g_gemm_variant == -3) {
+        const char *e = getenv("ONNXSHARP_HIP_GEMM_VARIANT");
+        g_gemm_variant = e ? atoi(e) : -1;
+    }
+    return g_gemm_variant;
 }
 
 __global__ void fill_u8_kernel(uint8_t *__restrict__ p, uint8_t v, size_t n) {
@@ -54,6 +63,12 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         g_exact_silu = value != 0;
         return OSH_OK;
     }
+    if (strcmp(key, "gemm_variant") == 0) {
+        if (value < -2 || value >= gemm16_variant_count())
+            return fail(OSH_E_INVALID, "gemm_variant %d out of range [-2, %d)", value, gemm16_variant_count());
+        g_gemm_variant = value;
+        return OSH_OK;
+    }
     return fail(OSH_E_INVALID, "unknown option '%s'", key);
 }
 
@@ -61,6 +76,14 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     if (!key || !value) return fail(OSH_E_INVALID, "NULL argument");
     if (strcmp(key, "exact_silu") == 0) {
         *value = exact_silu() ? 1 : 0;
+        return OSH_OK;
+    }
+    if (strcmp(key, "gemm_variant") == 0) {
+        *value = gemm_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "gemm_variants") == 0) {
+        *value = gemm16_variant_count();
         return OSH_OK;
     }
     return fail(OSH_E_INVALID, "unknown option '%s'", key);

@@ -32,8 +32,10 @@ def test_gemm_column_bias(cuda, oracle, m, k, n):
     # the reference test's own bar (|d| / max(1, |x|) <= 1e-4 vs float64) ...
     exact = oracle.gemm_f64(a, b, col_bias=bias)
     assert (np.abs(y - exact) / np.maximum(1.0, np.abs(exact))).max() <= 1e-4
-    # ... and the parity bar against the FMA chain
+    # ... and the parity bar against the FMA chain: the MFMA kernels add the
+    # products in k order with one rounding per step, so the match is exact
     assert_fp32_close(y, ref, f"gemm {m}x{k}x{n}")
+    assert np.array_equal(y, ref), f"gemm {m}x{k}x{n}: not bit-identical to the FMA chain"
 
 
 def test_gemm_workload_1024x768x768(cuda, oracle):
@@ -47,6 +49,7 @@ def test_gemm_workload_1024x768x768(cuda, oracle):
     nbad, dmax = fp32_violations(y, ref)
     print(f"  violations={nbad} max|d|={dmax:.3e}", flush=True)
     assert_fp32_close(y, ref, "gemm 1024x768x768")
+    assert np.array_equal(y, ref), "gemm 1024x768x768: not bit-identical to the FMA chain"
 
 
 def test_gemm_row_bias_scale_and_activation(cuda, oracle):
