@@ -9,6 +9,8 @@ reference publishes a CPU number for).  Other workloads (--config):
   c1   MatMul + Add(bias) fused: A[1024,768] x B[768,768] + bias[768], U(-1,1)
   c3a  1x1 conv 256->128 @ 80x80 + bias + SiLU
   c3b  3x3 stride-2 conv 128->256, 80x80 -> 40x40 + bias + SiLU
+  c4   YOLO11n frame at 640x640 (87 convolutions + C2PSA attention + SPPF/upsample/concat/add glue),
+       replayed as one HIP graph; random N(0,0.05) weights, input U(0,1); DFL/NMS stay on the host
   c5   int8 DynamicQuantizeMatMul A f32[512,512] N(0,1), W s8[512,2048], per-column scales, bias
   copy 64 MiB device-to-device copy (osh_memcpy_d2d): calibrates the HBM byte counters
 
@@ -192,6 +194,69 @@ class DqmmWorkload(Workload):
         return oracle.dqmm(self.a_np, self.w_np, None, self.ws_np, self.bias_np)[0]
 
 
+class YoloWorkload(Workload):
+    """One YOLO11n frame per step: the frame's ~120 launches recorded once as a
+    HIP graph and replayed, inputs resident on the device."""
+
+    def __init__(self, dev):
+        from onnxsharp_amd import synth, yolo11n
+        self.name = "c4"
+        self.kernel = "yolo11n frame (HIP graph)"
+        self.model = yolo11n.build(640)
+        self.fr = yolo11n.Frame(self.model, dev)
+        self.x_np = synth.uniform(4000, (1, 3, 640, 640))
+        self.fr.set_input(self.x_np)
+        self.fr.run()
+        self.fr.sync()
+        self.fr.capture()
+        self.stream = self.fr.stream
+        self.flops = self.model.flops
+        # each tensor read or written once per op that touches it
+        self.bytes = 4.0 * sum(op.x.c * op.x.h * op.x.w + op.w.size + op.b.size + op.y.c * op.y.h * op.y.w
+                               for op in self.model.convs)
+        nconv = len(self.model.convs)
+        self.config = {"workload": "YOLO11n backbone+neck+head, batch 1, 640x640, FP32 NCHW, "
+                                   f"{nconv} conv launches + attention/SPPF/upsample/add glue in one HIP graph",
+                       "input": "U(0,1) [1,3,640,640], splitmix64 seed 4000",
+                       "weights": "N(0,0.05) conv weights, N(0,0.01) biases (BatchNorm folded), seeds 7000+",
+                       "conv_gflop": round(sum(o.flops for o in self.model.convs) / 1e9, 4),
+                       "outputs": "3 head tensors [1,144,80,80], [1,144,40,40], [1,144,20,20]; "
+                                  "DFL/NMS on the host"}
+
+    def step(self, stream):
+        self.fr.launch()
+
+    def cpu_step(self, oracle):
+        from oracle import yolo_frame
+        return yolo_frame.Frame(self.model).run(oracle, self.x_np)
+
+    def host_roundtrip_ms(self, frames=20):
+        """ms per frame with the input copied in and the head tensors copied
+        out through pinned host memory (PCIe included)."""
+        import torch
+        from onnxsharp_amd import native as N
+        hin = torch.from_numpy(self.x_np).pin_memory()
+        outs = self.fr.outputs()
+        houts = [torch.empty(t.shape, dtype=t.dtype).pin_memory() for t in outs]
+        nb_in = hin.numel() * 4
+        dst_in = C.c_void_p(self.model.input.tensor.data_ptr())
+
+        def frame():
+            N.call("osh_memcpy_h2d", dst_in, C.c_void_p(hin.data_ptr()), nb_in, self.stream)
+            self.fr.launch()
+            for h, d in zip(houts, outs):
+                N.call("osh_memcpy_d2h", C.c_void_p(h.data_ptr()), C.c_void_p(d.data_ptr()), h.numel() * 4,
+                       self.stream)
+            N.call("osh_stream_sync", self.stream)
+
+        for _ in range(3):
+            frame()
+        t0 = time.perf_counter()
+        for _ in range(frames):
+            frame()
+        return (time.perf_counter() - t0) / frames * 1e3
+
+
 class CopyWorkload(Workload):
     """Plain 64 MiB device copy: its FETCH_SIZE / WRITE_SIZE counter readings
     calibrate the per-dispatch HBM traffic of the other workloads."""
@@ -229,6 +294,8 @@ def make_workload(name, dev):
         return GemmWorkload(dev)
     if name == "c5":
         return DqmmWorkload(dev)
+    if name == "c4":
+        return YoloWorkload(dev)
     if name == "copy":
         return CopyWorkload(dev)
     raise SystemExit(f"unknown --config {name}")
@@ -237,8 +304,9 @@ def make_workload(name, dev):
 def time_gpu(wl, steps, warmup):
     import torch
     from onnxsharp_amd import native as N
-    stream = torch.cuda.current_stream().cuda_stream
-    sp = C.c_void_p(stream)
+    sp = getattr(wl, "stream", None)
+    if sp is None:
+        sp = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     for _ in range(warmup):
         wl.step(sp)
     torch.cuda.synchronize()
@@ -324,6 +392,10 @@ def main():
         roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
                 "frac": round(tflops / PEAK["fp32_mfma_tflops"], 4)}
     roof["traffic"] = read_traffic(wl.kernel, wl.name)
+    extra = {}
+    if wl.name == "c4":
+        extra["ms_per_frame"] = round(ms_step, 4)
+        extra["ms_per_frame_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
     roof["kernel"] = wl.kernel
     roof["algorithmic_per_launch"] = {"flops": wl.flops, "bytes": wl.bytes}
 
@@ -335,6 +407,8 @@ def main():
         cpu = {"value": round(v4, 5), "unit": unit, "cores": 4, "kind": "port",
                "sample": f"{n4} full steps of the same workload in {el4:.1f} s (oracle, 4 threads)",
                "host": hi}
+        if wl.name == "c4":
+            cpu["ms_per_frame"] = round(el4 / n4 * 1e3, 2)
         allc = hi.get("affinity_cpus") or hi.get("physical_cores") or 4
         allc = int(min(allc, hi.get("physical_cores", allc), 16))
         if allc != 4:
@@ -362,6 +436,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
     }
+    out.update(extra)
     print(json.dumps(out), flush=True)
 
 

@@ -230,6 +230,60 @@ OSH_API osh_status osh_dynamic_quantize_linear(int64_t n, const float *d_x, uint
 /* In-place activation pass (TensorOps.ElementWiseUnary, src/OnnxSharp/Tensors/TensorOps.cs:267-300). */
 OSH_API osh_status osh_activation_f32(int64_t n, const float *d_x, int act, float *d_y, osh_stream s);
 
+/* ------------------------------------------ segment-continuity ops (NCHW) */
+/* These keep a run of convolutions on the device between the ops a segment
+ * would otherwise hand back to the CPU.  Concat and Split along channels of a
+ * batch-1 NCHW tensor need no kernel: producers write into, and consumers read
+ * from, channel slices (pointer offsets) of one buffer (ConcatLayer
+ * src/OnnxSharp/Ops/ShapeOps.cs:211, SplitLayer :302). */
+
+/* y = a + b elementwise, same shape (NaryEltwiseLayer Add,
+ * src/OnnxSharp/Ops/NaryEltwiseLayer.cs:7-20).  y may alias a or b. */
+OSH_API osh_status osh_add_f32(int64_t n, const float *d_a, const float *d_b, float *d_y, osh_stream s);
+
+typedef struct osh_pool_params {
+    int n, c, h, w;     /* input */
+    int kh, kw, sh, sw; /* window and strides */
+    int pt, pl;         /* leading pads (positions outside the input are skipped) */
+    int oh, ow;         /* output */
+} osh_pool_params;
+
+/* MaxPool 2-D over NCHW (MaxPoolLayer, src/OnnxSharp/Ops/DnnOps.cs:1335-1480):
+ * y[n][c][oy][ox] = max over the window rows oy*sh - pt + ky, columns
+ * ox*sw - pl + kx that fall inside the input. */
+OSH_API osh_status osh_maxpool2d_f32(const osh_pool_params *p, const float *d_x, float *d_y, osh_stream s);
+
+/* Nearest-neighbour upsampling by integer factors (ResizeLayer mode "nearest",
+ * src/OnnxSharp/Ops/DnnOps.cs:2215-2330): y[n][c][oy][ox] = x[n][c][oy/fh][ox/fw],
+ * the index both "asymmetric"/"floor" and "half_pixel"/"round_prefer_floor"
+ * give for an integer factor.  Output plane n starts at d_y + n * y_batch_stride
+ * (c*oh*ow for a dense output; larger to write into a channel slice). */
+OSH_API osh_status osh_resize_nearest_f32(int n, int c, int h, int w, int fh, int fw, const float *d_x, float *d_y,
+                                          int64_t y_batch_stride, osh_stream s);
+
+/* Swap the last two axes: y[b][j][i] = x[b][i][j] for x [batch][rows][cols]
+ * (TransposeLayer with perm (..., -1, -2), src/OnnxSharp/Ops/ShapeOps.cs:394).
+ * Batch b reads d_x + b * x_batch_stride and writes d_y + b * y_batch_stride. */
+OSH_API osh_status osh_transpose_f32(int batch, int rows, int cols, const float *d_x, int64_t x_batch_stride,
+                                     float *d_y, int64_t y_batch_stride, osh_stream s);
+
+/* Softmax along rows of x [rows][cols] after a constant scale (the Mul that
+ * precedes it in attention): y = e / sum(e), e = exp(scale*x - max(scale*x))
+ * (SoftmaxLayer + VectorMath.SoftmaxRow, src/OnnxSharp/Ops/DnnOps.cs:2547-2675,
+ * src/OnnxSharp/Tensors/VectorMath.cs:282-287; exp is the reference polynomial). */
+OSH_API osh_status osh_softmax_f32(int64_t rows, int cols, float scale, const float *d_x, float *d_y, osh_stream s);
+
+/* ----------------------------------------------------------- HIP graphs */
+/* A segment's launches recorded once and replayed per Forward, the role of
+ * the Vulkan backend's recorded command buffers (src/OnnxSharp.Vulkan/VkSegment.cs:324-600).
+ * Capture runs on a stream from osh_stream_create (not the legacy default
+ * stream); nothing may allocate or memset on it while capturing. */
+typedef void *osh_graph; /* hipGraphExec_t */
+OSH_API osh_status osh_graph_begin(osh_stream s);
+OSH_API osh_status osh_graph_end(osh_stream s, osh_graph *g);
+OSH_API osh_status osh_graph_launch(osh_graph g, osh_stream s);
+OSH_API osh_status osh_graph_destroy(osh_graph g);
+
 #ifdef __cplusplus
 }
 #endif

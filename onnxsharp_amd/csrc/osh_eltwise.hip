@@ -1,8 +1,12 @@
-// osh_eltwise.hip -- elementwise passes of the C ABI.
+// osh_eltwise.hip -- elementwise and data-movement passes of the C ABI.
 //
 // osh_activation_f32 is the standalone form of the activation epilogue that
 // the GEMM/conv kernels fuse (TensorOps.ElementWiseUnary,
 // src/OnnxSharp/Tensors/TensorOps.cs:267-300): Relu and the reference SiLU.
+// The rest are the segment-continuity ops that keep a YOLO-style network on
+// the device between convolutions: residual Add, MaxPool, nearest Resize,
+// Transpose and the attention Softmax.  All are HBM-bound; each thread moves
+// a handful of values with coalesced accesses.
 #include "osh_common.h"
 
 using namespace osh;
@@ -17,9 +21,200 @@ __global__ __launch_bounds__(256) void activation_kernel(const float *__restrict
     for (; i < n; i += stride) y[i] = activate<ACT>(x[i]);
 }
 
+__global__ __launch_bounds__(256) void add_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                                                   float *__restrict__ y, long long n) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long stride = (long long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) y[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(256) void add4_kernel(const float4 *__restrict__ a, const float4 *__restrict__ b,
+                                                    float4 *__restrict__ y, long long n4) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long stride = (long long)gridDim.x * blockDim.x;
+    for (; i < n4; i += stride) {
+        const float4 u = a[i], v = b[i];
+        y[i] = make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
+    }
+}
+
+// One thread per output element.  The running maximum starts at the first
+// in-range window element; later elements replace it only when greater.
+__global__ __launch_bounds__(256) void maxpool2d_kernel(osh_pool_params p, const float *__restrict__ x,
+                                                         float *__restrict__ y, long long total) {
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int ox = (int)(idx % p.ow);
+    long long t = idx / p.ow;
+    const int oy = (int)(t % p.oh);
+    const long long plane = t / p.oh;
+    const float *xp = x + plane * p.h * p.w;
+    const int iy0 = oy * p.sh - p.pt, ix0 = ox * p.sw - p.pl;
+    float m = 0.f;
+    bool any = false;
+    for (int ky = 0; ky < p.kh; ky++) {
+        const int iy = iy0 + ky;
+        if ((unsigned)iy >= (unsigned)p.h) continue;
+        for (int kx = 0; kx < p.kw; kx++) {
+            const int ix = ix0 + kx;
+            if ((unsigned)ix >= (unsigned)p.w) continue;
+            const float v = xp[(long long)iy * p.w + ix];
+            if (!any || v > m) m = v;
+            any = true;
+        }
+    }
+    y[idx] = m;
+}
+
+__global__ __launch_bounds__(256) void resize_nearest_kernel(int c, int h, int w, int fh, int fw,
+                                                              const float *__restrict__ x, float *__restrict__ y,
+                                                              long long y_batch_stride, long long total) {
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int ow = w * fw, oh = h * fh;
+    const int ox = (int)(idx % ow);
+    long long t = idx / ow;
+    const int oy = (int)(t % oh);
+    t /= oh;
+    const int ch = (int)(t % c);
+    const long long n = t / c;
+    const float v = x[((n * c + ch) * h + oy / fh) * (long long)w + ox / fw];
+    y[n * y_batch_stride + ((long long)ch * oh + oy) * ow + ox] = v;
+}
+
+// 32 x 32 tiles through LDS so that both the read and the write are coalesced.
+__global__ __launch_bounds__(256) void transpose_kernel(int rows, int cols, const float *__restrict__ x,
+                                                         long long xs, float *__restrict__ y, long long ys) {
+    __shared__ float tile[32][33];
+    const float *xb = x + blockIdx.z * xs;
+    float *yb = y + blockIdx.z * ys;
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int r = ty; r < 32; r += 8) {
+        const int gr = r0 + r, gc = c0 + tx;
+        if (gr < rows && gc < cols) tile[r][tx] = xb[(long long)gr * cols + gc];
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int gc = c0 + r, gr = r0 + tx;  // output row gc, column gr
+        if (gc < cols && gr < rows) yb[(long long)gc * rows + gr] = tile[tx][r];
+    }
+}
+
+__device__ __forceinline__ float wave_max_f(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// One wave per row: max of scale*x, e = exp_ref(v - max) stored and summed,
+// then y = e * (1 / sum) (VectorMath.SoftmaxRow scales by the reciprocal).
+__global__ __launch_bounds__(256) void softmax_kernel(long long rows, int cols, float scale,
+                                                       const float *__restrict__ x, float *__restrict__ y) {
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + row * cols;
+    float *yr = y + row * cols;
+    float m = -__builtin_inff();
+    for (int c = lane; c < cols; c += 64) m = __builtin_fmaxf(m, xr[c] * scale);
+    m = wave_max_f(m);
+    float sum = 0.f;
+    for (int c = lane; c < cols; c += 64) {
+        const float e = exp_ref(xr[c] * scale - m);
+        yr[c] = e;
+        sum += e;
+    }
+    sum = wave_sum_f(sum);
+    const float inv = 1.0f / sum;
+    for (int c = lane; c < cols; c += 64) yr[c] = yr[c] * inv;
+}
+
+static unsigned grid_for(long long n, long long per_block, long long cap) {
+    long long b = (n + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > cap) b = cap;
+    return (unsigned)b;
+}
+
 }  // namespace osh
 
 extern "C" {
+
+OSH_API osh_status osh_add_f32(int64_t n, const float *d_a, const float *d_b, float *d_y, osh_stream s) {
+    if (n < 0) return fail(OSH_E_INVALID, "Add: negative element count");
+    if (n == 0) return OSH_OK;
+    if (!d_a || !d_b || !d_y) return fail(OSH_E_INVALID, "Add: NULL pointer");
+    const bool vec = n % 4 == 0 && ((reinterpret_cast<uintptr_t>(d_a) | reinterpret_cast<uintptr_t>(d_b) |
+                                     reinterpret_cast<uintptr_t>(d_y)) & 15) == 0;
+    if (vec) {
+        hipLaunchKernelGGL(add4_kernel, dim3(grid_for(n / 4, 256, 8192)), dim3(256), 0, to_stream(s),
+                           reinterpret_cast<const float4 *>(d_a), reinterpret_cast<const float4 *>(d_b),
+                           reinterpret_cast<float4 *>(d_y), (long long)(n / 4));
+    } else {
+        hipLaunchKernelGGL(add_kernel, dim3(grid_for(n, 256, 8192)), dim3(256), 0, to_stream(s), d_a, d_b, d_y,
+                           (long long)n);
+    }
+    OSH_LAUNCH_CHECK("add_kernel");
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_maxpool2d_f32(const osh_pool_params *p, const float *d_x, float *d_y, osh_stream s) {
+    if (!p || !d_x || !d_y) return fail(OSH_E_INVALID, "MaxPool: NULL argument");
+    if (p->n <= 0 || p->c <= 0 || p->h <= 0 || p->w <= 0 || p->kh <= 0 || p->kw <= 0 || p->sh <= 0 || p->sw <= 0 ||
+        p->oh <= 0 || p->ow <= 0 || p->pt < 0 || p->pl < 0)
+        return fail(OSH_E_INVALID, "MaxPool: bad parameters");
+    // every window must hold at least one input element
+    if ((long long)(p->oh - 1) * p->sh - p->pt >= p->h || (long long)(p->ow - 1) * p->sw - p->pl >= p->w ||
+        p->kh <= p->pt || p->kw <= p->pl)
+        return fail(OSH_E_INVALID, "MaxPool: output window outside the input");
+    const long long total = (long long)p->n * p->c * p->oh * p->ow;
+    hipLaunchKernelGGL(maxpool2d_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), *p,
+                       d_x, d_y, total);
+    OSH_LAUNCH_CHECK("maxpool2d_kernel");
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_resize_nearest_f32(int n, int c, int h, int w, int fh, int fw, const float *d_x, float *d_y,
+                                          int64_t y_batch_stride, osh_stream s) {
+    if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || fh <= 0 || fw <= 0) return fail(OSH_E_INVALID, "Resize: bad sizes");
+    if (!d_x || !d_y) return fail(OSH_E_INVALID, "Resize: NULL pointer");
+    const long long plane = (long long)c * h * fh * w * fw;
+    if (y_batch_stride < plane) return fail(OSH_E_INVALID, "Resize: output batch stride below c*oh*ow");
+    const long long total = (long long)n * plane;
+    hipLaunchKernelGGL(resize_nearest_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), c,
+                       h, w, fh, fw, d_x, d_y, (long long)y_batch_stride, total);
+    OSH_LAUNCH_CHECK("resize_nearest_kernel");
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_transpose_f32(int batch, int rows, int cols, const float *d_x, int64_t x_batch_stride,
+                                     float *d_y, int64_t y_batch_stride, osh_stream s) {
+    if (batch < 0 || rows < 0 || cols < 0) return fail(OSH_E_INVALID, "Transpose: negative size");
+    if (batch == 0 || rows == 0 || cols == 0) return OSH_OK;
+    if (!d_x || !d_y) return fail(OSH_E_INVALID, "Transpose: NULL pointer");
+    if (batch > 65535) return fail(OSH_E_UNSUPPORTED, "Transpose: batch %d exceeds the grid limit", batch);
+    dim3 grid(ceil_div(cols, 32), ceil_div(rows, 32), batch);
+    if (grid.y > 65535) return fail(OSH_E_UNSUPPORTED, "Transpose: %d rows exceed the grid limit", rows);
+    hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, to_stream(s), rows, cols, d_x, (long long)x_batch_stride,
+                       d_y, (long long)y_batch_stride);
+    OSH_LAUNCH_CHECK("transpose_kernel");
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_softmax_f32(int64_t rows, int cols, float scale, const float *d_x, float *d_y, osh_stream s) {
+    if (rows < 0 || cols < 0) return fail(OSH_E_INVALID, "Softmax: negative size");
+    if (rows == 0 || cols == 0) return OSH_OK;
+    if (!d_x || !d_y) return fail(OSH_E_INVALID, "Softmax: NULL pointer");
+    if (d_x == d_y) return fail(OSH_E_INVALID, "Softmax: in-place is not supported");
+    hipLaunchKernelGGL(softmax_kernel, dim3(grid_for(rows, 4, 0x7fffffff)), dim3(256), 0, to_stream(s),
+                       (long long)rows, cols, scale, d_x, d_y);
+    OSH_LAUNCH_CHECK("softmax_kernel");
+    return OSH_OK;
+}
 
 OSH_API osh_status osh_activation_f32(int64_t n, const float *d_x, int act, float *d_y, osh_stream s) {
     if (n < 0) return fail(OSH_E_INVALID, "negative element count");

@@ -224,4 +224,34 @@ OSH_API osh_status osh_event_elapsed_ms(osh_event start, osh_event stop, float *
     return OSH_OK;
 }
 
+OSH_API osh_status osh_graph_begin(osh_stream s) {
+    if (!s) return fail(OSH_E_INVALID, "graph capture needs a stream from osh_stream_create");
+    OSH_HIP_CHECK(hipStreamBeginCapture(to_stream(s), hipStreamCaptureModeThreadLocal));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_graph_end(osh_stream s, osh_graph *g) {
+    if (!s || !g) return fail(OSH_E_INVALID, "NULL argument");
+    *g = nullptr;
+    hipGraph_t graph = nullptr;
+    OSH_HIP_CHECK(hipStreamEndCapture(to_stream(s), &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return fail(OSH_E_DEVICE, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
+    *g = exec;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_graph_launch(osh_graph g, osh_stream s) {
+    if (!g) return fail(OSH_E_INVALID, "graph is NULL");
+    OSH_HIP_CHECK(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(g), to_stream(s)));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_graph_destroy(osh_graph g) {
+    if (g) OSH_HIP_CHECK(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(g)));
+    return OSH_OK;
+}
+
 }  // extern "C"

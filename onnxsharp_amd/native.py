@@ -54,6 +54,10 @@ class ConvParams(C.Structure):
                                        "pt", "pl", "pb", "pr", "oh", "ow")]
 
 
+class PoolParams(C.Structure):
+    _fields_ = [(f, C.c_int) for f in ("n", "c", "h", "w", "kh", "kw", "sh", "sw", "pt", "pl", "oh", "ow")]
+
+
 _vp, _i, _i64, _sz = C.c_void_p, C.c_int, C.c_int64, C.c_size_t
 _i64p = C.POINTER(C.c_int64)
 
@@ -93,6 +97,15 @@ _SIGS = {
     "osh_dqmm_u8s8": ([_i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "osh_dynamic_quantize_linear": ([_i64, _vp, _vp, _vp, _vp, _vp], _i),
     "osh_activation_f32": ([_i64, _vp, _i, _vp, _vp], _i),
+    "osh_add_f32": ([_i64, _vp, _vp, _vp, _vp], _i),
+    "osh_maxpool2d_f32": ([C.POINTER(PoolParams), _vp, _vp, _vp], _i),
+    "osh_resize_nearest_f32": ([_i, _i, _i, _i, _i, _i, _vp, _vp, _i64, _vp], _i),
+    "osh_transpose_f32": ([_i, _i, _i, _vp, _i64, _vp, _i64, _vp], _i),
+    "osh_softmax_f32": ([_i64, _i, C.c_float, _vp, _vp, _vp], _i),
+    "osh_graph_begin": ([_vp], _i),
+    "osh_graph_end": ([_vp, C.POINTER(_vp)], _i),
+    "osh_graph_launch": ([_vp, _vp], _i),
+    "osh_graph_destroy": ([_vp], _i),
 }
 
 # Every symbol include/osh_hip.h declares (checked by the CPU test suite).

@@ -1,0 +1,461 @@
+"""YOLO11n backbone + neck + head (batch 1, NCHW FP32) on the device.
+
+The network is the one the reference benchmarks as a whole frame: 87 Conv
+(+SiLU) layers, the C2PSA attention, SPPF max pools, nearest upsampling and
+the channel Concat/Split/Add glue between them (node list in the reference's
+tests/data/yolo11n.shapes.tsv; the CPU path per layer is the dispatch of
+ConvLayer.Forward, src/OnnxSharp/Ops/DnnOps.cs:411-500).  The Detect head's
+DFL/NMS stay on the host: a frame ends with the three per-scale head tensors
+[1, 64 + 80, H, W] (box distribution logits, class logits).
+
+Layout: every activation lives in a device buffer; Concat and Split along
+channels cost nothing because producers write into, and consumers read from,
+channel slices of one buffer (batch 1, so a slice is a pointer offset).  The
+op list is in execution order; `Frame` issues it on one stream and can record
+it once as a HIP graph and replay it per frame.
+
+Weights are random (no checkpoint is available): conv weights N(0, 0.05) and
+biases N(0, 0.01) standing for BatchNorm folded into the conv, from the
+counter-based generator in `synth` with a fixed seed per layer.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import native as N
+from . import synth
+
+
+@dataclass(eq=False)
+class Buf:
+    name: str
+    c: int
+    h: int
+    w: int
+    tensor: object = None  # torch tensor once allocated
+
+    @property
+    def numel(self):
+        return self.c * self.h * self.w
+
+
+@dataclass(eq=False)
+class Slice:
+    buf: Buf
+    c0: int
+    c: int
+
+    @property
+    def h(self):
+        return self.buf.h
+
+    @property
+    def w(self):
+        return self.buf.w
+
+    @property
+    def shape(self):
+        return (1, self.c, self.buf.h, self.buf.w)
+
+    def ptr(self):
+        return C.c_void_p(self.buf.tensor.data_ptr() + 4 * self.c0 * self.buf.h * self.buf.w)
+
+    def sub(self, c0, c):
+        assert 0 <= c0 and c0 + c <= self.c
+        return Slice(self.buf, self.c0 + c0, c)
+
+
+def whole(buf: Buf) -> Slice:
+    return Slice(buf, 0, buf.c)
+
+
+@dataclass(eq=False)
+class ConvOp:
+    name: str
+    x: Slice
+    y: Slice
+    k: int
+    s: int
+    group: int
+    act: str | None
+    w: np.ndarray
+    b: np.ndarray
+
+    @property
+    def flops(self):
+        return 2.0 * self.y.c * (self.x.c // self.group) * self.k * self.k * self.y.h * self.y.w
+
+
+@dataclass(eq=False)
+class AddOp:
+    name: str
+    a: Slice
+    b: Slice
+    y: Slice
+
+
+@dataclass(eq=False)
+class MaxPoolOp:
+    name: str
+    x: Slice
+    y: Slice
+    k: int = 5
+    s: int = 1
+    p: int = 2
+
+
+@dataclass(eq=False)
+class UpsampleOp:
+    name: str
+    x: Slice
+    y: Slice
+    f: int = 2
+
+
+@dataclass(eq=False)
+class AttentionOp:
+    """Attention core of C2PSA (ultralytics Attention.forward, exported as the
+    Reshape/Split/Transpose/MatMul/Mul/Softmax/MatMul nodes of /model.10/m/m.0/attn):
+    per head h, q = qkv[h, :kd], k = qkv[h, kd:2kd], v = qkv[h, 2kd:] (each
+    [rows, N], N = H*W); attn = softmax(scale * q^T k); y[h] = v attn^T."""
+    name: str
+    qkv: Slice
+    y: Slice
+    heads: int
+    key_dim: int
+    head_dim: int
+    scale: float
+    qt: Buf = None     # [heads, N, key_dim]
+    attn: Buf = None   # [heads, N, N] scores, then probabilities
+    attn_t: Buf = None  # [heads, N, N] probabilities transposed
+
+
+@dataclass
+class Model:
+    size: int
+    bufs: list = field(default_factory=list)
+    ops: list = field(default_factory=list)
+    input: Buf = None
+    outputs: list = field(default_factory=list)
+
+    @property
+    def convs(self):
+        return [o for o in self.ops if isinstance(o, ConvOp)]
+
+    @property
+    def flops(self):
+        att = sum(2.0 * o.heads * (o.y.h * o.y.w) ** 2 * (o.key_dim + o.head_dim)
+                  for o in self.ops if isinstance(o, AttentionOp))
+        return sum(o.flops for o in self.convs) + att
+
+
+class _Builder:
+    def __init__(self, size, seed):
+        self.m = Model(size)
+        self.seed = seed
+        self.nconv = 0
+
+    def buf(self, name, c, h, w):
+        b = Buf(name, c, h, w)
+        self.m.bufs.append(b)
+        return b
+
+    def conv(self, name, x: Slice, cout, k, s, act="Silu", group=1, y: Slice = None):
+        pad = k // 2
+        oh = (x.h + 2 * pad - k) // s + 1
+        ow = (x.w + 2 * pad - k) // s + 1
+        if y is None:
+            y = whole(self.buf(name + "_out", cout, oh, ow))
+        assert (y.c, y.h, y.w) == (cout, oh, ow), (name, y.c, y.h, y.w, cout, oh, ow)
+        i = self.nconv
+        self.nconv += 1
+        w = synth.normal(self.seed + 2 * i, (cout, x.c // group, k, k), 0.0, 0.05)
+        b = synth.normal(self.seed + 2 * i + 1, (cout,), 0.0, 0.01)
+        self.m.ops.append(ConvOp(name, x, y, k, s, group, act, w, b))
+        return y
+
+    def add(self, name, a, b, y=None):
+        if y is None:
+            y = whole(self.buf(name + "_out", a.c, a.h, a.w))
+        self.m.ops.append(AddOp(name, a, b, y))
+        return y
+
+    # ---- ultralytics modules (names follow the exported ONNX node names)
+    def bottleneck(self, p, x: Slice, c_out, k, e, shortcut, y: Slice = None):
+        c_ = int(c_out * e)
+        t = self.conv(f"{p}/cv1/conv/Conv", x, c_, k, 1)
+        if shortcut and x.c == c_out:
+            u = self.conv(f"{p}/cv2/conv/Conv", t, c_out, k, 1)
+            return self.add(f"{p}/Add", x, u, y)
+        return self.conv(f"{p}/cv2/conv/Conv", t, c_out, k, 1, y=y)
+
+    def c3k(self, p, x: Slice, c_out, n, shortcut, y: Slice):
+        c_ = c_out // 2
+        cat = self.buf(f"{p}/Concat", 2 * c_, x.h, x.w)
+        h = self.conv(f"{p}/cv1/conv/Conv", x, c_, 1, 1)
+        for i in range(n):
+            last = i == n - 1
+            h = self.bottleneck(f"{p}/m/m.{i}", h, c_, 3, 1.0, shortcut,
+                                y=Slice(cat, 0, c_) if last else None)
+        self.conv(f"{p}/cv2/conv/Conv", x, c_, 1, 1, y=Slice(cat, c_, c_))
+        return self.conv(f"{p}/cv3/conv/Conv", whole(cat), c_out, 1, 1, y=y)
+
+    def c3k2(self, p, x: Slice, c_out, c3k, e, shortcut=True, y: Slice = None):
+        c = int(c_out * e)
+        cat = self.buf(f"{p}/Concat", 3 * c, x.h, x.w)
+        self.conv(f"{p}/cv1/conv/Conv", x, 2 * c, 1, 1, y=Slice(cat, 0, 2 * c))
+        b = Slice(cat, c, c)
+        if c3k:
+            self.c3k(f"{p}/m.0", b, c, 2, shortcut, y=Slice(cat, 2 * c, c))
+        else:
+            self.bottleneck(f"{p}/m.0", b, c, 3, 0.5, shortcut, y=Slice(cat, 2 * c, c))
+        return self.conv(f"{p}/cv2/conv/Conv", whole(cat), c_out, 1, 1, y=y)
+
+    def sppf(self, p, x: Slice, c_out, y: Slice = None):
+        c_ = x.c // 2
+        cat = self.buf(f"{p}/Concat", 4 * c_, x.h, x.w)
+        prev = self.conv(f"{p}/cv1/conv/Conv", x, c_, 1, 1, y=Slice(cat, 0, c_))
+        for i, nm in enumerate(["m", "m_1", "m_2"]):
+            nxt = Slice(cat, (i + 1) * c_, c_)
+            self.m.ops.append(MaxPoolOp(f"{p}/{nm}/MaxPool", prev, nxt))
+            prev = nxt
+        return self.conv(f"{p}/cv2/conv/Conv", whole(cat), c_out, 1, 1, y=y)
+
+    def c2psa(self, p, x: Slice, c_out, y: Slice = None):
+        c = c_out // 2
+        heads = c // 64
+        head_dim = c // heads
+        key_dim = head_dim // 2
+        hw = x.h * x.w
+        cat = self.buf(f"{p}/Concat", 2 * c, x.h, x.w)
+        self.conv(f"{p}/cv1/conv/Conv", x, 2 * c, 1, 1, y=Slice(cat, 0, 2 * c))
+        b = Slice(cat, c, c)
+        q = f"{p}/m/m.0"
+        qkv = self.conv(f"{q}/attn/qkv/conv/Conv", b, c + 2 * key_dim * heads, 1, 1, act=None)
+        att = whole(self.buf(f"{q}/attn/Reshape_1", c, x.h, x.w))
+        op = AttentionOp(f"{q}/attn", qkv, att, heads, key_dim, head_dim, float(key_dim) ** -0.5,
+                         qt=self.buf(f"{q}/attn/Transpose", heads, hw, key_dim),
+                         attn=self.buf(f"{q}/attn/Softmax", heads, hw, hw),
+                         attn_t=self.buf(f"{q}/attn/Transpose_1", heads, hw, hw))
+        self.m.ops.append(op)
+        # positional term: depthwise 3x3 over v seen as [1, c, H, W]; the heads'
+        # v blocks are not adjacent inside qkv, so the conv runs per head
+        pe = self.buf(f"{q}/attn/pe/conv/Conv", c, x.h, x.w)
+        rows = 2 * key_dim + head_dim
+        w = synth.normal(self.seed + 2 * self.nconv, (c, 1, 3, 3), 0.0, 0.05)
+        bias = synth.normal(self.seed + 2 * self.nconv + 1, (c,), 0.0, 0.01)
+        self.nconv += 1
+        for h in range(heads):
+            v = qkv.sub(h * rows + 2 * key_dim, head_dim)
+            sl = slice(h * head_dim, (h + 1) * head_dim)
+            self.m.ops.append(ConvOp(f"{q}/attn/pe/conv/Conv" + (f"#head{h}" if heads > 1 else ""), v,
+                                     Slice(pe, h * head_dim, head_dim), 3, 1, head_dim, None, w[sl], bias[sl]))
+        s1 = self.add(f"{q}/attn/Add", att, whole(pe))
+        pr = self.conv(f"{q}/attn/proj/conv/Conv", s1, c, 1, 1, act=None)
+        b1 = self.add(f"{q}/Add", b, pr)
+        f0 = self.conv(f"{q}/ffn/ffn.0/conv/Conv", b1, 2 * c, 1, 1)
+        f1 = self.conv(f"{q}/ffn/ffn.1/conv/Conv", f0, c, 1, 1, act=None)
+        cat2 = self.buf(f"{p}/Concat#out", 2 * c, x.h, x.w)
+        self.m.ops.append(AddOp(f"{q}/Add_1", b1, f1, Slice(cat2, c, c)))
+        # the first half of the concat is cv1's first split output
+        self.m.ops.append(CopyOp(f"{p}/Split#0", Slice(cat, 0, c), Slice(cat2, 0, c)))
+        return self.conv(f"{p}/cv2/conv/Conv", whole(cat2), c_out, 1, 1, y=y)
+
+    def detect(self, p, xs, nc=80, reg_max=16):
+        c2 = max(16, xs[0].c // 4, reg_max * 4)
+        c3 = max(xs[0].c, min(nc, 100))
+        outs = []
+        for i, x in enumerate(xs):
+            out = self.buf(f"{p}/out{i}", 4 * reg_max + nc, x.h, x.w)
+            t = self.conv(f"{p}/cv2.{i}/cv2.{i}.0/conv/Conv", x, c2, 3, 1)
+            t = self.conv(f"{p}/cv2.{i}/cv2.{i}.1/conv/Conv", t, c2, 3, 1)
+            self.conv(f"{p}/cv2.{i}/cv2.{i}.2/Conv", t, 4 * reg_max, 1, 1, act=None, y=Slice(out, 0, 4 * reg_max))
+            u = self.conv(f"{p}/cv3.{i}/cv3.{i}.0/cv3.{i}.0.0/conv/Conv", x, x.c, 3, 1, group=x.c)
+            u = self.conv(f"{p}/cv3.{i}/cv3.{i}.0/cv3.{i}.0.1/conv/Conv", u, c3, 1, 1)
+            u = self.conv(f"{p}/cv3.{i}/cv3.{i}.1/cv3.{i}.1.0/conv/Conv", u, c3, 3, 1, group=c3)
+            u = self.conv(f"{p}/cv3.{i}/cv3.{i}.1/cv3.{i}.1.1/conv/Conv", u, c3, 1, 1)
+            self.conv(f"{p}/cv3.{i}/cv3.{i}.2/Conv", u, nc, 1, 1, act=None, y=Slice(out, 4 * reg_max, nc))
+            outs.append(out)
+        return outs
+
+
+@dataclass(eq=False)
+class CopyOp:
+    name: str
+    x: Slice
+    y: Slice
+
+
+def build(size: int = 640, seed: int = 7000) -> Model:
+    """YOLO11n at an input of size x size (a multiple of 32)."""
+    if size % 32:
+        raise ValueError("YOLO11n input size must be a multiple of 32")
+    bd = _Builder(size, seed)
+    m = bd.m
+    m.input = bd.buf("images", 3, size, size)
+    s8, s16, s32 = size // 8, size // 16, size // 32
+    # concat buffers of the neck, so that producers write straight into them
+    cat12 = bd.buf("/model.12/Concat", 256 + 128, s16, s16)
+    cat15 = bd.buf("/model.15/Concat", 128 + 128, s8, s8)
+    cat18 = bd.buf("/model.18/Concat", 64 + 128, s16, s16)
+    cat21 = bd.buf("/model.21/Concat", 128 + 256, s32, s32)
+
+    x = bd.conv("/model.0/conv/Conv", whole(m.input), 16, 3, 2)
+    x = bd.conv("/model.1/conv/Conv", x, 32, 3, 2)
+    x = bd.c3k2("/model.2", x, 64, False, 0.25)
+    x = bd.conv("/model.3/conv/Conv", x, 64, 3, 2)
+    p3 = bd.c3k2("/model.4", x, 128, False, 0.25, y=Slice(cat15, 128, 128))
+    x = bd.conv("/model.5/conv/Conv", p3, 128, 3, 2)
+    p4 = bd.c3k2("/model.6", x, 128, True, 0.5, y=Slice(cat12, 256, 128))
+    x = bd.conv("/model.7/conv/Conv", p4, 256, 3, 2)
+    x = bd.c3k2("/model.8", x, 256, True, 0.5)
+    x = bd.sppf("/model.9", x, 256)
+    p5 = bd.c2psa("/model.10", x, 256, y=Slice(cat21, 128, 256))
+    m.ops.append(UpsampleOp("/model.11/Resize", p5, Slice(cat12, 0, 256)))
+    h13 = bd.c3k2("/model.13", whole(cat12), 128, False, 0.5, y=Slice(cat18, 64, 128))
+    m.ops.append(UpsampleOp("/model.14/Resize", h13, Slice(cat15, 0, 128)))
+    o16 = bd.c3k2("/model.16", whole(cat15), 64, False, 0.5)
+    bd.conv("/model.17/conv/Conv", o16, 64, 3, 2, y=Slice(cat18, 0, 64))
+    o19 = bd.c3k2("/model.19", whole(cat18), 128, False, 0.5)
+    bd.conv("/model.20/conv/Conv", o19, 128, 3, 2, y=Slice(cat21, 0, 128))
+    o22 = bd.c3k2("/model.22", whole(cat21), 256, True, 0.5)
+    m.outputs = bd.detect("/model.23", [o16, o19, o22])
+    return m
+
+
+# --------------------------------------------------------------- device side
+
+class Frame:
+    """Device buffers, packed weights and the launch list of one model."""
+
+    def __init__(self, model: Model, device):
+        import torch
+        self.model = model
+        self.device = device
+        for b in model.bufs:
+            b.tensor = torch.empty((1, b.c, b.h, b.w), dtype=torch.float32, device=device)
+        self.stream = C.c_void_p()
+        N.call("osh_stream_create", C.byref(self.stream))
+        self.graph = None
+        self._calls = []
+        self._keep = []
+        for op in model.ops:
+            self._calls.append(self._prepare(op))
+        torch.cuda.synchronize()
+
+    def _prepare(self, op):
+        import torch
+        lib = N.lib()
+        if isinstance(op, ConvOp):
+            attrs = N.ConvAttrs()
+            attrs.group = op.group
+            attrs.n_kernel_shape, attrs.kernel_shape[0], attrs.kernel_shape[1] = 2, op.k, op.k
+            attrs.n_strides, attrs.strides[0], attrs.strides[1] = 2, op.s, op.s
+            attrs.n_pads = 4
+            for i in range(4):
+                attrs.pads[i] = op.k // 2
+            p = N.ConvParams()
+            N.call("osh_conv_resolve", C.byref(attrs), N.dims64(op.x.shape), N.dims64(op.w.shape), C.byref(p))
+            assert (p.m, p.oh, p.ow) == (op.y.c, op.y.h, op.y.w), op.name
+            nbytes = C.c_size_t()
+            N.call("osh_conv_packed_weight_bytes", C.byref(p), C.byref(nbytes))
+            w = torch.from_numpy(np.ascontiguousarray(op.w)).to(self.device)
+            b = torch.from_numpy(np.ascontiguousarray(op.b)).to(self.device)
+            packed = torch.empty(max(1, nbytes.value // 4), dtype=torch.float32, device=self.device)
+            torch.cuda.synchronize()  # the uploads ran on torch's stream; packing runs on the frame's
+            N.call("osh_conv_pack_weights", C.byref(p), C.c_void_p(w.data_ptr()), C.c_void_p(packed.data_ptr()),
+                   self.stream)
+            self._keep += [p, w, b, packed]
+            act = N.ACTIVATIONS[op.act]
+            return lambda: N.check(lib.osh_conv2d_f32(C.byref(p), op.x.ptr(), C.c_void_p(packed.data_ptr()),
+                                                      C.c_void_p(b.data_ptr()), act, op.y.ptr(), self.stream))
+        if isinstance(op, AddOp):
+            n = op.y.c * op.y.h * op.y.w
+            return lambda: N.check(lib.osh_add_f32(n, op.a.ptr(), op.b.ptr(), op.y.ptr(), self.stream))
+        if isinstance(op, CopyOp):
+            nb = 4 * op.y.c * op.y.h * op.y.w
+            return lambda: N.check(lib.osh_memcpy_d2d(op.y.ptr(), op.x.ptr(), nb, self.stream))
+        if isinstance(op, MaxPoolOp):
+            pp = N.PoolParams(1, op.x.c, op.x.h, op.x.w, op.k, op.k, op.s, op.s, op.p, op.p, op.y.h, op.y.w)
+            self._keep.append(pp)
+            return lambda: N.check(lib.osh_maxpool2d_f32(C.byref(pp), op.x.ptr(), op.y.ptr(), self.stream))
+        if isinstance(op, UpsampleOp):
+            return lambda: N.check(lib.osh_resize_nearest_f32(1, op.x.c, op.x.h, op.x.w, op.f, op.f, op.x.ptr(),
+                                                              op.y.ptr(), op.y.c * op.y.h * op.y.w, self.stream))
+        if isinstance(op, AttentionOp):
+            return self._prepare_attention(op)
+        raise TypeError(op)
+
+    def _prepare_attention(self, op: AttentionOp):
+        lib = N.lib()
+        n = op.qkv.h * op.qkv.w
+        rows = 2 * op.key_dim + op.head_dim
+        hs = rows * n  # head stride inside qkv
+        base = op.qkv.ptr().value
+        q = C.c_void_p(base)
+        k = C.c_void_p(base + 4 * op.key_dim * n)
+        v = C.c_void_p(base + 4 * 2 * op.key_dim * n)
+        qt, sc, st = (C.c_void_p(b.tensor.data_ptr()) for b in (op.qt, op.attn, op.attn_t))
+        y = op.y.ptr()
+
+        def run():
+            # q^T per head: [kd, N] -> [N, kd]
+            N.check(lib.osh_transpose_f32(op.heads, op.key_dim, n, q, hs, qt, n * op.key_dim, self.stream))
+            # scores[h] = q^T k: [N, kd] x [kd, N]
+            N.check(lib.osh_gemm_f32_batched(op.heads, n, n, op.key_dim, qt, op.key_dim, n * op.key_dim, k, n, hs,
+                                             None, N.ACT_NONE, sc, n, n * n, self.stream))
+            N.check(lib.osh_softmax_f32(op.heads * n, n, C.c_float(op.scale), sc, st, self.stream))
+            # probabilities transposed back into the scores buffer
+            N.check(lib.osh_transpose_f32(op.heads, n, n, st, n * n, sc, n * n, self.stream))
+            # y[h] = v attn^T: [hd, N] x [N, N]
+            N.check(lib.osh_gemm_f32_batched(op.heads, op.head_dim, n, n, v, n, hs, sc, n, n * n, None, N.ACT_NONE,
+                                             y, n, op.head_dim * n, self.stream))
+        return run
+
+    def run(self):
+        """Issue every op of one frame on the frame's stream (no sync)."""
+        for c in self._calls:
+            c()
+
+    def capture(self):
+        """Record one frame as a HIP graph (replayed by `launch`)."""
+        if self.graph is None:
+            g = C.c_void_p()
+            N.call("osh_graph_begin", self.stream)
+            try:
+                self.run()
+            finally:
+                N.call("osh_graph_end", self.stream, C.byref(g))
+            self.graph = g
+        return self.graph
+
+    def launch(self):
+        if self.graph is not None:
+            N.call("osh_graph_launch", self.graph, self.stream)
+        else:
+            self.run()
+
+    def sync(self):
+        N.call("osh_stream_sync", self.stream)
+
+    def set_input(self, x):
+        """Copy an input image into the frame (synchronous: the frame's stream
+        does not order itself after torch's)."""
+        import torch
+        t = x if isinstance(x, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(x, np.float32))
+        self.model.input.tensor.copy_(t.reshape(self.model.input.tensor.shape))
+        torch.cuda.synchronize()
+
+    def outputs(self):
+        return [b.tensor for b in self.model.outputs]
+
+    def close(self):
+        if self.graph is not None:
+            N.call("osh_graph_destroy", self.graph)
+            self.graph = None
+        if self.stream:
+            N.call("osh_stream_destroy", self.stream)
+            self.stream = C.c_void_p()

@@ -51,6 +51,9 @@ def lib():
         l.orc_winograd_f23.argtypes = [C.c_int] * 5 + [_fp, _fp, _fp, _fp]
         for f in (l.orc_exp_ref, l.orc_silu_ref, l.orc_silu_scalar, l.orc_relu):
             f.argtypes = [C.c_long, _fp, _fp]
+        l.orc_softmax_f32.argtypes = [C.c_long, C.c_int, C.c_float, _fp, _fp]
+        l.orc_maxpool2d_f32.argtypes = [C.c_int] * 12 + [_fp, _fp]
+        l.orc_resize_nearest.argtypes = [C.c_int] * 6 + [_fp, _fp]
         l.orc_minmax.argtypes = [C.c_long, _fp, _fp, _fp]
         l.orc_dql_params.argtypes = [C.c_float, C.c_float, _fp, _ip]
         l.orc_quantize_u8.argtypes = [C.c_long, _fp, C.c_float, C.c_int, _u8p]
@@ -178,6 +181,34 @@ def silu_scalar(x):
 
 def relu(x):
     return _unary(lib().orc_relu, x)
+
+
+def softmax(x, scale=1.0):
+    """Mul by a constant then Softmax over the last axis (SoftmaxLayer, VectorMath.SoftmaxRow)."""
+    x = _c32(x)
+    y = np.empty_like(x)
+    cols = x.shape[-1]
+    lib().orc_softmax_f32(x.size // cols, cols, scale, _f(x), _f(y))
+    return y
+
+
+def maxpool2d(x, k, s, p):
+    """MaxPool 2-D, symmetric pads p (MaxPoolLayer)."""
+    x = _c32(x)
+    n, c, h, w = x.shape
+    oh, ow = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+    y = np.empty((n, c, oh, ow), np.float32)
+    lib().orc_maxpool2d_f32(n, c, h, w, k, k, s, s, p, p, oh, ow, _f(x), _f(y))
+    return y
+
+
+def resize_nearest(x, f):
+    """Nearest upsampling by an integer factor (ResizeLayer, mode nearest)."""
+    x = _c32(x)
+    n, c, h, w = x.shape
+    y = np.empty((n, c, h * f, w * f), np.float32)
+    lib().orc_resize_nearest(n, c, h, w, f, f, _f(x), _f(y))
+    return y
 
 
 # ---------------------------------------------------------------- int8

@@ -30,6 +30,12 @@
  *   orc_quantize_u8     QuantizedMatMulOps.cs:280-335, Quantization.cs:68-103
  *   orc_dqmm            QuantizedMatMulOps.cs:115-201 (+ Int8F32Gemm.cs:124-174 weight widening)
  *   orc_matmul_integer  Int8Gemm.cs:212-236 (int64 sum of (a - a_zp)(b - b_zp[col]))
+ *   orc_softmax_f32     DnnOps.cs:2547-2675 + VectorMath.cs:282-287 (Mul by the constant, then per
+ *                       row: max, e = exp(x - max) summed, scale by 1/sum; the sum runs
+ *                       sequentially here, in 8 vector lanes there: parity unpinned at that
+ *                       rounding)
+ *   orc_maxpool2d_f32   DnnOps.cs:1335-1480 (max over the in-range window elements)
+ *   orc_resize_nearest  DnnOps.cs:2215-2330 (nearest, integer factor: source index dst / factor)
  *
  * Build: see oracle/Makefile (gcc, -O3 -ffp-contract=off; fmaf is explicit).
  */
@@ -471,6 +477,64 @@ ORC_API void orc_silu_scalar(long n, const float *x, float *y)
 ORC_API void orc_relu(long n, const float *x, float *y)
 {
     for (long i = 0; i < n; i++) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+
+/* ------------------------------------------------- segment-continuity ops */
+
+ORC_API void orc_softmax_f32(long rows, int cols, float scale, const float *x, float *y)
+{
+    for (long r = 0; r < rows; r++) {
+        const float *xr = x + r * cols;
+        float *yr = y + r * cols;
+        float mx = -INFINITY;
+        for (int c = 0; c < cols; c++) {
+            float v = xr[c] * scale;
+            if (v > mx) mx = v;
+        }
+        float sum = 0.0f;
+        for (int c = 0; c < cols; c++) {
+            float e = exp_ref(xr[c] * scale - mx);
+            yr[c] = e;
+            sum += e;
+        }
+        float inv = 1.0f / sum;
+        for (int c = 0; c < cols; c++) yr[c] = yr[c] * inv;
+    }
+}
+
+ORC_API void orc_maxpool2d_f32(int N, int C, int H, int W, int kh, int kw, int sh, int sw, int pt, int pl,
+                               int OH, int OW, const float *x, float *y)
+{
+    for (long pl_ = 0; pl_ < (long)N * C; pl_++) {
+        const float *xp = x + pl_ * H * W;
+        float *yp = y + pl_ * OH * OW;
+        for (int oy = 0; oy < OH; oy++)
+            for (int ox = 0; ox < OW; ox++) {
+                float m = 0.0f;
+                int any = 0;
+                for (int ky = 0; ky < kh; ky++) {
+                    int iy = oy * sh - pt + ky;
+                    if (iy < 0 || iy >= H) continue;
+                    for (int kx = 0; kx < kw; kx++) {
+                        int ix = ox * sw - pl + kx;
+                        if (ix < 0 || ix >= W) continue;
+                        float v = xp[(long)iy * W + ix];
+                        if (!any || v > m) m = v;
+                        any = 1;
+                    }
+                }
+                yp[(long)oy * OW + ox] = m;
+            }
+    }
+}
+
+ORC_API void orc_resize_nearest(int N, int C, int H, int W, int fh, int fw, const float *x, float *y)
+{
+    int OH = H * fh, OW = W * fw;
+    for (long pl_ = 0; pl_ < (long)N * C; pl_++)
+        for (int oy = 0; oy < OH; oy++)
+            for (int ox = 0; ox < OW; ox++)
+                y[(pl_ * OH + oy) * OW + ox] = x[(pl_ * H + oy / fh) * W + ox / fw];
 }
 
 /* ------------------------------------------------------------------ int8 DQM */

@@ -1,0 +1,92 @@
+"""CPU execution of a yolo11n.Model with the oracle.
+
+TEST INFRASTRUCTURE ONLY: used by tests/ and by bench.py's cpu_baseline leg.
+
+Each op is restated with the oracle's functions in the order the reference's
+AVX-512 dispatch uses for that layer (ConvLayer.Forward,
+src/OnnxSharp/Ops/DnnOps.cs:437-482): depthwise for g == C == M, the NCHWc
+order for 3x3 convolutions whose input channels are a multiple of 16, the
+im2col/pointwise FMA chain otherwise; SiLU is the reference polynomial.  The
+attention core uses the GEMM chain for both MatMuls and the oracle softmax.
+"""
+import numpy as np
+
+
+def conv(oracle, op, x):
+    k, s, pad = op.k, op.s, op.k // 2
+    out_hw = (op.y.h, op.y.w)
+    if op.group > 1 and op.group == op.x.c == op.y.c:
+        y = oracle.conv_dw_f32(x, op.w, op.b, (s, s), (pad, pad), (1, 1), out_hw)
+    else:
+        nchwc = k == 3 and op.group == 1 and op.x.c % 16 == 0
+        y = oracle.conv2d_f32(x, op.w, op.b, (s, s), (pad, pad), (1, 1), op.group, out_hw,
+                              order=oracle.ORDER_NCHWC if nchwc else oracle.ORDER_IM2COL)
+    if op.act == "Silu":
+        y = oracle.silu_ref(y)
+    return y
+
+
+def attention(oracle, op, qkv):
+    n = op.qkv.h * op.qkv.w
+    rows = 2 * op.key_dim + op.head_dim
+    q3 = qkv.reshape(op.heads, rows, n)
+    ys = []
+    for h in range(op.heads):
+        q = q3[h, :op.key_dim]
+        k = q3[h, op.key_dim:2 * op.key_dim]
+        v = q3[h, 2 * op.key_dim:]
+        scores = oracle.gemm_f32(np.ascontiguousarray(q.T), k)
+        probs = oracle.softmax(scores, op.scale)
+        ys.append(oracle.gemm_f32(v, np.ascontiguousarray(probs.T)))
+    return np.concatenate(ys, axis=0).reshape(1, op.y.c, op.y.h, op.y.w)
+
+
+def run_op(oracle, op, inputs):
+    """Output of one op from its input arrays (in the op's own input order)."""
+    from onnxsharp_amd import yolo11n as Y
+    if isinstance(op, Y.ConvOp):
+        return conv(oracle, op, inputs[0])
+    if isinstance(op, Y.AddOp):
+        return (inputs[0] + inputs[1]).astype(np.float32)
+    if isinstance(op, Y.CopyOp):
+        return inputs[0].copy()
+    if isinstance(op, Y.MaxPoolOp):
+        return oracle.maxpool2d(inputs[0], op.k, op.s, op.p)
+    if isinstance(op, Y.UpsampleOp):
+        return oracle.resize_nearest(inputs[0], op.f)
+    if isinstance(op, Y.AttentionOp):
+        return attention(oracle, op, inputs[0])
+    raise TypeError(op)
+
+
+def op_inputs(op):
+    """The slices an op reads, in run_op order."""
+    from onnxsharp_amd import yolo11n as Y
+    if isinstance(op, Y.AddOp):
+        return [op.a, op.b]
+    if isinstance(op, Y.AttentionOp):
+        return [op.qkv]
+    return [op.x]
+
+
+class Frame:
+    """The whole model on numpy buffers (one array per device buffer).
+    `oracle` is the oracle.oracle module."""
+
+    def __init__(self, model):
+        self.model = model
+        self.arrays = {id(b): np.zeros((1, b.c, b.h, b.w), np.float32) for b in model.bufs}
+
+    def get(self, sl):
+        return self.arrays[id(sl.buf)][:, sl.c0:sl.c0 + sl.c]
+
+    def put(self, sl, val):
+        self.arrays[id(sl.buf)][:, sl.c0:sl.c0 + sl.c] = val
+
+    def run(self, oracle, x):
+        from onnxsharp_amd import yolo11n as Y
+        self.put(Y.whole(self.model.input), x)
+        for op in self.model.ops:
+            ins = [np.ascontiguousarray(self.get(s)) for s in op_inputs(op)]
+            self.put(op.y, run_op(oracle, op, ins))
+        return [self.arrays[id(b)] for b in self.model.outputs]

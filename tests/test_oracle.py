@@ -265,3 +265,35 @@ def test_planted_mistake_is_caught(oracle):
     ref = oracle.conv2d_f64(x, w, None, (1, 1), (1, 1), (1, 1), 1, (7, 7))
     bad = oracle.conv2d_f32(x, np.ascontiguousarray(w.transpose(0, 1, 3, 2)), None, (1, 1), (1, 1), (1, 1), 1, (7, 7))
     assert np.abs(bad - ref).max() > 1e-3
+
+
+# ---- segment-continuity ops (YOLO11n glue): pinned by closed forms
+
+def test_softmax_matches_float64(oracle):
+    x = np.random.default_rng(5).standard_normal((37, 401)).astype(np.float32) * 4
+    scale = np.float32(32.0 ** -0.5)
+    y = oracle.softmax(x, float(scale))
+    v = (x * scale).astype(np.float64)
+    e = np.exp(v - v.max(axis=1, keepdims=True))
+    ref = e / e.sum(axis=1, keepdims=True)
+    assert np.abs(y - ref).max() <= 2e-6 + 1e-5 * np.abs(ref).max()
+    # the product is rounded to float before the row max (the Mul node runs first)
+    assert oracle.softmax(np.array([[1.0, 2.0]], np.float32), 3.0).argmax() == 1
+
+
+def test_maxpool_matches_brute_force(oracle):
+    x = np.random.default_rng(6).standard_normal((2, 3, 11, 9)).astype(np.float32)
+    for k, s, p in [(5, 1, 2), (3, 2, 1), (2, 2, 0)]:
+        y = oracle.maxpool2d(x, k, s, p)
+        xp = np.pad(x, ((0, 0), (0, 0), (p, p), (p, p)), constant_values=-np.inf)
+        oh, ow = y.shape[2:]
+        ref = np.empty_like(y)
+        for i in range(oh):
+            for j in range(ow):
+                ref[:, :, i, j] = xp[:, :, i * s:i * s + k, j * s:j * s + k].max(axis=(2, 3))
+        assert np.array_equal(y, ref), (k, s, p)
+
+
+def test_resize_nearest_is_repeat(oracle):
+    x = np.random.default_rng(7).standard_normal((1, 4, 5, 3)).astype(np.float32)
+    assert np.array_equal(oracle.resize_nearest(x, 2), x.repeat(2, axis=2).repeat(2, axis=3))
