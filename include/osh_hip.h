@@ -83,7 +83,19 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 where the operands allow it (tuning and tests); -2 = always
  *                 use the LDS-staged GEMM tile.  Every choice sums k in the
  *                 same order.  Initial value from ONNXSHARP_HIP_GEMM_VARIANT.
- *   "gemm_variants" (get only): N, the number of wave tiles. */
+ *   "gemm_variants" (get only): N, the number of wave tiles.
+ *   "conv16_variant": -1 (default) = 3x3 convolutions with C % 16 == 0 run
+ *                 the in-order 16x16x4 MFMA kernel (the reference's NCHWc
+ *                 chain, bit for bit) with a wave tile picked per shape;
+ *                 0..11 forces a tile (6..11: weights held in LDS);
+ *                 -2 = use the weight-stationary 3x3
+ *                 kernels instead (summation order differs; within the FP32
+ *                 tolerance).  Initial value from ONNXSHARP_HIP_CONV16_VARIANT.
+ *   "tune": 1 (default) = the first launch of a 3x3 conv shape on a stream
+ *                 that is not capturing times every conv16 tile (they all give
+ *                 identical outputs) and keeps the fastest for that shape;
+ *                 0 = pick tiles by the cost model only.  Initial value from
+ *                 ONNXSHARP_HIP_TUNE. */
 OSH_API osh_status osh_config_set(const char *key, int value);
 OSH_API osh_status osh_config_get(const char *key, int *value);
 

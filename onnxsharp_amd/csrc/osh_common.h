@@ -117,6 +117,14 @@ inline int device_cus() {
 int gemm_variant();
 int gemm16_variant_count();
 
+// Forced conv16 wave tile for 3x3 convolutions (-1 = automatic, -2 = use the
+// weight-stationary kernels instead).
+int conv16_variant();
+
+// Whether kernels whose tiles all give identical results may pick their tile
+// by timing it on first use (osh_config "tune", ONNXSHARP_HIP_TUNE; default on).
+bool tuning_enabled();
+
 // Dispatch a runtime activation code to a template instantiation of a fused epilogue.
 #define OSH_DISPATCH_ACT(act, ACT, ...)                      \
     switch (act) {                                           \

@@ -3,6 +3,11 @@
 // of ConvLayer.Forward (DnnOps.cs:411-500), re-planned for gfx950:
 //
 //   depthwise (group == C == M)         -> dw_conv_kernel (direct, ky -> kx FMA chain)
+//   3x3 / dil 1 / stride any, C % 16 == 0
+//                                       -> in-order 16x16x4 MFMA implicit GEMM (osh_conv16.h),
+//                                          the NCHWc chain bit for bit
+//   3x3, C <= 4, M = 8/16/32, group 1    -> first_conv_kernel (direct; the network's first
+//                                          layer, FirstConv.cs: ic -> ky -> kx FMA chain)
 //   1x1 / stride 1 / pad 0 / dil 1      -> MFMA GEMM over NCHW (W[M,C] x X[C,H*W])
 //   3x3 / pad 1 / dil 1 / stride 1, C = 16, 32, 64, OW % 8 == 0
 //                                       -> wave-independent MFMA kernel (osh_conv3x3_wi.h)
@@ -14,7 +19,11 @@
 // Bias and the fused activation (Relu / SiLU, GraphFusion.cs:1713-1718) are
 // applied in registers before the single store.
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
 
+#include "osh_conv16.h"
 #include "osh_conv3x3.h"
 #include "osh_conv3x3_wi.h"
 #include "osh_conv3x3_ws.h"
@@ -105,10 +114,70 @@ __global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const f
     y[idx] = activate<ACT>(acc);
 }
 
-enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3, ALGO_WS3X3 = 4, ALGO_WI3X3 = 5 };
+// ------------------------------------------------------- small-C first layer
+//
+// The first layer of an image network (C = 3 colour planes): too little K for
+// MFMA tiles (27 for 3x3) and HBM-bound (it reads the image once and writes M
+// planes).  One thread per output pixel keeps all M accumulators in registers;
+// the weight index is the same for every lane, so the weights come through
+// the scalar cache.  Per output channel the chain is bias, then fmaf over
+// ic -> ky -> kx (the panel order of FirstConv.cs:344-362); padding taps add
+// nothing.
+template <int MM, int CC, int ACT>
+__global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, const float *__restrict__ x,
+                                                         const float *__restrict__ w,
+                                                         const float *__restrict__ bias, float *__restrict__ y) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long plane = (long long)p.oh * p.ow;
+    if (idx >= (long long)p.n * plane) return;
+    const int ox = (int)(idx % p.ow);
+    const long long t = idx / p.ow;
+    const int oy = (int)(t % p.oh);
+    const int n = (int)(t / p.oh);
+    const int m = p.m;
+    // all CC*9 input taps are loaded before the first FMA (independent loads)
+    float v[CC][3][3];
+    const float *xn = x + (long long)n * CC * p.h * p.w;
+#pragma unroll
+    for (int ic = 0; ic < CC; ic++)
+#pragma unroll
+        for (int ky = 0; ky < 3; ky++) {
+            const int iy = oy * p.sh - p.pt + ky;
+#pragma unroll
+            for (int kx = 0; kx < 3; kx++) {
+                const int ix = ox * p.sw - p.pl + kx;
+                const bool ok = (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
+                v[ic][ky][kx] = ok ? xn[((long long)ic * p.h + iy) * p.w + ix] : 0.f;
+            }
+        }
+    float *yp = y + (long long)n * m * plane + (long long)oy * p.ow + ox;
+    // 3x3 taps at compile-time offsets: the weights arrive in wide scalar loads
+#pragma unroll
+    for (int oc = 0; oc < MM; oc++) {  // MM == m (eligibility)
+        float acc = bias ? bias[oc] : 0.f;
+        const float *wo = w + oc * CC * 9;
+#pragma unroll
+        for (int ic = 0; ic < CC; ic++)
+#pragma unroll
+            for (int ky = 0; ky < 3; ky++)
+#pragma unroll
+                for (int kx = 0; kx < 3; kx++) acc = __builtin_fmaf(wo[(ic * 3 + ky) * 3 + kx], v[ic][ky][kx], acc);
+        yp[oc * plane] = activate<ACT>(acc);
+    }
+}
+
+static bool first_conv_eligible(const osh_conv_params *p) {
+    return p->group == 1 && p->c <= 4 && (p->m == 8 || p->m == 16 || p->m == 32) && p->kh == 3 && p->kw == 3 &&
+           p->dh == 1 && p->dw == 1;
+}
+
+enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3, ALGO_WS3X3 = 4, ALGO_WI3X3 = 5,
+                ALGO_FIRST = 6, ALGO_CONV16 = 7 };
 
 static ConvAlgo select_algo(const osh_conv_params *p) {
     if (p->group == p->c && p->group == p->m && p->group > 1) return ALGO_DEPTHWISE;
+    if (first_conv_eligible(p)) return ALGO_FIRST;
+    if (conv16_variant() != -2 && conv16_eligible(p)) return ALGO_CONV16;
     if (p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 && p->oh == p->h &&
         p->ow == p->w)
         return ALGO_POINTWISE;
@@ -116,6 +185,71 @@ static ConvAlgo select_algo(const osh_conv_params *p) {
     if (conv3x3_ws_eligible(p)) return ALGO_WS3X3;
     if (conv3x3_eligible(p)) return ALGO_DIRECT3X3;
     return ALGO_IM2COL;
+}
+
+// ------------------------------------------------------------ conv16 tuning
+//
+// Every conv16 wave tile computes the same chain, so the fastest one can be
+// chosen by measurement without changing any result: the first launch of a
+// shape on a stream that is not being captured times each tile that fits
+// (HIP events, one warm-up and three timed launches each, writing the real
+// output every time) and remembers the winner per shape.  Launches recorded
+// into a graph before that use the cost model.
+static std::mutex g_tune_mu;
+static std::map<std::tuple<int, int, int, int, int, int, int, int, int, int, int, int>, int> g_tuned;
+
+static std::tuple<int, int, int, int, int, int, int, int, int, int, int, int> conv_key(const osh_conv_params *p) {
+    return std::make_tuple(p->n, p->c, p->h, p->w, p->m, p->sh, p->sw, p->pt, p->pl, p->oh, p->ow, p->group);
+}
+
+static bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+}
+
+static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                      int act, float *y, hipStream_t st) {
+    const int forced = conv16_variant();
+    if (forced >= 0 || !tuning_enabled()) return conv16_launch(p, x, w, bias, act, y, st, forced);
+    const auto key = conv_key(p);
+    {
+        std::lock_guard<std::mutex> lk(g_tune_mu);
+        auto it = g_tuned.find(key);
+        if (it != g_tuned.end()) return conv16_launch(p, x, w, bias, act, y, st, it->second);
+    }
+    if (capturing(st)) return conv16_launch(p, x, w, bias, act, y, st, -1);
+    hipEvent_t e0, e1;
+    OSH_HIP_CHECK(hipEventCreate(&e0));
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return fail(OSH_E_DEVICE, "hipEventCreate failed");
+    }
+    int best = -1;
+    float best_ms = 0.f;
+    osh_status rc = OSH_OK;
+    for (int v = 0; v < kC16Count && rc == OSH_OK; v++) {
+        if (!conv16_fits(p, kC16[v])) continue;
+        rc = conv16_launch(p, x, w, bias, act, y, st, v);
+        if (rc != OSH_OK) break;
+        if (hipEventRecord(e0, st) != hipSuccess) { rc = fail(OSH_E_DEVICE, "hipEventRecord failed"); break; }
+        for (int r = 0; r < 3 && rc == OSH_OK; r++) rc = conv16_launch(p, x, w, bias, act, y, st, v);
+        if (rc != OSH_OK) break;
+        float ms = 0.f;
+        if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+            hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
+            rc = fail(OSH_E_DEVICE, "conv16 tuning: event timing failed");
+            break;
+        }
+        if (best < 0 || ms < best_ms) best = v, best_ms = ms;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc != OSH_OK) return rc;
+    {
+        std::lock_guard<std::mutex> lk(g_tune_mu);
+        g_tuned[key] = best;
+    }
+    return OSH_OK;  // y already holds the result (every tile computes the same values)
 }
 
 static osh_status check_params(const osh_conv_params *p) {
@@ -196,6 +330,7 @@ OSH_API osh_status osh_conv_packed_weight_bytes(const osh_conv_params *p, size_t
     if (!bytes) return fail(OSH_E_INVALID, "bytes is NULL");
     size_t oihw = (size_t)p->m * (p->c / p->group) * p->kh * p->kw * sizeof(float);
     switch (select_algo(p)) {
+    case ALGO_CONV16: *bytes = conv16_packed_bytes(p); break;
     case ALGO_WI3X3: *bytes = conv3x3_wi_packed_bytes(p); break;
     case ALGO_WS3X3: *bytes = conv3x3_ws_packed_bytes(p); break;
     case ALGO_DIRECT3X3: *bytes = conv3x3_packed_bytes(p); break;
@@ -209,6 +344,7 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
     osh_status st = check_params(p);
     if (st != OSH_OK) return st;
     if (!d_w || !d_packed) return fail(OSH_E_INVALID, "Conv pack: NULL pointer");
+    if (select_algo(p) == ALGO_CONV16) return conv16_pack(p, d_w, d_packed, to_stream(s));
     if (select_algo(p) == ALGO_WI3X3) return conv3x3_wi_pack(p, d_w, d_packed, to_stream(s));
     if (select_algo(p) == ALGO_WS3X3) return conv3x3_ws_pack(p, d_w, d_packed, to_stream(s));
     if (select_algo(p) == ALGO_DIRECT3X3) return conv3x3_pack(p, d_w, d_packed, to_stream(s));
@@ -237,6 +373,31 @@ OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, co
         OSH_LAUNCH_CHECK("dw_conv_kernel");
         return OSH_OK;
     }
+    case ALGO_FIRST: {
+        long long total = (long long)p->n * out_hw;
+        dim3 grid((unsigned)((total + 255) / 256));
+#define OSH_FIRST(MM, CC)                                                                                      \
+    OSH_DISPATCH_ACT(act, ACT, hipLaunchKernelGGL((first_conv_kernel<MM, CC, ACT>), grid, dim3(256), 0, stream, \
+                                                  *p, d_x, w, d_bias, d_y))
+#define OSH_FIRST_C(MM)            \
+    do {                           \
+        switch (p->c) {            \
+        case 1: OSH_FIRST(MM, 1); break; \
+        case 2: OSH_FIRST(MM, 2); break; \
+        case 3: OSH_FIRST(MM, 3); break; \
+        default: OSH_FIRST(MM, 4); break; \
+        }                          \
+    } while (0)
+        if (p->m == 8) OSH_FIRST_C(8);
+        else if (p->m == 16) OSH_FIRST_C(16);
+        else OSH_FIRST_C(32);
+#undef OSH_FIRST_C
+#undef OSH_FIRST
+        OSH_LAUNCH_CHECK("first_conv_kernel");
+        return OSH_OK;
+    }
+    case ALGO_CONV16:
+        return conv16_tuned_launch(p, d_x, w, d_bias, act, d_y, stream);
     case ALGO_WI3X3:
         return conv3x3_wi_launch(p, d_x, w, d_bias, act, d_y, stream, device_cus());
     case ALGO_WS3X3:

@@ -13,10 +13,12 @@
 //     (32 oc x channel pair), B = patch (channel pair x 32 pixels), one
 //     ds_read_b128 per operand per four k-steps;
 //   - bias, activation and the NCHW store straight from the accumulators.
-// Accumulation order per output: bias, then tap (ky, kx) -> groups of 8
-// channels -> channel pairs (j, j + 4); the reference's NchwcConv / Im2Col
-// chains (src/OnnxSharp/Kernels/NchwcConv.cs:533-605, ConvKernels.cs:554-563)
-// differ from it by rounding only.
+// Accumulation order per output: bias, then 16-channel block -> tap (ky, kx)
+// -> channel pairs (2i, 2i + 1) in ascending order.  The MFMA adds the pair's
+// two products one after the other with one rounding each, so this is the
+// reference's NCHWc chain (src/OnnxSharp/Kernels/NchwcConv.cs:533-605: bias,
+// then icb -> ky -> kx -> lane16) bit for bit.  A lane-half's float4 holds
+// the even (lower half) or odd (upper half) channels of a group of 8.
 #pragma once
 
 #include <type_traits>
@@ -36,7 +38,7 @@ inline size_t conv3x3_wi_packed_bytes(const osh_conv_params *p) {
     return (size_t)((p->m + 31) / 32) * 9 * p->c * 32 * sizeof(float);
 }
 
-// packed[mt][tap][g (C/8)][lhi][oc 32][j 4] = w[mt*32 + oc][8g + 4*lhi + j][tap]  (0 beyond M)
+// packed[mt][tap][g (C/8)][lhi][oc 32][j 4] = w[mt*32 + oc][8g + 2j + lhi][tap]  (0 beyond M)
 __global__ void conv3x3_wi_pack_kernel(int M, int C, const float *__restrict__ w, float *__restrict__ out,
                                        long long total) {
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -51,7 +53,7 @@ __global__ void conv3x3_wi_pack_kernel(int M, int C, const float *__restrict__ w
     t /= C / 8;
     int tap = (int)(t % 9);
     int mt = (int)(t / 9);
-    int m = mt * 32 + oc, ch = 8 * g + 4 * lhi + j;
+    int m = mt * 32 + oc, ch = 8 * g + 2 * j + lhi;
     out[idx] = m < M ? w[((long long)m * C + ch) * 9 + tap] : 0.f;
 }
 
@@ -130,10 +132,10 @@ __global__ __launch_bounds__(256) void conv3x3_wi_kernel(osh_conv_params p, cons
 #pragma unroll
             for (int g = 0; g < G; g++)
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int c0 = 8 * g + 4 * h;
+                for (int h = 0; h < 2; h++) {  // slot h: channels 8g + h, +2, +4, +6
+                    const int c0 = 8 * g + h;
                     *reinterpret_cast<float4 *>(&pw[chan_lds(g, h) + pos_lds]) =
-                        make_float4(rp[c0], rp[c0 + 1], rp[c0 + 2], rp[c0 + 3]);
+                        make_float4(rp[c0], rp[c0 + 2], rp[c0 + 4], rp[c0 + 6]);
                 }
         } else {
 #pragma unroll
@@ -184,45 +186,56 @@ __global__ __launch_bounds__(256) void conv3x3_wi_kernel(osh_conv_params p, cons
         f32x16 acc;
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[r] = bacc[r];
-        // taps stay rolled loops (the 8 channel groups of a tap are unrolled) so
-        // the scheduler cannot hoist all 144 operand loads of the tile at once
-        // operands of the next k-group are read while the current four MFMAs run,
-        // including across the tap boundary
+        // k order: 16-channel block -> tap -> the block's two groups of 8 -> four
+        // channel pairs.  The ky loop stays rolled (kx and the groups are
+        // unrolled: 24 MFMAs per iteration) so the scheduler cannot hoist all
+        // operand loads of the tile at once; the operands of the next k-group
+        // are read while the current four MFMAs run, across tap and block
+        // boundaries.
+        constexpr int ICB = C / 16;
         float4 av = *aptr(0, 0), bv = *bptr(0, 0, 0);
-        auto run_taps = [&](int tap0, int tap1) {
+        auto run_blocks = [&](int icb0, int icb1) {
+            for (int icb = icb0; icb < icb1; icb++) {
+                const int g0 = 2 * icb;
+                const int gnext = icb + 1 < ICB ? g0 + 2 : g0;  // after the last block: a harmless re-read
 #pragma unroll 1
-            for (int tap = tap0; tap < tap1; tap++) {
-                const int ky = tap / 3, kx = tap - 3 * ky;
-                const int tn1 = tap + 1 < 9 ? tap + 1 : 8, nky = tn1 / 3, nkx = tn1 - 3 * nky;
-                const float4 *ap = aptr(tap, 0), *bp = bptr(0, ky, kx);
-                const float4 *nap = aptr(tn1, 0), *nbp = bptr(0, nky, nkx);
-                constexpr int ASTEP = 2 * 32;        // float4 between channel groups in Wsh
-                constexpr int BSTEP = PR * 2 * PCP;  // float4 between channel groups in the patch
+                for (int ky = 0; ky < 3; ky++) {
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    float4 an, bn;
-                    if (g + 1 < G) {
-                        an = ap[(g + 1) * ASTEP];
-                        bn = bp[(g + 1) * BSTEP];
-                    } else {
-                        an = *nap;  // next tap (re-reads tap 8 harmlessly after the last one)
-                        bn = *nbp;
+                    for (int kx = 0; kx < 3; kx++) {
+                        const int tap = ky * 3 + kx;
+#pragma unroll
+                        for (int gg = 0; gg < 2; gg++) {
+                            float4 an, bn;
+                            if (gg == 0) {
+                                an = *aptr(tap, g0 + 1);
+                                bn = *bptr(g0 + 1, ky, kx);
+                            } else if (kx < 2) {
+                                an = *aptr(tap + 1, g0);
+                                bn = *bptr(g0, ky, kx + 1);
+                            } else if (ky < 2) {
+                                an = *aptr(tap + 1, g0);
+                                bn = *bptr(g0, ky + 1, 0);
+                            } else {
+                                an = *aptr(0, gnext);
+                                bn = *bptr(gnext, 0, 0);
+                            }
+                            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
+                            av = an;
+                            bv = bn;
+                        }
                     }
-                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc, 0, 0, 0);
-                    av = an;
-                    bv = bn;
                 }
             }
         };
         if constexpr (C > LB) {
-            run_taps(0, 4);
+            run_blocks(0, ICB / 2);
             if (tn < total) load_tile(tn, std::integral_constant<int, 1>{});
-            run_taps(4, 9);
+            run_blocks(ICB / 2, ICB);
         } else {
-            run_taps(0, 9);
+            run_blocks(0, ICB);
         }
 
         // Epilogue.  Full 32-channel tiles use buffer stores with each accumulator

@@ -26,6 +26,8 @@ const char *last_error() { return g_err; }
 
 static int g_exact_silu = -1;  // -1: read ONNXSHARP_HIP_EXACT_SILU on first use
 static int g_gemm_variant = -3;  // -3: read ONNXSHARP_HIP_GEMM_VARIANT on first use
+static int g_conv16_variant = -3;  // -3: read ONNXSHARP_HIP_CONV16_VARIANT on first use
+static int g_tune = -1;             // -1: read ONNXSHARP_HIP_TUNE on first use
 
 bool exact_silu() {
     if (g_exact_silu < 0) {
@@ -41,6 +43,22 @@ int gemm_variant() {
         g_gemm_variant = e ? atoi(e) : -1;
     }
     return g_gemm_variant;
+}
+
+bool tuning_enabled() {
+    if (g_tune < 0) {
+        const char *e = getenv("ONNXSHARP_HIP_TUNE");
+        g_tune = (e && atoi(e) == 0) ? 0 : 1;
+    }
+    return g_tune == 1;
+}
+
+int conv16_variant() {
+    if (g_conv16_variant == -3) {
+        const char *e = getenv("ONNXSHARP_HIP_CONV16_VARIANT");
+        g_conv16_variant = e ? atoi(e) : -1;
+    }
+    return g_conv16_variant;
 }
 
 __global__ void fill_u8_kernel(uint8_t *__restrict__ p, uint8_t v, size_t n) {
@@ -63,6 +81,15 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         g_exact_silu = value != 0;
         return OSH_OK;
     }
+    if (strcmp(key, "tune") == 0) {
+        g_tune = value != 0;
+        return OSH_OK;
+    }
+    if (strcmp(key, "conv16_variant") == 0) {
+        if (value < -2 || value > 11) return fail(OSH_E_INVALID, "conv16_variant %d out of range [-2, 12)", value);
+        g_conv16_variant = value;
+        return OSH_OK;
+    }
     if (strcmp(key, "gemm_variant") == 0) {
         if (value < -2 || value >= gemm16_variant_count())
             return fail(OSH_E_INVALID, "gemm_variant %d out of range [-2, %d)", value, gemm16_variant_count());
@@ -80,6 +107,14 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     }
     if (strcmp(key, "gemm_variant") == 0) {
         *value = gemm_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "conv16_variant") == 0) {
+        *value = conv16_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "tune") == 0) {
+        *value = tuning_enabled() ? 1 : 0;
         return OSH_OK;
     }
     if (strcmp(key, "gemm_variants") == 0) {

@@ -108,3 +108,61 @@ def test_conv_silu_epilogue_on_bias_only_input(cuda, oracle):
         assert rel.max() < 2e-6
     finally:
         N.call("osh_config_set", b"exact_silu", old.value)
+
+
+@pytest.mark.parametrize("xs,ws,attrs", [
+    ((1, 3, 640, 640), (16, 3, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),  # the YOLO11n stem
+    ((1, 3, 37, 41), (8, 3, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ((2, 4, 20, 18), (32, 4, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ((1, 1, 9, 11), (8, 1, 3, 3), dict(auto_pad="SAME_UPPER", strides=[2, 2])),
+], ids=["stem_640", "c3_m8_s1", "c4_m32_s2_batch2", "c1_m8_same_upper"])
+def test_first_layer_conv_is_the_fma_chain(cuda, oracle, xs, ws, attrs):
+    # C <= 4 takes the direct first-layer kernel: per output channel the bias,
+    # then fmaf over ic -> ky -> kx, the im2col chain -- bit for bit.
+    from onnxsharp_amd import native as N
+    seed = sum(xs) + sum(ws)
+    x = synth.uniform(seed, xs)
+    w = synth.normal(seed + 1, ws, 0, 0.05)
+    b = synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    N.call("osh_config_set", b"exact_silu", 1)
+    try:
+        y, p = run_conv(cuda, x, w, b, "Silu", **attrs)
+    finally:
+        N.call("osh_config_set", b"exact_silu", 0)
+    ref = oracle_conv(oracle, x, w, b, p, "Silu", order=oracle.ORDER_IM2COL)
+    assert np.array_equal(y, ref), f"max |d| {np.abs(y - ref).max():.3e}"
+
+
+CONV16_CASES = [
+    ("c2_3x3s1_64to64_160", (1, 64, 160, 160), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ("c3b_3x3s2_128to256_80", (1, 128, 80, 80), (256, 128, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ("deep_256to64_20", (1, 256, 20, 20), (64, 256, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ("odd_16to40_s1_33x45", (1, 16, 33, 45), (40, 16, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ("odd_32to72_s2_41x37", (2, 32, 41, 37), (72, 32, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ("pads_0_2_valid_like", (1, 48, 17, 23), (24, 48, 3, 3), dict(pads=[0, 2, 2, 0])),
+]
+
+
+@pytest.mark.parametrize("name,xs,ws,attrs", CONV16_CASES, ids=[c[0] for c in CONV16_CASES])
+def test_conv16_is_the_nchwc_chain(cuda, oracle, name, xs, ws, attrs):
+    # 3x3 convolutions with C % 16 == 0 run the in-order 16x16x4 kernel: bit for
+    # bit the reference's NCHWc chain (bias, then icb -> ky -> kx -> lane16),
+    # whatever wave tile is forced.
+    from onnxsharp_amd import native as N
+    seed = sum(xs) * 3 + sum(ws)
+    x = synth.uniform(seed, xs)
+    w = synth.normal(seed + 1, ws, 0, 0.05)
+    b = synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    N.call("osh_config_set", b"exact_silu", 1)
+    try:
+        ref = None
+        for v in [-1] + list(range(12)):
+            print(f"conv16 {name} variant {v}", flush=True)
+            N.call("osh_config_set", b"conv16_variant", v)
+            y, p = run_conv(cuda, x, w, b, "Silu", **attrs)
+            if ref is None:
+                ref = oracle_conv(oracle, x, w, b, p, "Silu", order=oracle.ORDER_NCHWC)
+            assert np.array_equal(y, ref), f"variant {v}: max |d| {np.abs(y - ref).max():.3e}"
+    finally:
+        N.call("osh_config_set", b"exact_silu", 0)
+        N.call("osh_config_set", b"conv16_variant", -1)
