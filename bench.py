@@ -208,7 +208,7 @@ class YoloWorkload(Workload):
         self.fr.set_input(self.x_np)
         self.fr.run()
         self.fr.sync()
-        self.fr.capture()
+        self.fr.capture(parallel=os.environ.get("ONNXSHARP_HIP_FRAME_PARALLEL", "0") == "1")
         self.stream = self.fr.stream
         self.flops = self.model.flops
         # each tensor read or written once per op that touches it

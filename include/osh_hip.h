@@ -129,6 +129,10 @@ OSH_API osh_status osh_event_create(osh_event *e);
 OSH_API osh_status osh_event_destroy(osh_event e);
 OSH_API osh_status osh_event_record(osh_event e, osh_stream s);
 OSH_API osh_status osh_event_elapsed_ms(osh_event start, osh_event stop, float *ms);
+/* Make stream s wait for the work recorded in event e before its later work
+ * (fork/join between the streams of one segment; captured into a graph as a
+ * dependency edge). */
+OSH_API osh_status osh_stream_wait_event(osh_stream s, osh_event e);
 
 /* ------------------------------------------------------------ Conv (A1-A8) */
 
@@ -295,6 +299,19 @@ OSH_API osh_status osh_graph_begin(osh_stream s);
 OSH_API osh_status osh_graph_end(osh_stream s, osh_graph *g);
 OSH_API osh_status osh_graph_launch(osh_graph g, osh_stream s);
 OSH_API osh_status osh_graph_destroy(osh_graph g);
+
+/* Building a graph whose nodes run concurrently where the segment's data
+ * allows: each op is captured on its own (osh_graph_begin on a stream, the op's
+ * launches, then osh_graph_add_captured), becomes one child-graph node, and
+ * depends on the nodes listed in deps.  osh_graph_instantiate turns the
+ * builder into a launchable osh_graph; the builder is destroyed separately. */
+typedef void *osh_graph_builder; /* hipGraph_t */
+typedef void *osh_graph_node;    /* hipGraphNode_t */
+OSH_API osh_status osh_graph_builder_create(osh_graph_builder *b);
+OSH_API osh_status osh_graph_add_captured(osh_graph_builder b, osh_stream s, const osh_graph_node *deps, int ndeps,
+                                          osh_graph_node *node);
+OSH_API osh_status osh_graph_instantiate(osh_graph_builder b, osh_graph *g);
+OSH_API osh_status osh_graph_builder_destroy(osh_graph_builder b);
 
 #ifdef __cplusplus
 }

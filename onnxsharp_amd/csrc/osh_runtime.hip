@@ -259,6 +259,12 @@ OSH_API osh_status osh_event_elapsed_ms(osh_event start, osh_event stop, float *
     return OSH_OK;
 }
 
+OSH_API osh_status osh_stream_wait_event(osh_stream s, osh_event e) {
+    if (!e) return fail(OSH_E_INVALID, "e is NULL");
+    OSH_HIP_CHECK(hipStreamWaitEvent(to_stream(s), reinterpret_cast<hipEvent_t>(e), 0));
+    return OSH_OK;
+}
+
 OSH_API osh_status osh_graph_begin(osh_stream s) {
     if (!s) return fail(OSH_E_INVALID, "graph capture needs a stream from osh_stream_create");
     OSH_HIP_CHECK(hipStreamBeginCapture(to_stream(s), hipStreamCaptureModeThreadLocal));
@@ -286,6 +292,43 @@ OSH_API osh_status osh_graph_launch(osh_graph g, osh_stream s) {
 
 OSH_API osh_status osh_graph_destroy(osh_graph g) {
     if (g) OSH_HIP_CHECK(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(g)));
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_graph_builder_create(osh_graph_builder *b) {
+    if (!b) return fail(OSH_E_INVALID, "NULL argument");
+    hipGraph_t g = nullptr;
+    OSH_HIP_CHECK(hipGraphCreate(&g, 0));
+    *b = g;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_graph_add_captured(osh_graph_builder b, osh_stream s, const osh_graph_node *deps, int ndeps,
+                                          osh_graph_node *node) {
+    if (!b || !s || !node || ndeps < 0 || (ndeps > 0 && !deps)) return fail(OSH_E_INVALID, "bad argument");
+    *node = nullptr;
+    hipGraph_t child = nullptr;
+    OSH_HIP_CHECK(hipStreamEndCapture(to_stream(s), &child));
+    hipGraphNode_t n = nullptr;
+    hipError_t e = hipGraphAddChildGraphNode(&n, reinterpret_cast<hipGraph_t>(b),
+                                             reinterpret_cast<const hipGraphNode_t *>(deps), (size_t)ndeps, child);
+    (void)hipGraphDestroy(child);  // the node holds its own copy
+    if (e != hipSuccess) return fail(OSH_E_DEVICE, "hipGraphAddChildGraphNode failed: %s", hipGetErrorString(e));
+    *node = n;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_graph_instantiate(osh_graph_builder b, osh_graph *g) {
+    if (!b || !g) return fail(OSH_E_INVALID, "NULL argument");
+    *g = nullptr;
+    hipGraphExec_t exec = nullptr;
+    OSH_HIP_CHECK(hipGraphInstantiate(&exec, reinterpret_cast<hipGraph_t>(b), nullptr, nullptr, 0));
+    *g = exec;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_graph_builder_destroy(osh_graph_builder b) {
+    if (b) OSH_HIP_CHECK(hipGraphDestroy(reinterpret_cast<hipGraph_t>(b)));
     return OSH_OK;
 }
 

@@ -83,6 +83,7 @@ _SIGS = {
     "osh_event_destroy": ([_vp], _i),
     "osh_event_record": ([_vp, _vp], _i),
     "osh_event_elapsed_ms": ([_vp, _vp, C.POINTER(C.c_float)], _i),
+    "osh_stream_wait_event": ([_vp, _vp], _i),
     "osh_conv_infer_shape": ([C.POINTER(ConvAttrs), _i64p, _i64p, _i64p], _i),
     "osh_conv_resolve": ([C.POINTER(ConvAttrs), _i64p, _i64p, C.POINTER(ConvParams)], _i),
     "osh_conv_packed_weight_bytes": ([C.POINTER(ConvParams), C.POINTER(_sz)], _i),
@@ -106,6 +107,10 @@ _SIGS = {
     "osh_graph_end": ([_vp, C.POINTER(_vp)], _i),
     "osh_graph_launch": ([_vp, _vp], _i),
     "osh_graph_destroy": ([_vp], _i),
+    "osh_graph_builder_create": ([C.POINTER(_vp)], _i),
+    "osh_graph_add_captured": ([_vp, _vp, C.POINTER(_vp), _i, C.POINTER(_vp)], _i),
+    "osh_graph_instantiate": ([_vp, C.POINTER(_vp)], _i),
+    "osh_graph_builder_destroy": ([_vp], _i),
 }
 
 # Every symbol include/osh_hip.h declares (checked by the CPU test suite).

@@ -326,19 +326,103 @@ def build(size: int = 640, seed: int = 7000) -> Model:
     return m
 
 
+# ------------------------------------------------------------ stream planning
+
+def op_access(op):
+    """(reads, writes) of an op as lists of channel slices."""
+    if isinstance(op, AddOp):
+        return [op.a, op.b], [op.y]
+    if isinstance(op, AttentionOp):
+        return [op.qkv], [op.y, whole(op.qt), whole(op.attn), whole(op.attn_t)]
+    return [op.x], [op.y]
+
+
+def _overlap(a: Slice, b: Slice) -> bool:
+    return a.buf is b.buf and a.c0 < b.c0 + b.c and b.c0 < a.c0 + a.c
+
+
+def plan_streams(ops, nstreams=4):
+    """Spread the op list over `nstreams` streams along its data dependencies.
+
+    An op depends on every earlier op it reads after (RAW), writes after (WAW)
+    or overwrites the input of (WAR).  It continues the stream whose last op
+    is its latest dependency; an op that starts a new branch takes the least
+    recently used stream.  Returns (stream per op, waits per op: indices of
+    earlier ops on other streams to wait for, ops whose completion some other
+    stream waits for)."""
+    acc = [op_access(o) for o in ops]
+    deps = []
+    for i, (ri, wi) in enumerate(acc):
+        d = []
+        for j in range(i):
+            rj, wj = acc[j]
+            if (any(_overlap(a, b) for a in wj for b in ri + wi) or any(_overlap(a, b) for a in rj for b in wi)):
+                d.append(j)
+        deps.append(d)
+    stream_of, waits = [], []
+    last = [-1] * nstreams
+    seen = [[-1] * nstreams for _ in range(nstreams)]  # seen[s][t]: latest op of t that s has waited for
+    recorded = set()
+    for i, d in enumerate(deps):
+        d = list(d)
+        cands = [stream_of[j] for j in d if last[stream_of[j]] == j]
+        if cands:
+            s = max(cands, key=lambda t: last[t])
+        else:
+            s = min(range(nstreams), key=lambda t: last[t])
+        w = []
+        for j in sorted(d, reverse=True):
+            t = stream_of[j]
+            if t != s and seen[s][t] < j:
+                w.append(j)
+                seen[s][t] = j
+                recorded.add(j)
+        stream_of.append(s)
+        waits.append(sorted(w))
+        last[s] = i
+    return stream_of, waits, recorded
+
+
+def op_dependencies(ops):
+    """For each op, the earlier ops it must follow (RAW, WAW and WAR on channel slices)."""
+    acc = [op_access(o) for o in ops]
+    out = []
+    for i, (ri, wi) in enumerate(acc):
+        d = []
+        for j in range(i):
+            rj, wj = acc[j]
+            if (any(_overlap(a, b) for a in wj for b in ri + wi) or any(_overlap(a, b) for a in rj for b in wi)):
+                d.append(j)
+        out.append(d)
+    return out
+
+
 # --------------------------------------------------------------- device side
 
 class Frame:
-    """Device buffers, packed weights and the launch list of one model."""
+    """Device buffers, packed weights and the launch list of one model, spread
+    over `nstreams` streams (fork/join through events) so that independent
+    branches -- the detection head's six chains, the P3 head beside the rest
+    of the neck -- run side by side."""
 
-    def __init__(self, model: Model, device):
+    def __init__(self, model: Model, device, nstreams: int = 4):
         import torch
         self.model = model
         self.device = device
         for b in model.bufs:
             b.tensor = torch.empty((1, b.c, b.h, b.w), dtype=torch.float32, device=device)
-        self.stream = C.c_void_p()
-        N.call("osh_stream_create", C.byref(self.stream))
+        self.streams = []
+        for _ in range(max(1, nstreams)):
+            st = C.c_void_p()
+            N.call("osh_stream_create", C.byref(st))
+            self.streams.append(st)
+        self.stream = self.streams[0]  # the frame's stream: joins every branch
+        self.plan, self.waits, rec = plan_streams(model.ops, len(self.streams))
+        self.events = {}
+        for i in sorted(rec) + ["fork"] + ["join%d" % k for k in range(1, len(self.streams))]:
+            ev = C.c_void_p()
+            N.call("osh_event_create", C.byref(ev))
+            self.events[i] = ev
         self.graph = None
         self._calls = []
         self._keep = []
@@ -370,21 +454,21 @@ class Frame:
                    self.stream)
             self._keep += [p, w, b, packed]
             act = N.ACTIVATIONS[op.act]
-            return lambda: N.check(lib.osh_conv2d_f32(C.byref(p), op.x.ptr(), C.c_void_p(packed.data_ptr()),
-                                                      C.c_void_p(b.data_ptr()), act, op.y.ptr(), self.stream))
+            return lambda st: N.check(lib.osh_conv2d_f32(C.byref(p), op.x.ptr(), C.c_void_p(packed.data_ptr()),
+                                                         C.c_void_p(b.data_ptr()), act, op.y.ptr(), st))
         if isinstance(op, AddOp):
             n = op.y.c * op.y.h * op.y.w
-            return lambda: N.check(lib.osh_add_f32(n, op.a.ptr(), op.b.ptr(), op.y.ptr(), self.stream))
+            return lambda st: N.check(lib.osh_add_f32(n, op.a.ptr(), op.b.ptr(), op.y.ptr(), st))
         if isinstance(op, CopyOp):
             nb = 4 * op.y.c * op.y.h * op.y.w
-            return lambda: N.check(lib.osh_memcpy_d2d(op.y.ptr(), op.x.ptr(), nb, self.stream))
+            return lambda st: N.check(lib.osh_memcpy_d2d(op.y.ptr(), op.x.ptr(), nb, st))
         if isinstance(op, MaxPoolOp):
             pp = N.PoolParams(1, op.x.c, op.x.h, op.x.w, op.k, op.k, op.s, op.s, op.p, op.p, op.y.h, op.y.w)
             self._keep.append(pp)
-            return lambda: N.check(lib.osh_maxpool2d_f32(C.byref(pp), op.x.ptr(), op.y.ptr(), self.stream))
+            return lambda st: N.check(lib.osh_maxpool2d_f32(C.byref(pp), op.x.ptr(), op.y.ptr(), st))
         if isinstance(op, UpsampleOp):
-            return lambda: N.check(lib.osh_resize_nearest_f32(1, op.x.c, op.x.h, op.x.w, op.f, op.f, op.x.ptr(),
-                                                              op.y.ptr(), op.y.c * op.y.h * op.y.w, self.stream))
+            return lambda st: N.check(lib.osh_resize_nearest_f32(1, op.x.c, op.x.h, op.x.w, op.f, op.f, op.x.ptr(),
+                                                                 op.y.ptr(), op.y.c * op.y.h * op.y.w, st))
         if isinstance(op, AttentionOp):
             return self._prepare_attention(op)
         raise TypeError(op)
@@ -401,35 +485,103 @@ class Frame:
         qt, sc, st = (C.c_void_p(b.tensor.data_ptr()) for b in (op.qt, op.attn, op.attn_t))
         y = op.y.ptr()
 
-        def run():
+        def run(stream):
             # q^T per head: [kd, N] -> [N, kd]
-            N.check(lib.osh_transpose_f32(op.heads, op.key_dim, n, q, hs, qt, n * op.key_dim, self.stream))
+            N.check(lib.osh_transpose_f32(op.heads, op.key_dim, n, q, hs, qt, n * op.key_dim, stream))
             # scores[h] = q^T k: [N, kd] x [kd, N]
             N.check(lib.osh_gemm_f32_batched(op.heads, n, n, op.key_dim, qt, op.key_dim, n * op.key_dim, k, n, hs,
-                                             None, N.ACT_NONE, sc, n, n * n, self.stream))
-            N.check(lib.osh_softmax_f32(op.heads * n, n, C.c_float(op.scale), sc, st, self.stream))
+                                             None, N.ACT_NONE, sc, n, n * n, stream))
+            N.check(lib.osh_softmax_f32(op.heads * n, n, C.c_float(op.scale), sc, st, stream))
             # probabilities transposed back into the scores buffer
-            N.check(lib.osh_transpose_f32(op.heads, n, n, st, n * n, sc, n * n, self.stream))
+            N.check(lib.osh_transpose_f32(op.heads, n, n, st, n * n, sc, n * n, stream))
             # y[h] = v attn^T: [hd, N] x [N, N]
             N.check(lib.osh_gemm_f32_batched(op.heads, op.head_dim, n, n, v, n, hs, sc, n, n * n, None, N.ACT_NONE,
-                                             y, n, op.head_dim * n, self.stream))
+                                             y, n, op.head_dim * n, stream))
         return run
 
-    def run(self):
-        """Issue every op of one frame on the frame's stream (no sync)."""
-        for c in self._calls:
-            c()
+    def run_op(self, i):
+        """Issue op i on its planned stream, after the events it waits for."""
+        st = self.streams[self.plan[i]]
+        for j in self.waits[i]:
+            N.call("osh_stream_wait_event", st, self.events[j])
+        self._calls[i](st)
+        if i in self.events:
+            N.call("osh_event_record", self.events[i], st)
 
-    def capture(self):
-        """Record one frame as a HIP graph (replayed by `launch`)."""
-        if self.graph is None:
+    def run(self):
+        """Issue every op of one frame (no sync); every branch joins the
+        frame's stream at the end."""
+        # the side streams start after the frame stream's earlier work (the input)
+        start = self.events["fork"] if len(self.streams) > 1 else None
+        if start is not None:
+            N.call("osh_event_record", start, self.stream)
+            for st in self.streams[1:]:
+                N.call("osh_stream_wait_event", st, start)
+        for i in range(len(self._calls)):
+            self.run_op(i)
+        for k, st in enumerate(self.streams[1:], start=1):
+            ev = self.events["join%d" % k]
+            N.call("osh_event_record", ev, st)
+            N.call("osh_stream_wait_event", self.stream, ev)
+
+    def segments(self):
+        """Runs of ops of one planned stream between cross-stream waits:
+        [(first op index, op indices, dependency segment indices)]."""
+        segs, open_seg, seg_of = [], {}, {}
+        for i, st in enumerate(self.plan):
+            k = open_seg.get(st)
+            if k is None or self.waits[i]:
+                deps = set()
+                if k is not None:
+                    deps.add(k)
+                deps.update(seg_of[j] for j in self.waits[i])
+                k = len(segs)
+                segs.append((i, [], sorted(deps)))
+                open_seg[st] = k
+            segs[k][1].append(i)
+            seg_of[i] = k
+        return segs
+
+    def capture(self, parallel=False):
+        """Record one frame as a HIP graph (replayed by `launch`).
+
+        parallel=False: the ops in program order on the frame's stream (one
+        chain of kernels).  parallel=True: each stream segment of the plan is
+        captured alone and becomes one child-graph node that depends on the
+        segments it waits for, so independent branches may overlap at replay.
+        On one MI355X the chain replays faster (0.66 vs 1.3 ms per 640 x 640
+        frame with per-op nodes), so it is the default."""
+        if self.graph is not None:
+            return self.graph
+        if not parallel:
             g = C.c_void_p()
             N.call("osh_graph_begin", self.stream)
             try:
-                self.run()
+                for c in self._calls:
+                    c(self.stream)
             finally:
                 N.call("osh_graph_end", self.stream, C.byref(g))
             self.graph = g
+            return g
+        b = C.c_void_p()
+        N.call("osh_graph_builder_create", C.byref(b))
+        try:
+            nodes = []
+            for first, ops, deps in self.segments():
+                arr = (C.c_void_p * max(1, len(deps)))(*[nodes[k] for k in deps])
+                node = C.c_void_p()
+                N.call("osh_graph_begin", self.stream)
+                try:
+                    for i in ops:
+                        self._calls[i](self.stream)
+                finally:
+                    N.call("osh_graph_add_captured", b, self.stream, arr, len(deps), C.byref(node))
+                nodes.append(node.value)
+            g = C.c_void_p()
+            N.call("osh_graph_instantiate", b, C.byref(g))
+            self.graph = g
+        finally:
+            N.call("osh_graph_builder_destroy", b)
         return self.graph
 
     def launch(self):
@@ -456,6 +608,10 @@ class Frame:
         if self.graph is not None:
             N.call("osh_graph_destroy", self.graph)
             self.graph = None
-        if self.stream:
-            N.call("osh_stream_destroy", self.stream)
-            self.stream = C.c_void_p()
+        for ev in self.events.values():
+            N.call("osh_event_destroy", ev)
+        self.events = {}
+        for st in self.streams:
+            N.call("osh_stream_destroy", st)
+        self.streams = []
+        self.stream = C.c_void_p()

@@ -52,7 +52,7 @@ def test_yolo_per_op_parity(cuda, oracle, exact_silu):
         worst = (0.0, "")
         for i, op in enumerate(model.ops):
             ins = [_host(s) for s in YO.op_inputs(op)]
-            fr._calls[i]()
+            fr._calls[i](fr.stream)
             fr.sync()
             got = _host(op.y)
             ref = YO.run_op(oracle, op, ins)
@@ -93,7 +93,8 @@ def test_yolo_end_to_end(cuda, oracle, exact_silu):
         fr.close()
 
 
-def test_yolo_graph_replay_matches_eager(cuda):
+@pytest.mark.parametrize("parallel", [False, True], ids=["chain", "segments"])
+def test_yolo_graph_replay_matches_eager(cuda, parallel):
     import torch
     from onnxsharp_amd import native as N
     model, fr = _frame(cuda, 128)
@@ -104,8 +105,11 @@ def test_yolo_graph_replay_matches_eager(cuda):
         fr.run()
         fr.sync()
         eager = [t.cpu().numpy().copy() for t in fr.outputs()]
-        fr.capture()
+        print(f"capturing {len(model.ops)} ops (parallel={parallel})", flush=True)
+        fr.capture(parallel=parallel)
+        print("captured", flush=True)
         for rep in range(3):
+            print(f"replay {rep}", flush=True)
             for t in fr.outputs():
                 t.fill_(float("nan"))  # the replay must rewrite every output
             torch.cuda.synchronize()

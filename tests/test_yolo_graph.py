@@ -74,3 +74,34 @@ def test_outputs_and_flops(model):
     conv = sum(op.flops for op in model.convs)
     assert abs(conv / 1e9 - 6.48) < 0.01, conv / 1e9
     assert model.flops - conv == 2 * 2 * 400 ** 2 * (32 + 64)
+
+
+@pytest.mark.parametrize("nstreams", [1, 2, 4])
+def test_stream_plan_orders_every_dependency(model, nstreams):
+    # Vector clocks over the planned streams: for each op, the latest op of
+    # each stream known complete when it starts (stream order plus the event
+    # waits).  Every read-after-write, write-after-write and write-after-read
+    # pair of ops must be ordered.
+    from onnxsharp_amd import yolo11n as Y
+    plan, waits, recorded = Y.plan_streams(model.ops, nstreams)
+    acc = [Y.op_access(o) for o in model.ops]
+    clock = [[-1] * nstreams for _ in range(nstreams)]  # per stream: clock before its next op
+    after = []
+    for i, s in enumerate(plan):
+        c = clock[s]
+        for j in waits[i]:
+            assert j in recorded and plan[j] != s
+            c = [max(a, b) for a, b in zip(c, after[j])]
+        ri, wi = acc[i]
+        for j in range(i):
+            rj, wj = acc[j]
+            dep = (any(Y._overlap(a, b) for a in wj for b in ri + wi) or
+                   any(Y._overlap(a, b) for a in rj for b in wi))
+            if dep:
+                assert plan[j] == s or c[plan[j]] >= j, f"op {i} {model.ops[i].name} not ordered after op {j}"
+        c = list(c)
+        c[s] = i
+        clock[s] = c
+        after.append(c)
+    if nstreams > 1:
+        assert len(set(plan)) > 1  # the head and the P3 branch do fork
