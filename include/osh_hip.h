@@ -209,6 +209,19 @@ OSH_API osh_status osh_gemm_f32_batched(int batch, int m, int n, int k, const fl
 OSH_API osh_status osh_matmul_infer_shape(const int64_t *a_dims, int ra, const int64_t *b_dims, int rb,
                                           int64_t *y_dims, int *ry);
 
+/* ONNX Gemm (GemmLayer, src/OnnxSharp/Ops/AttnOps.cs:31-135):
+ *   Y[m,n] = alpha * (A' B') + beta * C,   A' = transA ? A^T : A, B' = transB ? B^T : B
+ * with A stored [m,k] ([k,m] if trans_a), B [k,n] ([n,k] if trans_b), dense rows.
+ * As in the reference: the transposes are materialized (into d_workspace,
+ * osh_gemm_ex_workspace_bytes), the product is the FMA chain from 0, then
+ * each element takes alpha * y (if alpha != 1) and + beta * c (if beta != 0 and
+ * C is given), each rounded on its own.  C has c_len elements: m*n (full),
+ * 1 (scalar) or any other length, indexed by column j % c_len. */
+OSH_API osh_status osh_gemm_ex_workspace_bytes(int trans_a, int trans_b, int m, int n, int k, size_t *bytes);
+OSH_API osh_status osh_gemm_ex_f32(int trans_a, int trans_b, int m, int n, int k, float alpha, const float *d_a,
+                                   const float *d_b, float beta, const float *d_c, int64_t c_len, float *d_y,
+                                   void *d_workspace, osh_stream s);
+
 /* ------------------------------------------- DynamicQuantizeMatMul (A13-A15) */
 
 /* Bytes of the packed int8 weight buffer and of the scratch buffer that

@@ -149,9 +149,72 @@ osh_status launch_igemm(const IgemmArgs &a, int zcount, int bmode, int act, hipS
     return OSH_OK;
 }
 
+// y = alpha * y (alpha != 1), then y += beta * c (beta != 0 and C given): the
+// reference's two separately rounded steps (AttnOps.cs:111-131), no contraction.
+__global__ __launch_bounds__(256) void gemm_ex_epilogue_kernel(float *__restrict__ y, int m, int n, float alpha,
+                                                               int scale, float beta, const float *__restrict__ c,
+                                                               long long c_len) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)m * n;
+    if (idx >= total) return;
+    const int j = (int)(idx % n);
+    float v = y[idx];
+    if (scale) v = alpha * v;
+    if (c) {
+        const float cv = c_len >= total ? c[idx] : (c_len == 1 ? c[0] : c[j % c_len]);
+        v = v + beta * cv;
+    }
+    y[idx] = v;
+}
+
 }  // namespace osh
 
 extern "C" {
+
+OSH_API osh_status osh_gemm_ex_workspace_bytes(int trans_a, int trans_b, int m, int n, int k, size_t *bytes) {
+    if (!bytes || m < 0 || n < 0 || k < 0) return fail(OSH_E_INVALID, "Gemm: bad argument");
+    size_t b = 0;
+    if (trans_a) b += ((size_t)m * k * sizeof(float) + 255) & ~(size_t)255;
+    if (trans_b) b += (size_t)k * n * sizeof(float);
+    *bytes = b;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_gemm_ex_f32(int trans_a, int trans_b, int m, int n, int k, float alpha, const float *d_a,
+                                   const float *d_b, float beta, const float *d_c, int64_t c_len, float *d_y,
+                                   void *d_workspace, osh_stream s) {
+    if (m < 0 || n < 0 || k < 0) return fail(OSH_E_INVALID, "Gemm: negative size");
+    if (m == 0 || n == 0) return OSH_OK;
+    if (!d_a || !d_b || !d_y) return fail(OSH_E_INVALID, "Gemm: A, B and Y must be non-NULL");
+    if ((trans_a || trans_b) && !d_workspace) return fail(OSH_E_INVALID, "Gemm: transposes need the workspace");
+    if (d_c && c_len <= 0) return fail(OSH_E_INVALID, "Gemm: C given with %lld elements", (long long)c_len);
+    hipStream_t st = to_stream(s);
+    const float *a = d_a, *b = d_b;
+    char *ws = static_cast<char *>(d_workspace);
+    if (trans_a) {  // A is [k, m]
+        float *t = reinterpret_cast<float *>(ws);
+        osh_status r = osh_transpose_f32(1, k, m, d_a, 0, t, 0, s);
+        if (r != OSH_OK) return r;
+        a = t;
+        ws += ((size_t)m * k * sizeof(float) + 255) & ~(size_t)255;
+    }
+    if (trans_b) {  // B is [n, k]
+        float *t = reinterpret_cast<float *>(ws);
+        osh_status r = osh_transpose_f32(1, n, k, d_b, 0, t, 0, s);
+        if (r != OSH_OK) return r;
+        b = t;
+    }
+    osh_status r = osh_gemm_f32(m, n, k, a, k, b, n, nullptr, nullptr, nullptr, OSH_ACT_NONE, d_y, n, s);
+    if (r != OSH_OK) return r;
+    const bool scale = alpha != 1.0f;
+    const bool bias = beta != 0.0f && d_c && c_len > 0;
+    if (!scale && !bias) return OSH_OK;
+    const long long total = (long long)m * n;
+    hipLaunchKernelGGL(gemm_ex_epilogue_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, d_y, m, n,
+                       alpha, scale ? 1 : 0, beta, bias ? d_c : nullptr, (long long)c_len);
+    OSH_LAUNCH_CHECK("gemm_ex_epilogue_kernel");
+    return OSH_OK;
+}
 
 OSH_API osh_status osh_gemm_f32_batched(int batch, int m, int n, int k, const float *d_a, int lda,
                                         int64_t stride_a, const float *d_b, int ldb, int64_t stride_b,

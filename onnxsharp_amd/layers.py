@@ -5,6 +5,7 @@ relative to the OnnxSharp source tree):
 
   ConvLayer                    src/OnnxSharp/Ops/DnnOps.cs:101-501
   MatMulLayer (+ FusedBias)    src/OnnxSharp/Ops/DnnOps.cs:2789-3103
+  GemmLayer                    src/OnnxSharp/Ops/AttnOps.cs:31-135
   DynamicQuantizeMatMulLayer   src/OnnxSharp/Ops/QuantizedMatMulOps.cs:28-376
   DynamicQuantizeLinearLayer   src/OnnxSharp/Ops/QuantOps.cs:166-227
 
@@ -171,6 +172,53 @@ class MatMulLayer:
         batch = max(ab.shape[0], bb.shape[0])
         N.call("osh_gemm_f32_batched", batch, m, n, k, _ptr(ab), k, sa, _ptr(bb), n, sb, _ptr(bias), N.ACT_NONE,
                _ptr(out), n, m * n, stream)
+        return out
+
+
+class GemmLayer:
+    """ONNX Gemm: Y = alpha * A' B' + beta * C on 2-D A and B."""
+
+    def __init__(self, alpha: float = 1.0, beta: float = 1.0, transA: int = 0, transB: int = 0,
+                 name: str = "gemm"):
+        self.alpha = float(alpha)
+        self.beta = float(beta)
+        self.trans_a = bool(transA)
+        self.trans_b = bool(transB)
+        self.name = name
+
+    def resolve(self, a_shape: Sequence[int], b_shape: Sequence[int]):
+        """(m, k, n) as GemmLayer.Resolve (AttnOps.cs:48-66)."""
+        if len(a_shape) != 2 or len(b_shape) != 2:
+            raise N.OshError(N.OSH_E_INVALID, f"Gemm '{self.name}': only 2-D A/B are supported")
+        m = a_shape[1] if self.trans_a else a_shape[0]
+        k = a_shape[0] if self.trans_a else a_shape[1]
+        n = b_shape[0] if self.trans_b else b_shape[1]
+        bk = b_shape[1] if self.trans_b else b_shape[0]
+        if bk != k:
+            raise N.OshError(N.OSH_E_INVALID, f"Gemm '{self.name}': K mismatch ({list(a_shape)} / {list(b_shape)})")
+        return m, k, n
+
+    def get_memory_shapes(self, a_shape: Sequence[int], b_shape: Sequence[int]) -> tuple:
+        m, _, n = self.resolve(a_shape, b_shape)
+        return (m, n)
+
+    def forward(self, a: torch.Tensor, b: torch.Tensor, c: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        a = _need_f32("A", a)
+        b = _need_f32("B", b)
+        m, k, n = self.resolve(tuple(a.shape), tuple(b.shape))
+        if c is not None:
+            c = _need_f32("C", c)
+            if c.numel() == 0:
+                c = None
+        if out is None:
+            out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+        nbytes = C.c_size_t()
+        N.call("osh_gemm_ex_workspace_bytes", int(self.trans_a), int(self.trans_b), m, n, k, C.byref(nbytes))
+        ws = torch.empty(max(1, nbytes.value // 4), dtype=torch.float32, device=a.device) if nbytes.value else None
+        N.call("osh_gemm_ex_f32", int(self.trans_a), int(self.trans_b), m, n, k, C.c_float(self.alpha), _ptr(a),
+               _ptr(b), C.c_float(self.beta), _ptr(c), 0 if c is None else c.numel(), _ptr(out), _ptr(ws),
+               C.c_void_p(_stream()))
         return out
 
 

@@ -92,6 +92,8 @@ _SIGS = {
     "osh_gemm_f32": ([_i, _i, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _vp], _i),
     "osh_gemm_f32_batched": ([_i, _i, _i, _i, _vp, _i, _i64, _vp, _i, _i64, _vp, _i, _vp, _i, _i64, _vp], _i),
     "osh_matmul_infer_shape": ([_i64p, _i, _i64p, _i, _i64p, C.POINTER(C.c_int)], _i),
+    "osh_gemm_ex_workspace_bytes": ([_i, _i, _i, _i, _i, C.POINTER(_sz)], _i),
+    "osh_gemm_ex_f32": ([_i, _i, _i, _i, _i, C.c_float, _vp, _vp, C.c_float, _vp, _i64, _vp, _vp, _vp], _i),
     "osh_dqmm_packed_weight_bytes": ([_i, _i, C.POINTER(_sz)], _i),
     "osh_dqmm_scratch_bytes": ([_i, _i, C.POINTER(_sz)], _i),
     "osh_dqmm_pack_weights": ([_i, _i, _vp, _i, _vp, _i, _vp, _vp], _i),

@@ -94,6 +94,28 @@ def gemm_f32(a, b, row_bias=None, col_bias=None, col_scale=None, fused=True):
     return c
 
 
+def gemm_ex(a, b, c=None, alpha=1.0, beta=1.0, trans_a=False, trans_b=False):
+    """ONNX Gemm as GemmLayer.Forward (AttnOps.cs:82-131): materialized transposes,
+    the FMA chain from 0, then alpha * y and + beta * c, each rounded in float."""
+    a = _c32(a).T.copy() if trans_a else _c32(a)
+    b = _c32(b).T.copy() if trans_b else _c32(b)
+    y = gemm_f32(a, b)
+    alpha, beta = np.float32(alpha), np.float32(beta)
+    if alpha != 1:
+        y = (alpha * y).astype(np.float32)
+    if beta != 0 and c is not None and np.size(c) > 0:
+        c = _c32(c).ravel()
+        m, n = y.shape
+        if c.size >= m * n:
+            cv = c[:m * n].reshape(m, n)
+        elif c.size == 1:
+            cv = np.full((m, n), c[0], np.float32)
+        else:
+            cv = np.broadcast_to(c[np.arange(n) % c.size], (m, n))
+        y = (y + (beta * cv).astype(np.float32)).astype(np.float32)
+    return y
+
+
 def gemm_f64(a, b, col_bias=None, row_bias=None):
     """Double-precision naive product (GemmKernelTests' naive loop)."""
     a, b = _c32(a), _c32(b)

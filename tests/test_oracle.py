@@ -297,3 +297,29 @@ def test_maxpool_matches_brute_force(oracle):
 def test_resize_nearest_is_repeat(oracle):
     x = np.random.default_rng(7).standard_normal((1, 4, 5, 3)).astype(np.float32)
     assert np.array_equal(oracle.resize_nearest(x, 2), x.repeat(2, axis=2).repeat(2, axis=3))
+
+
+def test_gemm_ex_against_float64(oracle):
+    # ONNX Gemm restated: transposes, chain from 0, alpha * y + beta * c -- checked
+    # against a float64 evaluation of the definition for every transpose pair
+    rng = np.random.default_rng(9)
+    m, k, n = 13, 29, 7
+    for ta in (False, True):
+        for tb in (False, True):
+            a = rng.uniform(-1, 1, (k, m) if ta else (m, k)).astype(np.float32)
+            b = rng.uniform(-1, 1, (n, k) if tb else (k, n)).astype(np.float32)
+            c = rng.uniform(-1, 1, (n,)).astype(np.float32)
+            y = oracle.gemm_ex(a, b, c, 0.5, 2.0, ta, tb)
+            a64 = a.T.astype(np.float64) if ta else a.astype(np.float64)
+            b64 = b.T.astype(np.float64) if tb else b.astype(np.float64)
+            ref = 0.5 * (a64 @ b64) + 2.0 * c[None, :]
+            assert np.abs(y - ref).max() < 1e-5, (ta, tb)
+    # C indexing: full, scalar, and the reference's j % len for other lengths
+    a = rng.uniform(-1, 1, (4, 3)).astype(np.float32)
+    b = rng.uniform(-1, 1, (3, 6)).astype(np.float32)
+    base = oracle.gemm_ex(a, b)
+    cs = np.arange(4, dtype=np.float32)
+    y = oracle.gemm_ex(a, b, cs, 1.0, 1.0)
+    assert np.array_equal(y, (base + cs[np.arange(6) % 4][None, :]).astype(np.float32))
+    y = oracle.gemm_ex(a, b, np.float32([3.0]), 1.0, 1.0)
+    assert np.array_equal(y, base + np.float32(3.0))
