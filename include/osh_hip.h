@@ -251,6 +251,15 @@ OSH_API osh_status osh_dqmm_u8s8(int m, int k, int n, const float *d_a, const vo
 
 /* DynamicQuantizeLinear (src/OnnxSharp/Ops/QuantOps.cs:166-227) on the device:
  * q (u8, n values), scale and zero point into d_qparams {scale bits, zp}. */
+/* MatMulInteger (MatMulIntegerLayer, src/OnnxSharp/Ops/QuantOps.cs:235-428):
+ *   C[i,j] = sum_k (a[i,k] - a_zp) * (w[k,j] - w_zp[j])   exactly, int32
+ * A is u8 (a_signed = 0) or s8 [m,k] (s8 read as signed values, as the
+ * reference's widening path does, Int8F32Gemm.cs:109-125; its VNNI path reads
+ * the same bytes as u8); W packed by osh_dqmm_pack_weights (u8/s8, per-column
+ * zero points); d_scratch has osh_dqmm_scratch_bytes(m, k). */
+OSH_API osh_status osh_matmul_integer(int m, int k, int n, const void *d_a, int a_signed, int a_zp,
+                                      const void *d_wpacked, int32_t *d_c, void *d_scratch, osh_stream s);
+
 OSH_API osh_status osh_dynamic_quantize_linear(int64_t n, const float *d_x, uint8_t *d_q, int32_t *d_qparams,
                                                void *d_scratch, osh_stream s);
 

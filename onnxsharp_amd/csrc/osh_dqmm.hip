@@ -42,7 +42,8 @@ struct DqScratch {  // layout of the caller's scratch buffer
     int zp;
     float scale;
     float inv;
-    int pad[61];
+    int alpha;  // a - a_zp = a'' + alpha for the packed a'' (128 - zp for quantized u8)
+    int pad[60];
     // followed by: int rowsum[mpad]; int rownan[mpad]; int8 a_packed[mpad * kpad]
 };
 
@@ -135,6 +136,7 @@ __device__ void dq_params(DqScratch *__restrict__ sc, int nparts, int *__restric
             sc->scale = scale;
             sc->zp = zp;
             sc->inv = inv;
+            sc->alpha = 128 - zp;
             if (qparams) {
                 qparams[0] = __float_as_int(scale);
                 qparams[1] = zp;
@@ -233,6 +235,46 @@ __global__ __launch_bounds__(DQ_THREADS) void dqmm_quantize_kernel(const float *
     }
 }
 
+// MatMulInteger's activations: one wave per row turns u8 (a - 128) or s8 (a)
+// into the s8 a'' of the MFMA layout and sums each row; block 0 publishes
+// alpha = (u8 ? 128 : 0) - a_zp so that a - a_zp = a'' + alpha.
+__global__ __launch_bounds__(DQ_THREADS) void mmi_pack_a_kernel(const uint8_t *__restrict__ a, int m, int k,
+                                                                 int a_signed, int a_zp, DqScratch *__restrict__ sc,
+                                                                 int *__restrict__ rowsum, int8_t *__restrict__ apk) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (DQ_THREADS / 64) + (threadIdx.x >> 6);
+    const int kpad = pad32(k), mpad = pad32(m);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        sc->alpha = (a_signed ? 0 : 128) - a_zp;
+        sc->scale = 1.0f;
+        sc->zp = a_zp;
+    }
+    if (row >= mpad) return;
+    const bool live = row < m;
+    const uint8_t *src = a + (long long)(live ? row : 0) * k;
+    int *dst = reinterpret_cast<int *>(apk) + (long long)(row >> 5) * (kpad / 32) * 256 + (row & 31) * 4;
+    int sum = 0;
+    for (int kk = 4 * lane; kk < kpad; kk += 256) {
+        unsigned packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            int v = 0;  // padding rows/columns carry a'' = 0
+            if (live && kk + b < k) {
+                const int raw = src[kk + b];
+                v = a_signed ? (int)(int8_t)raw : raw - 128;
+                sum += v;
+            }
+            packed |= (unsigned)(v & 0xff) << (8 * b);
+        }
+        dst[(kk >> 5) * 256 + ((kk >> 4) & 1) * 128 + ((kk & 15) >> 2)] = (int)packed;
+    }
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    if (lane == 0) {
+        rowsum[row] = sum;
+        rowsum[mpad + row] = 0;
+    }
+}
+
 // DynamicQuantizeLinear output: u8 q in the input's own layout.
 __global__ __launch_bounds__(DQ_THREADS) void dql_quantize_kernel(const float *__restrict__ x, long long n,
                                                                    DqScratch *__restrict__ sc, int nparts,
@@ -308,9 +350,9 @@ __global__ __launch_bounds__(256) void dqmm_gemm_kernel(int m, int k, int n, con
     // two's-complement wrap-around below is exact as long as the final sum fits in int32
     const unsigned offj = (unsigned)off[j];
     const int csum = colsum[j];
-    const float ws = j < n ? (n_wscale == 1 ? wscale[0] : wscale[j]) : 0.0f;
+    const float ws = (wscale && j < n) ? (n_wscale == 1 ? wscale[0] : wscale[j]) : 0.0f;
     const float bj = (bias && j < n) ? bias[j] : 0.0f;
-    const int azp = sc->zp;
+    const int aalpha = sc->alpha;
     const float ascale = sc->scale;
     // k in chunks of DQ_KC steps: the next chunk's 2*DQ_KC loads are in flight
     // while the current chunk's MFMAs run.
@@ -348,7 +390,7 @@ __global__ __launch_bounds__(256) void dqmm_gemm_kernel(int m, int k, int n, con
         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[s * 64], B[s * 64], acc, 0, 0, 0);
 
     if (j >= n) return;
-    const unsigned alpha = (unsigned)(128 - azp);
+    const unsigned alpha = (unsigned)aalpha;
     const unsigned colterm = alpha * (unsigned)csum + (unsigned)k * alpha * offj;
     const float comb = ascale * ws;  // CombinedScale, QuantizedMatMulOps.cs:203-221
 #pragma unroll
@@ -360,9 +402,11 @@ __global__ __launch_bounds__(256) void dqmm_gemm_kernel(int m, int k, int n, con
         if (i < m) {
             int v = (int)((unsigned)acc[r] + offj * (unsigned)rsum + colterm);
             if (acc_out) acc_out[(long long)i * n + j] = v;
-            float o = __builtin_fmaf((float)v, comb, bj);
-            if (rnan) o = __builtin_nanf("");
-            out[(long long)i * n + j] = o;
+            if (out) {
+                float o = __builtin_fmaf((float)v, comb, bj);
+                if (rnan) o = __builtin_nanf("");
+                out[(long long)i * n + j] = o;
+            }
         }
     }
 }
@@ -454,6 +498,35 @@ OSH_API osh_status osh_dqmm_u8s8(int m, int k, int n, const float *d_a, const vo
     dim3 grid((pad32(n) / 32 + 1) / 2, (pad32(m) / 32 + 1) / 2);
     hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
                        d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
+    OSH_LAUNCH_CHECK("dqmm_gemm_kernel");
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_matmul_integer(int m, int k, int n, const void *d_a, int a_signed, int a_zp,
+                                      const void *d_wpacked, int32_t *d_c, void *d_scratch, osh_stream s) {
+    if (m < 0 || k <= 0 || n <= 0) return fail(OSH_E_INVALID, "MatMulInteger: bad size m=%d k=%d n=%d", m, k, n);
+    if (m == 0) return OSH_OK;
+    if (!d_a || !d_wpacked || !d_c || !d_scratch) return fail(OSH_E_INVALID, "MatMulInteger: NULL pointer");
+    if (a_zp < -32768 || a_zp > 32767) return fail(OSH_E_UNSUPPORTED, "MatMulInteger: a_zero_point %d", a_zp);
+    if ((long long)k * 255 * 255 > 2147483647LL)
+        return fail(OSH_E_UNSUPPORTED, "MatMulInteger: K=%d can overflow the int32 accumulator", k);
+    if (pad32(m) / 32 > 2 * 65535) return fail(OSH_E_UNSUPPORTED, "MatMulInteger: m too large");
+    hipStream_t st = to_stream(s);
+    DqScratch *sc = static_cast<DqScratch *>(d_scratch);
+    int *rowsum = reinterpret_cast<int *>(sc + 1);
+    int8_t *apk = reinterpret_cast<int8_t *>(rowsum + 2 * pad32(m));
+    const int rows_per_block = DQ_THREADS / 64;
+    hipLaunchKernelGGL(mmi_pack_a_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
+                       dim3(DQ_THREADS), 0, st, static_cast<const uint8_t *>(d_a), m, k, a_signed, a_zp, sc, rowsum,
+                       apk);
+    OSH_LAUNCH_CHECK("mmi_pack_a_kernel");
+    const int8_t *frag = static_cast<const int8_t *>(d_wpacked);
+    const int *colsum = reinterpret_cast<const int *>(frag + (size_t)pad32(n) * pad32(k));
+    const int *off = colsum + pad32(n);
+    dim3 grid((pad32(n) / 32 + 1) / 2, (pad32(m) / 32 + 1) / 2);
+    hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
+                       static_cast<const float *>(nullptr), 1, static_cast<const float *>(nullptr),
+                       static_cast<float *>(nullptr), (int *)d_c);
     OSH_LAUNCH_CHECK("dqmm_gemm_kernel");
     return OSH_OK;
 }

@@ -8,6 +8,7 @@ relative to the OnnxSharp source tree):
   GemmLayer                    src/OnnxSharp/Ops/AttnOps.cs:31-135
   DynamicQuantizeMatMulLayer   src/OnnxSharp/Ops/QuantizedMatMulOps.cs:28-376
   DynamicQuantizeLinearLayer   src/OnnxSharp/Ops/QuantOps.cs:166-227
+  MatMulIntegerLayer           src/OnnxSharp/Ops/QuantOps.cs:235-428
 
 Shape inference, pad resolution and kernel choice run inside libosh_hip.so
 (C++); this module only moves torch device pointers across the C ABI.  Tensors
@@ -301,3 +302,50 @@ class DynamicQuantizeLinearLayer:
         qh = qp.cpu()
         scale = qh[0:1].view(torch.float32).item()
         return q, scale, int(qh[1].item())
+
+
+class MatMulIntegerLayer:
+    """MatMulInteger: int32 C = (A - a_zero_point) x (B - b_zero_point[col]),
+    A u8/s8 [M,K] (or [1,M,K]), B u8/s8 [K,N] (or [1,K,N]); B is packed once per
+    (tensor, zero points) like the reference's constant-weight cache."""
+
+    def __init__(self, name: str = "matmulinteger"):
+        self.name = name
+        self._packed = None
+
+    def resolve(self, a_shape: Sequence[int], b_shape: Sequence[int]):
+        """(m, k, n, batched) as MatMulIntegerLayer.Resolve (QuantOps.cs:255-272)."""
+        ar = 2 if (len(a_shape) == 3 and a_shape[0] == 1) else len(a_shape)
+        br = 2 if (len(b_shape) == 3 and b_shape[0] == 1) else len(b_shape)
+        if ar != 2 or br != 2:
+            raise N.OshError(N.OSH_E_INVALID,
+                             f"MatMulInteger: only 2-D (or batch=1 3-D) is supported, got {list(a_shape)} x {list(b_shape)}")
+        m, k, n = a_shape[-2], a_shape[-1], b_shape[-1]
+        if b_shape[-2] != k:
+            raise N.OshError(N.OSH_E_INVALID, f"MatMulInteger: K mismatch ({list(a_shape)} x {list(b_shape)})")
+        return m, k, n, len(a_shape) == 3 or len(b_shape) == 3
+
+    def forward(self, a: torch.Tensor, b: torch.Tensor, a_zero_point=None, b_zero_point=None) -> torch.Tensor:
+        if a.dtype not in (torch.uint8, torch.int8) or b.dtype not in (torch.uint8, torch.int8):
+            raise TypeError("MatMulInteger takes uint8/int8 tensors")
+        m, k, n, batched = self.resolve(tuple(a.shape), tuple(b.shape))
+        a_zp = 0 if a_zero_point is None or len(list(a_zero_point)) == 0 else int(list(a_zero_point)[0])
+        zps = [0] if b_zero_point is None or len(list(b_zero_point)) == 0 else [int(v) for v in b_zero_point]
+        key = (b.data_ptr(), tuple(b.shape), b.dtype, tuple(zps), getattr(b, "_version", 0))
+        if self._packed is None or self._packed[0] != key:
+            nbytes = C.c_size_t()
+            N.call("osh_dqmm_packed_weight_bytes", k, n, C.byref(nbytes))
+            buf = torch.empty(nbytes.value, dtype=torch.uint8, device=b.device)
+            z = (C.c_int32 * len(zps))(*zps)
+            bb = b.reshape(k, n).contiguous()
+            N.call("osh_dqmm_pack_weights", k, n, _ptr(bb), 1 if b.dtype == torch.int8 else 0, z, len(zps),
+                   _ptr(buf), C.c_void_p(_stream()))
+            self._packed = (key, buf)
+        sbytes = C.c_size_t()
+        N.call("osh_dqmm_scratch_bytes", m, k, C.byref(sbytes))
+        scratch = torch.empty(sbytes.value, dtype=torch.uint8, device=a.device)
+        out = torch.empty((1, m, n) if batched else (m, n), dtype=torch.int32, device=a.device)
+        aa = a.reshape(m, k).contiguous()
+        N.call("osh_matmul_integer", m, k, n, _ptr(aa), 1 if a.dtype == torch.int8 else 0, a_zp,
+               _ptr(self._packed[1]), _ptr(out), _ptr(scratch), C.c_void_p(_stream()))
+        return out

@@ -60,8 +60,7 @@ def lib():
         l.orc_dynamic_quantize_linear.argtypes = [C.c_long, _fp, _u8p, _fp, _ip]
         l.orc_dqmm.argtypes = [C.c_int, C.c_int, C.c_int, _fp, _vp, C.c_int, _ip, C.c_int, _fp, C.c_int, _fp,
                                _fp, _i32p, _fp, C.c_int, _fp, _ip]
-        l.orc_matmul_integer.argtypes = [C.c_int, C.c_int, C.c_int, _u8p, C.c_int, _vp, C.c_int, _ip, C.c_int,
-                                         _i32p]
+        l.orc_matmul_integer.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, _ip, C.c_int, _i32p]
         l.orc_set_threads.argtypes = [C.c_int]
         _lib = l
     return _lib
@@ -294,14 +293,16 @@ def dqmm(a, w, w_zp=None, w_scale=None, bias=None, fused=True):
 
 
 def matmul_integer(a, b, a_zp=0, b_zp=None):
-    """MatMulInteger (Int8Gemm.MultiplyIntegerScalar): exact int32."""
-    a = np.ascontiguousarray(a, np.uint8)
+    """MatMulInteger (Int8Gemm.MultiplyIntegerScalar; s8 A read as signed): exact int32."""
+    a = np.ascontiguousarray(a)
+    if a.dtype != np.int8:
+        a = a.astype(np.uint8)
     b = np.ascontiguousarray(b)
     m, k = a.shape
     n = b.shape[1]
     z, nz = _zp_arr(b_zp)
     c = np.empty((m, n), np.int32)
-    lib().orc_matmul_integer(m, k, n, a.ctypes.data_as(_u8p), int(a_zp), b.ctypes.data,
+    lib().orc_matmul_integer(m, k, n, a.ctypes.data, 1 if a.dtype == np.int8 else 0, int(a_zp), b.ctypes.data,
                              1 if b.dtype == np.int8 else 0, None if z is None else z.ctypes.data_as(_ip), nz,
                              c.ctypes.data_as(_i32p))
     return c

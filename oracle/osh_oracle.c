@@ -652,15 +652,17 @@ ORC_API void orc_dqmm(int m, int k, int n, const float *a, const void *w, int w_
 }
 
 /* MatMulInteger: int64 sum of (a - a_zp)(b - b_zp[col]) (Int8Gemm.MultiplyIntegerScalar). */
-ORC_API void orc_matmul_integer(int m, int k, int n, const uint8_t *a, int a_zp, const void *b, int b_signed,
-                                const int *b_zp, int n_bzp, int32_t *c)
+/* a_signed: s8 activations read as signed values (Int8F32Gemm.WidenActivation(sbyte),
+ * Int8F32Gemm.cs:109-125, and the ONNX definition); u8 otherwise. */
+ORC_API void orc_matmul_integer(int m, int k, int n, const void *a, int a_signed, int a_zp, const void *b,
+                                int b_signed, const int *b_zp, int n_bzp, int32_t *c)
 {
     for (int i = 0; i < m; i++)
         for (int j = 0; j < n; j++) {
             int zp = b_zp ? (n_bzp == 1 ? b_zp[0] : b_zp[j]) : 0;
             int64_t s = 0;
             for (int t = 0; t < k; t++)
-                s += (int64_t)((int)a[(long)i * k + t] - a_zp) * (wval(b, b_signed, (long)t * n + j) - zp);
+                s += (int64_t)(wval(a, a_signed, (long)i * k + t) - a_zp) * (wval(b, b_signed, (long)t * n + j) - zp);
             c[(long)i * n + j] = (int32_t)s;
         }
 }
