@@ -130,7 +130,7 @@ class GemmWorkload(Workload):
         import torch
         from onnxsharp_amd import native as N, synth
         self.name = "c1"
-        self.kernel = "igemm_f32_kernel"
+        self.kernel = "gemm16_kernel"
         m, k, n = 1024, 768, 768
         self.a_np = synth.uniform(101, (m, k), -1, 1)
         self.b_np = synth.uniform(102, (k, n), -1, 1)
@@ -208,7 +208,14 @@ class YoloWorkload(Workload):
         self.fr.set_input(self.x_np)
         self.fr.run()
         self.fr.sync()
-        self.fr.capture(parallel=os.environ.get("ONNXSHARP_HIP_FRAME_PARALLEL", "0") == "1")
+        # ONNXSHARP_HIP_FRAME_MODE: "graph" (default, one serial HIP graph),
+        # "segments" (per-stream segments as child graphs of one DAG) or
+        # "eager" (launches issued from the host on the planned streams)
+        self.mode = os.environ.get("ONNXSHARP_HIP_FRAME_MODE", "graph")
+        if self.mode not in ("graph", "segments", "eager"):
+            raise SystemExit(f"ONNXSHARP_HIP_FRAME_MODE={self.mode!r}: expected graph, segments or eager")
+        if self.mode != "eager":
+            self.fr.capture(parallel=self.mode == "segments")
         self.stream = self.fr.stream
         self.flops = self.model.flops
         # each tensor read or written once per op that touches it
@@ -224,7 +231,10 @@ class YoloWorkload(Workload):
                                   "DFL/NMS on the host"}
 
     def step(self, stream):
-        self.fr.launch()
+        if self.mode == "eager":
+            self.fr.run()
+        else:
+            self.fr.launch()
 
     def cpu_step(self, oracle):
         from oracle import yolo_frame
@@ -243,7 +253,7 @@ class YoloWorkload(Workload):
 
         def frame():
             N.call("osh_memcpy_h2d", dst_in, C.c_void_p(hin.data_ptr()), nb_in, self.stream)
-            self.fr.launch()
+            self.step(self.stream)
             for h, d in zip(houts, outs):
                 N.call("osh_memcpy_d2h", C.c_void_p(h.data_ptr()), C.c_void_p(d.data_ptr()), h.numel() * 4,
                        self.stream)
@@ -285,11 +295,11 @@ class CopyWorkload(Workload):
 
 def make_workload(name, dev):
     if name == "c2":
-        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "conv3x3_wi_kernel", 1)
+        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "conv16_kernel", 1)
     if name == "c3a":
-        return ConvWorkload(dev, "c3a", (1, 256, 80, 80), (128, 256, 1, 1), 1, "Silu", "igemm_f32_kernel", 11)
+        return ConvWorkload(dev, "c3a", (1, 256, 80, 80), (128, 256, 1, 1), 1, "Silu", "gemm16_kernel", 11)
     if name == "c3b":
-        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "conv3x3_ws_kernel", 21)
+        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "conv16_kernel", 21)
     if name == "c1":
         return GemmWorkload(dev)
     if name == "c5":
