@@ -87,10 +87,13 @@ OSH_API osh_status osh_device_synchronize(void);
  *   "conv16_variant": -1 (default) = 3x3 convolutions with C % 16 == 0 run
  *                 the in-order 16x16x4 MFMA kernel (the reference's NCHWc
  *                 chain, bit for bit) with a wave tile picked per shape;
- *                 0..11 forces a tile (6..11: weights held in LDS);
+ *                 0..N-1 forces a tile where the shape allows it (6..11:
+ *                 weights held in LDS; 12..N-1: input patch staged in LDS
+ *                 and shared by a workgroup's four waves, stride 1 or 2);
  *                 -2 = use the weight-stationary 3x3
  *                 kernels instead (summation order differs; within the FP32
  *                 tolerance).  Initial value from ONNXSHARP_HIP_CONV16_VARIANT.
+ *   "conv16_variants" (get only): N, the number of 3x3 tiles.
  *   "tune": 1 (default) = the first launch of a 3x3 conv shape on a stream
  *                 that is not capturing times every conv16 tile (they all give
  *                 identical outputs) and keeps the fastest for that shape;
@@ -181,6 +184,16 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
  * d_wpacked is the output of osh_conv_pack_weights for the same p. */
 OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,
                                   const float *d_bias, int act, float *d_y, osh_stream s);
+
+/* Conv followed by a residual Add in one launch: y = act(conv(x) + bias) + res,
+ * res laid out as y (NCHW [n, m, oh, ow]) and not overlapping it.  This is the
+ * ONNX pair Conv(+fused activation) -> Add(shortcut, conv output) of a
+ * bottleneck block (ConvLayer.Forward, src/OnnxSharp/Ops/DnnOps.cs:411-500,
+ * then the same-shape Add of NaryEltwiseLayer.Forward, src/OnnxSharp/Ops/NaryEltwiseLayer.cs:41),
+ * with the same two roundings: the activation output, then the sum. */
+OSH_API osh_status osh_conv2d_add_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,
+                                      const float *d_bias, int act, const float *d_res, float *d_y,
+                                      osh_stream s);
 
 /* ------------------------------------------------- MatMul + bias (A9, A10) */
 
@@ -290,6 +303,16 @@ typedef struct osh_pool_params {
  * y[n][c][oy][ox] = max over the window rows oy*sh - pt + ky, columns
  * ox*sw - pl + kx that fall inside the input. */
 OSH_API osh_status osh_maxpool2d_f32(const osh_pool_params *p, const float *d_x, float *d_y, osh_stream s);
+
+/* The SPPF block's three chained MaxPools (k x k, stride 1, pad k/2; k = 3, 5
+ * or 7) in one launch: y1 = pool(x), y2 = pool(y1), y3 = pool(y2), each the
+ * same result as osh_maxpool2d_f32 (MaxPoolLayer, DnnOps.cs:1335-1480) applied
+ * in turn.  All tensors are [n, c, h, w] planes; x_batch_stride and
+ * y_batch_stride (elements) step between images, so the outputs may be
+ * channel slices of one concat buffer.  The outputs must not overlap x. */
+OSH_API osh_status osh_maxpool_chain3_f32(int n, int c, int h, int w, int k, const float *d_x,
+                                          int64_t x_batch_stride, float *d_y1, float *d_y2, float *d_y3,
+                                          int64_t y_batch_stride, osh_stream s);
 
 /* Nearest-neighbour upsampling by integer factors (ResizeLayer mode "nearest",
  * src/OnnxSharp/Ops/DnnOps.cs:2215-2330): y[n][c][oy][ox] = x[n][c][oy/fh][ox/fw],

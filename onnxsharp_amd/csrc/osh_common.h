@@ -118,8 +118,9 @@ int gemm_variant();
 int gemm16_variant_count();
 
 // Forced conv16 wave tile for 3x3 convolutions (-1 = automatic, -2 = use the
-// weight-stationary kernels instead).
+// weight-stationary kernels instead) and the number of tiles.
 int conv16_variant();
+int conv16_variant_count();
 
 // Whether kernels whose tiles all give identical results may pick their tile
 // by timing it on first use (osh_config "tune", ONNXSHARP_HIP_TUNE; default on).

@@ -24,6 +24,7 @@
 #include <tuple>
 
 #include "osh_conv16.h"
+#include "osh_conv16s.h"
 #include "osh_conv3x3.h"
 #include "osh_conv3x3_wi.h"
 #include "osh_conv3x3_ws.h"
@@ -89,7 +90,7 @@ static osh_status check_attrs(const osh_conv_attrs *at, const int64_t x[4], cons
 template <int ACT>
 __global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const float *__restrict__ x,
                                                       const float *__restrict__ w, const float *__restrict__ bias,
-                                                      float *__restrict__ y) {
+                                                      const float *__restrict__ res, float *__restrict__ y) {
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long total = (long long)p.n * p.m * p.oh * p.ow;
     if (idx >= total) return;
@@ -111,7 +112,17 @@ __global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const f
             acc = __builtin_fmaf(wc[ky * p.kw + kx], xc[(long long)iy * p.w + ix], acc);
         }
     }
-    y[idx] = activate<ACT>(acc);
+    float v = activate<ACT>(acc);
+    if (res) v += res[idx];
+    y[idx] = v;
+}
+
+// y += res after a kernel whose epilogue has no residual input: the same two
+// roundings (activation output, then the sum) as the fused epilogues.
+__global__ __launch_bounds__(256) void residual_add_kernel(long long n, const float *__restrict__ res,
+                                                           float *__restrict__ y) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = y[i] + res[i];
 }
 
 // ------------------------------------------------------- small-C first layer
@@ -207,17 +218,61 @@ static bool capturing(hipStream_t st) {
     return hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
 }
 
+// The 3x3 variant space: ids 0 .. kC16Count-1 are conv16 / conv16l tiles,
+// the next kC16sCount ids the LDS-patch kernel (stride 1 or 2 only).  All
+// compute the same chain.
+constexpr int kC3Count = kC16Count + kC16sCount;
+int conv16_variant_count() { return kC3Count; }
+
+static bool c3_fits(const osh_conv_params *p, int v) {
+    if (v < kC16Count) return conv16_fits(p, kC16[v]);
+    return conv16s_eligible(p);
+}
+
+// Predicted cost of an LDS-patch tile: rounds of waves over the SIMDs times
+// one wave's MFMAs (tiles past the map edge included), inflated a little for
+// the weight loads and the per-block barrier.
+static double conv16s_cost(const osh_conv_params *p, const C16sVariant &v, int cus) {
+    const int th = 16 / v.twl * v.bv;
+    const long long tiles = (long long)ceil_div(p->ow, v.twl) * ceil_div(p->oh, th);
+    const long long waves = tiles * ceil_div(ceil_div(p->m, 16), v.tm) * p->n;
+    const long long rounds = (waves + 4LL * cus - 1) / (4LL * cus);
+    const double u = (double)v.tm * v.bv;
+    return rounds * u * (9.0 * p->c / 4) * (1.0 + 0.25 / u);
+}
+
+static osh_status c3_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                            const float *res, int act, float *y, hipStream_t st, int v) {
+    if (v < 0) {  // cost model over both families
+        const int cus = device_cus();
+        double bc = 0;
+        for (int i = 0; i < kC16Count; i++) {
+            if (!conv16_fits(p, kC16[i])) continue;
+            const double c = conv16_cost(p, kC16[i], cus);
+            if (v < 0 || c < bc) v = i, bc = c;
+        }
+        if (conv16s_eligible(p))
+            for (int i = 0; i < kC16sCount; i++) {
+                const double c = conv16s_cost(p, kC16s[i], cus);
+                if (c < bc) v = kC16Count + i, bc = c;
+            }
+    }
+    if (v >= kC16Count && v < kC3Count && conv16s_eligible(p))
+        return conv16s_launch(p, x, w, bias, res, act, y, st, v - kC16Count);
+    return conv16_launch(p, x, w, bias, res, act, y, st, v < kC16Count ? v : -1);
+}
+
 static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                      int act, float *y, hipStream_t st) {
+                                      const float *res, int act, float *y, hipStream_t st) {
     const int forced = conv16_variant();
-    if (forced >= 0 || !tuning_enabled()) return conv16_launch(p, x, w, bias, act, y, st, forced);
+    if (forced >= 0 || !tuning_enabled()) return c3_launch(p, x, w, bias, res, act, y, st, forced);
     const auto key = conv_key(p);
     {
         std::lock_guard<std::mutex> lk(g_tune_mu);
         auto it = g_tuned.find(key);
-        if (it != g_tuned.end()) return conv16_launch(p, x, w, bias, act, y, st, it->second);
+        if (it != g_tuned.end()) return c3_launch(p, x, w, bias, res, act, y, st, it->second);
     }
-    if (capturing(st)) return conv16_launch(p, x, w, bias, act, y, st, -1);
+    if (capturing(st)) return c3_launch(p, x, w, bias, res, act, y, st, -1);
     hipEvent_t e0, e1;
     OSH_HIP_CHECK(hipEventCreate(&e0));
     if (hipEventCreate(&e1) != hipSuccess) {
@@ -227,12 +282,12 @@ static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, 
     int best = -1;
     float best_ms = 0.f;
     osh_status rc = OSH_OK;
-    for (int v = 0; v < kC16Count && rc == OSH_OK; v++) {
-        if (!conv16_fits(p, kC16[v])) continue;
-        rc = conv16_launch(p, x, w, bias, act, y, st, v);
+    for (int v = 0; v < kC3Count && rc == OSH_OK; v++) {
+        if (!c3_fits(p, v)) continue;
+        rc = c3_launch(p, x, w, bias, res, act, y, st, v);
         if (rc != OSH_OK) break;
         if (hipEventRecord(e0, st) != hipSuccess) { rc = fail(OSH_E_DEVICE, "hipEventRecord failed"); break; }
-        for (int r = 0; r < 3 && rc == OSH_OK; r++) rc = conv16_launch(p, x, w, bias, act, y, st, v);
+        for (int r = 0; r < 3 && rc == OSH_OK; r++) rc = c3_launch(p, x, w, bias, res, act, y, st, v);
         if (rc != OSH_OK) break;
         float ms = 0.f;
         if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
@@ -250,6 +305,14 @@ static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, 
         g_tuned[key] = best;
     }
     return OSH_OK;  // y already holds the result (every tile computes the same values)
+}
+
+static osh_status residual_add(const osh_conv_params *p, const float *res, float *y, hipStream_t st) {
+    if (!res) return OSH_OK;
+    const long long n = (long long)p->n * p->m * p->oh * p->ow;
+    hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, n, res, y);
+    OSH_LAUNCH_CHECK("residual_add_kernel");
+    return OSH_OK;
 }
 
 static osh_status check_params(const osh_conv_params *p) {
@@ -353,13 +416,14 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
     return OSH_OK;
 }
 
-OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,
-                                  const float *d_bias, int act, float *d_y, osh_stream s) {
-    osh_status st = check_params(p);
-    if (st != OSH_OK) return st;
-    if (!d_x || !d_wpacked || !d_y) return fail(OSH_E_INVALID, "Conv: NULL tensor pointer");
-    if (act < OSH_ACT_NONE || act > OSH_ACT_SILU) return fail(OSH_E_INVALID, "Conv: unknown activation %d", act);
-    hipStream_t stream = to_stream(s);
+}  // extern "C"
+
+namespace osh {
+
+// Launches the conv of p: y = act(conv(x) + bias) (+ res when res is not NULL;
+// res has y's layout and does not overlap it).
+static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void *d_wpacked, const float *d_bias,
+                         int act, const float *d_res, float *d_y, hipStream_t stream) {
     const float *w = static_cast<const float *>(d_wpacked);
     const int cpg = p->c / p->group, opg = p->m / p->group;
     const long long in_hw = (long long)p->h * p->w, out_hw = (long long)p->oh * p->ow;
@@ -369,7 +433,8 @@ OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, co
         long long total = (long long)p->n * p->m * out_hw;
         dim3 grid((unsigned)((total + 255) / 256));
         OSH_DISPATCH_ACT(act, ACT,
-                         hipLaunchKernelGGL(dw_conv_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, w, d_bias, d_y));
+                         hipLaunchKernelGGL(dw_conv_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, w, d_bias, d_res,
+                                            d_y));
         OSH_LAUNCH_CHECK("dw_conv_kernel");
         return OSH_OK;
     }
@@ -394,16 +459,20 @@ OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, co
 #undef OSH_FIRST_C
 #undef OSH_FIRST
         OSH_LAUNCH_CHECK("first_conv_kernel");
-        return OSH_OK;
+        return residual_add(p, d_res, d_y, stream);
     }
     case ALGO_CONV16:
-        return conv16_tuned_launch(p, d_x, w, d_bias, act, d_y, stream);
-    case ALGO_WI3X3:
-        return conv3x3_wi_launch(p, d_x, w, d_bias, act, d_y, stream, device_cus());
-    case ALGO_WS3X3:
-        return conv3x3_ws_launch(p, d_x, w, d_bias, act, d_y, stream);
+        return conv16_tuned_launch(p, d_x, w, d_bias, d_res, act, d_y, stream);
+    case ALGO_WI3X3: {
+        osh_status st = conv3x3_wi_launch(p, d_x, w, d_bias, act, d_y, stream, device_cus());
+        return st != OSH_OK ? st : residual_add(p, d_res, d_y, stream);
+    }
+    case ALGO_WS3X3: {
+        osh_status st = conv3x3_ws_launch(p, d_x, w, d_bias, act, d_y, stream);
+        return st != OSH_OK ? st : residual_add(p, d_res, d_y, stream);
+    }
     case ALGO_DIRECT3X3:
-        return conv3x3_launch(p, d_x, w, d_bias, act, d_y, stream);
+        return conv3x3_launch(p, d_x, w, d_bias, d_res, act, d_y, stream);
     case ALGO_POINTWISE:
     case ALGO_IM2COL: {
         const bool pw = select_algo(p) == ALGO_POINTWISE;
@@ -424,6 +493,7 @@ OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, co
         a.strideC = (long long)p->m * out_hw;
         a.strideC_in = (long long)opg * out_hw;
         a.row_bias = d_bias;
+        a.res = d_res;
         a.bias_stride = opg;
         a.zdiv = p->group;
         a.H = p->h; a.W = p->w; a.KH = p->kh; a.KW = p->kw;
@@ -433,6 +503,38 @@ OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, co
     }
     }
     return fail(OSH_E_INVALID, "Conv: no kernel");
+}
+
+static osh_status check_launch(const osh_conv_params *p, const float *d_x, const void *d_wpacked, int act,
+                                float *d_y) {
+    osh_status st = check_params(p);
+    if (st != OSH_OK) return st;
+    if (!d_x || !d_wpacked || !d_y) return fail(OSH_E_INVALID, "Conv: NULL tensor pointer");
+    if (act < OSH_ACT_NONE || act > OSH_ACT_SILU) return fail(OSH_E_INVALID, "Conv: unknown activation %d", act);
+    return OSH_OK;
+}
+
+}  // namespace osh
+
+extern "C" {
+
+OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,
+                                  const float *d_bias, int act, float *d_y, osh_stream s) {
+    osh_status st = check_launch(p, d_x, d_wpacked, act, d_y);
+    if (st != OSH_OK) return st;
+    return conv2d(p, d_x, d_wpacked, d_bias, act, nullptr, d_y, to_stream(s));
+}
+
+OSH_API osh_status osh_conv2d_add_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,
+                                      const float *d_bias, int act, const float *d_res, float *d_y, osh_stream s) {
+    osh_status st = check_launch(p, d_x, d_wpacked, act, d_y);
+    if (st != OSH_OK) return st;
+    if (!d_res) return fail(OSH_E_INVALID, "Conv+Add: residual is NULL");
+    const uintptr_t bytes = (uintptr_t)p->n * p->m * p->oh * p->ow * sizeof(float);
+    const uintptr_t r0 = reinterpret_cast<uintptr_t>(d_res), y0 = reinterpret_cast<uintptr_t>(d_y);
+    if (r0 < y0 + bytes && y0 < r0 + bytes)
+        return fail(OSH_E_INVALID, "Conv+Add: the residual overlaps the output");
+    return conv2d(p, d_x, d_wpacked, d_bias, act, d_res, d_y, to_stream(s));
 }
 
 }  // extern "C"

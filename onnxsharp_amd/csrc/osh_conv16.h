@@ -45,7 +45,8 @@ struct C16Chunk {
 template <int TM, int BV, int ACT>
 __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const float *__restrict__ x,
                                                      const float *__restrict__ wpk, const float *__restrict__ bias,
-                                                     float *__restrict__ y, int tiles_p) {
+                                                     const float *__restrict__ res, float *__restrict__ y,
+                                                     int tiles_p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15, g = lane >> 4;
@@ -58,6 +59,7 @@ __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const fl
     const int icbs = C / 16;
     const float *xn = x + (long long)n * C * HW;
     float *yn = y + (long long)n * M * OHW;
+    const float *rn = res ? res + (long long)n * M * OHW : nullptr;
 
     // per pixel: the nine tap offsets (bytes, lane group g's channel included)
     int off[BV][9];
@@ -168,7 +170,11 @@ __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const fl
 #pragma unroll
             for (int q = 0; q < BV; q++) {
                 const int pix = pt * 16 * BV + BV * j + q;
-                if (pix < OHW) yn[(long long)oc * OHW + pix] = activate<ACT>(acc[tm][q][r]);
+                if (pix < OHW) {
+                    float v = activate<ACT>(acc[tm][q][r]);
+                    if (rn) v += rn[(long long)oc * OHW + pix];
+                    yn[(long long)oc * OHW + pix] = v;
+                }
             }
         }
 }
@@ -183,7 +189,8 @@ constexpr int CONV16L_LDS = 147456;  // 16 * 4 * 9 * 64 floats: TM * C <= 256
 template <int TM, int BV, int ACT>
 __global__ __launch_bounds__(256) void conv16l_kernel(osh_conv_params p, const float *__restrict__ x,
                                                       const float *__restrict__ wpk, const float *__restrict__ bias,
-                                                      float *__restrict__ y, int tiles_p) {
+                                                      const float *__restrict__ res, float *__restrict__ y,
+                                                      int tiles_p) {
     __shared__ __align__(16) float wl[CONV16L_LDS / 4];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -221,6 +228,7 @@ __global__ __launch_bounds__(256) void conv16l_kernel(osh_conv_params p, const f
     for (int n = 0; n < p.n; n++) {
         const float *xn = x + (long long)n * C * HW;
         float *yn = y + (long long)n * M * OHW;
+        const float *rn = res ? res + (long long)n * M * OHW : nullptr;
         for (int pt = blockIdx.x * 4 + wave; pt < tiles_p; pt += gridDim.x * 4) {
             int off[BV][9];
 #pragma unroll
@@ -309,7 +317,11 @@ __global__ __launch_bounds__(256) void conv16l_kernel(osh_conv_params p, const f
 #pragma unroll
                     for (int q = 0; q < BV; q++) {
                         const int pix = pt * 16 * BV + BV * j + q;
-                        if (pix < OHW) yn[(long long)oc * OHW + pix] = activate<ACT>(acc[tm][q][r]);
+                        if (pix < OHW) {
+                            float v = activate<ACT>(acc[tm][q][r]);
+                            if (rn) v += rn[(long long)oc * OHW + pix];
+                            yn[(long long)oc * OHW + pix] = v;
+                        }
                     }
                 }
         }
@@ -358,21 +370,22 @@ inline osh_status conv16_pack(const osh_conv_params *p, const float *w, void *ou
 // larger tiles load fewer operands per MFMA.
 template <int TM, int BV>
 inline osh_status conv16_launch_t(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                  int act, float *y, hipStream_t st) {
+                                  const float *res, int act, float *y, hipStream_t st) {
     const int ohw = p->oh * p->ow;
     const int tiles_p = ceil_div(ohw, 16 * BV);
     // output-channel tiles: TM 16-blocks each; the packed weights hold ceil(M/16) blocks
     const int mtiles = ceil_div(ceil_div(p->m, 16), TM);
     dim3 grid((unsigned)ceil_div(tiles_p, 4), (unsigned)mtiles, (unsigned)p->n);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16_kernel<TM, BV, ACT>), grid, dim3(256), 0, st, *p, x, w, bias, y, tiles_p));
+                     hipLaunchKernelGGL((conv16_kernel<TM, BV, ACT>), grid, dim3(256), 0, st, *p, x, w, bias, res, y,
+                                        tiles_p));
     OSH_LAUNCH_CHECK("conv16_kernel");
     return OSH_OK;
 }
 
 template <int TM, int BV>
 inline osh_status conv16l_launch_t(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                   int act, float *y, hipStream_t st) {
+                                   const float *res, int act, float *y, hipStream_t st) {
     const int ohw = p->oh * p->ow;
     const int tiles_p = ceil_div(ohw, 16 * BV);
     const int mtiles = ceil_div(ceil_div(p->m, 16), TM);
@@ -382,8 +395,8 @@ inline osh_status conv16l_launch_t(const osh_conv_params *p, const float *x, con
     per = per > ceil_div(tiles_p, 4) ? ceil_div(tiles_p, 4) : per;
     dim3 grid((unsigned)per, (unsigned)mtiles, 1);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16l_kernel<TM, BV, ACT>), grid, dim3(256), 0, st, *p, x, w, bias, y,
-                                        tiles_p));
+                     hipLaunchKernelGGL((conv16l_kernel<TM, BV, ACT>), grid, dim3(256), 0, st, *p, x, w, bias, res,
+                                        y, tiles_p));
     OSH_LAUNCH_CHECK("conv16l_kernel");
     return OSH_OK;
 }
@@ -414,8 +427,8 @@ inline double conv16_cost(const osh_conv_params *p, const C16Variant &v, int cus
     return rounds * u * (9.0 * p->c / 4) * (1.0 + 0.6 * loads / u);
 }
 
-inline osh_status conv16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias, int act,
-                                float *y, hipStream_t st, int forced) {
+inline osh_status conv16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                const float *res, int act, float *y, hipStream_t st, int forced) {
     int best = -1;
     if (forced >= 0 && forced < kC16Count) {
         best = forced;
@@ -430,18 +443,18 @@ inline osh_status conv16_launch(const osh_conv_params *p, const float *x, const 
     }
     if (!conv16_fits(p, kC16[best])) best -= 6;  // forced LDS tile too large: same tile from L2
     switch (best) {
-    case 0: return conv16_launch_t<1, 1>(p, x, w, bias, act, y, st);
-    case 1: return conv16_launch_t<2, 1>(p, x, w, bias, act, y, st);
-    case 2: return conv16_launch_t<4, 1>(p, x, w, bias, act, y, st);
-    case 3: return conv16_launch_t<1, 2>(p, x, w, bias, act, y, st);
-    case 4: return conv16_launch_t<2, 2>(p, x, w, bias, act, y, st);
-    case 5: return conv16_launch_t<4, 2>(p, x, w, bias, act, y, st);
-    case 6: return conv16l_launch_t<1, 1>(p, x, w, bias, act, y, st);
-    case 7: return conv16l_launch_t<2, 1>(p, x, w, bias, act, y, st);
-    case 8: return conv16l_launch_t<4, 1>(p, x, w, bias, act, y, st);
-    case 9: return conv16l_launch_t<1, 2>(p, x, w, bias, act, y, st);
-    case 10: return conv16l_launch_t<2, 2>(p, x, w, bias, act, y, st);
-    default: return conv16l_launch_t<4, 2>(p, x, w, bias, act, y, st);
+    case 0: return conv16_launch_t<1, 1>(p, x, w, bias, res, act, y, st);
+    case 1: return conv16_launch_t<2, 1>(p, x, w, bias, res, act, y, st);
+    case 2: return conv16_launch_t<4, 1>(p, x, w, bias, res, act, y, st);
+    case 3: return conv16_launch_t<1, 2>(p, x, w, bias, res, act, y, st);
+    case 4: return conv16_launch_t<2, 2>(p, x, w, bias, res, act, y, st);
+    case 5: return conv16_launch_t<4, 2>(p, x, w, bias, res, act, y, st);
+    case 6: return conv16l_launch_t<1, 1>(p, x, w, bias, res, act, y, st);
+    case 7: return conv16l_launch_t<2, 1>(p, x, w, bias, res, act, y, st);
+    case 8: return conv16l_launch_t<4, 1>(p, x, w, bias, res, act, y, st);
+    case 9: return conv16l_launch_t<1, 2>(p, x, w, bias, res, act, y, st);
+    case 10: return conv16l_launch_t<2, 2>(p, x, w, bias, res, act, y, st);
+    default: return conv16l_launch_t<4, 2>(p, x, w, bias, res, act, y, st);
     }
 }
 

@@ -1,0 +1,281 @@
+// osh_conv16s.h -- 3x3 convolution with the input patch staged in LDS: the
+// same in-order 16x16x4 MFMA chain as osh_conv16.h (bias, then
+// icb -> ky -> kx -> four steps of four channels; NchwcConv.Row,
+// src/OnnxSharp/Kernels/NchwcConv.cs:533-605), so the same bits, with the
+// operand traffic reorganised for small and mid-size maps:
+//
+//   * a workgroup's four waves share one output-pixel tile and take four
+//     different 16*TM-channel output blocks, so the input patch of the tile is
+//     read from memory once per workgroup, not once per wave;
+//   * per 16-channel input block the patch ((TH-1)*S+3 rows x (TWL-1)*S+3
+//     columns x 16 channels) is copied to LDS by all 256 threads, one element
+//     each per pass: block icb+2 is fetched into registers and block icb+1
+//     written to the second LDS buffer while block icb is multiplied;
+//   * the tile is 2-D: a 16-lane MFMA column group covers (16/TWL) rows x TWL
+//     columns, and BV such groups are stacked vertically, so narrow maps
+//     (20, 40 wide) waste no lanes;
+//   * B comes from LDS (one ds_read_b32 per step and pixel group at a
+//     compile-time offset from the lane's base); A (weights, packed as for
+//     conv16_kernel) from global memory with 16-byte loads, one block ahead.
+// Row pitch and channel-plane pitch of the patch are padded so that the 32
+// lanes of each half-wave LDS read fall in distinct banks.
+#pragma once
+
+#include "osh_conv16.h"
+
+namespace osh {
+
+// Whether lane groups g = 0 and 1 (one half-wave) of an LDS read at row
+// pitch `pitch` and channel-plane pitch `plane` fall in 32 distinct banks.
+constexpr bool c16s_conflict_free(int pitch, int plane, int twl, int s) {
+    bool used[32] = {};
+    for (int g = 0; g < 2; g++)
+        for (int j = 0; j < 16; j++) {
+            const int b = (g * plane + (j / twl) * s * pitch + (j % twl) * s) % 32;
+            if (used[b]) return false;
+            used[b] = true;
+        }
+    return true;
+}
+
+// Smallest channel-plane pitch in [base, base + 32) that is conflict-free at
+// this row pitch, or -1.
+constexpr int c16s_plane_for(int base, int pitch, int twl, int s) {
+    for (int pl = base; pl < base + 32; pl++)
+        if (c16s_conflict_free(pitch, pl, twl, s)) return pl;
+    return -1;
+}
+
+// Smallest row pitch in [pc, pc + 32) that admits a conflict-free plane pitch
+// (pc itself if none does: the reads then take an extra pass).
+constexpr int c16s_pitch(int pc, int pr, int twl, int s) {
+    for (int p = pc; p < pc + 32; p++)
+        if (c16s_plane_for(pr * p, p, twl, s) >= 0) return p;
+    return pc;
+}
+
+constexpr int c16s_plane(int pr, int pitch, int twl, int s) {
+    return c16s_plane_for(pr * pitch, pitch, twl, s) >= 0 ? c16s_plane_for(pr * pitch, pitch, twl, s) : pr * pitch;
+}
+
+template <int TM, int BV, int TWL, int S>
+struct C16sGeom {
+    static constexpr int THL = 16 / TWL;                          // rows per lane group
+    static constexpr int TH = THL * BV;                           // tile rows
+    static constexpr int PR = (TH - 1) * S + 3;                   // patch rows
+    static constexpr int PC = (TWL - 1) * S + 3;                  // patch columns
+    static constexpr int PITCH = c16s_pitch(PC, PR, TWL, S);      // floats per patch row
+    static constexpr int PLANE = c16s_plane(PR, PITCH, TWL, S);   // floats per channel
+    static constexpr int CHUNK = 16 * PLANE;                      // one 16-channel block
+    static constexpr int ELEMS = 16 * PR * PC;                    // patch elements per block
+    static constexpr int NE = (ELEMS + 255) / 256;                // per thread
+};
+
+template <int TM, int BV, int TWL, int S, int ACT>
+__global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const float *__restrict__ x,
+                                                      const float *__restrict__ wpk, const float *__restrict__ bias,
+                                                      const float *__restrict__ res, float *__restrict__ y,
+                                                      int tiles_w) {
+    using G = C16sGeom<TM, BV, TWL, S>;
+    static_assert(16 % TWL == 0, "a lane group covers whole rows of the tile");
+    __shared__ __align__(16) float lds[2 * G::CHUNK];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, g = lane >> 4;
+    const int ty = blockIdx.x / tiles_w, tx = blockIdx.x - ty * tiles_w;
+    const int oy0 = ty * G::TH, ox0 = tx * TWL;
+    const int n = blockIdx.z;
+    const int HW = p.h * p.w, OHW = p.oh * p.ow;
+    const int C = p.c, M = p.m;
+    const int icbs = C / 16;
+    const int kgroups = icbs * 9;
+    const int mb0 = (blockIdx.y * 4 + wave) * TM;       // first 16-channel output block of this wave
+    const bool active = mb0 * 16 < M;                    // uniform per wave
+    const float *xn = x + (long long)n * C * HW;
+    const int iy0 = oy0 * S - p.pt, ix0 = ox0 * S - p.pl;
+
+    // staging: element e = tid + 256 i of a block -> (channel, patch row, patch column)
+    int goff[G::NE], loff[G::NE];
+#pragma unroll
+    for (int i = 0; i < G::NE; i++) {
+        const int e = tid + 256 * i;
+        const int ch = e / (G::PR * G::PC), rem = e - ch * (G::PR * G::PC);
+        const int r = rem / G::PC, c = rem - r * G::PC;
+        const int iy = iy0 + r, ix = ix0 + c;
+        const bool ok = e < G::ELEMS && (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
+        goff[i] = ok ? (ch * HW + iy * p.w + ix) * 4 : (int)C16_OOB;
+        loff[i] = e < G::ELEMS ? ch * G::PLANE + r * G::PITCH + c : -1;
+    }
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void *)xn, (short)0, C * HW * 4, 0x00020000);
+    // two register sets: a block's patch is fetched two blocks before it is
+    // multiplied and written to LDS one block before
+    float sv0[G::NE], sv1[G::NE];
+    auto stage_load = [&](float (&sv)[G::NE], int icb) {
+#pragma unroll
+        for (int i = 0; i < G::NE; i++)
+            sv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, goff[i], icb * 16 * HW * 4, 0));
+    };
+    auto stage_store = [&](const float (&sv)[G::NE], int buf) {
+#pragma unroll
+        for (int i = 0; i < G::NE; i++)
+            if (loff[i] >= 0) lds[buf * G::CHUNK + loff[i]] = sv[i];
+    };
+
+    // A: packed [mblock16][icb*9 + tap][64 lanes][4 steps]
+    const int bytes_w = ((M + 15) / 16) * kgroups * 64 * 16;
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void *)wpk, (short)0, bytes_w, 0x00020000);
+    int voa[TM];
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) voa[tm] = (((mb0 + tm) * kgroups) * 64 + lane) * 16;
+    float4 A0[9][TM], A1[9][TM];
+    auto load_a = [&](float4 (&A)[9][TM], int icb) {
+#pragma unroll
+        for (int t = 0; t < 9; t++)
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++) {
+                auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, voa[tm], (icb * 9 + t) * 1024, 0);
+                A[t][tm] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                                       __uint_as_float(v[3]));
+            }
+    };
+
+    f32x4 acc[TM][BV];
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int oc = (mb0 + tm) * 16 + 4 * g + r;
+            const float b = (bias && oc < M) ? bias[oc] : 0.f;
+#pragma unroll
+            for (int q = 0; q < BV; q++) acc[tm][q][r] = b;
+        }
+
+    // the lane's pixel (row j / TWL + THL q, column j % TWL) in patch coordinates
+    const int lbase = g * G::PLANE + (j / TWL) * S * G::PITCH + (j % TWL) * S;
+    auto compute = [&](const float4 (&A)[9][TM], int buf) {
+        const float *lb = lds + buf * G::CHUNK + lbase;
+#pragma unroll
+        for (int t = 0; t < 9; t++) {
+            const int ky = t / 3, kx = t - 3 * (t / 3);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                float b[BV];
+#pragma unroll
+                for (int q = 0; q < BV; q++) b[q] = lb[4 * s * G::PLANE + (G::THL * q * S + ky) * G::PITCH + kx];
+#pragma unroll
+                for (int tm = 0; tm < TM; tm++) {
+                    const float4 &a4 = A[t][tm];
+                    const float a = s == 0 ? a4.x : s == 1 ? a4.y : s == 2 ? a4.z : a4.w;
+#pragma unroll
+                    for (int q = 0; q < BV; q++)
+                        acc[tm][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[q], acc[tm][q], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // prologue: block 0 in LDS, block 1 in flight, block 0's weights loaded
+    const int last = icbs - 1;
+    stage_load(sv0, 0);
+    if (active) load_a(A0, 0);
+    stage_store(sv0, 0);
+    stage_load(sv1, min(1, last));
+    __syncthreads();
+    // trip k multiplies block k from LDS buffer k % 2 with weight set k % 2,
+    // fetches block k + 2 into register set k % 2 and block k + 1's weights,
+    // and writes block k + 1 (fetched during trip k - 1) into the other LDS
+    // buffer.  Two trips per loop pass keep every set in fixed registers;
+    // prefetch indices are clamped (reloads of the last block, never stored
+    // past the patch) and every wave runs the same trips and barriers.
+    for (int icb = 0; icb < icbs; icb += 2) {
+        stage_load(sv0, min(icb + 2, last));
+        if (active) {
+            load_a(A1, min(icb + 1, last));
+            compute(A0, 0);
+        }
+        stage_store(sv1, 1);
+        __syncthreads();
+        if (icb + 1 >= icbs) break;
+        stage_load(sv1, min(icb + 3, last));
+        if (active) {
+            load_a(A0, min(icb + 2, last));
+            compute(A1, 1);
+        }
+        stage_store(sv0, 0);
+        __syncthreads();
+    }
+    if (!active) return;
+
+    // epilogue: lane (j, g) holds output channels 4g + r of pixel column j
+    float *yn = y + (long long)n * M * OHW;
+    const float *rn = res ? res + (long long)n * M * OHW : nullptr;
+#pragma unroll
+    for (int q = 0; q < BV; q++) {
+        const int oy = oy0 + j / TWL + G::THL * q, ox = ox0 + j % TWL;
+        if (oy >= p.oh || ox >= p.ow) continue;
+        const int pix = oy * p.ow + ox;
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int oc = (mb0 + tm) * 16 + 4 * g + r;
+                if (oc >= M) continue;
+                float v = activate<ACT>(acc[tm][q][r]);
+                if (rn) v += rn[(long long)oc * OHW + pix];
+                yn[(long long)oc * OHW + pix] = v;
+            }
+    }
+}
+
+struct C16sVariant {
+    int tm, bv, twl;
+};
+constexpr C16sVariant kC16s[] = {{1, 1, 16}, {1, 2, 16}, {1, 4, 16}, {2, 2, 16}, {1, 1, 8},
+                                 {1, 2, 8},  {2, 2, 8},  {1, 2, 4},  {1, 4, 4}};
+constexpr int kC16sCount = sizeof(kC16s) / sizeof(kC16s[0]);
+
+// Stride 1 or 2 in both directions (the patch geometry is compile-time).
+inline bool conv16s_eligible(const osh_conv_params *p) {
+    return conv16_eligible(p) && p->sh == p->sw && (p->sh == 1 || p->sh == 2);
+}
+
+template <int TM, int BV, int TWL, int S>
+inline osh_status conv16s_launch_t(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                   const float *res, int act, float *y, hipStream_t st) {
+    using G = C16sGeom<TM, BV, TWL, S>;
+    const int tiles_w = ceil_div(p->ow, TWL), tiles_h = ceil_div(p->oh, G::TH);
+    const int mgroups = ceil_div(ceil_div(p->m, 16), 4 * TM);
+    dim3 grid((unsigned)(tiles_w * tiles_h), (unsigned)mgroups, (unsigned)p->n);
+    OSH_DISPATCH_ACT(act, ACT,
+                     hipLaunchKernelGGL((conv16s_kernel<TM, BV, TWL, S, ACT>), grid, dim3(256), 0, st, *p, x, w, bias,
+                                        res, y, tiles_w));
+    OSH_LAUNCH_CHECK("conv16s_kernel");
+    return OSH_OK;
+}
+
+template <int TM, int BV, int TWL>
+inline osh_status conv16s_launch_s(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                   const float *res, int act, float *y, hipStream_t st) {
+    if (p->sh == 1) return conv16s_launch_t<TM, BV, TWL, 1>(p, x, w, bias, res, act, y, st);
+    return conv16s_launch_t<TM, BV, TWL, 2>(p, x, w, bias, res, act, y, st);
+}
+
+inline osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                 const float *res, int act, float *y, hipStream_t st, int v) {
+    switch (v) {
+    case 0: return conv16s_launch_s<1, 1, 16>(p, x, w, bias, res, act, y, st);
+    case 1: return conv16s_launch_s<1, 2, 16>(p, x, w, bias, res, act, y, st);
+    case 2: return conv16s_launch_s<1, 4, 16>(p, x, w, bias, res, act, y, st);
+    case 3: return conv16s_launch_s<2, 2, 16>(p, x, w, bias, res, act, y, st);
+    case 4: return conv16s_launch_s<1, 1, 8>(p, x, w, bias, res, act, y, st);
+    case 5: return conv16s_launch_s<1, 2, 8>(p, x, w, bias, res, act, y, st);
+    case 6: return conv16s_launch_s<2, 2, 8>(p, x, w, bias, res, act, y, st);
+    case 7: return conv16s_launch_s<1, 2, 4>(p, x, w, bias, res, act, y, st);
+    default: return conv16s_launch_s<1, 4, 4>(p, x, w, bias, res, act, y, st);
+    }
+}
+
+}  // namespace osh

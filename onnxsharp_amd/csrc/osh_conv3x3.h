@@ -71,6 +71,7 @@ template <int S, int TH, int ACT>
 __global__ __launch_bounds__(TH * 2 * 64) void conv3x3_kernel(osh_conv_params p, const float *__restrict__ x,
                                                              const float *__restrict__ wpk,
                                                              const float *__restrict__ bias,
+                                                             const float *__restrict__ res,
                                                              float *__restrict__ y) {
     constexpr int CI = C3_CI;
     static_assert(CI == 8, "the operand layout splits a chunk into two groups of four channels");
@@ -194,25 +195,30 @@ __global__ __launch_bounds__(TH * 2 * 64) void conv3x3_kernel(osh_conv_params p,
 
     const int oy = oy0 + wrow, ox = ox0 + l32;
     if (oy < p.oh && ox < p.ow) {
-        float *yrow = y + ((long long)n * p.m) * p.oh * p.ow + (long long)oy * p.ow + ox;
+        const long long base = ((long long)n * p.m) * p.oh * p.ow + (long long)oy * p.ow + ox;
+        float *yrow = y + base;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             int oc = oc_base + 8 * (r >> 2) + 4 * lhi + (r & 3);
-            if (oc < p.m) yrow[(long long)oc * p.oh * p.ow] = activate<ACT>(acc[r]);
+            if (oc < p.m) {
+                float v = activate<ACT>(acc[r]);
+                if (res) v += res[base + (long long)oc * p.oh * p.ow];
+                yrow[(long long)oc * p.oh * p.ow] = v;
+            }
         }
     }
 }
 
 inline osh_status conv3x3_launch(const osh_conv_params *p, const float *x, const float *wpk, const float *bias,
-                                 int act, float *y, hipStream_t st) {
+                                 const float *res, int act, float *y, hipStream_t st) {
     constexpr int TH = 2;
     const int mtiles = (p->m + C3_BM - 1) / C3_BM;
     dim3 grid((p->ow + 31) / 32, (p->oh + TH - 1) / TH, p->n * mtiles);
     dim3 block(TH * 2 * 64);
     if (p->sh == 1) {
-        OSH_DISPATCH_ACT(act, ACT, hipLaunchKernelGGL((conv3x3_kernel<1, TH, ACT>), grid, block, 0, st, *p, x, wpk, bias, y));
+        OSH_DISPATCH_ACT(act, ACT, hipLaunchKernelGGL((conv3x3_kernel<1, TH, ACT>), grid, block, 0, st, *p, x, wpk, bias, res, y));
     } else {
-        OSH_DISPATCH_ACT(act, ACT, hipLaunchKernelGGL((conv3x3_kernel<2, TH, ACT>), grid, block, 0, st, *p, x, wpk, bias, y));
+        OSH_DISPATCH_ACT(act, ACT, hipLaunchKernelGGL((conv3x3_kernel<2, TH, ACT>), grid, block, 0, st, *p, x, wpk, bias, res, y));
     }
     OSH_LAUNCH_CHECK("conv3x3_kernel");
     return OSH_OK;

@@ -38,8 +38,12 @@ __global__ __launch_bounds__(256) void add4_kernel(const float4 *__restrict__ a,
     }
 }
 
-// One thread per output element.  The running maximum starts at the first
-// in-range window element; later elements replace it only when greater.
+// One thread per output element.  The comparison of the reference's scalar
+// path (MaxPoolLayer.Forward, src/OnnxSharp/Ops/DnnOps.cs:1564-1579): the
+// maximum starts at -inf and takes an in-range element only when it is
+// greater, so NaN inputs are skipped.  (The reference's 8-wide path uses
+// Vector256.Max, whose NaN result depends on the operand order; for inputs
+// without NaN both paths give the same bits.)
 __global__ __launch_bounds__(256) void maxpool2d_kernel(osh_pool_params p, const float *__restrict__ x,
                                                          float *__restrict__ y, long long total) {
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -50,8 +54,7 @@ __global__ __launch_bounds__(256) void maxpool2d_kernel(osh_pool_params p, const
     const long long plane = t / p.oh;
     const float *xp = x + plane * p.h * p.w;
     const int iy0 = oy * p.sh - p.pt, ix0 = ox * p.sw - p.pl;
-    float m = 0.f;
-    bool any = false;
+    float m = -__builtin_inff();
     for (int ky = 0; ky < p.kh; ky++) {
         const int iy = iy0 + ky;
         if ((unsigned)iy >= (unsigned)p.h) continue;
@@ -59,11 +62,88 @@ __global__ __launch_bounds__(256) void maxpool2d_kernel(osh_pool_params p, const
             const int ix = ix0 + kx;
             if ((unsigned)ix >= (unsigned)p.w) continue;
             const float v = xp[(long long)iy * p.w + ix];
-            if (!any || v > m) m = v;
-            any = true;
+            if (v > m) m = v;
         }
     }
     y[idx] = m;
+}
+
+// Three chained k x k, stride 1, pad k/2 max pools (SPPF: y1 = pool(x),
+// y2 = pool(y1), y3 = pool(y2)) in one launch.  A workgroup owns a PT x PT
+// tile of one plane: it stages x over the tile plus a 3r halo in LDS, then
+// computes y1 over the tile plus 2r, y2 over the tile plus r and y3 over the
+// tile, each from the previous level in LDS.  Every output is the same
+// comparison as maxpool2d_kernel (start at -inf, keep v when v > max, so
+// positions outside the image and NaNs are never taken), so the chain is
+// bit-identical to three separate pools.
+template <int K>
+__global__ __launch_bounds__(256) void maxpool_chain3_kernel(int h, int w, int c, const float *__restrict__ x,
+                                                             long long x_bstride, float *__restrict__ y1,
+                                                             float *__restrict__ y2, float *__restrict__ y3,
+                                                             long long y_bstride, int tiles_x) {
+    constexpr int PT = 32, R = K / 2;
+    constexpr int S0 = PT + 6 * R, S1 = PT + 4 * R, S2 = PT + 2 * R;
+    __shared__ float l0[S0 * S0], l1[S1 * S1], l2[S2 * S2];
+    const int plane = blockIdx.y;  // n * c + channel
+    const int n = plane / c, ch = plane - n * c;
+    const int ty = blockIdx.x / tiles_x, tx = blockIdx.x - ty * tiles_x;
+    const int oy0 = ty * PT, ox0 = tx * PT;
+    const long long xoff = (long long)n * x_bstride + (long long)ch * h * w;
+    const long long yoff = (long long)n * y_bstride + (long long)ch * h * w;
+    const float *xp = x + xoff;
+    // level 0: x at rows oy0 - 3R + i (only positions inside the image are read later)
+    for (int e = threadIdx.x; e < S0 * S0; e += 256) {
+        const int i = e / S0, jx = e - i * S0;
+        const int iy = oy0 - 3 * R + i, ix = ox0 - 3 * R + jx;
+        l0[e] = ((unsigned)iy < (unsigned)h && (unsigned)ix < (unsigned)w) ? xp[(long long)iy * w + ix] : 0.f;
+    }
+    __syncthreads();
+    // one pooling level: dst (size SD, origin o - DR) from src (size SS, origin o - SR)
+    auto level = [&](const float *src, int SS, int SR, float *dst, int SD, int DR) {
+        for (int e = threadIdx.x; e < SD * SD; e += 256) {
+            const int i = e / SD, jx = e - i * SD;
+            const int py = oy0 - DR + i, px = ox0 - DR + jx;
+            float m = -__builtin_inff();
+            if ((unsigned)py < (unsigned)h && (unsigned)px < (unsigned)w) {
+                for (int ky = 0; ky < K; ky++) {
+                    const int iy = py - R + ky;
+                    if ((unsigned)iy >= (unsigned)h) continue;
+                    for (int kx = 0; kx < K; kx++) {
+                        const int ix = px - R + kx;
+                        if ((unsigned)ix >= (unsigned)w) continue;
+                        const float v = src[(iy - (oy0 - SR)) * SS + (ix - (ox0 - SR))];
+                        if (v > m) m = v;
+                    }
+                }
+            }
+            dst[e] = m;
+        }
+    };
+    level(l0, S0, 3 * R, l1, S1, 2 * R);
+    __syncthreads();
+    level(l1, S1, 2 * R, l2, S2, R);
+    __syncthreads();
+    // y3 over the tile, and the tile's part of y1 and y2
+    for (int e = threadIdx.x; e < PT * PT; e += 256) {
+        const int i = e / PT, jx = e - i * PT;
+        const int py = oy0 + i, px = ox0 + jx;
+        if (py >= h || px >= w) continue;
+        float m = -__builtin_inff();
+        for (int ky = 0; ky < K; ky++) {
+            const int iy = py - R + ky;
+            if ((unsigned)iy >= (unsigned)h) continue;
+            for (int kx = 0; kx < K; kx++) {
+                const int ix = px - R + kx;
+                if ((unsigned)ix >= (unsigned)w) continue;
+                const float v = l2[(iy - (oy0 - R)) * S2 + (ix - (ox0 - R))];
+                if (v > m) m = v;
+            }
+        }
+        const long long o = yoff + (long long)py * w + px;
+        y1[o] = l1[(i + 2 * R) * S1 + jx + 2 * R];
+        y2[o] = l2[(i + R) * S2 + jx + R];
+        y3[o] = m;
+    }
 }
 
 __global__ __launch_bounds__(256) void resize_nearest_kernel(int c, int h, int w, int fh, int fw,
@@ -175,6 +255,33 @@ OSH_API osh_status osh_maxpool2d_f32(const osh_pool_params *p, const float *d_x,
     hipLaunchKernelGGL(maxpool2d_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), *p,
                        d_x, d_y, total);
     OSH_LAUNCH_CHECK("maxpool2d_kernel");
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_maxpool_chain3_f32(int n, int c, int h, int w, int k, const float *d_x, int64_t x_batch_stride,
+                                          float *d_y1, float *d_y2, float *d_y3, int64_t y_batch_stride,
+                                          osh_stream s) {
+    if (n <= 0 || c <= 0 || h <= 0 || w <= 0) return fail(OSH_E_INVALID, "MaxPool chain: bad sizes");
+    if (k != 3 && k != 5 && k != 7) return fail(OSH_E_UNSUPPORTED, "MaxPool chain: kernel %d (3, 5 or 7 supported)", k);
+    if (!d_x || !d_y1 || !d_y2 || !d_y3) return fail(OSH_E_INVALID, "MaxPool chain: NULL pointer");
+    const long long plane = (long long)c * h * w;
+    if (x_batch_stride < plane || y_batch_stride < plane)
+        return fail(OSH_E_INVALID, "MaxPool chain: batch stride below c*h*w");
+    if ((long long)n * c > 65535) return fail(OSH_E_UNSUPPORTED, "MaxPool chain: more than 65535 planes");
+    const int tiles_x = (w + 31) / 32, tiles_y = (h + 31) / 32;
+    if ((long long)tiles_x * tiles_y > 0x7fffffff) return fail(OSH_E_UNSUPPORTED, "MaxPool chain: image too large");
+    dim3 grid((unsigned)(tiles_x * tiles_y), (unsigned)(n * c));
+    hipStream_t st = to_stream(s);
+    if (k == 3)
+        hipLaunchKernelGGL(maxpool_chain3_kernel<3>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
+                           d_y1, d_y2, d_y3, (long long)y_batch_stride, tiles_x);
+    else if (k == 5)
+        hipLaunchKernelGGL(maxpool_chain3_kernel<5>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
+                           d_y1, d_y2, d_y3, (long long)y_batch_stride, tiles_x);
+    else
+        hipLaunchKernelGGL(maxpool_chain3_kernel<7>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
+                           d_y1, d_y2, d_y3, (long long)y_batch_stride, tiles_x);
+    OSH_LAUNCH_CHECK("maxpool_chain3_kernel");
     return OSH_OK;
 }
 

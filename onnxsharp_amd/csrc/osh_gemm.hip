@@ -52,6 +52,7 @@ static bool g16_fits(const IgemmArgs &a, const G16Variant &v) {
     if (a.lda % 4 || !aligned_to(a.A, 16) || a.strideA % 4 || a.strideA_in % 4) return false;
     if (a.ldb % al || !aligned_to(a.B, 4 * al) || a.strideB % al || a.strideB_in % al) return false;
     if (a.ldc % al || !aligned_to(a.C, 4 * al) || a.strideC % al || a.strideC_in % al) return false;
+    if (a.res && !aligned_to(a.res, 4 * al)) return false;  // residual rows share C's strides
     if (((long long)(a.M - 1) * a.lda + a.K) * 4 >= (1LL << 31)) return false;
     if (((long long)(a.K - 1) * a.ldb + a.N) * 4 >= (1LL << 31)) return false;
     return true;

@@ -108,6 +108,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(IgemmArgs p, int tiles_m) {
     const float *__restrict__ A = p.A + zo * p.strideA + zi * p.strideA_in;
     const float *__restrict__ B = p.B + zo * p.strideB + zi * p.strideB_in;
     float *__restrict__ C = p.C + zo * p.strideC + zi * p.strideC_in;
+    const float *__restrict__ R = p.res ? p.res + zo * p.strideC + zi * p.strideC_in : nullptr;
     const float *__restrict__ row_bias = p.row_bias ? p.row_bias + zi * p.bias_stride : nullptr;
     const int M = p.M, N = p.N, K = p.K, lda = p.lda, ldb = p.ldb;
     const int bytes_a = (int)(((long long)(M - 1) * lda + K) * 4);
@@ -301,6 +302,19 @@ __global__ __launch_bounds__(256) void gemm16_kernel(IgemmArgs p, int tiles_m) {
                     float v = acc[tm][tn * BV + q][r];
                     if (p.col_scale) v = __builtin_fmaf(v, cs[q], cb[q]);
                     o[q] = activate<ACT>(v);
+                }
+                if (R) {  // residual: same layout as C, BV-wide loads
+                    const float *src = R + (long long)row * p.ldc + col;
+                    if constexpr (BV == 4) {
+                        const float4 t = *reinterpret_cast<const float4 *>(src);
+                        o[0] += t.x, o[1] += t.y, o[2] += t.z, o[3] += t.w;
+                    } else if constexpr (BV == 2) {
+                        const float2 t = *reinterpret_cast<const float2 *>(src);
+                        o[0] += t.x, o[1] += t.y;
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < BV; q++) o[q] += src[q];
+                    }
                 }
                 float *dst = C + (long long)row * p.ldc + col;
                 if constexpr (BV == 4) *reinterpret_cast<float4 *>(dst) = make_float4(o[0], o[1], o[2], o[3]);

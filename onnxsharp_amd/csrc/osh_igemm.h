@@ -34,6 +34,7 @@ struct IgemmArgs {
     const float *row_bias;   // indexed by m (+ z-slice offset bias_stride)
     const float *col_bias;   // indexed by n
     const float *col_scale;  // indexed by n
+    const float *res;        // optional residual, laid out as C: C = act(...) + res
     int bias_stride;         // row_bias offset per z-slice (conv groups)
     int zdiv;                // z = outer * zdiv + inner; strides apply as below
     long long strideA_in, strideB_in, strideC_in;  // per inner index (conv group)
@@ -72,6 +73,7 @@ __global__ __launch_bounds__(WM *WN * 64) void igemm_f32_kernel(IgemmArgs p) {
     const float *__restrict__ A = p.A + zo * p.strideA + zi * p.strideA_in;
     const float *__restrict__ B = p.B + zo * p.strideB + zi * p.strideB_in;
     float *__restrict__ Cp = p.C + zo * p.strideC + zi * p.strideC_in;
+    const float *__restrict__ Rp = p.res ? p.res + zo * p.strideC + zi * p.strideC_in : nullptr;
     const float *__restrict__ row_bias = p.row_bias ? p.row_bias + zi * p.bias_stride : nullptr;
     const int M = p.M, N = p.N, K = p.K;
 
@@ -254,7 +256,9 @@ __global__ __launch_bounds__(WM *WN * 64) void igemm_f32_kernel(IgemmArgs p) {
                 if (gm < M) {
                     float v = acc[tm][tn][r];
                     if (p.col_scale) v = __builtin_fmaf(v, cs, cb);
-                    Cp[(long long)gm * p.ldc + gn] = activate<ACT>(v);
+                    v = activate<ACT>(v);
+                    if (Rp) v += Rp[(long long)gm * p.ldc + gn];
+                    Cp[(long long)gm * p.ldc + gn] = v;
                 }
             }
         }

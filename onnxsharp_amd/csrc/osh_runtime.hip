@@ -86,7 +86,8 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         return OSH_OK;
     }
     if (strcmp(key, "conv16_variant") == 0) {
-        if (value < -2 || value > 11) return fail(OSH_E_INVALID, "conv16_variant %d out of range [-2, 12)", value);
+        if (value < -2 || value >= conv16_variant_count())
+            return fail(OSH_E_INVALID, "conv16_variant %d out of range [-2, %d)", value, conv16_variant_count());
         g_conv16_variant = value;
         return OSH_OK;
     }
@@ -111,6 +112,10 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     }
     if (strcmp(key, "conv16_variant") == 0) {
         *value = conv16_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "conv16_variants") == 0) {
+        *value = conv16_variant_count();
         return OSH_OK;
     }
     if (strcmp(key, "tune") == 0) {

@@ -100,7 +100,9 @@ class ConvLayer:
         return p, buf
 
     def forward(self, x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
-                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                out: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """y = act(conv(x) + bias), plus `residual` (the shortcut operand of a
+        following Add, same shape as y) when given: one launch for both."""
         x = _need_f32("input", x)
         key = (w.data_ptr(), tuple(w.shape), tuple(x.shape), w._version)
         if self._packed is None or self._packed[0] != key:
@@ -115,6 +117,13 @@ class ConvLayer:
             out = torch.empty(y_shape, dtype=torch.float32, device=x.device)
         elif tuple(out.shape) != y_shape or not out.is_contiguous():
             raise ValueError(f"Conv '{self.name}': output must be a contiguous {y_shape} tensor")
+        if residual is not None:
+            residual = _need_f32("residual", residual)
+            if tuple(residual.shape) != y_shape:
+                raise ValueError(f"Conv '{self.name}': residual must have the output shape {y_shape}")
+            N.call("osh_conv2d_add_f32", C.byref(p), _ptr(x), _ptr(buf), _ptr(bias),
+                   N.ACTIVATIONS[self.fused_activation], _ptr(residual), _ptr(out), C.c_void_p(_stream()))
+            return out
         N.call("osh_conv2d_f32", C.byref(p), _ptr(x), _ptr(buf), _ptr(bias), N.ACTIVATIONS[self.fused_activation],
                _ptr(out), C.c_void_p(_stream()))
         return out

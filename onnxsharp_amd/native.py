@@ -89,6 +89,7 @@ _SIGS = {
     "osh_conv_packed_weight_bytes": ([C.POINTER(ConvParams), C.POINTER(_sz)], _i),
     "osh_conv_pack_weights": ([C.POINTER(ConvParams), _vp, _vp, _vp], _i),
     "osh_conv2d_f32": ([C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp], _i),
+    "osh_conv2d_add_f32": ([C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp, _vp], _i),
     "osh_gemm_f32": ([_i, _i, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _vp], _i),
     "osh_gemm_f32_batched": ([_i, _i, _i, _i, _vp, _i, _i64, _vp, _i, _i64, _vp, _i, _vp, _i, _i64, _vp], _i),
     "osh_matmul_infer_shape": ([_i64p, _i, _i64p, _i, _i64p, C.POINTER(C.c_int)], _i),
@@ -103,6 +104,7 @@ _SIGS = {
     "osh_activation_f32": ([_i64, _vp, _i, _vp, _vp], _i),
     "osh_add_f32": ([_i64, _vp, _vp, _vp, _vp], _i),
     "osh_maxpool2d_f32": ([C.POINTER(PoolParams), _vp, _vp, _vp], _i),
+    "osh_maxpool_chain3_f32": ([_i, _i, _i, _i, _i, _vp, _i64, _vp, _vp, _vp, _i64, _vp], _i),
     "osh_resize_nearest_f32": ([_i, _i, _i, _i, _i, _i, _vp, _vp, _i64, _vp], _i),
     "osh_transpose_f32": ([_i, _i, _i, _vp, _i64, _vp, _i64, _vp], _i),
     "osh_softmax_f32": ([_i64, _i, C.c_float, _vp, _vp, _vp], _i),

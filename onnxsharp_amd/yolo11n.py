@@ -83,6 +83,7 @@ class ConvOp:
     act: str | None
     w: np.ndarray
     b: np.ndarray
+    res: Slice = None  # residual added after the activation (a fused Add)
 
     @property
     def flops(self):
@@ -105,6 +106,16 @@ class MaxPoolOp:
     k: int = 5
     s: int = 1
     p: int = 2
+
+
+@dataclass(eq=False)
+class PoolChainOp:
+    """Three chained k x k, stride 1, pad k/2 MaxPools whose outputs are the
+    three adjacent channel slices of y (y1, y2, y3), as in SPPF."""
+    name: str
+    x: Slice
+    y: Slice
+    k: int = 5
 
 
 @dataclass(eq=False)
@@ -258,11 +269,11 @@ class _Builder:
         b1 = self.add(f"{q}/Add", b, pr)
         f0 = self.conv(f"{q}/ffn/ffn.0/conv/Conv", b1, 2 * c, 1, 1)
         f1 = self.conv(f"{q}/ffn/ffn.1/conv/Conv", f0, c, 1, 1, act=None)
-        cat2 = self.buf(f"{p}/Concat#out", 2 * c, x.h, x.w)
-        self.m.ops.append(AddOp(f"{q}/Add_1", b1, f1, Slice(cat2, c, c)))
-        # the first half of the concat is cv1's first split output
-        self.m.ops.append(CopyOp(f"{p}/Split#0", Slice(cat, 0, c), Slice(cat2, 0, c)))
-        return self.conv(f"{p}/cv2/conv/Conv", whole(cat2), c_out, 1, 1, y=y)
+        # Concat(split output 0, block output): the block output replaces the
+        # split's second half (b is not read after the ffn's residual Add), so
+        # the concat is cv1's own buffer and needs no copy
+        self.m.ops.append(AddOp(f"{q}/Add_1", b1, f1, Slice(cat, c, c)))
+        return self.conv(f"{p}/cv2/conv/Conv", whole(cat), c_out, 1, 1, y=y)
 
     def detect(self, p, xs, nc=80, reg_max=16):
         c2 = max(16, xs[0].c // 4, reg_max * 4)
@@ -328,10 +339,106 @@ def build(size: int = 640, seed: int = 7000) -> Model:
 
 # ------------------------------------------------------------ stream planning
 
+def fuse_residual_adds(model: Model) -> Model:
+    """The model with every Add whose operand is a conv output read by nothing
+    else folded into that conv as a residual input (ConvOp.res), so that
+    conv + Add run as one launch (osh_conv2d_add_f32).  The operand may also be
+    tiled by several convs (the per-head parts of one depthwise conv): each
+    part then takes the matching channels of the other operand and of the
+    Add's output.  Results are unchanged: the conv's output is rounded as
+    before and the sum is the same single addition."""
+    ops = list(model.ops)
+    readers = {}
+    for i, op in enumerate(ops):
+        for r in op_access(op)[0]:
+            readers.setdefault(id(r.buf), set()).add(i)
+    out_bufs = {id(b) for b in model.outputs}
+    fused, drop = {}, set()
+    for i, op in enumerate(ops):
+        if not isinstance(op, AddOp):
+            continue
+        for opnd, other in ((op.b, op.a), (op.a, op.b)):
+            buf = opnd.buf
+            if opnd.c0 != 0 or opnd.c != buf.c or id(buf) in out_bufs or readers.get(id(buf)) != {i}:
+                continue
+            prod = [j for j in range(i) if any(w.buf is buf for w in op_access(ops[j])[1])]
+            if not prod or any(not isinstance(ops[j], ConvOp) or ops[j].res is not None or j in fused
+                               for j in prod):
+                continue
+            if sorted((ops[j].y.c0, ops[j].y.c) for j in prod) != _tiling(buf.c, [ops[j].y for j in prod]):
+                continue
+            # the convs move their write of the Add's output back to their own
+            # position: nothing in between may touch it or rewrite the other operand
+            first = min(prod)
+            between = [k for k in range(first + 1, i) if k not in prod]
+            if any(_overlap(a, op.y) for k in between for a in op_access(ops[k])[0] + op_access(ops[k])[1]):
+                continue
+            if any(_overlap(w, other) for k in between for w in op_access(ops[k])[1]):
+                continue
+            if _overlap(other, op.y) or any(_overlap(ops[j].x, op.y) for j in prod):
+                continue
+            for j in prod:
+                cv = ops[j]
+                fused[j] = ConvOp(cv.name + "+" + op.name, cv.x, op.y.sub(cv.y.c0, cv.y.c), cv.k, cv.s, cv.group,
+                                  cv.act, cv.w, cv.b, res=other.sub(cv.y.c0, cv.y.c))
+            drop.add(i)
+            break
+    new_ops = [fused.get(j, o) for j, o in enumerate(ops) if j not in drop]
+    used = {id(model.input)} | out_bufs
+    for o in new_ops:
+        r, w = op_access(o)
+        used.update(id(t.buf) for t in r + w)
+    m = Model(model.size, [b for b in model.bufs if id(b) in used], new_ops, model.input, list(model.outputs))
+    return m
+
+
+def fuse_pool_chains(model: Model) -> Model:
+    """Every run of three MaxPools (k x k, stride 1, pad k/2) that pool each
+    other's output into three adjacent slices of one buffer becomes one
+    PoolChainOp (osh_maxpool_chain3_f32: one launch, same results)."""
+    ops = list(model.ops)
+    out, i = [], 0
+    while i < len(ops):
+        t = ops[i:i + 3]
+        if (len(t) == 3 and all(isinstance(o, MaxPoolOp) for o in t)
+                and all(o.k == t[0].k and o.s == 1 and o.p == o.k // 2 for o in t)
+                and t[1].x == t[0].y and t[2].x == t[1].y
+                and t[0].y.buf is t[1].y.buf is t[2].y.buf
+                and t[1].y.c0 == t[0].y.c0 + t[0].y.c and t[2].y.c0 == t[1].y.c0 + t[1].y.c
+                and t[0].y.c == t[0].x.c == t[1].y.c == t[2].y.c
+                and not _overlap(t[0].x, Slice(t[0].y.buf, t[0].y.c0, 3 * t[0].y.c))):
+            out.append(PoolChainOp(t[0].name.rsplit("/", 2)[0] + "/MaxPool#chain3", t[0].x,
+                                   Slice(t[0].y.buf, t[0].y.c0, 3 * t[0].y.c), t[0].k))
+            i += 3
+        else:
+            out.append(ops[i])
+            i += 1
+    return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
+
+
+def fuse_launches(model: Model) -> Model:
+    """The launch-saving rewrites of the op list (residual Adds into their
+    convs, SPPF's pool chain into one op); results are unchanged."""
+    return fuse_pool_chains(fuse_residual_adds(model))
+
+
+def _tiling(c, slices):
+    """[(c0, c)] of slices that tile channels [0, c) exactly, in order, else None."""
+    parts = sorted((s.c0, s.c) for s in slices)
+    at = 0
+    for c0, n in parts:
+        if c0 != at:
+            return None
+        at += n
+    return parts if at == c else None
+
+
 def op_access(op):
     """(reads, writes) of an op as lists of channel slices."""
     if isinstance(op, AddOp):
         return [op.a, op.b], [op.y]
+    if isinstance(op, ConvOp) and op.res is not None:
+        return [op.x, op.res], [op.y]
     if isinstance(op, AttentionOp):
         return [op.qkv], [op.y, whole(op.qt), whole(op.attn), whole(op.attn_t)]
     return [op.x], [op.y]
@@ -405,8 +512,10 @@ class Frame:
     branches -- the detection head's six chains, the P3 head beside the rest
     of the neck -- run side by side."""
 
-    def __init__(self, model: Model, device, nstreams: int = 4):
+    def __init__(self, model: Model, device, nstreams: int = 4, fuse: bool = True):
         import torch
+        if fuse:  # conv -> residual Add pairs and SPPF's pools run as single launches
+            model = fuse_launches(model)
         self.model = model
         self.device = device
         for b in model.bufs:
@@ -454,6 +563,10 @@ class Frame:
                    self.stream)
             self._keep += [p, w, b, packed]
             act = N.ACTIVATIONS[op.act]
+            if op.res is not None:
+                return lambda st: N.check(lib.osh_conv2d_add_f32(C.byref(p), op.x.ptr(), C.c_void_p(packed.data_ptr()),
+                                                                 C.c_void_p(b.data_ptr()), act, op.res.ptr(),
+                                                                 op.y.ptr(), st))
             return lambda st: N.check(lib.osh_conv2d_f32(C.byref(p), op.x.ptr(), C.c_void_p(packed.data_ptr()),
                                                          C.c_void_p(b.data_ptr()), act, op.y.ptr(), st))
         if isinstance(op, AddOp):
@@ -466,6 +579,13 @@ class Frame:
             pp = N.PoolParams(1, op.x.c, op.x.h, op.x.w, op.k, op.k, op.s, op.s, op.p, op.p, op.y.h, op.y.w)
             self._keep.append(pp)
             return lambda st: N.check(lib.osh_maxpool2d_f32(C.byref(pp), op.x.ptr(), op.y.ptr(), st))
+        if isinstance(op, PoolChainOp):
+            c, hw = op.x.c, op.x.h * op.x.w
+            y1 = op.y.sub(0, c)
+            y2, y3 = op.y.sub(c, c), op.y.sub(2 * c, c)
+            xs, ys = op.x.buf.c * hw, op.y.buf.c * hw
+            return lambda st: N.check(lib.osh_maxpool_chain3_f32(1, c, op.x.h, op.x.w, op.k, op.x.ptr(), xs, y1.ptr(),
+                                                                 y2.ptr(), y3.ptr(), ys, st))
         if isinstance(op, UpsampleOp):
             return lambda st: N.check(lib.osh_resize_nearest_f32(1, op.x.c, op.x.h, op.x.w, op.f, op.f, op.x.ptr(),
                                                                  op.y.ptr(), op.y.c * op.y.h * op.y.w, st))

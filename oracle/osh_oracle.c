@@ -34,7 +34,7 @@
  *                       row: max, e = exp(x - max) summed, scale by 1/sum; the sum runs
  *                       sequentially here, in 8 vector lanes there: parity unpinned at that
  *                       rounding)
- *   orc_maxpool2d_f32   DnnOps.cs:1335-1480 (max over the in-range window elements)
+ *   orc_maxpool2d_f32   DnnOps.cs:1335-1580 (scalar path :1564-1579: -inf, then v > best)
  *   orc_resize_nearest  DnnOps.cs:2215-2330 (nearest, integer factor: source index dst / factor)
  *
  * Build: see oracle/Makefile (gcc, -O3 -ffp-contract=off; fmaf is explicit).
@@ -510,8 +510,9 @@ ORC_API void orc_maxpool2d_f32(int N, int C, int H, int W, int kh, int kw, int s
         float *yp = y + pl_ * OH * OW;
         for (int oy = 0; oy < OH; oy++)
             for (int ox = 0; ox < OW; ox++) {
-                float m = 0.0f;
-                int any = 0;
+                /* the scalar path of the reference (DnnOps.cs:1564-1579): start at
+                 * -inf, keep v when v > best, so NaN inputs are never taken */
+                float m = -INFINITY;
                 for (int ky = 0; ky < kh; ky++) {
                     int iy = oy * sh - pt + ky;
                     if (iy < 0 || iy >= H) continue;
@@ -519,8 +520,7 @@ ORC_API void orc_maxpool2d_f32(int N, int C, int H, int W, int kh, int kw, int s
                         int ix = ox * sw - pl + kx;
                         if (ix < 0 || ix >= W) continue;
                         float v = xp[(long)iy * W + ix];
-                        if (!any || v > m) m = v;
-                        any = 1;
+                        if (v > m) m = v;
                     }
                 }
                 yp[(long)oy * OW + ox] = m;

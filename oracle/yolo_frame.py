@@ -12,7 +12,7 @@ attention core uses the GEMM chain for both MatMuls and the oracle softmax.
 import numpy as np
 
 
-def conv(oracle, op, x):
+def conv(oracle, op, x, res=None):
     k, s, pad = op.k, op.s, op.k // 2
     out_hw = (op.y.h, op.y.w)
     if op.group > 1 and op.group == op.x.c == op.y.c:
@@ -23,6 +23,8 @@ def conv(oracle, op, x):
                               order=oracle.ORDER_NCHWC if nchwc else oracle.ORDER_IM2COL)
     if op.act == "Silu":
         y = oracle.silu_ref(y)
+    if res is not None:  # a fused residual Add: one float addition per element
+        y = (y + res).astype(np.float32)
     return y
 
 
@@ -45,13 +47,18 @@ def run_op(oracle, op, inputs):
     """Output of one op from its input arrays (in the op's own input order)."""
     from onnxsharp_amd import yolo11n as Y
     if isinstance(op, Y.ConvOp):
-        return conv(oracle, op, inputs[0])
+        return conv(oracle, op, inputs[0], inputs[1] if op.res is not None else None)
     if isinstance(op, Y.AddOp):
         return (inputs[0] + inputs[1]).astype(np.float32)
     if isinstance(op, Y.CopyOp):
         return inputs[0].copy()
     if isinstance(op, Y.MaxPoolOp):
         return oracle.maxpool2d(inputs[0], op.k, op.s, op.p)
+    if isinstance(op, Y.PoolChainOp):  # three pools in turn, outputs side by side
+        y1 = oracle.maxpool2d(inputs[0], op.k, 1, op.k // 2)
+        y2 = oracle.maxpool2d(y1, op.k, 1, op.k // 2)
+        y3 = oracle.maxpool2d(y2, op.k, 1, op.k // 2)
+        return np.concatenate([y1, y2, y3], axis=1)
     if isinstance(op, Y.UpsampleOp):
         return oracle.resize_nearest(inputs[0], op.f)
     if isinstance(op, Y.AttentionOp):
@@ -66,6 +73,8 @@ def op_inputs(op):
         return [op.a, op.b]
     if isinstance(op, Y.AttentionOp):
         return [op.qkv]
+    if isinstance(op, Y.ConvOp) and op.res is not None:
+        return [op.x, op.res]
     return [op.x]
 
 

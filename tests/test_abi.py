@@ -131,3 +131,18 @@ def test_size_queries():
     p = ConvLayer(pads=[1, 1, 1, 1]).resolve((1, 64, 160, 160), (64, 64, 3, 3))
     N.call("osh_conv_packed_weight_bytes", C.byref(p), C.byref(s))
     assert s.value == 64 * 64 * 9 * 4
+
+
+def test_conv_add_rejects_a_residual_overlapping_the_output():
+    # checked before anything touches memory: the pointers are never dereferenced
+    p = ConvLayer(pads=[1, 1, 1, 1]).resolve((1, 16, 8, 8), (16, 16, 3, 3))
+    lib = N.lib()
+    base = 1 << 40
+    nbytes = 16 * 8 * 8 * 4
+    for res in (base, base + nbytes - 4, base - nbytes + 4):
+        st = lib.osh_conv2d_add_f32(C.byref(p), C.c_void_p(1 << 41), C.c_void_p(1 << 42), None, 0,
+                                    C.c_void_p(res), C.c_void_p(base), None)
+        assert st == N.OSH_E_INVALID and "overlaps" in N.last_error(), hex(res)
+    st = lib.osh_conv2d_add_f32(C.byref(p), C.c_void_p(1 << 41), C.c_void_p(1 << 42), None, 0, None,
+                                C.c_void_p(base), None)
+    assert st == N.OSH_E_INVALID and "NULL" in N.last_error()

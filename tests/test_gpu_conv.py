@@ -140,23 +140,29 @@ CONV16_CASES = [
     ("odd_16to40_s1_33x45", (1, 16, 33, 45), (40, 16, 3, 3), dict(pads=[1, 1, 1, 1])),
     ("odd_32to72_s2_41x37", (2, 32, 41, 37), (72, 32, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
     ("pads_0_2_valid_like", (1, 48, 17, 23), (24, 48, 3, 3), dict(pads=[0, 2, 2, 0])),
+    ("stride3_16to16_20", (1, 16, 20, 20), (16, 16, 3, 3), dict(strides=[3, 3], pads=[1, 1, 1, 1])),
+    ("tall_narrow_32to16_70x9", (1, 32, 70, 9), (16, 32, 3, 3), dict(pads=[1, 1, 1, 1])),
 ]
 
 
 @pytest.mark.parametrize("name,xs,ws,attrs", CONV16_CASES, ids=[c[0] for c in CONV16_CASES])
 def test_conv16_is_the_nchwc_chain(cuda, oracle, name, xs, ws, attrs):
-    # 3x3 convolutions with C % 16 == 0 run the in-order 16x16x4 kernel: bit for
-    # bit the reference's NCHWc chain (bias, then icb -> ky -> kx -> lane16),
-    # whatever wave tile is forced.
+    # 3x3 convolutions with C % 16 == 0 run the in-order 16x16x4 kernels: bit
+    # for bit the reference's NCHWc chain (bias, then icb -> ky -> kx -> lane16),
+    # whatever tile is forced -- weights streamed or in LDS, or the input patch
+    # staged in LDS (stride 1 and 2; other strides fall back to the cost model).
     from onnxsharp_amd import native as N
     seed = sum(xs) * 3 + sum(ws)
     x = synth.uniform(seed, xs)
     w = synth.normal(seed + 1, ws, 0, 0.05)
     b = synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    nv = C.c_int()
+    N.call("osh_config_get", b"conv16_variants", C.byref(nv))
+    assert nv.value >= 21
     N.call("osh_config_set", b"exact_silu", 1)
     try:
         ref = None
-        for v in [-1] + list(range(12)):
+        for v in [-1] + list(range(nv.value)):
             print(f"conv16 {name} variant {v}", flush=True)
             N.call("osh_config_set", b"conv16_variant", v)
             y, p = run_conv(cuda, x, w, b, "Silu", **attrs)
@@ -199,3 +205,47 @@ def test_weight_stationary_kernels(cuda, oracle, name, xs, ws, attrs, exact):
     assert_fp32_close(y, ref, name)
     if exact:
         assert np.array_equal(y, ref), f"{name}: max |d| {np.abs(y - ref).max():.3e}"
+
+
+RESIDUAL_CASES = [
+    # (name, x, w, attrs, conv16_variant) -- one per kernel family of the dispatch
+    ("conv16_3x3_64to64_40", (1, 64, 40, 40), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1]), 4),
+    ("conv16l_3x3_32to32_20_batch2", (2, 32, 20, 20), (32, 32, 3, 3), dict(pads=[1, 1, 1, 1]), 10),
+    ("conv16s_3x3_32to48_s2_batch2", (2, 32, 21, 19), (48, 32, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), 17),
+    ("conv16s_3x3_64to64_40", (1, 64, 40, 40), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1]), 13),
+    ("conv16_tuned_16to32_80", (1, 16, 80, 80), (32, 16, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
+    ("gemm16_1x1_128to64_20", (1, 128, 20, 20), (64, 128, 1, 1), dict(), -1),
+    ("igemm_1x1_c6_odd", (2, 6, 13, 11), (10, 6, 1, 1), dict(), -1),
+    ("direct3x3_c8_160", (1, 8, 160, 160), (16, 8, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
+    ("depthwise_64_20", (1, 64, 20, 20), (64, 1, 3, 3), dict(group=64, pads=[1, 1, 1, 1]), -1),
+    ("first_conv_c3", (1, 3, 64, 64), (16, 3, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
+    ("im2col_dilated_5x5", (1, 5, 23, 21), (7, 5, 5, 5), dict(pads=[4, 4, 4, 4], dilations=[2, 2]), -1),
+    ("wave_independent_16", (1, 16, 24, 32), (16, 16, 3, 3), dict(pads=[1, 1, 1, 1]), -2),
+    ("weight_stationary_s2", (1, 64, 40, 40), (64, 64, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), -2),
+]
+
+
+@pytest.mark.parametrize("name,xs,ws,attrs,variant", RESIDUAL_CASES, ids=[c[0] for c in RESIDUAL_CASES])
+def test_conv_residual_add_is_conv_then_add(cuda, name, xs, ws, attrs, variant):
+    # osh_conv2d_add_f32 = osh_conv2d_f32 followed by the Add, bit for bit:
+    # the epilogue rounds the activation output, then adds the residual once.
+    import torch
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    print(f"conv+add {name} x={xs} w={ws} variant={variant}", flush=True)
+    seed = sum(xs) * 11 + sum(ws)
+    x = _t(synth.uniform(seed, xs), cuda)
+    w = _t(synth.normal(seed + 1, ws, 0, 0.05), cuda)
+    b = _t(synth.normal(seed + 2, (ws[0],), 0, 0.01), cuda)
+    N.call("osh_config_set", b"conv16_variant", variant)
+    try:
+        layer = ConvLayer(fused_activation="Silu", **attrs)
+        plain = layer.forward(x, w, b)
+        res = torch.from_numpy(synth.normal(seed + 3, tuple(plain.shape), 0, 1)).to(cuda)
+        fused = layer.forward(x, w, b, residual=res)
+        torch.cuda.synchronize()
+    finally:
+        N.call("osh_config_set", b"conv16_variant", -1)
+    expect = plain.cpu().numpy() + res.cpu().numpy()
+    got = fused.cpu().numpy()
+    assert np.array_equal(got, expect), f"max |d| {np.abs(got - expect).max():.3e}"

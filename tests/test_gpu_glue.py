@@ -1,0 +1,150 @@
+"""GPU parity of the frame's continuity ops through the C ABI: Add, MaxPool,
+the SPPF pool chain, nearest Resize, Transpose and Softmax against the
+oracle's restatements (bit-exact for the exact ops; Softmax within the FP32
+bar), including odd sizes and batch strides.  MaxPool inputs carry NaNs: the
+device follows the reference's scalar comparison (start at -inf, take v when
+v > max: NaNs are skipped).  The reference's 8-wide path (Vector256.Max)
+treats a NaN by operand order instead, so NaN results are pinned to the
+scalar path only; inputs without NaN give the same bits on both paths."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from conftest import assert_fp32_close
+from onnxsharp_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, cuda):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(cuda)
+
+
+def _p(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("n,aligned", [(1 << 20, True), (1001, True), (4096, False)])
+def test_add_exact_and_in_place(cuda, n, aligned):
+    import torch
+    from onnxsharp_amd import native as N
+    a = synth.normal(900 + n, (n + 1,), 0, 1)
+    b = synth.normal(901 + n, (n + 1,), 0, 1)
+    off = 0 if aligned else 1  # a 4-byte offset takes the scalar kernel
+    da, db = _dev(a, cuda), _dev(b, cuda)
+    y = torch.empty(n + 1, device=cuda)
+    N.call("osh_add_f32", n, C.c_void_p(da.data_ptr() + 4 * off), C.c_void_p(db.data_ptr() + 4 * off),
+           C.c_void_p(y.data_ptr() + 4 * off), None)
+    # in place: y aliases a
+    N.call("osh_add_f32", n, C.c_void_p(da.data_ptr() + 4 * off), C.c_void_p(db.data_ptr() + 4 * off),
+           C.c_void_p(da.data_ptr() + 4 * off), None)
+    torch.cuda.synchronize()
+    expect = (a[off:off + n] + b[off:off + n]).astype(np.float32)
+    assert np.array_equal(y.cpu().numpy()[off:off + n], expect)
+    assert np.array_equal(da.cpu().numpy()[off:off + n], expect)
+
+
+POOLS = [((1, 128, 20, 20), 5, 1, 2), ((2, 3, 33, 47), 3, 2, 1), ((1, 4, 16, 16), 2, 2, 0), ((1, 2, 9, 7), 7, 1, 3)]
+
+
+@pytest.mark.parametrize("shape,k,s,p", POOLS, ids=[f"{s}_k{k}s{st}p{p}" for s, k, st, p in POOLS])
+def test_maxpool_matches_oracle_with_nans(cuda, oracle, shape, k, s, p):
+    import torch
+    from onnxsharp_amd import native as N
+    x = synth.normal(910 + k, shape, 0, 1)
+    x.reshape(-1)[::37] = np.nan  # skipped by the comparison
+    n, c, h, w = shape
+    oh, ow = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+    pp = N.PoolParams(n, c, h, w, k, k, s, s, p, p, oh, ow)
+    dx = _dev(x, cuda)
+    y = torch.empty((n, c, oh, ow), device=cuda)
+    N.call("osh_maxpool2d_f32", C.byref(pp), _p(dx), _p(y), None)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y.cpu().numpy()), _bits(oracle.maxpool2d(x, k, s, p)))
+
+
+CHAINS = [((1, 128, 20, 20), 5), ((2, 5, 70, 45), 5), ((1, 3, 40, 33), 3), ((1, 2, 37, 64), 7), ((1, 1, 1, 1), 5)]
+
+
+@pytest.mark.parametrize("shape,k", CHAINS, ids=[f"{s}_k{k}" for s, k in CHAINS])
+def test_pool_chain_is_three_pools(cuda, oracle, shape, k):
+    # one launch = three osh_maxpool2d_f32 launches in turn, bit for bit (NaNs
+    # included), with the outputs written as channel slices of one buffer
+    import torch
+    from onnxsharp_amd import native as N
+    n, c, h, w = shape
+    print(f"pool chain {shape} k={k}", flush=True)
+    x = synth.normal(920 + k + h, shape, 0, 1)
+    x.reshape(-1)[::29] = np.nan
+    cat = torch.full((n, 4 * c, h, w), float("inf"), device=cuda)
+    cat[:, :c] = _dev(x, cuda)
+    hw = h * w
+    base = cat.data_ptr()
+    ys = [C.c_void_p(base + 4 * (i + 1) * c * hw) for i in range(3)]
+    N.call("osh_maxpool_chain3_f32", n, c, h, w, k, C.c_void_p(base), 4 * c * hw, ys[0], ys[1], ys[2], 4 * c * hw,
+           None)
+    # the same through three single pools
+    pp = N.PoolParams(n, c, h, w, k, k, 1, 1, k // 2, k // 2, h, w)
+    prev = _dev(x, cuda)
+    singles = []
+    for _ in range(3):
+        nxt = torch.empty((n, c, h, w), device=cuda)
+        N.call("osh_maxpool2d_f32", C.byref(pp), _p(prev), _p(nxt), None)
+        singles.append(nxt)
+        prev = nxt
+    torch.cuda.synchronize()
+    got = cat.cpu().numpy()
+    assert np.array_equal(_bits(got[:, :c]), _bits(x))  # input untouched
+    ref = x
+    for i in range(3):
+        ref = oracle.maxpool2d(ref, k, 1, k // 2)
+        part = got[:, (i + 1) * c:(i + 2) * c]
+        assert np.array_equal(_bits(part), _bits(singles[i].cpu().numpy())), f"pool {i + 1} vs single launch"
+        assert np.array_equal(_bits(part), _bits(ref)), f"pool {i + 1} vs oracle"
+
+
+@pytest.mark.parametrize("shape,f", [((1, 256, 20, 20), 2), ((2, 3, 7, 5), 3)])
+def test_resize_nearest_into_a_channel_slice(cuda, oracle, shape, f):
+    import torch
+    from onnxsharp_amd import native as N
+    n, c, h, w = shape
+    x = synth.normal(930 + f, shape, 0, 1)
+    out = torch.zeros((n, c + 5, h * f, w * f), device=cuda)
+    dx = _dev(x, cuda)
+    N.call("osh_resize_nearest_f32", n, c, h, w, f, f, _p(dx), _p(out), (c + 5) * h * f * w * f, None)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:, :c], oracle.resize_nearest(x, f))
+    assert not got[:, c:].any()
+
+
+@pytest.mark.parametrize("batch,rows,cols", [(2, 400, 32), (1, 33, 65), (3, 1, 17)])
+def test_transpose_last_two_axes(cuda, batch, rows, cols):
+    import torch
+    from onnxsharp_amd import native as N
+    x = synth.normal(940 + rows, (batch, rows, cols), 0, 1)
+    dx = _dev(x, cuda)
+    y = torch.empty((batch, cols, rows), device=cuda)
+    N.call("osh_transpose_f32", batch, rows, cols, _p(dx), rows * cols, _p(y), rows * cols, None)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), x.transpose(0, 2, 1))
+
+
+@pytest.mark.parametrize("rows,cols,scale", [(800, 400, 32 ** -0.5), (7, 1000, 1.0), (3, 5, 10.0)])
+def test_softmax_within_fp32_bar(cuda, oracle, rows, cols, scale):
+    import torch
+    from onnxsharp_amd import native as N
+    x = synth.normal(950 + cols, (rows, cols), 0, 4)
+    dx = _dev(x, cuda)
+    y = torch.empty_like(dx)
+    N.call("osh_softmax_f32", rows, cols, C.c_float(scale), _p(dx), _p(y), None)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert_fp32_close(got, oracle.softmax(x, scale), f"softmax {rows}x{cols}")
+    assert np.allclose(got.sum(axis=1), 1.0, atol=1e-5)

@@ -294,6 +294,19 @@ def test_maxpool_matches_brute_force(oracle):
         assert np.array_equal(y, ref), (k, s, p)
 
 
+def test_maxpool_skips_nans_like_the_scalar_path(oracle):
+    # DnnOps.cs:1564-1579: best = -inf; best = v when v > best.  A NaN never
+    # wins, wherever it sits in the window; a window of NaNs only stays -inf.
+    x = np.array([[[[np.nan, 1.0, -2.0], [np.nan, np.nan, np.nan], [3.0, np.nan, -5.0]]]], np.float32)
+    y = oracle.maxpool2d(x, 3, 1, 1)
+    xp = np.pad(x[0, 0], 1, constant_values=-np.inf)
+    expect = np.array([[np.nanmax(xp[i:i + 3, j:j + 3]) for j in range(3)] for i in range(3)], np.float32)
+    assert np.array_equal(y[0, 0], expect)
+    assert y[0, 0, 0, 0] == 1.0 and y[0, 0, 2, 0] == 3.0 and y[0, 0, 2, 2] == -5.0
+    z = oracle.maxpool2d(np.full((1, 1, 2, 2), np.nan, np.float32), 1, 1, 0)
+    assert (z == -np.inf).all()
+
+
 def test_resize_nearest_is_repeat(oracle):
     x = np.random.default_rng(7).standard_normal((1, 4, 5, 3)).astype(np.float32)
     assert np.array_equal(oracle.resize_nearest(x, 2), x.repeat(2, axis=2).repeat(2, axis=3))

@@ -6,6 +6,7 @@ graph has the fixture's 87 device convolutions (its 88th, the DFL conv, stays
 on the host).  CPU only: shape inference, no kernels."""
 import os
 
+import numpy as np
 import pytest
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -76,13 +77,72 @@ def test_outputs_and_flops(model):
     assert model.flops - conv == 2 * 2 * 400 ** 2 * (32 + 64)
 
 
+def test_residual_fusion_folds_every_add(model):
+    # every Add of the frame follows the conv that feeds it and is that conv's
+    # only reader: all 14 fold into their convs (the attention Add into both
+    # per-head parts of the positional depthwise conv)
+    from onnxsharp_amd import yolo11n as Y
+    f = Y.fuse_residual_adds(model)
+    adds = [op for op in model.ops if isinstance(op, Y.AddOp)]
+    assert len(adds) == 14
+    assert not any(isinstance(op, Y.AddOp) for op in f.ops)
+    fused = [op for op in f.ops if isinstance(op, Y.ConvOp) and op.res is not None]
+    assert len(fused) == 15
+    assert len(f.ops) == len(model.ops) - 14
+    for op in fused:
+        assert not Y._overlap(op.res, op.y) and not Y._overlap(op.x, op.y)
+    # the outputs the adds produced are now written by the convs
+    assert {id(op.y.buf) for op in adds} <= {id(op.y.buf) for op in fused}
+    # buffers of the folded conv outputs are gone
+    assert len(f.bufs) < len(model.bufs)
+
+
+def test_residual_fusion_keeps_a_shared_conv_output():
+    # a conv output that another op also reads must stay a tensor of its own
+    from onnxsharp_amd import yolo11n as Y
+    bd = Y._Builder(32, 1)
+    x = Y.whole(bd.buf("x", 16, 8, 8))
+    bd.m.input = x.buf
+    t = bd.conv("c1", x, 16, 3, 1)
+    a = bd.add("a1", x, t)
+    u = bd.conv("c2", t, 16, 1, 1)  # second reader of t
+    bd.m.outputs = [a.buf, u.buf]
+    f = Y.fuse_residual_adds(bd.m)
+    assert [type(o).__name__ for o in f.ops] == ["ConvOp", "AddOp", "ConvOp"]
+
+
+def test_sppf_pools_become_one_chain(model):
+    from onnxsharp_amd import yolo11n as Y
+    f = Y.fuse_launches(model)
+    chains = [op for op in f.ops if isinstance(op, Y.PoolChainOp)]
+    assert len(chains) == 1 and not any(isinstance(op, Y.MaxPoolOp) for op in f.ops)
+    ch = chains[0]
+    assert (ch.x.c, ch.y.c, ch.y.c0, ch.k, ch.x.h) == (128, 384, 128, 5, 20)
+    assert len(f.ops) == len(model.ops) - 14 - 2
+
+
+def test_fused_frame_equals_unfused_frame_on_the_oracle(model, oracle):
+    # the fused op list computes the same bits as the ONNX node order
+    from onnxsharp_amd import synth, yolo11n as Y
+    from oracle import yolo_frame as YO
+    small = Y.build(64)
+    x = synth.uniform(4245, (1, 3, 64, 64))
+    ref = YO.Frame(small).run(oracle, x)
+    got = YO.Frame(Y.fuse_launches(small)).run(oracle, x)
+    for g, r in zip(got, ref):
+        assert np.array_equal(g, r)
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["onnx_order", "fused"])
 @pytest.mark.parametrize("nstreams", [1, 2, 4])
-def test_stream_plan_orders_every_dependency(model, nstreams):
+def test_stream_plan_orders_every_dependency(model, nstreams, fused):
     # Vector clocks over the planned streams: for each op, the latest op of
     # each stream known complete when it starts (stream order plus the event
     # waits).  Every read-after-write, write-after-write and write-after-read
     # pair of ops must be ordered.
     from onnxsharp_amd import yolo11n as Y
+    if fused:
+        model = Y.fuse_launches(model)
     plan, waits, recorded = Y.plan_streams(model.ops, nstreams)
     acc = [Y.op_access(o) for o in model.ops]
     clock = [[-1] * nstreams for _ in range(nstreams)]  # per stream: clock before its next op
