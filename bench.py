@@ -9,6 +9,7 @@ reference publishes a CPU number for).  Other workloads (--config):
   c1   MatMul + Add(bias) fused: A[1024,768] x B[768,768] + bias[768], U(-1,1)
   c3a  1x1 conv 256->128 @ 80x80 + bias + SiLU
   c3b  3x3 stride-2 conv 128->256, 80x80 -> 40x40 + bias + SiLU
+  c3c  C2f bottleneck block 128->128 @ 80x80 (1x1, 3x3, 3x3 + residual Add, 1x1; concat/split by slices)
   c4   YOLO11n frame at 640x640 (87 convolutions + C2PSA attention + SPPF/upsample/concat/add glue),
        replayed as one HIP graph; random N(0,0.05) weights, input U(0,1); DFL/NMS stay on the host
   c5   int8 DynamicQuantizeMatMul A f32[512,512] N(0,1), W s8[512,2048], per-column scales, bias
@@ -194,23 +195,23 @@ class DqmmWorkload(Workload):
         return oracle.dqmm(self.a_np, self.w_np, None, self.ws_np, self.bias_np)[0]
 
 
-class YoloWorkload(Workload):
-    """One YOLO11n frame per step: the frame's ~120 launches recorded once as a
-    HIP graph and replayed, inputs resident on the device."""
+class FrameWorkload(Workload):
+    """A block of ops (yolo11n.Model) per step: the launches recorded once as
+    a HIP graph and replayed, inputs resident on the device.
+    ONNXSHARP_HIP_FRAME_MODE: "graph" (default, one serial HIP graph),
+    "segments" (per-stream segments as child graphs of one DAG) or "eager"
+    (launches issued from the host on the planned streams)."""
 
-    def __init__(self, dev):
-        from onnxsharp_amd import synth, yolo11n
-        self.name = "c4"
-        self.kernel = "yolo11n frame (HIP graph)"
-        self.model = yolo11n.build(640)
+    def __init__(self, dev, name, model, x_np, label):
+        from onnxsharp_amd import yolo11n
+        self.name = name
+        self.kernel = label
+        self.model = model
         self.fr = yolo11n.Frame(self.model, dev)
-        self.x_np = synth.uniform(4000, (1, 3, 640, 640))
+        self.x_np = x_np
         self.fr.set_input(self.x_np)
         self.fr.run()
         self.fr.sync()
-        # ONNXSHARP_HIP_FRAME_MODE: "graph" (default, one serial HIP graph),
-        # "segments" (per-stream segments as child graphs of one DAG) or
-        # "eager" (launches issued from the host on the planned streams)
         self.mode = os.environ.get("ONNXSHARP_HIP_FRAME_MODE", "graph")
         if self.mode not in ("graph", "segments", "eager"):
             raise SystemExit(f"ONNXSHARP_HIP_FRAME_MODE={self.mode!r}: expected graph, segments or eager")
@@ -221,14 +222,6 @@ class YoloWorkload(Workload):
         # each tensor read or written once per op that touches it
         self.bytes = 4.0 * sum(op.x.c * op.x.h * op.x.w + op.w.size + op.b.size + op.y.c * op.y.h * op.y.w
                                for op in self.model.convs)
-        nconv = len(self.model.convs)
-        self.config = {"workload": "YOLO11n backbone+neck+head, batch 1, 640x640, FP32 NCHW, "
-                                   f"{nconv} conv launches + attention/SPPF/upsample/add glue in one HIP graph",
-                       "input": "U(0,1) [1,3,640,640], splitmix64 seed 4000",
-                       "weights": "N(0,0.05) conv weights, N(0,0.01) biases (BatchNorm folded), seeds 7000+",
-                       "conv_gflop": round(sum(o.flops for o in self.model.convs) / 1e9, 4),
-                       "outputs": "3 head tensors [1,144,80,80], [1,144,40,40], [1,144,20,20]; "
-                                  "DFL/NMS on the host"}
 
     def step(self, stream):
         if self.mode == "eager":
@@ -241,8 +234,8 @@ class YoloWorkload(Workload):
         return yolo_frame.Frame(self.model).run(oracle, self.x_np)
 
     def host_roundtrip_ms(self, frames=20):
-        """ms per frame with the input copied in and the head tensors copied
-        out through pinned host memory (PCIe included)."""
+        """ms per step with the input copied in and the outputs copied out
+        through pinned host memory (PCIe included)."""
         import torch
         from onnxsharp_amd import native as N
         hin = torch.from_numpy(self.x_np).pin_memory()
@@ -265,6 +258,40 @@ class YoloWorkload(Workload):
         for _ in range(frames):
             frame()
         return (time.perf_counter() - t0) / frames * 1e3
+
+
+class YoloWorkload(FrameWorkload):
+    """One YOLO11n frame per step (about a hundred launches in one graph)."""
+
+    def __init__(self, dev):
+        from onnxsharp_amd import synth, yolo11n
+        model = yolo11n.build(640)
+        super().__init__(dev, "c4", model, synth.uniform(4000, (1, 3, 640, 640)), "yolo11n frame (HIP graph)")
+        nconv = len(self.model.convs)
+        self.config = {"workload": "YOLO11n backbone+neck+head, batch 1, 640x640, FP32 NCHW, "
+                                   f"{nconv} conv launches + attention/SPPF/upsample/add glue in one HIP graph",
+                       "input": "U(0,1) [1,3,640,640], splitmix64 seed 4000",
+                       "weights": "N(0,0.05) conv weights, N(0,0.01) biases (BatchNorm folded), seeds 7000+",
+                       "conv_gflop": round(sum(o.flops for o in self.model.convs) / 1e9, 4),
+                       "outputs": "3 head tensors [1,144,80,80], [1,144,40,40], [1,144,20,20]; "
+                                  "DFL/NMS on the host"}
+
+
+class C2fWorkload(FrameWorkload):
+    """One depthwise-free C2f bottleneck block per step (four convolutions,
+    the shortcut Add folded into the second 3x3 conv), as one HIP graph."""
+
+    def __init__(self, dev):
+        from onnxsharp_amd import synth, yolo11n
+        model = yolo11n.build_c2f(80, 128, 128, 1, True)
+        super().__init__(dev, "c3c", model, synth.uniform(3300, (1, 128, 80, 80)), "C2f block (HIP graph)")
+        self.config = {"workload": "C2f(128->128, n=1, shortcut) @ 80x80, batch 1, FP32 NCHW: cv1 1x1 128->128 "
+                                   "+SiLU, split 64/64, bottleneck 3x3 64->64 +SiLU -> 3x3 64->64 +SiLU + residual "
+                                   "Add, concat 192, cv2 1x1 192->128 +SiLU",
+                       "input": "U(0,1) [1,128,80,80], splitmix64 seed 3300",
+                       "weights": "N(0,0.05) conv weights, N(0,0.01) biases, seeds 9000+",
+                       "conv_gflop": round(sum(o.flops for o in self.model.convs) / 1e9, 4),
+                       "launches": len(self.fr.model.ops)}
 
 
 class CopyWorkload(Workload):
@@ -306,6 +333,8 @@ def make_workload(name, dev):
         return DqmmWorkload(dev)
     if name == "c4":
         return YoloWorkload(dev)
+    if name == "c3c":
+        return C2fWorkload(dev)
     if name == "copy":
         return CopyWorkload(dev)
     raise SystemExit(f"unknown --config {name}")
@@ -406,6 +435,9 @@ def main():
     if wl.name == "c4":
         extra["ms_per_frame"] = round(ms_step, 4)
         extra["ms_per_frame_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
+    if wl.name == "c3c":
+        extra["ms_per_block"] = round(ms_step, 4)
+        extra["ms_per_block_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
     roof["kernel"] = wl.kernel
     roof["algorithmic_per_launch"] = {"flops": wl.flops, "bytes": wl.bytes}
 
@@ -419,6 +451,8 @@ def main():
                "host": hi}
         if wl.name == "c4":
             cpu["ms_per_frame"] = round(el4 / n4 * 1e3, 2)
+        if wl.name == "c3c":
+            cpu["ms_per_block"] = round(el4 / n4 * 1e3, 2)
         allc = hi.get("affinity_cpus") or hi.get("physical_cores") or 4
         allc = int(min(allc, hi.get("physical_cores", allc), 16))
         if allc != 4:

@@ -225,6 +225,18 @@ class _Builder:
             self.bottleneck(f"{p}/m.0", b, c, 3, 0.5, shortcut, y=Slice(cat, 2 * c, c))
         return self.conv(f"{p}/cv2/conv/Conv", whole(cat), c_out, 1, 1, y=y)
 
+    def c2f(self, p, x: Slice, c_out, n=1, shortcut=False, e=0.5, y: Slice = None):
+        """YOLOv8 C2f: cv1 (1x1) into two halves, n bottlenecks (two 3x3 convs,
+        e = 1.0, shortcut Add) on the second half, each appended to the
+        concat, then cv2 (1x1) over all (2 + n) parts."""
+        c = int(c_out * e)
+        cat = self.buf(f"{p}/Concat", (2 + n) * c, x.h, x.w)
+        self.conv(f"{p}/cv1/conv/Conv", x, 2 * c, 1, 1, y=Slice(cat, 0, 2 * c))
+        prev = Slice(cat, c, c)
+        for i in range(n):
+            prev = self.bottleneck(f"{p}/m.{i}", prev, c, 3, 1.0, shortcut, y=Slice(cat, (2 + i) * c, c))
+        return self.conv(f"{p}/cv2/conv/Conv", whole(cat), c_out, 1, 1, y=y)
+
     def sppf(self, p, x: Slice, c_out, y: Slice = None):
         c_ = x.c // 2
         cat = self.buf(f"{p}/Concat", 4 * c_, x.h, x.w)
@@ -334,6 +346,20 @@ def build(size: int = 640, seed: int = 7000) -> Model:
     bd.conv("/model.20/conv/Conv", o19, 128, 3, 2, y=Slice(cat21, 0, 128))
     o22 = bd.c3k2("/model.22", whole(cat21), 256, True, 0.5)
     m.outputs = bd.detect("/model.23", [o16, o19, o22])
+    return m
+
+
+def build_c2f(size: int = 80, c_in: int = 128, c_out: int = 128, n: int = 1, shortcut: bool = True,
+              seed: int = 9000) -> Model:
+    """One depthwise-free C2f block (batch 1, c_in x size x size in, c_out
+    out): cv1 1x1 c_in -> c_out, split in halves, n bottlenecks 3x3 -> 3x3 on
+    the second half with the shortcut Add, concat of (2 + n) halves, cv2 1x1.
+    Weights N(0, 0.05), biases N(0, 0.01) from `seed`."""
+    bd = _Builder(size, seed)
+    m = bd.m
+    m.input = bd.buf("x", c_in, size, size)
+    out = bd.c2f("/c2f", whole(m.input), c_out, n, shortcut)
+    m.outputs = [out.buf]
     return m
 
 

@@ -126,3 +126,32 @@ def test_yolo_graph_replay_matches_eager(cuda, parallel):
             torch.cuda.synchronize()
     finally:
         fr.close()
+
+
+@pytest.mark.parametrize("size,shortcut", [(80, True), (36, False)])
+def test_c2f_block_is_bit_exact(cuda, oracle, exact_silu, size, shortcut):
+    # every op of the C2f block is an exact restatement (1x1 convs: the GEMM
+    # chain; 3x3 convs: the NCHWc chain; the shortcut Add folded into the
+    # second 3x3 conv's epilogue), so the whole block matches the oracle bit
+    # for bit, eagerly and as a replayed graph
+    import torch
+    from oracle import yolo_frame as YO
+    from onnxsharp_amd import yolo11n
+    model = yolo11n.build_c2f(size, 128, 128, 1, shortcut)
+    fr = yolo11n.Frame(model, cuda)
+    try:
+        x = synth.uniform(4246 + size, (1, 128, size, size))
+        fr.set_input(x)
+        fr.run()
+        fr.sync()
+        got = fr.outputs()[0].cpu().numpy()
+        ref = YO.Frame(model).run(oracle, x)[0]
+        assert np.array_equal(got, ref), f"max |d| {np.abs(got - ref).max():.3e}"
+        fr.capture()
+        fr.outputs()[0].fill_(float("nan"))
+        torch.cuda.synchronize()
+        fr.launch()
+        fr.sync()
+        assert np.array_equal(fr.outputs()[0].cpu().numpy(), ref)
+    finally:
+        fr.close()

@@ -165,3 +165,20 @@ def test_stream_plan_orders_every_dependency(model, nstreams, fused):
         after.append(c)
     if nstreams > 1:
         assert len(set(plan)) > 1  # the head and the P3 branch do fork
+
+
+def test_c2f_block_structure():
+    # C2f(128 -> 128, n=1, shortcut) at 80 x 80: cv1 1x1 into the concat, the
+    # bottleneck's two 3x3 convs and the shortcut Add on the second half, cv2
+    # 1x1 over the 192-channel concat; the Add folds into the second 3x3 conv
+    from onnxsharp_amd import yolo11n as Y
+    m = Y.build_c2f(80, 128, 128, 1, True)
+    convs = [(o.k, o.x.c, o.y.c) for o in m.convs]
+    assert convs == [(1, 128, 128), (3, 64, 64), (3, 64, 64), (1, 192, 128)]
+    add = [o for o in m.ops if isinstance(o, Y.AddOp)]
+    assert len(add) == 1 and (add[0].y.c0, add[0].y.c, add[0].y.buf.c) == (128, 64, 192)
+    assert add[0].a.buf is add[0].y.buf and add[0].a.c0 == 64  # the shortcut is the split's second half
+    assert abs(sum(o.flops for o in m.convs) / 1e9 - 1.4680064) < 1e-9
+    f = Y.fuse_launches(m)
+    assert len(f.ops) == 4 and f.ops[2].res is not None and f.ops[2].res.c0 == 64
+    assert [(b.c, b.h, b.w) for b in m.outputs] == [(128, 80, 80)]
