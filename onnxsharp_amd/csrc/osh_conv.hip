@@ -203,7 +203,7 @@ static ConvAlgo select_algo(const osh_conv_params *p) {
 // Every conv16 wave tile computes the same chain, so the fastest one can be
 // chosen by measurement without changing any result: the first launch of a
 // shape on a stream that is not being captured times each tile that fits
-// (HIP events, one warm-up and three timed launches each, writing the real
+// (HIP events, two warm-up and ten timed launches each, writing the real
 // output every time) and remembers the winner per shape.  Launches recorded
 // into a graph before that use the cost model.
 static std::mutex g_tune_mu;
@@ -284,10 +284,10 @@ static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, 
     osh_status rc = OSH_OK;
     for (int v = 0; v < kC3Count && rc == OSH_OK; v++) {
         if (!c3_fits(p, v)) continue;
-        rc = c3_launch(p, x, w, bias, res, act, y, st, v);
+        for (int r = 0; r < 2 && rc == OSH_OK; r++) rc = c3_launch(p, x, w, bias, res, act, y, st, v);
         if (rc != OSH_OK) break;
         if (hipEventRecord(e0, st) != hipSuccess) { rc = fail(OSH_E_DEVICE, "hipEventRecord failed"); break; }
-        for (int r = 0; r < 3 && rc == OSH_OK; r++) rc = c3_launch(p, x, w, bias, res, act, y, st, v);
+        for (int r = 0; r < 10 && rc == OSH_OK; r++) rc = c3_launch(p, x, w, bias, res, act, y, st, v);
         if (rc != OSH_OK) break;
         float ms = 0.f;
         if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
