@@ -16,7 +16,10 @@ reference publishes a CPU number for).  Other workloads (--config):
   copy 64 MiB device-to-device copy (osh_memcpy_d2d): calibrates the HBM byte counters
 
 Prints ONE JSON line.  `value` is whole-job TFLOP/s (TOP/s for c5) from HIP
-events on the launch stream over exactly K back-to-back steps; `roofline`
+events on the launch stream over exactly K back-to-back steps (single-launch
+workloads: the K launches recorded once as a HIP graph after the warm-up and
+replayed, so host launch cost is not in the figure; `ms_per_step_eager` gives
+the same K steps issued one by one; `--eager` makes that the value); `roofline`
 prices the dominant kernel against the MI355X peak; `cpu_baseline` times the
 CPU oracle (a restatement of the reference's CPU kernels) on this host.
 """
@@ -85,6 +88,8 @@ def _t(x, dev):
 
 
 class ConvWorkload(Workload):
+    graphable = True
+
     def __init__(self, dev, name, xs, ws, stride, act, kernel, seed):
         import torch
         from onnxsharp_amd import native as N, synth
@@ -127,6 +132,8 @@ class ConvWorkload(Workload):
 
 
 class GemmWorkload(Workload):
+    graphable = True
+
     def __init__(self, dev):
         import torch
         from onnxsharp_amd import native as N, synth
@@ -157,6 +164,8 @@ class GemmWorkload(Workload):
 
 
 class DqmmWorkload(Workload):
+    graphable = True
+
     def __init__(self, dev):
         import torch
         from onnxsharp_amd import native as N, synth
@@ -340,31 +349,70 @@ def make_workload(name, dev):
     raise SystemExit(f"unknown --config {name}")
 
 
-def time_gpu(wl, steps, warmup):
+def time_gpu(wl, steps, warmup, graph=True):
+    """(device ms over exactly `steps` back-to-back steps, host wall s, eager
+    device ms or None).  Single-launch workloads (wl.graphable) are timed as
+    one HIP graph holding the `steps` launches, recorded after the warm-up
+    (which also runs the first-use tile tuning), so the figure is the device's
+    and not the Python launch loop's; the same steps issued one by one are
+    timed too and reported beside it.  Frame workloads replay their own graph
+    per step."""
     import torch
     from onnxsharp_amd import native as N
     sp = getattr(wl, "stream", None)
+    own = None
+    use_graph = graph and getattr(wl, "graphable", False)
     if sp is None:
-        sp = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        if use_graph:  # capture needs a stream of its own
+            own = C.c_void_p()
+            N.call("osh_stream_create", C.byref(own))
+            sp = own
+        else:
+            sp = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
     for _ in range(warmup):
         wl.step(sp)
+    N.call("osh_stream_sync", sp)
     torch.cuda.synchronize()
     e0, e1 = C.c_void_p(), C.c_void_p()
     N.call("osh_event_create", C.byref(e0))
     N.call("osh_event_create", C.byref(e1))
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    N.call("osh_event_record", e0, sp)
-    for _ in range(steps):
-        wl.step(sp)
-    N.call("osh_event_record", e1, sp)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = C.c_float()
-    N.call("osh_event_elapsed_ms", e0, e1, C.byref(ms))
+
+    def timed(run):
+        N.call("osh_stream_sync", sp)
+        t0 = time.perf_counter()
+        N.call("osh_event_record", e0, sp)
+        run()
+        N.call("osh_event_record", e1, sp)
+        N.call("osh_stream_sync", sp)
+        wall = time.perf_counter() - t0
+        ms = C.c_float()
+        N.call("osh_event_elapsed_ms", e0, e1, C.byref(ms))
+        return ms.value, wall
+
+    def eager():
+        for _ in range(steps):
+            wl.step(sp)
+
+    eager_ms = None
+    if use_graph:
+        g = C.c_void_p()
+        N.call("osh_graph_begin", sp)
+        try:
+            eager()
+        finally:
+            N.call("osh_graph_end", sp, C.byref(g))
+        N.call("osh_graph_launch", g, sp)  # one untimed replay
+        ms, wall = timed(lambda: N.call("osh_graph_launch", g, sp))
+        eager_ms, _ = timed(eager)
+        N.call("osh_graph_destroy", g)
+    else:
+        ms, wall = timed(eager)
     N.call("osh_event_destroy", e0)
     N.call("osh_event_destroy", e1)
-    return ms.value, wall
+    if own is not None:
+        N.call("osh_stream_destroy", own)
+    return ms, wall, eager_ms
 
 
 def cpu_baseline(wl, threads, budget_s):
@@ -399,6 +447,8 @@ def main():
     ap.add_argument("--config", default="c2")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="time the steps issued one by one (default: one HIP graph of the K launches)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU (every box here has one MI355X); "
@@ -415,7 +465,7 @@ def main():
     dev = torch.device("cuda", 0)
 
     wl = make_workload(args.config, dev)
-    ms, wall = time_gpu(wl, args.steps, args.warmup)
+    ms, wall, eager_ms = time_gpu(wl, args.steps, args.warmup, graph=not args.eager)
     ms_step = ms / args.steps
     tflops = wl.flops / (ms_step * 1e-3) / 1e12
     if wl.name == "copy":
@@ -432,6 +482,11 @@ def main():
                 "frac": round(tflops / PEAK["fp32_mfma_tflops"], 4)}
     roof["traffic"] = read_traffic(wl.kernel, wl.name)
     extra = {}
+    if eager_ms is not None:
+        extra["timing"] = f"HIP events around one HIP graph of the {args.steps} launches (recorded after the warm-up)"
+        extra["ms_per_step_eager"] = round(eager_ms / args.steps, 5)
+    elif getattr(wl, "graphable", False):
+        extra["timing"] = "HIP events around the launches issued one by one"
     if wl.name == "c4":
         extra["ms_per_frame"] = round(ms_step, 4)
         extra["ms_per_frame_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)

@@ -94,6 +94,16 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 kernels instead (summation order differs; within the FP32
  *                 tolerance).  Initial value from ONNXSHARP_HIP_CONV16_VARIANT.
  *   "conv16_variants" (get only): N, the number of 3x3 tiles.
+ *   "pointwise_variant": -1 (default) = 1x1 stride-1 convolutions with
+ *                 C % 16 == 0 pick, by the same first-use timing, between the
+ *                 GEMM tile over raw weights (0) and the LDS-tile kernel's
+ *                 tiles (1..N-1); all sum in the GEMM chain's order.  -2 = the
+ *                 GEMM path only.  Initial value from
+ *                 ONNXSHARP_HIP_POINTWISE_VARIANT.
+ *   "pointwise_variants" (get only): N.
+ *                 The -2 settings of "conv16_variant" and "pointwise_variant"
+ *                 change the packed weight layout: pack again after changing
+ *                 them.
  *   "tune": 1 (default) = the first launch of a 3x3 conv shape on a stream
  *                 that is not capturing times every conv16 tile (they all give
  *                 identical outputs) and keeps the fastest for that shape;

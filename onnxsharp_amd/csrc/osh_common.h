@@ -122,6 +122,12 @@ int gemm16_variant_count();
 int conv16_variant();
 int conv16_variant_count();
 
+// Forced tile for 1x1 convolutions with C % 16 == 0 (-1 = automatic, 0 = the
+// GEMM tile over raw weights, 1.. = the LDS-tile kernel, -2 = the GEMM path
+// only, weights packed raw) and the number of choices.
+int pointwise_variant();
+int pointwise_variant_count();
+
 // Whether kernels whose tiles all give identical results may pick their tile
 // by timing it on first use (osh_config "tune", ONNXSHARP_HIP_TUNE; default on).
 bool tuning_enabled();

@@ -183,12 +183,13 @@ static bool first_conv_eligible(const osh_conv_params *p) {
 }
 
 enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3, ALGO_WS3X3 = 4, ALGO_WI3X3 = 5,
-                ALGO_FIRST = 6, ALGO_CONV16 = 7 };
+                ALGO_FIRST = 6, ALGO_CONV16 = 7, ALGO_PW16 = 8 };
 
 static ConvAlgo select_algo(const osh_conv_params *p) {
     if (p->group == p->c && p->group == p->m && p->group > 1) return ALGO_DEPTHWISE;
     if (first_conv_eligible(p)) return ALGO_FIRST;
     if (conv16_variant() != -2 && conv16_eligible(p)) return ALGO_CONV16;
+    if (pointwise_variant() != -2 && pw16_eligible(p)) return ALGO_PW16;
     if (p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 && p->oh == p->h &&
         p->ow == p->w)
         return ALGO_POINTWISE;
@@ -203,14 +204,17 @@ static ConvAlgo select_algo(const osh_conv_params *p) {
 // Every conv16 wave tile computes the same chain, so the fastest one can be
 // chosen by measurement without changing any result: the first launch of a
 // shape on a stream that is not being captured times each tile that fits
-// (HIP events, two warm-up and ten timed launches each, writing the real
-// output every time) and remembers the winner per shape.  Launches recorded
+// (HIP events, two warm-up and ten timed launches each, in two passes over
+// the tiles, writing the real output every time) and remembers the winner
+// per shape.  Launches recorded
 // into a graph before that use the cost model.
 static std::mutex g_tune_mu;
-static std::map<std::tuple<int, int, int, int, int, int, int, int, int, int, int, int>, int> g_tuned;
+using ConvKey = std::tuple<int, int, int, int, int, int, int, int, int, int, int, int, int, int>;
+static std::map<std::tuple<int, ConvKey>, int> g_tuned;
 
-static std::tuple<int, int, int, int, int, int, int, int, int, int, int, int> conv_key(const osh_conv_params *p) {
-    return std::make_tuple(p->n, p->c, p->h, p->w, p->m, p->sh, p->sw, p->pt, p->pl, p->oh, p->ow, p->group);
+static ConvKey conv_key(const osh_conv_params *p) {
+    return std::make_tuple(p->n, p->c, p->h, p->w, p->m, p->kh, p->kw, p->sh, p->sw, p->pt, p->pl, p->oh, p->ow,
+                           p->group);
 }
 
 static bool capturing(hipStream_t st) {
@@ -223,6 +227,7 @@ static bool capturing(hipStream_t st) {
 // compute the same chain.
 constexpr int kC3Count = kC16Count + kC16sCount;
 int conv16_variant_count() { return kC3Count; }
+int pointwise_variant_count() { return 1 + kPW16Count; }
 
 static bool c3_fits(const osh_conv_params *p, int v) {
     if (v < kC16Count) return conv16_fits(p, kC16[v]);
@@ -262,41 +267,46 @@ static osh_status c3_launch(const osh_conv_params *p, const float *x, const floa
     return conv16_launch(p, x, w, bias, res, act, y, st, v < kC16Count ? v : -1);
 }
 
-static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                      const float *res, int act, float *y, hipStream_t st) {
-    const int forced = conv16_variant();
-    if (forced >= 0 || !tuning_enabled()) return c3_launch(p, x, w, bias, res, act, y, st, forced);
-    const auto key = conv_key(p);
+// Launches variant v (0 .. count-1) of a tile family, or the family's
+// cost-model pick for v < 0.  Tag separates families in the tuning table.
+template <class Fits, class Launch>
+static osh_status tuned_launch(const osh_conv_params *p, int tag, int count, int forced, Fits fits, Launch launch,
+                               hipStream_t st) {
+    if (forced >= 0 || !tuning_enabled()) return launch(forced >= 0 && forced < count && fits(forced) ? forced : -1);
+    const auto key = std::make_tuple(tag, conv_key(p));
     {
         std::lock_guard<std::mutex> lk(g_tune_mu);
         auto it = g_tuned.find(key);
-        if (it != g_tuned.end()) return c3_launch(p, x, w, bias, res, act, y, st, it->second);
+        if (it != g_tuned.end()) return launch(it->second);
     }
-    if (capturing(st)) return c3_launch(p, x, w, bias, res, act, y, st, -1);
+    if (capturing(st)) return launch(-1);
     hipEvent_t e0, e1;
     OSH_HIP_CHECK(hipEventCreate(&e0));
     if (hipEventCreate(&e1) != hipSuccess) {
         (void)hipEventDestroy(e0);
         return fail(OSH_E_DEVICE, "hipEventCreate failed");
     }
+    // two passes over all tiles, each tile keeping its faster pass, so a
+    // tile timed while the clock was still rising is not ruled out
     int best = -1;
     float best_ms = 0.f;
     osh_status rc = OSH_OK;
-    for (int v = 0; v < kC3Count && rc == OSH_OK; v++) {
-        if (!c3_fits(p, v)) continue;
-        for (int r = 0; r < 2 && rc == OSH_OK; r++) rc = c3_launch(p, x, w, bias, res, act, y, st, v);
-        if (rc != OSH_OK) break;
-        if (hipEventRecord(e0, st) != hipSuccess) { rc = fail(OSH_E_DEVICE, "hipEventRecord failed"); break; }
-        for (int r = 0; r < 10 && rc == OSH_OK; r++) rc = c3_launch(p, x, w, bias, res, act, y, st, v);
-        if (rc != OSH_OK) break;
-        float ms = 0.f;
-        if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
-            hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
-            rc = fail(OSH_E_DEVICE, "conv16 tuning: event timing failed");
-            break;
+    for (int pass = 0; pass < 2 && rc == OSH_OK; pass++)
+        for (int v = 0; v < count && rc == OSH_OK; v++) {
+            if (!fits(v)) continue;
+            for (int r = 0; r < 2 && rc == OSH_OK; r++) rc = launch(v);
+            if (rc != OSH_OK) break;
+            if (hipEventRecord(e0, st) != hipSuccess) { rc = fail(OSH_E_DEVICE, "hipEventRecord failed"); break; }
+            for (int r = 0; r < 10 && rc == OSH_OK; r++) rc = launch(v);
+            if (rc != OSH_OK) break;
+            float ms = 0.f;
+            if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
+                rc = fail(OSH_E_DEVICE, "conv tuning: event timing failed");
+                break;
+            }
+            if (best < 0 || ms < best_ms) best = v, best_ms = ms;
         }
-        if (best < 0 || ms < best_ms) best = v, best_ms = ms;
-    }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     if (rc != OSH_OK) return rc;
@@ -305,6 +315,13 @@ static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, 
         g_tuned[key] = best;
     }
     return OSH_OK;  // y already holds the result (every tile computes the same values)
+}
+
+static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                      const float *res, int act, float *y, hipStream_t st) {
+    return tuned_launch(
+        p, 3, kC3Count, conv16_variant(), [&](int v) { return c3_fits(p, v); },
+        [&](int v) { return c3_launch(p, x, w, bias, res, act, y, st, v); }, st);
 }
 
 static osh_status residual_add(const osh_conv_params *p, const float *res, float *y, hipStream_t st) {
@@ -394,6 +411,7 @@ OSH_API osh_status osh_conv_packed_weight_bytes(const osh_conv_params *p, size_t
     size_t oihw = (size_t)p->m * (p->c / p->group) * p->kh * p->kw * sizeof(float);
     switch (select_algo(p)) {
     case ALGO_CONV16: *bytes = conv16_packed_bytes(p); break;
+    case ALGO_PW16: *bytes = conv16_packed_bytes(p) + oihw; break;  // LDS-tile layout, then the raw GEMM operand
     case ALGO_WI3X3: *bytes = conv3x3_wi_packed_bytes(p); break;
     case ALGO_WS3X3: *bytes = conv3x3_ws_packed_bytes(p); break;
     case ALGO_DIRECT3X3: *bytes = conv3x3_packed_bytes(p); break;
@@ -408,6 +426,14 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
     if (st != OSH_OK) return st;
     if (!d_w || !d_packed) return fail(OSH_E_INVALID, "Conv pack: NULL pointer");
     if (select_algo(p) == ALGO_CONV16) return conv16_pack(p, d_w, d_packed, to_stream(s));
+    if (select_algo(p) == ALGO_PW16) {
+        st = conv16_pack(p, d_w, d_packed, to_stream(s));
+        if (st != OSH_OK) return st;
+        const size_t oihw = (size_t)p->m * p->c * sizeof(float);
+        OSH_HIP_CHECK(hipMemcpyAsync(static_cast<char *>(d_packed) + conv16_packed_bytes(p), d_w, oihw,
+                                     hipMemcpyDeviceToDevice, to_stream(s)));
+        return OSH_OK;
+    }
     if (select_algo(p) == ALGO_WI3X3) return conv3x3_wi_pack(p, d_w, d_packed, to_stream(s));
     if (select_algo(p) == ALGO_WS3X3) return conv3x3_ws_pack(p, d_w, d_packed, to_stream(s));
     if (select_algo(p) == ALGO_DIRECT3X3) return conv3x3_pack(p, d_w, d_packed, to_stream(s));
@@ -419,6 +445,15 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
 }  // extern "C"
 
 namespace osh {
+
+static osh_status igemm_conv(const osh_conv_params *p, const float *d_x, const float *w, const float *d_bias,
+                             const float *d_res, int act, float *d_y, hipStream_t stream, int bmode);
+
+// Pick among the pointwise LDS tiles without timing: on one MI355X the
+// smallest tile (16 channels x 16 pixels per wave, many waves per SIMD) was
+// fastest for every YOLO11n and C2f 1x1 shape measured; a map narrower than
+// 16 takes the 4-wide tile instead.
+static int pw16_pick(const osh_conv_params *p) { return p->ow >= 16 ? 0 : 5; }
 
 // Launches the conv of p: y = act(conv(x) + bias) (+ res when res is not NULL;
 // res has y's layout and does not overlap it).
@@ -473,9 +508,34 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
     }
     case ALGO_DIRECT3X3:
         return conv3x3_launch(p, d_x, w, d_bias, d_res, act, d_y, stream);
+    case ALGO_PW16: {
+        // 0: the GEMM tile over the raw weights; 1..: the LDS-tile kernel
+        const float *wraw = reinterpret_cast<const float *>(static_cast<const char *>(d_wpacked) +
+                                                            conv16_packed_bytes(p));
+        return tuned_launch(
+            p, 1, 1 + kPW16Count, pointwise_variant(), [](int) { return true; },
+            [&](int v) {
+                if (v == 0) return igemm_conv(p, d_x, wraw, d_bias, d_res, act, d_y, stream, B_DENSE);
+                if (v < 0) v = 1 + pw16_pick(p);
+                return pw16_launch(p, d_x, w, d_bias, d_res, act, d_y, stream, v - 1);
+            },
+            stream);
+    }
     case ALGO_POINTWISE:
-    case ALGO_IM2COL: {
-        const bool pw = select_algo(p) == ALGO_POINTWISE;
+    case ALGO_IM2COL:
+        return igemm_conv(p, d_x, w, d_bias, d_res, act, d_y, stream,
+                          select_algo(p) == ALGO_POINTWISE ? B_DENSE : B_IM2COL);
+    }
+    return fail(OSH_E_INVALID, "Conv: no kernel");
+}
+
+// The conv as an implicit GEMM over raw OIHW weights: W[M/g][C/g*kh*kw] x
+// (X dense for 1x1 s1 p0, else gathered), per image and group.
+static osh_status igemm_conv(const osh_conv_params *p, const float *d_x, const float *w, const float *d_bias,
+                             const float *d_res, int act, float *d_y, hipStream_t stream, int bmode) {
+    const int cpg = p->c / p->group, opg = p->m / p->group;
+    const long long in_hw = (long long)p->h * p->w, out_hw = (long long)p->oh * p->ow;
+    {
         IgemmArgs a{};
         a.M = opg;
         a.N = (int)out_hw;
@@ -499,10 +559,8 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         a.H = p->h; a.W = p->w; a.KH = p->kh; a.KW = p->kw;
         a.sh = p->sh; a.sw = p->sw; a.dh = p->dh; a.dw = p->dw;
         a.pt = p->pt; a.pl = p->pl; a.OW = p->ow;
-        return launch_igemm(a, p->n * p->group, pw ? B_DENSE : B_IM2COL, act, stream);
+        return launch_igemm(a, p->n * p->group, bmode, act, stream);
     }
-    }
-    return fail(OSH_E_INVALID, "Conv: no kernel");
 }
 
 static osh_status check_launch(const osh_conv_params *p, const float *d_x, const void *d_wpacked, int act,

@@ -328,11 +328,12 @@ __global__ __launch_bounds__(256) void conv16l_kernel(osh_conv_params p, const f
     }
 }
 
-// Pack OIHW weights into [ceil(M/16)][9C/16 k-groups][64 lanes][4 steps]:
-// lane (j, g), step s of k-group (icb, tap) holds w[16 mb + j][16 icb + 4 s + g][tap]
-// (zero for output channels past M).
-__global__ void conv16_pack_kernel(int M, int C, const float *__restrict__ w, float *__restrict__ out) {
-    const long long kgroups = (long long)(C / 16) * 9;
+// Pack OIHW weights (T taps per channel) into
+// [ceil(M/16)][C/16 * T k-groups][64 lanes][4 steps]: lane (j, g), step s of
+// k-group (icb, tap) holds w[16 mb + j][16 icb + 4 s + g][tap] (zero for output
+// channels past M).
+__global__ void conv16_pack_kernel(int M, int C, int T, const float *__restrict__ w, float *__restrict__ out) {
+    const long long kgroups = (long long)(C / 16) * T;
     const long long total = (long long)((M + 15) / 16) * kgroups * 256;
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= total) return;
@@ -342,9 +343,9 @@ __global__ void conv16_pack_kernel(int M, int C, const float *__restrict__ w, fl
     const int kg = (int)(t % kgroups);
     const int mb = (int)(t / kgroups);
     const int j = lane & 15, g = lane >> 4;
-    const int icb = kg / 9, tap = kg % 9;
+    const int icb = kg / T, tap = kg % T;
     const int oc = mb * 16 + j, ic = icb * 16 + 4 * s + g;
-    out[idx] = oc < M ? w[((long long)oc * C + ic) * 9 + tap] : 0.f;
+    out[idx] = oc < M ? w[((long long)oc * C + ic) * T + tap] : 0.f;
 }
 
 inline bool conv16_eligible(const osh_conv_params *p) {
@@ -354,13 +355,13 @@ inline bool conv16_eligible(const osh_conv_params *p) {
 }
 
 inline size_t conv16_packed_bytes(const osh_conv_params *p) {
-    return (size_t)((p->m + 15) / 16) * (p->c / 16) * 9 * 256 * sizeof(float);
+    return (size_t)((p->m + 15) / 16) * (p->c / 16) * p->kh * p->kw * 256 * sizeof(float);
 }
 
 inline osh_status conv16_pack(const osh_conv_params *p, const float *w, void *out, hipStream_t st) {
     const long long total = (long long)conv16_packed_bytes(p) / 4;
-    hipLaunchKernelGGL(conv16_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p->m, p->c, w,
-                       static_cast<float *>(out));
+    hipLaunchKernelGGL(conv16_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p->m, p->c,
+                       p->kh * p->kw, w, static_cast<float *>(out));
     OSH_LAUNCH_CHECK("conv16_pack_kernel");
     return OSH_OK;
 }

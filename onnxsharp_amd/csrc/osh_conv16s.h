@@ -58,26 +58,35 @@ constexpr int c16s_plane(int pr, int pitch, int twl, int s) {
     return c16s_plane_for(pr * pitch, pitch, twl, s) >= 0 ? c16s_plane_for(pr * pitch, pitch, twl, s) : pr * pitch;
 }
 
-template <int TM, int BV, int TWL, int S>
+// KS x KS kernel (3, or 1 for pointwise), stride S, CB 16-channel blocks per
+// staged chunk.
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC = false>
 struct C16sGeom {
+    static constexpr int T = KS * KS;                             // taps
     static constexpr int THL = 16 / TWL;                          // rows per lane group
     static constexpr int TH = THL * BV;                           // tile rows
-    static constexpr int PR = (TH - 1) * S + 3;                   // patch rows
-    static constexpr int PC = (TWL - 1) * S + 3;                  // patch columns
+    static constexpr int PR = (TH - 1) * S + KS;                  // patch rows
+    static constexpr int PC = (TWL - 1) * S + KS;                 // patch columns
     static constexpr int PITCH = c16s_pitch(PC, PR, TWL, S);      // floats per patch row
     static constexpr int PLANE = c16s_plane(PR, PITCH, TWL, S);   // floats per channel
-    static constexpr int CHUNK = 16 * PLANE;                      // one 16-channel block
-    static constexpr int ELEMS = 16 * PR * PC;                    // patch elements per block
-    static constexpr int NE = (ELEMS + 255) / 256;                // per thread
+    static constexpr int CHUNK = 16 * CB * PLANE;                 // one chunk of CB channel blocks
+    static constexpr int ELEMS = 16 * CB * PR * PC;               // patch elements per chunk
+    static constexpr int VW = VEC ? 4 : 1;                        // elements per staging load
+    static constexpr int NE = (ELEMS / VW + 255) / 256;           // staging loads per thread
+    static constexpr int NA = CB * T;                             // weight k-groups per chunk
 };
 
-template <int TM, int BV, int TWL, int S, int ACT>
+// VEC: the patch is staged with 16-byte loads of four adjacent columns (a
+// 1x1 stride-1 kernel on a map with W % 4 == 0 and a 16-byte aligned input).
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT>
 __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const float *__restrict__ x,
                                                       const float *__restrict__ wpk, const float *__restrict__ bias,
                                                       const float *__restrict__ res, float *__restrict__ y,
                                                       int tiles_w) {
-    using G = C16sGeom<TM, BV, TWL, S>;
+    using G = C16sGeom<TM, BV, TWL, S, KS, CB, VEC>;
     static_assert(16 % TWL == 0, "a lane group covers whole rows of the tile");
+    static_assert(!VEC || (KS == 1 && S == 1 && G::PC % 4 == 0 && G::PITCH % 4 == 0 && G::PLANE % 4 == 0),
+                  "16-byte staging needs whole, aligned four-column groups");
     __shared__ __align__(16) float lds[2 * G::CHUNK];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -89,54 +98,75 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
     const int HW = p.h * p.w, OHW = p.oh * p.ow;
     const int C = p.c, M = p.m;
     const int icbs = C / 16;
-    const int kgroups = icbs * 9;
+    const int kgroups = icbs * G::T;
+    const int nchunks = (icbs + CB - 1) / CB;
     const int mb0 = (blockIdx.y * 4 + wave) * TM;       // first 16-channel output block of this wave
     const bool active = mb0 * 16 < M;                    // uniform per wave
     const float *xn = x + (long long)n * C * HW;
     const int iy0 = oy0 * S - p.pt, ix0 = ox0 * S - p.pl;
 
-    // staging: element e = tid + 256 i of a block -> (channel, patch row, patch column)
+    // staging: element e = tid + 256 i of a chunk -> (channel, patch row, patch column);
+    // channels past C (a partial last chunk) lie past the buffer and read 0
+    // (with VEC, e counts groups of four columns; out-of-image groups lie wholly
+    // outside because W % 4 == 0 and tiles start at multiples of four)
+    constexpr int PCV = G::PC / G::VW;
     int goff[G::NE], loff[G::NE];
 #pragma unroll
     for (int i = 0; i < G::NE; i++) {
         const int e = tid + 256 * i;
-        const int ch = e / (G::PR * G::PC), rem = e - ch * (G::PR * G::PC);
-        const int r = rem / G::PC, c = rem - r * G::PC;
+        const int ch = e / (G::PR * PCV), rem = e - ch * (G::PR * PCV);
+        const int r = rem / PCV, c = (rem - r * PCV) * G::VW;
         const int iy = iy0 + r, ix = ix0 + c;
-        const bool ok = e < G::ELEMS && (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
+        const bool in = e < G::ELEMS / G::VW;
+        const bool ok = in && (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
         goff[i] = ok ? (ch * HW + iy * p.w + ix) * 4 : (int)C16_OOB;
-        loff[i] = e < G::ELEMS ? ch * G::PLANE + r * G::PITCH + c : -1;
+        loff[i] = in ? ch * G::PLANE + r * G::PITCH + c : -1;
     }
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc((void *)xn, (short)0, C * HW * 4, 0x00020000);
-    // two register sets: a block's patch is fetched two blocks before it is
-    // multiplied and written to LDS one block before
-    float sv0[G::NE], sv1[G::NE];
-    auto stage_load = [&](float (&sv)[G::NE], int icb) {
+    // two register sets: a chunk's patch is fetched two chunks before it is
+    // multiplied and written to LDS one chunk before
+    float sv0[G::NE * G::VW], sv1[G::NE * G::VW];
+    auto stage_load = [&](float (&sv)[G::NE * G::VW], int chunk) {
+        const int soff = chunk * CB * 16 * HW * 4;
 #pragma unroll
-        for (int i = 0; i < G::NE; i++)
-            sv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, goff[i], icb * 16 * HW * 4, 0));
+        for (int i = 0; i < G::NE; i++) {
+            if constexpr (VEC) {
+                auto v = __builtin_amdgcn_raw_buffer_load_b128(rx, goff[i], soff, 0);
+#pragma unroll
+                for (int u = 0; u < 4; u++) sv[4 * i + u] = __uint_as_float(v[u]);
+            } else {
+                sv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, goff[i], soff, 0));
+            }
+        }
     };
-    auto stage_store = [&](const float (&sv)[G::NE], int buf) {
+    auto stage_store = [&](const float (&sv)[G::NE * G::VW], int buf) {
 #pragma unroll
-        for (int i = 0; i < G::NE; i++)
-            if (loff[i] >= 0) lds[buf * G::CHUNK + loff[i]] = sv[i];
+        for (int i = 0; i < G::NE; i++) {
+            if (loff[i] < 0) continue;
+            if constexpr (VEC)
+                *reinterpret_cast<float4 *>(lds + buf * G::CHUNK + loff[i]) =
+                    make_float4(sv[4 * i], sv[4 * i + 1], sv[4 * i + 2], sv[4 * i + 3]);
+            else
+                lds[buf * G::CHUNK + loff[i]] = sv[i];
+        }
     };
 
-    // A: packed [mblock16][icb*9 + tap][64 lanes][4 steps]
+    // A: packed [mblock16][icb*T + tap][64 lanes][4 steps]; k-groups past the
+    // last block lie past the buffer and read 0
     const int bytes_w = ((M + 15) / 16) * kgroups * 64 * 16;
     const __amdgpu_buffer_rsrc_t rw =
         __builtin_amdgcn_make_buffer_rsrc((void *)wpk, (short)0, bytes_w, 0x00020000);
     int voa[TM];
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) voa[tm] = (((mb0 + tm) * kgroups) * 64 + lane) * 16;
-    float4 A0[9][TM], A1[9][TM];
-    auto load_a = [&](float4 (&A)[9][TM], int icb) {
+    float4 A0[G::NA][TM], A1[G::NA][TM];
+    auto load_a = [&](float4 (&A)[G::NA][TM], int chunk) {
 #pragma unroll
-        for (int t = 0; t < 9; t++)
+        for (int t = 0; t < G::NA; t++)
 #pragma unroll
             for (int tm = 0; tm < TM; tm++) {
-                auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, voa[tm], (icb * 9 + t) * 1024, 0);
+                auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, voa[tm], (chunk * G::NA + t) * 1024, 0);
                 A[t][tm] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                                        __uint_as_float(v[3]));
             }
@@ -155,16 +185,21 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
 
     // the lane's pixel (row j / TWL + THL q, column j % TWL) in patch coordinates
     const int lbase = g * G::PLANE + (j / TWL) * S * G::PITCH + (j % TWL) * S;
-    auto compute = [&](const float4 (&A)[9][TM], int buf) {
+    // a partial last chunk skips its missing channel blocks (no extra terms
+    // enter the chain)
+    auto compute = [&](const float4 (&A)[G::NA][TM], int buf, int chunk) {
         const float *lb = lds + buf * G::CHUNK + lbase;
 #pragma unroll
-        for (int t = 0; t < 9; t++) {
-            const int ky = t / 3, kx = t - 3 * (t / 3);
+        for (int t = 0; t < G::NA; t++) {
+            const int cb = t / G::T, tap = t - cb * G::T;
+            const int ky = tap / KS, kx = tap - KS * (tap / KS);
+            if (CB > 1 && chunk * CB + cb >= icbs) break;
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 float b[BV];
 #pragma unroll
-                for (int q = 0; q < BV; q++) b[q] = lb[4 * s * G::PLANE + (G::THL * q * S + ky) * G::PITCH + kx];
+                for (int q = 0; q < BV; q++)
+                    b[q] = lb[(16 * cb + 4 * s) * G::PLANE + (G::THL * q * S + ky) * G::PITCH + kx];
 #pragma unroll
                 for (int tm = 0; tm < TM; tm++) {
                     const float4 &a4 = A[t][tm];
@@ -178,7 +213,7 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
     };
 
     // prologue: block 0 in LDS, block 1 in flight, block 0's weights loaded
-    const int last = icbs - 1;
+    const int last = nchunks - 1;
     stage_load(sv0, 0);
     if (active) load_a(A0, 0);
     stage_store(sv0, 0);
@@ -190,19 +225,19 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
     // buffer.  Two trips per loop pass keep every set in fixed registers;
     // prefetch indices are clamped (reloads of the last block, never stored
     // past the patch) and every wave runs the same trips and barriers.
-    for (int icb = 0; icb < icbs; icb += 2) {
+    for (int icb = 0; icb < nchunks; icb += 2) {
         stage_load(sv0, min(icb + 2, last));
         if (active) {
             load_a(A1, min(icb + 1, last));
-            compute(A0, 0);
+            compute(A0, 0, icb);
         }
         stage_store(sv1, 1);
         __syncthreads();
-        if (icb + 1 >= icbs) break;
+        if (icb + 1 >= nchunks) break;
         stage_load(sv1, min(icb + 3, last));
         if (active) {
             load_a(A0, min(icb + 2, last));
-            compute(A1, 1);
+            compute(A1, 1, icb + 1);
         }
         stage_store(sv0, 0);
         __syncthreads();
@@ -242,16 +277,16 @@ inline bool conv16s_eligible(const osh_conv_params *p) {
     return conv16_eligible(p) && p->sh == p->sw && (p->sh == 1 || p->sh == 2);
 }
 
-template <int TM, int BV, int TWL, int S>
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC>
 inline osh_status conv16s_launch_t(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                    const float *res, int act, float *y, hipStream_t st) {
-    using G = C16sGeom<TM, BV, TWL, S>;
+    using G = C16sGeom<TM, BV, TWL, S, KS, CB, VEC>;
     const int tiles_w = ceil_div(p->ow, TWL), tiles_h = ceil_div(p->oh, G::TH);
     const int mgroups = ceil_div(ceil_div(p->m, 16), 4 * TM);
     dim3 grid((unsigned)(tiles_w * tiles_h), (unsigned)mgroups, (unsigned)p->n);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16s_kernel<TM, BV, TWL, S, ACT>), grid, dim3(256), 0, st, *p, x, w, bias,
-                                        res, y, tiles_w));
+                     hipLaunchKernelGGL((conv16s_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT>), grid, dim3(256), 0, st,
+                                        *p, x, w, bias, res, y, tiles_w));
     OSH_LAUNCH_CHECK("conv16s_kernel");
     return OSH_OK;
 }
@@ -259,8 +294,8 @@ inline osh_status conv16s_launch_t(const osh_conv_params *p, const float *x, con
 template <int TM, int BV, int TWL>
 inline osh_status conv16s_launch_s(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                    const float *res, int act, float *y, hipStream_t st) {
-    if (p->sh == 1) return conv16s_launch_t<TM, BV, TWL, 1>(p, x, w, bias, res, act, y, st);
-    return conv16s_launch_t<TM, BV, TWL, 2>(p, x, w, bias, res, act, y, st);
+    if (p->sh == 1) return conv16s_launch_t<TM, BV, TWL, 1, 3, 1, false>(p, x, w, bias, res, act, y, st);
+    return conv16s_launch_t<TM, BV, TWL, 2, 3, 1, false>(p, x, w, bias, res, act, y, st);
 }
 
 inline osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
@@ -275,6 +310,43 @@ inline osh_status conv16s_launch(const osh_conv_params *p, const float *x, const
     case 6: return conv16s_launch_s<2, 2, 8>(p, x, w, bias, res, act, y, st);
     case 7: return conv16s_launch_s<1, 2, 4>(p, x, w, bias, res, act, y, st);
     default: return conv16s_launch_s<1, 4, 4>(p, x, w, bias, res, act, y, st);
+    }
+}
+
+// ---- pointwise (1x1, stride 1, no pads): the same kernel with KS = 1 and
+// four 16-channel blocks per staged chunk; the chain is the GEMM chain over
+// input channels (bias, then ic ascending), as GemmKernel.Multiply sums it.
+constexpr int PW16_CB = 4;
+constexpr C16sVariant kPW16[] = {{1, 1, 16}, {1, 2, 16}, {1, 4, 16}, {2, 2, 16},
+                                 {2, 4, 16}, {1, 2, 4},  {1, 4, 4},  {2, 4, 4}};
+constexpr int kPW16Count = sizeof(kPW16) / sizeof(kPW16[0]);
+
+inline bool pw16_eligible(const osh_conv_params *p) {
+    return p->group == 1 && p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->dh == 1 && p->dw == 1 &&
+           p->pt == 0 && p->pl == 0 && p->oh == p->h && p->ow == p->w && p->c % 16 == 0 &&
+           (long long)p->c * p->h * p->w * 4 < (1LL << 31) && (long long)p->m * p->oh * p->ow * 4 < (1LL << 31) &&
+           (long long)((p->m + 15) / 16) * (p->c / 16) * 1024 < (1LL << 31) && p->n <= 65535;
+}
+
+template <int TM, int BV, int TWL>
+inline osh_status pw16_launch_v(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                const float *res, int act, float *y, hipStream_t st) {
+    const bool vec = p->w % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (vec) return conv16s_launch_t<TM, BV, TWL, 1, 1, PW16_CB, true>(p, x, w, bias, res, act, y, st);
+    return conv16s_launch_t<TM, BV, TWL, 1, 1, PW16_CB, false>(p, x, w, bias, res, act, y, st);
+}
+
+inline osh_status pw16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                              const float *res, int act, float *y, hipStream_t st, int v) {
+    switch (v) {
+    case 0: return pw16_launch_v<1, 1, 16>(p, x, w, bias, res, act, y, st);
+    case 1: return pw16_launch_v<1, 2, 16>(p, x, w, bias, res, act, y, st);
+    case 2: return pw16_launch_v<1, 4, 16>(p, x, w, bias, res, act, y, st);
+    case 3: return pw16_launch_v<2, 2, 16>(p, x, w, bias, res, act, y, st);
+    case 4: return pw16_launch_v<2, 4, 16>(p, x, w, bias, res, act, y, st);
+    case 5: return pw16_launch_v<1, 2, 4>(p, x, w, bias, res, act, y, st);
+    case 6: return pw16_launch_v<1, 4, 4>(p, x, w, bias, res, act, y, st);
+    default: return pw16_launch_v<2, 4, 4>(p, x, w, bias, res, act, y, st);
     }
 }
 

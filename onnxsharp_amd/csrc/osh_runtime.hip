@@ -28,6 +28,7 @@ static int g_exact_silu = -1;  // -1: read ONNXSHARP_HIP_EXACT_SILU on first use
 static int g_gemm_variant = -3;  // -3: read ONNXSHARP_HIP_GEMM_VARIANT on first use
 static int g_conv16_variant = -3;  // -3: read ONNXSHARP_HIP_CONV16_VARIANT on first use
 static int g_tune = -1;             // -1: read ONNXSHARP_HIP_TUNE on first use
+static int g_pw_variant = -3;       // -3: read ONNXSHARP_HIP_POINTWISE_VARIANT on first use
 
 bool exact_silu() {
     if (g_exact_silu < 0) {
@@ -61,6 +62,14 @@ int conv16_variant() {
     return g_conv16_variant;
 }
 
+int pointwise_variant() {
+    if (g_pw_variant == -3) {
+        const char *e = getenv("ONNXSHARP_HIP_POINTWISE_VARIANT");
+        g_pw_variant = e ? atoi(e) : -1;
+    }
+    return g_pw_variant;
+}
+
 __global__ void fill_u8_kernel(uint8_t *__restrict__ p, uint8_t v, size_t n) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -91,6 +100,12 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         g_conv16_variant = value;
         return OSH_OK;
     }
+    if (strcmp(key, "pointwise_variant") == 0) {
+        if (value < -2 || value >= pointwise_variant_count())
+            return fail(OSH_E_INVALID, "pointwise_variant %d out of range [-2, %d)", value, pointwise_variant_count());
+        g_pw_variant = value;
+        return OSH_OK;
+    }
     if (strcmp(key, "gemm_variant") == 0) {
         if (value < -2 || value >= gemm16_variant_count())
             return fail(OSH_E_INVALID, "gemm_variant %d out of range [-2, %d)", value, gemm16_variant_count());
@@ -112,6 +127,14 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     }
     if (strcmp(key, "conv16_variant") == 0) {
         *value = conv16_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "pointwise_variant") == 0) {
+        *value = pointwise_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "pointwise_variants") == 0) {
+        *value = pointwise_variant_count();
         return OSH_OK;
     }
     if (strcmp(key, "conv16_variants") == 0) {

@@ -215,6 +215,9 @@ RESIDUAL_CASES = [
     ("conv16s_3x3_64to64_40", (1, 64, 40, 40), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1]), 13),
     ("conv16_tuned_16to32_80", (1, 16, 80, 80), (32, 16, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
     ("gemm16_1x1_128to64_20", (1, 128, 20, 20), (64, 128, 1, 1), dict(), -1),
+    ("pw_gemm_tile_1x1_64to48_40", (1, 64, 40, 40), (48, 64, 1, 1), dict(), 0),
+    ("pw_lds_tile_1x1_80to64_20x24", (2, 80, 20, 24), (64, 80, 1, 1), dict(), 5),
+    ("pw_lds_tile_1x1_48to32_odd", (1, 48, 17, 19), (32, 48, 1, 1), dict(), 3),
     ("igemm_1x1_c6_odd", (2, 6, 13, 11), (10, 6, 1, 1), dict(), -1),
     ("direct3x3_c8_160", (1, 8, 160, 160), (16, 8, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
     ("depthwise_64_20", (1, 64, 20, 20), (64, 1, 3, 3), dict(group=64, pads=[1, 1, 1, 1]), -1),
@@ -237,7 +240,8 @@ def test_conv_residual_add_is_conv_then_add(cuda, name, xs, ws, attrs, variant):
     x = _t(synth.uniform(seed, xs), cuda)
     w = _t(synth.normal(seed + 1, ws, 0, 0.05), cuda)
     b = _t(synth.normal(seed + 2, (ws[0],), 0, 0.01), cuda)
-    N.call("osh_config_set", b"conv16_variant", variant)
+    key = b"pointwise_variant" if name.startswith("pw_") else b"conv16_variant"
+    N.call("osh_config_set", key, variant)
     try:
         layer = ConvLayer(fused_activation="Silu", **attrs)
         plain = layer.forward(x, w, b)
@@ -245,7 +249,46 @@ def test_conv_residual_add_is_conv_then_add(cuda, name, xs, ws, attrs, variant):
         fused = layer.forward(x, w, b, residual=res)
         torch.cuda.synchronize()
     finally:
-        N.call("osh_config_set", b"conv16_variant", -1)
+        N.call("osh_config_set", key, -1)
     expect = plain.cpu().numpy() + res.cpu().numpy()
     got = fused.cpu().numpy()
     assert np.array_equal(got, expect), f"max |d| {np.abs(got - expect).max():.3e}"
+
+
+POINTWISE_CASES = [
+    ("c3a_1x1_256to128_80", (1, 256, 80, 80), (128, 256, 1, 1)),
+    ("1x1_64to64_20", (1, 64, 20, 20), (64, 64, 1, 1)),
+    ("1x1_80to80_40_two_chunks", (1, 80, 40, 40), (80, 80, 1, 1)),
+    ("1x1_48to40_odd_17x19", (1, 48, 17, 19), (40, 48, 1, 1)),
+    ("1x1_32to24_batch2", (2, 32, 12, 16), (24, 32, 1, 1)),
+    ("1x1_512to256_20", (1, 512, 20, 20), (256, 512, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("name,xs,ws", POINTWISE_CASES, ids=[c[0] for c in POINTWISE_CASES])
+def test_pointwise_tiles_are_the_gemm_chain(cuda, oracle, name, xs, ws):
+    # 1x1 stride-1 convolutions with C % 16 == 0 choose between the GEMM tile
+    # (variant 0) and the LDS-tile kernel (1..): every choice is the GEMM chain
+    # (bias, then input channels ascending), bit for bit, including partial
+    # channel chunks and maps whose width is not a multiple of four
+    from onnxsharp_amd import native as N
+    seed = sum(xs) * 13 + sum(ws)
+    x = synth.uniform(seed, xs)
+    w = synth.normal(seed + 1, ws, 0, 0.05)
+    b = synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    nv = C.c_int()
+    N.call("osh_config_get", b"pointwise_variants", C.byref(nv))
+    assert nv.value >= 9
+    N.call("osh_config_set", b"exact_silu", 1)
+    try:
+        ref = None
+        for v in [-1] + list(range(nv.value)):
+            print(f"pointwise {name} variant {v}", flush=True)
+            N.call("osh_config_set", b"pointwise_variant", v)
+            y, p = run_conv(cuda, x, w, b, "Silu")
+            if ref is None:
+                ref = oracle_conv(oracle, x, w, b, p, "Silu", order=oracle.ORDER_IM2COL)
+            assert np.array_equal(y, ref), f"variant {v}: max |d| {np.abs(y - ref).max():.3e}"
+    finally:
+        N.call("osh_config_set", b"exact_silu", 0)
+        N.call("osh_config_set", b"pointwise_variant", -1)
