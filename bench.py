@@ -447,6 +447,8 @@ def main():
     ap.add_argument("--config", default="c2")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-host-copies", action="store_true",
+                    help="c3c/c4: skip the extra timing with PCIe copies")
     ap.add_argument("--eager", action="store_true",
                     help="time the steps issued one by one (default: one HIP graph of the K launches)")
     args = ap.parse_args()
@@ -489,10 +491,12 @@ def main():
         extra["timing"] = "HIP events around the launches issued one by one"
     if wl.name == "c4":
         extra["ms_per_frame"] = round(ms_step, 4)
-        extra["ms_per_frame_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
+        if not args.no_host_copies:
+            extra["ms_per_frame_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
     if wl.name == "c3c":
         extra["ms_per_block"] = round(ms_step, 4)
-        extra["ms_per_block_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
+        if not args.no_host_copies:
+            extra["ms_per_block_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
     roof["kernel"] = wl.kernel
     roof["algorithmic_per_launch"] = {"flops": wl.flops, "bytes": wl.bytes}
 
