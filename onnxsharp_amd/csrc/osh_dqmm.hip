@@ -34,7 +34,7 @@ namespace osh {
 
 constexpr int DQ_MINMAX_BLOCKS = 256;
 constexpr int DQ_THREADS = 256;
-constexpr int DQ_KC = 8;  // k-steps of 32 per GEMM load chunk
+constexpr int DQ_KC = 16;  // k-steps of 32 per GEMM load chunk (K = 512 in one chunk)
 
 struct DqScratch {  // layout of the caller's scratch buffer
     float partial_min[DQ_MINMAX_BLOCKS];

@@ -38,6 +38,8 @@ def run_dqmm(cuda, a, w, wzp, ws, bias):
     (17, 64, 40, np.uint8, "column"),
     (5, 1280, 32, np.int8, "column"),      # Int8Tests.F32SubstituteExactAtLongK shape
     (1, 7, 3, np.int8, "tensor"),
+    (3, 2100, 17, np.int8, None),          # K with a partial load chunk
+    (70, 96, 300, np.uint8, "column"),     # row and column tiles both partial
 ])
 def test_dqmm_parity(cuda, oracle, m, k, n, wdt, zp_kind):
     print(f"dqmm m={m} k={k} n={n} w={wdt.__name__} zp={zp_kind}", flush=True)
