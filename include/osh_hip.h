@@ -44,7 +44,7 @@ typedef void *osh_event;  /* hipEvent_t */
 /* Fused activation of a Conv, UnaryOpKind subset that
  * GraphFusion.FuseActivationIntoProducer moves into a producer
  * (src/OnnxSharp/Core/GraphFusion.cs:1713-1718). */
-enum { OSH_ACT_NONE = 0, OSH_ACT_RELU = 1, OSH_ACT_SILU = 2 };
+enum { OSH_ACT_NONE = 0, OSH_ACT_RELU = 1, OSH_ACT_SILU = 2, OSH_ACT_SIGMOID = 3 };
 
 /* ONNX auto_pad (src/OnnxSharp/Ops/DnnOps.cs:69-89). */
 enum { OSH_PAD_NOTSET = 0, OSH_PAD_SAME_UPPER = 1, OSH_PAD_SAME_LOWER = 2, OSH_PAD_VALID = 3 };
@@ -288,8 +288,25 @@ OSH_API osh_status osh_dynamic_quantize_linear(int64_t n, const float *d_x, uint
 
 /* ------------------------------------------------------ elementwise helpers */
 
-/* In-place activation pass (TensorOps.ElementWiseUnary, src/OnnxSharp/Tensors/TensorOps.cs:267-300). */
+/* Activation pass, d_y may equal d_x (TensorOps.ElementWiseUnary,
+ * src/OnnxSharp/Tensors/TensorOps.cs:267-300): Relu, SiLU and Sigmoid in the
+ * reference's vector-path arithmetic (VectorMath.Silu / Sigmoid,
+ * src/OnnxSharp/Tensors/VectorMath.cs:21-77).  OSH_ACT_SIGMOID is taken here
+ * only, not as a fused conv/GEMM epilogue (the reference fuses Relu and SiLU). */
 OSH_API osh_status osh_activation_f32(int64_t n, const float *d_x, int act, float *d_y, osh_stream s);
+
+/* DflSoftmax, the Detect head's distribution decode (DflLayer.Forward,
+ * src/OnnxSharp/Ops/DflOps.cs:97-240): x [batches][sides * bins][pixels] ->
+ * y [batches][sides][pixels], y = sum over b of softmax_b(x[side*bins + b]) * b,
+ * in the reference's arithmetic: the max over bins, exp by the reference
+ * polynomial of (x - max), the sum in bin order, inv = 1 / sum, then
+ * fma(e_b * inv, b, acc) from 0 in bin order.  The reference processes 256
+ * columns at a time, 8 per vector; the last (width % 8) columns of each
+ * 256-column block take its scalar lines, which are restated too.  Batch i
+ * reads d_x + i * x_batch_stride and writes d_y + i * y_batch_stride
+ * (elements), so x may be the first sides*bins channels of a head tensor. */
+OSH_API osh_status osh_dfl_f32(int batches, int sides, int bins, int pixels, const float *d_x,
+                               int64_t x_batch_stride, float *d_y, int64_t y_batch_stride, osh_stream s);
 
 /* ------------------------------------------ segment-continuity ops (NCHW) */
 /* These keep a run of convolutions on the device between the ops a segment

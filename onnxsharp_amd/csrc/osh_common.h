@@ -83,18 +83,22 @@ __device__ __forceinline__ float silu_fast(float x) {
     return x * r;
 }
 
+// Sigmoid of VectorMath.Sigmoid (VectorMath.cs:64-68): 1 / (1 + exp(x * -1)).
+__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + exp_ref(x * -1.0f)); }
+
 // TensorOps.Apply Relu (TensorOps.cs:951): x > 0 ? x : 0 (NaN -> 0).
 __device__ __forceinline__ float relu_ref(float x) { return x > 0.0f ? x : 0.0f; }
 
 // Internal activation code: the reference SiLU polynomial in a fused epilogue
 // (chosen by osh_config_set("exact_silu", 1) or ONNXSHARP_HIP_EXACT_SILU=1).
-constexpr int ACT_SILU_EXACT = 3;
+constexpr int ACT_SILU_EXACT = 103;
 
 template <int ACT>
 __device__ __forceinline__ float activate(float x) {
     if constexpr (ACT == OSH_ACT_SILU) return silu_fast(x);
     else if constexpr (ACT == ACT_SILU_EXACT) return silu_ref(x);
     else if constexpr (ACT == OSH_ACT_RELU) return relu_ref(x);
+    else if constexpr (ACT == OSH_ACT_SIGMOID) return sigmoid_ref(x);
     else return x;
 }
 

@@ -146,6 +146,52 @@ __global__ __launch_bounds__(256) void maxpool_chain3_kernel(int h, int w, int c
     }
 }
 
+// DflSoftmax, one thread per (image, side, pixel): three passes over the
+// pixel's bins (max; sum of exponentials; weighted sum), the exponentials
+// recomputed (same bits) rather than stored.  `tail` marks the columns the
+// reference handles on its scalar lines: the last (width % 8) of each block
+// of 256 pixels.
+__device__ __forceinline__ float dotnet_max(float a, float b) {
+    if (a != a || b != b) return __builtin_nanf("");
+    if (a > b) return a;
+    if (b > a) return b;
+    return __builtin_signbitf(a) ? b : a;  // equal: +0 over -0
+}
+
+__global__ __launch_bounds__(256) void dfl_kernel(int sides, int bins, int pixels, const float *__restrict__ x,
+                                                  long long x_bs, float *__restrict__ y, long long y_bs,
+                                                  long long total) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int n = (int)(idx % pixels);
+    const long long t = idx / pixels;
+    const int side = (int)(t % sides);
+    const long long img = t / sides;
+    const float *src = x + img * x_bs + (long long)side * bins * pixels + n;
+    const int col = n % 256;
+    const int width = min(256, pixels - (n - col));
+    const bool tail = col >= (width & ~7);
+    float m = -__builtin_inff();
+    for (int b = 0; b < bins; b++) {
+        const float v = src[(long long)b * pixels];
+        m = tail ? dotnet_max(m, v) : (m > v ? m : v);  // Avx.Max(max, row) keeps the row value unless max > row
+    }
+    float sum = 0.0f;
+    for (int b = 0; b < bins; b++) sum = sum + exp_ref(src[(long long)b * pixels] - m);
+    const float inv = 1.0f / sum;
+    float w = 0.0f;
+    for (int b = 0; b < bins; b++) {
+        const float p = exp_ref(src[(long long)b * pixels] - m) * inv;
+        if (tail) {
+            const float prod = p * (float)b;
+            w = w + prod;
+        } else {
+            w = __builtin_fmaf(p, (float)b, w);
+        }
+    }
+    y[img * y_bs + (long long)side * pixels + n] = w;
+}
+
 __global__ __launch_bounds__(256) void resize_nearest_kernel(int c, int h, int w, int fh, int fw,
                                                               const float *__restrict__ x, float *__restrict__ y,
                                                               long long y_batch_stride, long long total) {
@@ -285,6 +331,21 @@ OSH_API osh_status osh_maxpool_chain3_f32(int n, int c, int h, int w, int k, con
     return OSH_OK;
 }
 
+OSH_API osh_status osh_dfl_f32(int batches, int sides, int bins, int pixels, const float *d_x,
+                               int64_t x_batch_stride, float *d_y, int64_t y_batch_stride, osh_stream s) {
+    if (batches <= 0 || sides <= 0 || pixels <= 0) return fail(OSH_E_INVALID, "DflSoftmax: bad sizes");
+    if (bins < 2) return fail(OSH_E_INVALID, "DflSoftmax: bins=%d (need at least 2)", bins);
+    if (!d_x || !d_y) return fail(OSH_E_INVALID, "DflSoftmax: NULL pointer");
+    if (x_batch_stride < (long long)sides * bins * pixels || y_batch_stride < (long long)sides * pixels)
+        return fail(OSH_E_INVALID, "DflSoftmax: batch stride below one image");
+    const long long total = (long long)batches * sides * pixels;
+    if (total > 0x7fffffffLL * 256) return fail(OSH_E_UNSUPPORTED, "DflSoftmax: too many outputs");
+    hipLaunchKernelGGL(dfl_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), sides, bins,
+                       pixels, d_x, (long long)x_batch_stride, d_y, (long long)y_batch_stride, total);
+    OSH_LAUNCH_CHECK("dfl_kernel");
+    return OSH_OK;
+}
+
 OSH_API osh_status osh_resize_nearest_f32(int n, int c, int h, int w, int fh, int fw, const float *d_x, float *d_y,
                                           int64_t y_batch_stride, osh_stream s) {
     if (n <= 0 || c <= 0 || h <= 0 || w <= 0 || fh <= 0 || fw <= 0) return fail(OSH_E_INVALID, "Resize: bad sizes");
@@ -343,6 +404,10 @@ OSH_API osh_status osh_activation_f32(int64_t n, const float *d_x, int act, floa
     case ACT_SILU_EXACT:
         hipLaunchKernelGGL(activation_kernel<ACT_SILU_EXACT>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
                            d_y, (long long)n);
+        break;
+    case OSH_ACT_SIGMOID:
+        hipLaunchKernelGGL(activation_kernel<OSH_ACT_SIGMOID>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s),
+                           d_x, d_y, (long long)n);
         break;
     default:
         return fail(OSH_E_INVALID, "unknown activation %d", act);

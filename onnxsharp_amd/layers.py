@@ -358,3 +358,59 @@ class MatMulIntegerLayer:
         N.call("osh_matmul_integer", m, k, n, _ptr(aa), 1 if a.dtype == torch.int8 else 0, a_zp,
                _ptr(self._packed[1]), _ptr(out), _ptr(scratch), C.c_void_p(_stream()))
         return out
+
+
+class ActivationLayer:
+    """Standalone Relu / Silu / Sigmoid (ActivationLayer with its UnaryOpKind,
+    src/OnnxSharp/Ops/ActivationLayer.cs; vector-path arithmetic of
+    VectorMath.Silu / Sigmoid)."""
+
+    KINDS = {"Relu": N.ACT_RELU, "Silu": N.ACT_SILU, "Sigmoid": N.ACT_SIGMOID}
+
+    def __init__(self, kind: str, name: str = "activation"):
+        if kind not in self.KINDS:
+            raise ValueError(f"activation '{name}': unknown kind {kind!r}")
+        self.kind = kind
+        self.name = name
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        x = _need_f32("input", x)
+        if out is None:
+            out = torch.empty_like(x)
+        elif out.shape != x.shape or not out.is_contiguous():
+            raise ValueError(f"activation '{self.name}': output must be a contiguous {tuple(x.shape)} tensor")
+        N.call("osh_activation_f32", x.numel(), _ptr(x), self.KINDS[self.kind], _ptr(out), C.c_void_p(_stream()))
+        return out
+
+
+class DflSoftmaxLayer:
+    """The fused DFL decode of a YOLO Detect head (DflLayer, registered as
+    "DflSoftmax", src/OnnxSharp/Ops/DflOps.cs:31-240): input [B, sides*bins, N]
+    -> output [B, sides, N], the softmax over each side's bins weighted by the
+    bin index."""
+
+    def __init__(self, bins: int = 16, name: str = "dfl"):
+        self.bins = int(bins)
+        self.name = name
+
+    def get_memory_shapes(self, x_shape: Sequence[int]) -> tuple:
+        # DflLayer.Resolve (DflOps.cs:48-60)
+        if len(x_shape) != 3:
+            raise N.OshError(N.OSH_E_INVALID,
+                             f"DflSoftmax '{self.name}': input must be [B, sides*bins, N], got {tuple(x_shape)}")
+        if self.bins < 2 or x_shape[1] % self.bins != 0:
+            raise N.OshError(N.OSH_E_INVALID,
+                             f"DflSoftmax '{self.name}': {x_shape[1]} channels not divisible by bins={self.bins}")
+        return (int(x_shape[0]), int(x_shape[1]) // self.bins, int(x_shape[2]))
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        x = _need_f32("input", x)
+        b, sides, n = self.get_memory_shapes(tuple(x.shape))
+        if out is None:
+            out = torch.empty((b, sides, n), dtype=torch.float32, device=x.device)
+        elif tuple(out.shape) != (b, sides, n) or not out.is_contiguous():
+            raise ValueError(f"DflSoftmax '{self.name}': output must be a contiguous {(b, sides, n)} tensor")
+        if b and sides and n:
+            N.call("osh_dfl_f32", b, sides, self.bins, n, _ptr(x), sides * self.bins * n, _ptr(out), sides * n,
+                   C.c_void_p(_stream()))
+        return out

@@ -18,7 +18,7 @@ OSH_E_UNSUPPORTED = -2
 OSH_E_DEVICE = -3
 OSH_E_NOMEM = -4
 
-ACT_NONE, ACT_RELU, ACT_SILU = 0, 1, 2
+ACT_NONE, ACT_RELU, ACT_SILU, ACT_SIGMOID = 0, 1, 2, 3
 PAD_NOTSET, PAD_SAME_UPPER, PAD_SAME_LOWER, PAD_VALID = 0, 1, 2, 3
 AUTO_PAD = {"NOTSET": PAD_NOTSET, "SAME_UPPER": PAD_SAME_UPPER, "SAME_LOWER": PAD_SAME_LOWER, "VALID": PAD_VALID}
 ACTIVATIONS = {None: ACT_NONE, "Relu": ACT_RELU, "Silu": ACT_SILU}
@@ -105,6 +105,7 @@ _SIGS = {
     "osh_add_f32": ([_i64, _vp, _vp, _vp, _vp], _i),
     "osh_maxpool2d_f32": ([C.POINTER(PoolParams), _vp, _vp, _vp], _i),
     "osh_maxpool_chain3_f32": ([_i, _i, _i, _i, _i, _vp, _i64, _vp, _vp, _vp, _i64, _vp], _i),
+    "osh_dfl_f32": ([_i, _i, _i, _i, _vp, _i64, _vp, _i64, _vp], _i),
     "osh_resize_nearest_f32": ([_i, _i, _i, _i, _i, _i, _vp, _vp, _i64, _vp], _i),
     "osh_transpose_f32": ([_i, _i, _i, _vp, _i64, _vp, _i64, _vp], _i),
     "osh_softmax_f32": ([_i64, _i, C.c_float, _vp, _vp, _vp], _i),

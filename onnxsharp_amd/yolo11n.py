@@ -119,6 +119,23 @@ class PoolChainOp:
 
 
 @dataclass(eq=False)
+class DflOp:
+    """DflSoftmax over a head tensor's box channels (sides*bins of them):
+    y[side] = sum over b of softmax_b(x[side*bins + b]) * b."""
+    name: str
+    x: Slice
+    y: Slice
+    bins: int = 16
+
+
+@dataclass(eq=False)
+class SigmoidOp:
+    name: str
+    x: Slice
+    y: Slice
+
+
+@dataclass(eq=False)
 class UpsampleOp:
     name: str
     x: Slice
@@ -312,8 +329,11 @@ class CopyOp:
     y: Slice
 
 
-def build(size: int = 640, seed: int = 7000) -> Model:
-    """YOLO11n at an input of size x size (a multiple of 32)."""
+def build(size: int = 640, seed: int = 7000, decode: bool = False) -> Model:
+    """YOLO11n at an input of size x size (a multiple of 32).  With decode,
+    each head output also goes through the Detect head's DFL (box channels)
+    and class Sigmoid into a [4 + 80, H, W] tensor per scale, which become the
+    outputs (the anchor/stride box arithmetic and NMS stay with the caller)."""
     if size % 32:
         raise ValueError("YOLO11n input size must be a multiple of 32")
     bd = _Builder(size, seed)
@@ -346,6 +366,14 @@ def build(size: int = 640, seed: int = 7000) -> Model:
     bd.conv("/model.20/conv/Conv", o19, 128, 3, 2, y=Slice(cat21, 0, 128))
     o22 = bd.c3k2("/model.22", whole(cat21), 256, True, 0.5)
     m.outputs = bd.detect("/model.23", [o16, o19, o22])
+    if decode:
+        decoded = []
+        for i, out in enumerate(m.outputs):
+            dec = bd.buf(f"/model.23/decode{i}", 4 + 80, out.h, out.w)
+            m.ops.append(DflOp(f"/model.23/dfl#{i}", Slice(out, 0, 64), Slice(dec, 0, 4)))
+            m.ops.append(SigmoidOp(f"/model.23/Sigmoid#{i}", Slice(out, 64, 80), Slice(dec, 4, 80)))
+            decoded.append(dec)
+        m.outputs = decoded
     return m
 
 
@@ -612,6 +640,14 @@ class Frame:
             xs, ys = op.x.buf.c * hw, op.y.buf.c * hw
             return lambda st: N.check(lib.osh_maxpool_chain3_f32(1, c, op.x.h, op.x.w, op.k, op.x.ptr(), xs, y1.ptr(),
                                                                  y2.ptr(), y3.ptr(), ys, st))
+        if isinstance(op, DflOp):
+            hw = op.x.h * op.x.w
+            sides = op.x.c // op.bins
+            return lambda st: N.check(lib.osh_dfl_f32(1, sides, op.bins, hw, op.x.ptr(), op.x.buf.c * hw, op.y.ptr(),
+                                                      op.y.buf.c * hw, st))
+        if isinstance(op, SigmoidOp):
+            n = op.x.c * op.x.h * op.x.w
+            return lambda st: N.check(lib.osh_activation_f32(n, op.x.ptr(), N.ACT_SIGMOID, op.y.ptr(), st))
         if isinstance(op, UpsampleOp):
             return lambda st: N.check(lib.osh_resize_nearest_f32(1, op.x.c, op.x.h, op.x.w, op.f, op.f, op.x.ptr(),
                                                                  op.y.ptr(), op.y.c * op.y.h * op.y.w, st))

@@ -49,8 +49,9 @@ def lib():
         l.orc_conv2d_f64.argtypes = [C.c_int] * 16 + [_fp, _fp, _fp, _dp]
         l.orc_conv_dw_f32.argtypes = [C.c_int] * 14 + [_fp, _fp, _fp, _fp]
         l.orc_winograd_f23.argtypes = [C.c_int] * 5 + [_fp, _fp, _fp, _fp]
-        for f in (l.orc_exp_ref, l.orc_silu_ref, l.orc_silu_scalar, l.orc_relu):
+        for f in (l.orc_exp_ref, l.orc_silu_ref, l.orc_silu_scalar, l.orc_relu, l.orc_sigmoid_ref):
             f.argtypes = [C.c_long, _fp, _fp]
+        l.orc_dfl_f32.argtypes = [C.c_int] * 4 + [_fp, _fp]
         l.orc_softmax_f32.argtypes = [C.c_long, C.c_int, C.c_float, _fp, _fp]
         l.orc_maxpool2d_f32.argtypes = [C.c_int] * 12 + [_fp, _fp]
         l.orc_resize_nearest.argtypes = [C.c_int] * 6 + [_fp, _fp]
@@ -193,6 +194,20 @@ def exp_ref(x):
 def silu_ref(x):
     """VectorMath.Silu vector path."""
     return _unary(lib().orc_silu_ref, x)
+
+
+def sigmoid_ref(x):
+    """VectorMath.Sigmoid vector path."""
+    return _unary(lib().orc_sigmoid_ref, x)
+
+
+def dfl(x, bins=16):
+    """DflSoftmax: x [B, sides*bins, N] -> [B, sides, N] (DflOps.cs)."""
+    x = _c32(x)
+    b, c, n = x.shape
+    y = np.empty((b, c // bins, n), np.float32)
+    lib().orc_dfl_f32(b, c // bins, bins, n, _f(x), _f(y))
+    return y
 
 
 def silu_scalar(x):

@@ -36,6 +36,8 @@
  *                       rounding)
  *   orc_maxpool2d_f32   DnnOps.cs:1335-1580 (scalar path :1564-1579: -inf, then v > best)
  *   orc_resize_nearest  DnnOps.cs:2215-2330 (nearest, integer factor: source index dst / factor)
+ *   orc_sigmoid_ref     VectorMath.cs:64-68 (1 / (1 + Exp(x * -1)), vector path)
+ *   orc_dfl_f32         DflOps.cs:97-240 (softmax over bins, expectation of the bin index)
  *
  * Build: see oracle/Makefile (gcc, -O3 -ffp-contract=off; fmaf is explicit).
  */
@@ -472,6 +474,61 @@ ORC_API void orc_silu_ref(long n, const float *x, float *y)
 ORC_API void orc_silu_scalar(long n, const float *x, float *y)
 {
     for (long i = 0; i < n; i++) y[i] = x[i] * (1.0f / (1.0f + expf(-x[i])));
+}
+
+/* Sigmoid of the vector path (VectorMath.cs:64-68): 1 / (1 + exp(x * -1)). */
+ORC_API void orc_sigmoid_ref(long n, const float *x, float *y)
+{
+    for (long i = 0; i < n; i++) y[i] = 1.0f / (1.0f + exp_ref(x[i] * -1.0f));
+}
+
+/* DflSoftmax (DflOps.cs:97-240): x [B][sides*bins][N] -> y [B][sides][N],
+ * y = sum_b softmax_b(x[side*bins + b]) * b.  The reference works on blocks of
+ * 256 columns, 8 at a time (:108-146,168-240):
+ *   max  = Avx.Max(max, row)  -- maxps: the row value unless max > row;
+ *   e_b  = VectorMath.Exp(row - max), sum = sum + e_b in bin order;
+ *   inv  = 1 / sum;  w = fma(e_b * inv, b, w) from 0 in bin order.
+ * The last width % 8 columns of a block take the scalar lines: MathF.Max
+ * (NaN if either is NaN), MathF.Exp (here exp_ref: its bits are not pinned
+ * against .NET), and w += e_b * inv * b with three roundings. */
+static float dotnet_max(float a, float b)
+{
+    if (a != a || b != b) return NAN;
+    if (a > b) return a;
+    if (b > a) return b;
+    return signbit(a) ? b : a; /* equal: +0 over -0 */
+}
+
+ORC_API void orc_dfl_f32(int batches, int sides, int bins, int pixels, const float *x, float *y)
+{
+    for (int bt = 0; bt < batches; bt++)
+        for (int s = 0; s < sides; s++) {
+            const float *src = x + ((long)bt * sides + s) * bins * pixels;
+            float *dst = y + ((long)bt * sides + s) * pixels;
+            for (int n = 0; n < pixels; n++) {
+                const int col = n % 256, width = (pixels - (n - col)) < 256 ? pixels - (n - col) : 256;
+                const int tail = col >= (width & ~7);
+                float m = -INFINITY;
+                for (int b = 0; b < bins; b++) {
+                    const float v = src[(long)b * pixels + n];
+                    m = tail ? dotnet_max(m, v) : (m > v ? m : v);
+                }
+                float total = 0.0f;
+                for (int b = 0; b < bins; b++) total = total + exp_ref(src[(long)b * pixels + n] - m);
+                const float inv = 1.0f / total;
+                float w = 0.0f;
+                for (int b = 0; b < bins; b++) {
+                    const float p = exp_ref(src[(long)b * pixels + n] - m) * inv;
+                    if (tail) {
+                        const float t = p * (float)b;
+                        w = w + t;
+                    } else {
+                        w = fmaf(p, (float)b, w);
+                    }
+                }
+                dst[n] = w;
+            }
+        }
 }
 
 ORC_API void orc_relu(long n, const float *x, float *y)

@@ -61,6 +61,11 @@ def run_op(oracle, op, inputs):
         return np.concatenate([y1, y2, y3], axis=1)
     if isinstance(op, Y.UpsampleOp):
         return oracle.resize_nearest(inputs[0], op.f)
+    if isinstance(op, Y.DflOp):
+        x = inputs[0]
+        return oracle.dfl(x.reshape(1, x.shape[1], -1), op.bins).reshape(1, x.shape[1] // op.bins, *x.shape[2:])
+    if isinstance(op, Y.SigmoidOp):
+        return oracle.sigmoid_ref(inputs[0])
     if isinstance(op, Y.AttentionOp):
         return attention(oracle, op, inputs[0])
     raise TypeError(op)

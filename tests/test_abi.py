@@ -146,3 +146,14 @@ def test_conv_add_rejects_a_residual_overlapping_the_output():
     st = lib.osh_conv2d_add_f32(C.byref(p), C.c_void_p(1 << 41), C.c_void_p(1 << 42), None, 0, None,
                                 C.c_void_p(base), None)
     assert st == N.OSH_E_INVALID and "NULL" in N.last_error()
+
+
+def test_dfl_softmax_shapes():
+    from onnxsharp_amd.layers import DflSoftmaxLayer
+    assert DflSoftmaxLayer(16).get_memory_shapes((1, 64, 8400)) == (1, 4, 8400)
+    with pytest.raises(N.OshError, match="not divisible by bins"):
+        DflSoftmaxLayer(16).get_memory_shapes((1, 60, 10))
+    with pytest.raises(N.OshError, match="must be"):
+        DflSoftmaxLayer(16).get_memory_shapes((64, 10))
+    st = N.lib().osh_dfl_f32(1, 4, 1, 10, C.c_void_p(1 << 40), 40, C.c_void_p(1 << 41), 40, None)
+    assert st == N.OSH_E_INVALID and "bins" in N.last_error()

@@ -148,3 +148,47 @@ def test_softmax_within_fp32_bar(cuda, oracle, rows, cols, scale):
     got = y.cpu().numpy()
     assert_fp32_close(got, oracle.softmax(x, scale), f"softmax {rows}x{cols}")
     assert np.allclose(got.sum(axis=1), 1.0, atol=1e-5)
+
+
+DFL_CASES = [((1, 64, 8400), 16), ((1, 64, 6400), 16), ((2, 64, 400), 16), ((1, 64, 300), 16),
+             ((1, 32, 13), 16), ((3, 24, 77), 8)]
+
+
+@pytest.mark.parametrize("shape,bins", DFL_CASES, ids=[f"{s}_b{b}" for s, b in DFL_CASES])
+def test_dfl_matches_oracle(cuda, oracle, shape, bins):
+    # the vector-path columns and the scalar-line columns (the last width % 8
+    # of a 256-column block) both restate the reference; the scalar lines call
+    # MathF.Exp in the reference, whose bits are not pinned (exp_ref here)
+    from onnxsharp_amd.layers import DflSoftmaxLayer
+    x = synth.normal(960 + shape[2], shape, 0, 3)
+    if shape[2] == 300:
+        # a NaN bin: Avx.Max(max, row) drops it at the next bin and the exp
+        # clamp (maxps against -87.3) sends it to e^-87.3, so it weighs ~0
+        x[0, 5, 17] = np.nan
+    y = DflSoftmaxLayer(bins).forward(_dev(x, cuda)).cpu().numpy()
+    ref = oracle.dfl(x, bins)
+    assert np.array_equal(_bits(y), _bits(ref))
+    if shape[2] == 300:
+        assert np.isfinite(y).all()
+
+
+def test_dfl_reads_a_head_tensor_slice(cuda, oracle):
+    # the box channels of a [1, 144, H, W] head output, in place: batch stride
+    # of the whole head tensor, output into a wider buffer
+    import torch
+    from onnxsharp_amd import native as N
+    head = synth.normal(970, (2, 144, 20, 20), 0, 2)
+    dh = _dev(head, cuda)
+    out = torch.zeros((2, 6, 400), device=cuda)
+    N.call("osh_dfl_f32", 2, 4, 16, 400, _p(dh), 144 * 400, _p(out), 6 * 400, None)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = oracle.dfl(np.ascontiguousarray(head[:, :64].reshape(2, 64, 400)))
+    assert np.array_equal(got[:, :4], ref) and not got[:, 4:].any()
+
+
+def test_sigmoid_matches_oracle(cuda, oracle):
+    from onnxsharp_amd.layers import ActivationLayer
+    x = synth.normal(980, (1, 80, 40, 40), 0, 6)
+    y = ActivationLayer("Sigmoid").forward(_dev(x, cuda)).cpu().numpy()
+    assert np.array_equal(y, oracle.sigmoid_ref(x))

@@ -1,11 +1,13 @@
 """GPU parity of the YOLO11n frame (87 convolutions, C2PSA attention, SPPF,
 upsampling, concat/split/add glue) against the oracle.
 
-* Per op: every op of the frame runs on the device on the device's own inputs,
-  and its output is compared with the oracle's output for those same inputs:
-  FP32 bar from conftest (relative 1e-4, absolute 1e-5) for convolutions and
-  attention; bit-exact for Add, MaxPool, Resize and copies; bit-exact also
-  for 1x1 convolutions, whose in-order MFMA chain is the reference's.
+* Per op: every op of the frame (built with the head's DFL/Sigmoid decode, and
+  with the launch fusions applied) runs on the device on the device's own
+  inputs, and its output is compared with the oracle's output for those same
+  inputs: FP32 bar from conftest (relative 1e-4, absolute 1e-5) for
+  convolutions and attention; bit-exact for Add, MaxPool and the SPPF pool
+  chain, Resize, copies, DFL and Sigmoid; bit-exact also for 1x1
+  convolutions, whose in-order MFMA chain is the reference's.
 * End to end: the frame's three head tensors against the oracle frame run
   from the same input.  Differences of single ops compound through ~25
   layers in sequence, so this check uses a frame-level bar (stated below).
@@ -31,9 +33,9 @@ def exact_silu():
     N.call("osh_config_set", b"exact_silu", 0)
 
 
-def _frame(cuda, size):
+def _frame(cuda, size, decode=False):
     from onnxsharp_amd import yolo11n
-    model = yolo11n.build(size)
+    model = yolo11n.build(size, decode=decode)
     return model, yolo11n.Frame(model, cuda)
 
 
@@ -46,7 +48,7 @@ def _host(sl):
 def test_yolo_per_op_parity(cuda, oracle, exact_silu):
     from oracle import yolo_frame as YO
     from onnxsharp_amd import yolo11n as Y
-    model, fr = _frame(cuda, 128)
+    model, fr = _frame(cuda, 128, decode=True)
     try:
         fr.set_input(synth.uniform(4242, (1, 3, 128, 128)))
         worst = (0.0, "")
@@ -58,7 +60,8 @@ def test_yolo_per_op_parity(cuda, oracle, exact_silu):
             got = _host(op.y)
             ref = YO.run_op(oracle, op, ins)
             what = f"op {i} {type(op).__name__} {op.name}"
-            exact = isinstance(op, (Y.AddOp, Y.MaxPoolOp, Y.UpsampleOp, Y.CopyOp)) or (
+            exact = isinstance(op, (Y.AddOp, Y.MaxPoolOp, Y.PoolChainOp, Y.UpsampleOp, Y.CopyOp, Y.DflOp,
+                                    Y.SigmoidOp)) or (
                 isinstance(op, Y.ConvOp) and op.k == 1)
             nbad, dmax = fp32_violations(got, ref)
             worst = max(worst, (dmax / (1e-6 + np.abs(ref).max()), what))

@@ -336,3 +336,40 @@ def test_gemm_ex_against_float64(oracle):
     assert np.array_equal(y, (base + cs[np.arange(6) % 4][None, :]).astype(np.float32))
     y = oracle.gemm_ex(a, b, np.float32([3.0]), 1.0, 1.0)
     assert np.array_equal(y, base + np.float32(3.0))
+
+
+def test_dfl_against_float64_and_known_answers(oracle):
+    # DflOps.cs: y = sum_b softmax_b(x) * b over each side's bins
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((2, 64, 300)).astype(np.float32) * 3
+    y = oracle.dfl(x)
+    xd = x.astype(np.float64).reshape(2, 4, 16, 300)
+    p = np.exp(xd - xd.max(2, keepdims=True))
+    p /= p.sum(2, keepdims=True)
+    ref = (p * np.arange(16)[None, None, :, None]).sum(2)
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    # equal logits: every e_b is exactly 1, the sum 16, each p 1/16 -> 7.5 exactly
+    assert (oracle.dfl(np.full((1, 16, 20), 0.25, np.float32)) == 7.5).all()
+    # one bin far above the rest: the expectation is that bin's index (bin 0
+    # keeps the other bins' e^-40 weights, ~5e-16)
+    hot = np.zeros((1, 16, 11), np.float32)
+    hot[0, np.arange(11) % 16, np.arange(11)] = 40.0
+    got = oracle.dfl(hot)[0, 0]
+    assert np.array_equal(got[1:], np.arange(1, 11, dtype=np.float32)) and 0 < got[0] < 1e-12
+
+
+def test_dfl_subtracts_the_column_max(oracle):
+    # shifting a column's bins by an exactly representable constant leaves
+    # every (x - max) and so every output bit unchanged
+    rng = np.random.default_rng(12)
+    x = (rng.integers(-40, 40, (1, 32, 50)) / 8.0).astype(np.float32)
+    shifted = (x + np.float32(3.0)).astype(np.float32)
+    assert np.array_equal(oracle.dfl(x), oracle.dfl(shifted))
+
+
+def test_sigmoid_against_float64(oracle):
+    x = np.linspace(-30, 30, 20001).astype(np.float32)
+    y = oracle.sigmoid_ref(x)
+    ref = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    assert np.abs(y - ref).max() <= 2e-7
+    assert oracle.sigmoid_ref(np.zeros(3, np.float32))[0] == 0.5

@@ -182,3 +182,16 @@ def test_c2f_block_structure():
     f = Y.fuse_launches(m)
     assert len(f.ops) == 4 and f.ops[2].res is not None and f.ops[2].res.c0 == 64
     assert [(b.c, b.h, b.w) for b in m.outputs] == [(128, 80, 80)]
+
+
+def test_decode_appends_dfl_and_sigmoid_per_scale():
+    from onnxsharp_amd import yolo11n as Y
+    m = Y.build(640, decode=True)
+    dfl = [o for o in m.ops if isinstance(o, Y.DflOp)]
+    sig = [o for o in m.ops if isinstance(o, Y.SigmoidOp)]
+    assert len(dfl) == len(sig) == 3
+    assert [(b.c, b.h, b.w) for b in m.outputs] == [(84, 80, 80), (84, 40, 40), (84, 20, 20)]
+    for d, s_ in zip(dfl, sig):
+        assert (d.x.c0, d.x.c, d.y.c0, d.y.c) == (0, 64, 0, 4)
+        assert (s_.x.c0, s_.x.c, s_.y.c0, s_.y.c) == (64, 80, 4, 80)
+        assert d.y.buf is s_.y.buf
