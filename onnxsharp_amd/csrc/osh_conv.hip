@@ -1,23 +1,30 @@
 // osh_conv.hip -- Conv entry points of the C ABI: shape logic of ConvLayer
 // (src/OnnxSharp/Ops/DnnOps.cs:53-89,134-201,379-409) and the kernel choice
-// of ConvLayer.Forward (DnnOps.cs:411-500), re-planned for gfx950:
+// of ConvLayer.Forward (DnnOps.cs:411-500), re-planned for gfx950.  Every
+// default choice sums in the order the reference's own kernel for that shape
+// uses, so the outputs are its bits:
 //
-//   depthwise (group == C == M)         -> dw_conv_kernel (direct, ky -> kx FMA chain)
-//   3x3 / dil 1 / stride any, C % 16 == 0
-//                                       -> in-order 16x16x4 MFMA implicit GEMM (osh_conv16.h),
-//                                          the NCHWc chain bit for bit
-//   3x3, C <= 4, M = 8/16/32, group 1    -> first_conv_kernel (direct; the network's first
-//                                          layer, FirstConv.cs: ic -> ky -> kx FMA chain)
-//   1x1 / stride 1 / pad 0 / dil 1      -> MFMA GEMM over NCHW (W[M,C] x X[C,H*W])
-//   3x3 / pad 1 / dil 1 / stride 1, C = 16, 32, 64, OW % 8 == 0
-//                                       -> wave-independent MFMA kernel (osh_conv3x3_wi.h)
-//   3x3 / pad 1 / dil 1 / stride 1 or 2, C = 16..128 (C % 16 == 0), OW % 4 == 0
-//                                       -> weight-stationary MFMA kernel (osh_conv3x3_ws.h)
-//   other 3x3 / pad 1 / dil 1 / s 1, 2  -> MFMA implicit GEMM on an LDS halo tile (osh_conv3x3.h)
-//   everything else                     -> MFMA implicit GEMM with an im2col gather
+//   depthwise (group == C == M)         -> dw_conv_kernel (ky -> kx FMA chain, DepthwiseConv.cs)
+//   3x3, C <= 4 or 8, M = 8/16/32, group 1
+//                                       -> first_conv_kernel (the network's first layer,
+//                                          FirstConv.cs, and 8-channel layers: the
+//                                          ic -> ky -> kx FMA chain)
+//   3x3 / dil 1 / any stride, C % 16 == 0
+//                                       -> in-order 16x16x4 MFMA kernels (osh_conv16.h,
+//                                          osh_conv16s.h): the NCHWc chain icb -> ky -> kx -> ic16
+//   1x1 / stride 1 / pad 0, C % 16 == 0 -> the LDS-tile kernel with one tap, or the GEMM tile,
+//                                          tuned per shape (the GEMM chain over ic)
+//   other 1x1 / stride 1 / pad 0        -> MFMA GEMM over NCHW (W[M,C] x X[C,H*W])
+//   everything else                     -> MFMA implicit GEMM with an im2col gather, k in the
+//                                          im2col order ic -> ky -> kx (ConvKernels.cs)
+//
+// With osh_config_set("conv16_variant", -2) 3x3 shapes take the older
+// weight-stationary / LDS-halo kernels instead (osh_conv3x3_wi.h,
+// osh_conv3x3_ws.h, osh_conv3x3.h), which sum in orders of their own (within
+// the FP32 tolerance).
 //
 // Bias and the fused activation (Relu / SiLU, GraphFusion.cs:1713-1718) are
-// applied in registers before the single store.
+// applied in registers before the single store, then an optional residual.
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -137,7 +144,8 @@ __global__ __launch_bounds__(256) void residual_add_kernel(long long n, const fl
 template <int MM, int CC, int ACT>
 __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, const float *__restrict__ x,
                                                          const float *__restrict__ w,
-                                                         const float *__restrict__ bias, float *__restrict__ y) {
+                                                         const float *__restrict__ bias,
+                                                         const float *__restrict__ res, float *__restrict__ y) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const long long plane = (long long)p.oh * p.ow;
     if (idx >= (long long)p.n * plane) return;
@@ -161,7 +169,9 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
                 v[ic][ky][kx] = ok ? xn[((long long)ic * p.h + iy) * p.w + ix] : 0.f;
             }
         }
-    float *yp = y + (long long)n * m * plane + (long long)oy * p.ow + ox;
+    const long long yo = (long long)n * m * plane + (long long)oy * p.ow + ox;
+    float *yp = y + yo;
+    const float *rp = res ? res + yo : nullptr;
     // 3x3 taps at compile-time offsets: the weights arrive in wide scalar loads
 #pragma unroll
     for (int oc = 0; oc < MM; oc++) {  // MM == m (eligibility)
@@ -173,13 +183,19 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
             for (int ky = 0; ky < 3; ky++)
 #pragma unroll
                 for (int kx = 0; kx < 3; kx++) acc = __builtin_fmaf(wo[(ic * 3 + ky) * 3 + kx], v[ic][ky][kx], acc);
-        yp[oc * plane] = activate<ACT>(acc);
+        float o = activate<ACT>(acc);
+        if (rp) o += rp[oc * plane];
+        yp[oc * plane] = o;
     }
 }
 
+// Also the few-channel 3x3 layers inside a network (8 input channels, e.g.
+// YOLO11n's 8 -> 16 bottleneck conv at 160 x 160): the same per-pixel chain is
+// the reference's im2col order for them, and cheaper than a GEMM tile whose
+// M = 16 would idle most of its rows.
 static bool first_conv_eligible(const osh_conv_params *p) {
-    return p->group == 1 && p->c <= 4 && (p->m == 8 || p->m == 16 || p->m == 32) && p->kh == 3 && p->kw == 3 &&
-           p->dh == 1 && p->dw == 1;
+    return p->group == 1 && (p->c <= 4 || p->c == 8) && (p->m == 8 || p->m == 16 || p->m == 32) && p->kh == 3 &&
+           p->kw == 3 && p->dh == 1 && p->dw == 1;
 }
 
 enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3, ALGO_WS3X3 = 4, ALGO_WI3X3 = 5,
@@ -193,9 +209,15 @@ static ConvAlgo select_algo(const osh_conv_params *p) {
     if (p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 && p->oh == p->h &&
         p->ow == p->w)
         return ALGO_POINTWISE;
-    if (conv3x3_wi_eligible(p)) return ALGO_WI3X3;
-    if (conv3x3_ws_eligible(p)) return ALGO_WS3X3;
-    if (conv3x3_eligible(p)) return ALGO_DIRECT3X3;
+    // the weight-stationary and LDS-halo 3x3 kernels sum in their own orders:
+    // only on request (conv16_variant -2); by default the remaining shapes
+    // take the implicit-im2col GEMM, whose k order (ic -> ky -> kx) is the
+    // reference's im2col chain
+    if (conv16_variant() == -2) {
+        if (conv3x3_wi_eligible(p)) return ALGO_WI3X3;
+        if (conv3x3_ws_eligible(p)) return ALGO_WS3X3;
+        if (conv3x3_eligible(p)) return ALGO_DIRECT3X3;
+    }
     return ALGO_IM2COL;
 }
 
@@ -460,8 +482,7 @@ static int pw16_pick(const osh_conv_params *p) { return p->ow >= 16 ? 0 : 5; }
 static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void *d_wpacked, const float *d_bias,
                          int act, const float *d_res, float *d_y, hipStream_t stream) {
     const float *w = static_cast<const float *>(d_wpacked);
-    const int cpg = p->c / p->group, opg = p->m / p->group;
-    const long long in_hw = (long long)p->h * p->w, out_hw = (long long)p->oh * p->ow;
+    const long long out_hw = (long long)p->oh * p->ow;
 
     switch (select_algo(p)) {
     case ALGO_DEPTHWISE: {
@@ -478,14 +499,15 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         dim3 grid((unsigned)((total + 255) / 256));
 #define OSH_FIRST(MM, CC)                                                                                      \
     OSH_DISPATCH_ACT(act, ACT, hipLaunchKernelGGL((first_conv_kernel<MM, CC, ACT>), grid, dim3(256), 0, stream, \
-                                                  *p, d_x, w, d_bias, d_y))
+                                                  *p, d_x, w, d_bias, d_res, d_y))
 #define OSH_FIRST_C(MM)            \
     do {                           \
         switch (p->c) {            \
         case 1: OSH_FIRST(MM, 1); break; \
         case 2: OSH_FIRST(MM, 2); break; \
         case 3: OSH_FIRST(MM, 3); break; \
-        default: OSH_FIRST(MM, 4); break; \
+        case 4: OSH_FIRST(MM, 4); break; \
+        default: OSH_FIRST(MM, 8); break; \
         }                          \
     } while (0)
         if (p->m == 8) OSH_FIRST_C(8);
@@ -494,7 +516,7 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
 #undef OSH_FIRST_C
 #undef OSH_FIRST
         OSH_LAUNCH_CHECK("first_conv_kernel");
-        return residual_add(p, d_res, d_y, stream);
+        return OSH_OK;
     }
     case ALGO_CONV16:
         return conv16_tuned_launch(p, d_x, w, d_bias, d_res, act, d_y, stream);

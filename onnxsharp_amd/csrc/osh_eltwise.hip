@@ -13,6 +13,14 @@ using namespace osh;
 
 namespace osh {
 
+// MathF.Max: NaN if either operand is NaN; +0 over -0.
+__device__ __forceinline__ float dotnet_max(float a, float b) {
+    if (a != a || b != b) return __builtin_nanf("");
+    if (a > b) return a;
+    if (b > a) return b;
+    return __builtin_signbitf(a) ? b : a;  // equal: +0 over -0
+}
+
 template <int ACT>
 __global__ __launch_bounds__(256) void activation_kernel(const float *__restrict__ x, float *__restrict__ y,
                                                           long long n) {
@@ -151,12 +159,6 @@ __global__ __launch_bounds__(256) void maxpool_chain3_kernel(int h, int w, int c
 // recomputed (same bits) rather than stored.  `tail` marks the columns the
 // reference handles on its scalar lines: the last (width % 8) of each block
 // of 256 pixels.
-__device__ __forceinline__ float dotnet_max(float a, float b) {
-    if (a != a || b != b) return __builtin_nanf("");
-    if (a > b) return a;
-    if (b > a) return b;
-    return __builtin_signbitf(a) ? b : a;  // equal: +0 over -0
-}
 
 __global__ __launch_bounds__(256) void dfl_kernel(int sides, int bins, int pixels, const float *__restrict__ x,
                                                   long long x_bs, float *__restrict__ y, long long y_bs,
@@ -236,27 +238,50 @@ __device__ __forceinline__ float wave_sum_f(float v) {
     return v;
 }
 
-// One wave per row: max of scale*x, e = exp_ref(v - max) stored and summed,
-// then y = e * (1 / sum) (VectorMath.SoftmaxRow scales by the reciprocal).
+
+// VectorMath.SoftmaxRow (src/OnnxSharp/Tensors/VectorMath.cs:172-204,246-287)
+// on v = x * scale (the Mul node before the Softmax rounds it), summed in its
+// order: the reference's eight float lanes each add the exponentials of
+// v[8j + k] in order of j; the eight lane sums are added to 0 in lane order,
+// then the (cols % 8) tail values; y = e * (1 / sum).
+//   The max only enters through (v - max), whose exponential does not depend
+// on how equal candidates (+0 / -0) were ordered, so any order gives the
+// same bits for inputs without NaN (NaN inputs: not pinned).
+// One wave per row: all lanes compute the exponentials into the wave's LDS row
+// (SOFTMAX_LDS_COLS at most; longer rows use the row of y itself), lanes 0-7
+// form the lane sums from it, lane 0 the total.
+constexpr int SOFTMAX_LDS_COLS = 4096;
+
+template <bool LDS>
 __global__ __launch_bounds__(256) void softmax_kernel(long long rows, int cols, float scale,
-                                                       const float *__restrict__ x, float *__restrict__ y) {
-    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const float *xr = x + row * cols;
-    float *yr = y + row * cols;
+                                                      const float *__restrict__ x, float *__restrict__ y) {
+    extern __shared__ float srow[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long row = (long long)blockIdx.x * 4 + wave;
+    const bool live = row < rows;
+    const float *xr = x + (live ? row : 0) * cols;
+    float *yr = y + (live ? row : 0) * cols;
+    float *buf = LDS ? srow + wave * cols : yr;
     float m = -__builtin_inff();
-    for (int c = lane; c < cols; c += 64) m = __builtin_fmaxf(m, xr[c] * scale);
+    if (live)
+        for (int c = lane; c < cols; c += 64) m = __builtin_fmaxf(m, xr[c] * scale);
     m = wave_max_f(m);
-    float sum = 0.f;
-    for (int c = lane; c < cols; c += 64) {
-        const float e = exp_ref(xr[c] * scale - m);
-        yr[c] = e;
-        sum += e;
-    }
-    sum = wave_sum_f(sum);
-    const float inv = 1.0f / sum;
-    for (int c = lane; c < cols; c += 64) yr[c] = yr[c] * inv;
+    if (live)
+        for (int c = lane; c < cols; c += 64) buf[c] = exp_ref(xr[c] * scale - m);
+    if (LDS) __syncthreads();
+    else __threadfence();  // the lane sums read values other lanes wrote to y
+    const int vec = cols & ~7;
+    float part = 0.0f;
+    if (live && lane < 8)
+        for (int i = lane; i < vec; i += 8) part = part + buf[i];
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) sum = sum + __shfl(part, q);
+    if (live && lane == 0)
+        for (int i = vec; i < cols; i++) sum = sum + buf[i];
+    const float inv = 1.0f / __shfl(sum, 0);
+    if (live)
+        for (int c = lane; c < cols; c += 64) yr[c] = buf[c] * inv;
 }
 
 static unsigned grid_for(long long n, long long per_block, long long cap) {
@@ -378,8 +403,12 @@ OSH_API osh_status osh_softmax_f32(int64_t rows, int cols, float scale, const fl
     if (rows == 0 || cols == 0) return OSH_OK;
     if (!d_x || !d_y) return fail(OSH_E_INVALID, "Softmax: NULL pointer");
     if (d_x == d_y) return fail(OSH_E_INVALID, "Softmax: in-place is not supported");
-    hipLaunchKernelGGL(softmax_kernel, dim3(grid_for(rows, 4, 0x7fffffff)), dim3(256), 0, to_stream(s),
-                       (long long)rows, cols, scale, d_x, d_y);
+    if (cols <= SOFTMAX_LDS_COLS)
+        hipLaunchKernelGGL(softmax_kernel<true>, dim3(grid_for(rows, 4, 0x7fffffff)), dim3(256),
+                           (size_t)4 * cols * sizeof(float), to_stream(s), (long long)rows, cols, scale, d_x, d_y);
+    else
+        hipLaunchKernelGGL(softmax_kernel<false>, dim3(grid_for(rows, 4, 0x7fffffff)), dim3(256), 0, to_stream(s),
+                           (long long)rows, cols, scale, d_x, d_y);
     OSH_LAUNCH_CHECK("softmax_kernel");
     return OSH_OK;
 }

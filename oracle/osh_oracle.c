@@ -476,6 +476,15 @@ ORC_API void orc_silu_scalar(long n, const float *x, float *y)
     for (long i = 0; i < n; i++) y[i] = x[i] * (1.0f / (1.0f + expf(-x[i])));
 }
 
+/* MathF.Max: NaN if either operand is NaN; +0 over -0. */
+static float dotnet_max(float a, float b)
+{
+    if (a != a || b != b) return NAN;
+    if (a > b) return a;
+    if (b > a) return b;
+    return signbit(a) ? b : a; /* equal: +0 over -0 */
+}
+
 /* Sigmoid of the vector path (VectorMath.cs:64-68): 1 / (1 + exp(x * -1)). */
 ORC_API void orc_sigmoid_ref(long n, const float *x, float *y)
 {
@@ -491,13 +500,6 @@ ORC_API void orc_sigmoid_ref(long n, const float *x, float *y)
  * The last width % 8 columns of a block take the scalar lines: MathF.Max
  * (NaN if either is NaN), MathF.Exp (here exp_ref: its bits are not pinned
  * against .NET), and w += e_b * inv * b with three roundings. */
-static float dotnet_max(float a, float b)
-{
-    if (a != a || b != b) return NAN;
-    if (a > b) return a;
-    if (b > a) return b;
-    return signbit(a) ? b : a; /* equal: +0 over -0 */
-}
 
 ORC_API void orc_dfl_f32(int batches, int sides, int bins, int pixels, const float *x, float *y)
 {
@@ -538,23 +540,55 @@ ORC_API void orc_relu(long n, const float *x, float *y)
 
 /* ------------------------------------------------- segment-continuity ops */
 
+
+/* VectorMath.SoftmaxRow (VectorMath.cs:172-204,246-287) on rows of the
+ * scaled input (the Mul node runs first, so v = x * scale is rounded):
+ *   max: MaxRow -- eight lanes, lane k folding v[8j + k] with Avx.Max (maxps:
+ *        the later value unless the running one is greater), the lanes
+ *        combined as max(max(l0,l4), max(l2,l6)) vs max(max(l1,l5), max(l3,l7))
+ *        through MathF.Max, then the tail with MathF.Max; rows shorter than 8
+ *        fold MathF.Max from -inf;
+ *   sum: SumExp -- lane k sums e = Exp(v - max) over v[8j + k] in order; the
+ *        eight lane sums are added in lane order to 0, then the tail values
+ *        (MathF.Exp in the reference, its bits not pinned; exp_ref here);
+ *   y = e * (1 / sum). */
+static float maxps1(float a, float b) { return a > b ? a : b; }
+
 ORC_API void orc_softmax_f32(long rows, int cols, float scale, const float *x, float *y)
 {
     for (long r = 0; r < rows; r++) {
         const float *xr = x + r * cols;
         float *yr = y + r * cols;
+        const int vec = cols & ~7;
         float mx = -INFINITY;
-        for (int c = 0; c < cols; c++) {
-            float v = xr[c] * scale;
-            if (v > mx) mx = v;
+        if (cols >= 8) {
+            float acc[8];
+            for (int k = 0; k < 8; k++) acc[k] = xr[k] * scale;
+            for (int i = 8; i <= cols - 8; i += 8)
+                for (int k = 0; k < 8; k++) acc[k] = maxps1(acc[k], xr[i + k] * scale);
+            float lo[4];
+            for (int q = 0; q < 4; q++) lo[q] = maxps1(acc[q], acc[q + 4]);
+            const float l0 = maxps1(lo[0], lo[2]), l1 = maxps1(lo[1], lo[3]);
+            mx = dotnet_max(l0, l1);
+            for (int i = vec; i < cols; i++) mx = dotnet_max(mx, xr[i] * scale);
+        } else {
+            for (int i = 0; i < cols; i++) mx = dotnet_max(mx, xr[i] * scale);
         }
+        float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int i = 0; i < vec; i += 8)
+            for (int k = 0; k < 8; k++) {
+                const float e = exp_ref(xr[i + k] * scale - mx);
+                yr[i + k] = e;
+                lane[k] = lane[k] + e;
+            }
         float sum = 0.0f;
-        for (int c = 0; c < cols; c++) {
-            float e = exp_ref(xr[c] * scale - mx);
-            yr[c] = e;
-            sum += e;
+        for (int k = 0; k < 8; k++) sum = sum + lane[k];
+        for (int i = vec; i < cols; i++) {
+            const float e = exp_ref(xr[i] * scale - mx);
+            yr[i] = e;
+            sum = sum + e;
         }
-        float inv = 1.0f / sum;
+        const float inv = 1.0f / sum;
         for (int c = 0; c < cols; c++) yr[c] = yr[c] * inv;
     }
 }

@@ -61,6 +61,12 @@ CASES = [
 
 @pytest.mark.parametrize("name,xs,ws,attrs,act", CASES, ids=[c[0] for c in CASES])
 def test_conv_parity(cuda, oracle, name, xs, ws, attrs, act):
+    # Every default kernel sums in the order of the reference's kernel for the
+    # shape: the NCHWc chain for 3x3 with C % 16 == 0 (AVX-512 hosts), the
+    # depthwise chain, else the im2col / GEMM chain.  With the exact SiLU the
+    # output is the oracle's, bit for bit; with the default SiLU it is within
+    # the FP32 bar (and within it of the other ISA order too).
+    from onnxsharp_amd import native as N
     print(f"conv {name} x={xs} w={ws} {attrs} act={act}", flush=True)
     seed = sum(xs) * 7 + sum(ws)
     x = synth.uniform(seed, xs)
@@ -71,9 +77,19 @@ def test_conv_parity(cuda, oracle, name, xs, ws, attrs, act):
     nbad, dmax = fp32_violations(y, ref)
     print(f"  max|d|={dmax:.3e} violations={nbad}", flush=True)
     assert_fp32_close(y, ref, name)
-    # also within the bar of the other ISA order
     alt = oracle_conv(oracle, x, w, b, p, act, order=oracle.ORDER_IM2COL)
     assert_fp32_close(y, alt, name + " (im2col order)")
+    N.call("osh_config_set", b"exact_silu", 1)
+    try:
+        ye, _ = run_conv(cuda, x, w, b, act, **attrs)
+    finally:
+        N.call("osh_config_set", b"exact_silu", 0)
+    dw = p.group > 1 and p.group == p.c == p.m
+    ref = oracle_conv(oracle, x, w, b, p, act) if not dw else oracle.conv_dw_f32(
+        x, w, b, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), (p.oh, p.ow))
+    if dw and act == "Silu":
+        ref = oracle.silu_ref(ref)
+    assert np.array_equal(ye, ref), f"{name}: max |d| {np.abs(ye - ref).max():.3e}"
 
 
 def test_conv_known_answer_same_upper(cuda):
@@ -115,7 +131,9 @@ def test_conv_silu_epilogue_on_bias_only_input(cuda, oracle):
     ((1, 3, 37, 41), (8, 3, 3, 3), dict(pads=[1, 1, 1, 1])),
     ((2, 4, 20, 18), (32, 4, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
     ((1, 1, 9, 11), (8, 1, 3, 3), dict(auto_pad="SAME_UPPER", strides=[2, 2])),
-], ids=["stem_640", "c3_m8_s1", "c4_m32_s2_batch2", "c1_m8_same_upper"])
+    ((1, 8, 160, 160), (16, 8, 3, 3), dict(pads=[1, 1, 1, 1])),  # YOLO11n's 8 -> 16 bottleneck conv
+    ((2, 8, 21, 19), (32, 8, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+], ids=["stem_640", "c3_m8_s1", "c4_m32_s2_batch2", "c1_m8_same_upper", "c8_m16_160", "c8_m32_s2_batch2"])
 def test_first_layer_conv_is_the_fma_chain(cuda, oracle, xs, ws, attrs):
     # C <= 4 takes the direct first-layer kernel: per output channel the bias,
     # then fmaf over ic -> ky -> kx, the im2col chain -- bit for bit.
@@ -222,6 +240,7 @@ RESIDUAL_CASES = [
     ("direct3x3_c8_160", (1, 8, 160, 160), (16, 8, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
     ("depthwise_64_20", (1, 64, 20, 20), (64, 1, 3, 3), dict(group=64, pads=[1, 1, 1, 1]), -1),
     ("first_conv_c3", (1, 3, 64, 64), (16, 3, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
+    ("direct_c8_m16_160", (1, 8, 160, 160), (16, 8, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
     ("im2col_dilated_5x5", (1, 5, 23, 21), (7, 5, 5, 5), dict(pads=[4, 4, 4, 4], dilations=[2, 2]), -1),
     ("wave_independent_16", (1, 16, 24, 32), (16, 16, 3, 3), dict(pads=[1, 1, 1, 1]), -2),
     ("weight_stationary_s2", (1, 64, 40, 40), (64, 64, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), -2),
