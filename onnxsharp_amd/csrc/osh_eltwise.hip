@@ -78,20 +78,23 @@ __global__ __launch_bounds__(256) void maxpool2d_kernel(osh_pool_params p, const
 
 // Three chained k x k, stride 1, pad k/2 max pools (SPPF: y1 = pool(x),
 // y2 = pool(y1), y3 = pool(y2)) in one launch.  A workgroup owns a PT x PT
-// tile of one plane: it stages x over the tile plus a 3r halo in LDS, then
-// computes y1 over the tile plus 2r, y2 over the tile plus r and y3 over the
-// tile, each from the previous level in LDS.  Every output is the same
-// comparison as maxpool2d_kernel (start at -inf, keep v when v > max, so
-// positions outside the image and NaNs are never taken), so the chain is
-// bit-identical to three separate pools.
+// tile of one plane: it stages x over the tile plus a 3r halo in LDS (-inf
+// outside the image), then derives y1 over the tile plus 2r, y2 over the
+// tile plus r and y3 over the tile, each level as a row pass then a column
+// pass (outputs outside the image are set to -inf for the next level).
+// Every max is the comparison of maxpool2d_kernel (start at -inf, take v only
+// when v > max): with rows taken in order and each row's columns in order,
+// the two passes keep the first of equal maxima in row-major order exactly as
+// the k x k scan does, never take a NaN, and a -inf pad is never taken; so
+// the chain is bit-identical to three separate pools.
 template <int K>
 __global__ __launch_bounds__(256) void maxpool_chain3_kernel(int h, int w, int c, const float *__restrict__ x,
                                                              long long x_bstride, float *__restrict__ y1,
                                                              float *__restrict__ y2, float *__restrict__ y3,
                                                              long long y_bstride, int tiles_x) {
-    constexpr int PT = 32, R = K / 2;
+    constexpr int PT = 16, R = K / 2;
     constexpr int S0 = PT + 6 * R, S1 = PT + 4 * R, S2 = PT + 2 * R;
-    __shared__ float l0[S0 * S0], l1[S1 * S1], l2[S2 * S2];
+    __shared__ float l0[S0 * S0], l1[S1 * S1], l2[S2 * S2], tmp[S0 * S1];
     const int plane = blockIdx.y;  // n * c + channel
     const int n = plane / c, ch = plane - n * c;
     const int ty = blockIdx.x / tiles_x, tx = blockIdx.x - ty * tiles_x;
@@ -99,58 +102,51 @@ __global__ __launch_bounds__(256) void maxpool_chain3_kernel(int h, int w, int c
     const long long xoff = (long long)n * x_bstride + (long long)ch * h * w;
     const long long yoff = (long long)n * y_bstride + (long long)ch * h * w;
     const float *xp = x + xoff;
-    // level 0: x at rows oy0 - 3R + i (only positions inside the image are read later)
+    const float ninf = -__builtin_inff();
     for (int e = threadIdx.x; e < S0 * S0; e += 256) {
         const int i = e / S0, jx = e - i * S0;
         const int iy = oy0 - 3 * R + i, ix = ox0 - 3 * R + jx;
-        l0[e] = ((unsigned)iy < (unsigned)h && (unsigned)ix < (unsigned)w) ? xp[(long long)iy * w + ix] : 0.f;
+        l0[e] = ((unsigned)iy < (unsigned)h && (unsigned)ix < (unsigned)w) ? xp[(long long)iy * w + ix] : ninf;
     }
     __syncthreads();
-    // one pooling level: dst (size SD, origin o - DR) from src (size SS, origin o - SR)
-    auto level = [&](const float *src, int SS, int SR, float *dst, int SD, int DR) {
-        for (int e = threadIdx.x; e < SD * SD; e += 256) {
+    // dst (SD x SD, origin o - DR) from src ((SD + 2R) x (SD + 2R))
+    auto level = [&](const float *src, float *dst, int SD, int DR) {
+        const int SS = SD + 2 * R;
+        for (int e = threadIdx.x; e < SS * SD; e += 256) {  // row pass: SS rows x SD columns
+            const int i = e / SD, jx = e - i * SD;
+            float m = ninf;
+#pragma unroll
+            for (int kx = 0; kx < K; kx++) {
+                const float v = src[i * SS + jx + kx];
+                if (v > m) m = v;
+            }
+            tmp[e] = m;
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < SD * SD; e += 256) {  // column pass
             const int i = e / SD, jx = e - i * SD;
             const int py = oy0 - DR + i, px = ox0 - DR + jx;
-            float m = -__builtin_inff();
-            if ((unsigned)py < (unsigned)h && (unsigned)px < (unsigned)w) {
-                for (int ky = 0; ky < K; ky++) {
-                    const int iy = py - R + ky;
-                    if ((unsigned)iy >= (unsigned)h) continue;
-                    for (int kx = 0; kx < K; kx++) {
-                        const int ix = px - R + kx;
-                        if ((unsigned)ix >= (unsigned)w) continue;
-                        const float v = src[(iy - (oy0 - SR)) * SS + (ix - (ox0 - SR))];
-                        if (v > m) m = v;
-                    }
-                }
+            float m = ninf;
+#pragma unroll
+            for (int ky = 0; ky < K; ky++) {
+                const float v = tmp[(i + ky) * SD + jx];
+                if (v > m) m = v;
             }
-            dst[e] = m;
+            dst[e] = ((unsigned)py < (unsigned)h && (unsigned)px < (unsigned)w) ? m : ninf;
         }
+        __syncthreads();
     };
-    level(l0, S0, 3 * R, l1, S1, 2 * R);
-    __syncthreads();
-    level(l1, S1, 2 * R, l2, S2, R);
-    __syncthreads();
-    // y3 over the tile, and the tile's part of y1 and y2
+    level(l0, l1, S1, 2 * R);
+    level(l1, l2, S2, R);
+    level(l2, l0, PT, 0);  // y3 over the tile, into the (free) x buffer
     for (int e = threadIdx.x; e < PT * PT; e += 256) {
         const int i = e / PT, jx = e - i * PT;
         const int py = oy0 + i, px = ox0 + jx;
         if (py >= h || px >= w) continue;
-        float m = -__builtin_inff();
-        for (int ky = 0; ky < K; ky++) {
-            const int iy = py - R + ky;
-            if ((unsigned)iy >= (unsigned)h) continue;
-            for (int kx = 0; kx < K; kx++) {
-                const int ix = px - R + kx;
-                if ((unsigned)ix >= (unsigned)w) continue;
-                const float v = l2[(iy - (oy0 - R)) * S2 + (ix - (ox0 - R))];
-                if (v > m) m = v;
-            }
-        }
         const long long o = yoff + (long long)py * w + px;
         y1[o] = l1[(i + 2 * R) * S1 + jx + 2 * R];
         y2[o] = l2[(i + R) * S2 + jx + R];
-        y3[o] = m;
+        y3[o] = l0[i * PT + jx];
     }
 }
 
@@ -339,7 +335,7 @@ OSH_API osh_status osh_maxpool_chain3_f32(int n, int c, int h, int w, int k, con
     if (x_batch_stride < plane || y_batch_stride < plane)
         return fail(OSH_E_INVALID, "MaxPool chain: batch stride below c*h*w");
     if ((long long)n * c > 65535) return fail(OSH_E_UNSUPPORTED, "MaxPool chain: more than 65535 planes");
-    const int tiles_x = (w + 31) / 32, tiles_y = (h + 31) / 32;
+    const int tiles_x = (w + 15) / 16, tiles_y = (h + 15) / 16;
     if ((long long)tiles_x * tiles_y > 0x7fffffff) return fail(OSH_E_UNSUPPORTED, "MaxPool chain: image too large");
     dim3 grid((unsigned)(tiles_x * tiles_y), (unsigned)(n * c));
     hipStream_t st = to_stream(s);
