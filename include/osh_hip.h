@@ -361,6 +361,20 @@ OSH_API osh_status osh_transpose_f32(int batch, int rows, int cols, const float 
  * src/OnnxSharp/Tensors/VectorMath.cs:282-287; exp is the reference polynomial). */
 OSH_API osh_status osh_softmax_f32(int64_t rows, int cols, float scale, const float *d_x, float *d_y, osh_stream s);
 
+/* The attention core of a YOLO11n C2PSA block in one launch, equal bit for bit
+ * to the node sequence the reference runs for it (its attention fusion,
+ * src/OnnxSharp/Core/GraphFusion.cs:950-1150, does not match this form):
+ * MatMul(Transpose(q), k) -> Mul(scale) -> Softmax(-1) -> MatMul(v, Transpose(P))
+ * (MatMulLayer src/OnnxSharp/Ops/DnnOps.cs:2789, SoftmaxLayer DnnOps.cs:2547-2675).
+ * Head h reads q = rows [0, key_dim), k = rows [key_dim, 2 key_dim) and
+ * v = rows [2 key_dim, 2 key_dim + head_dim) of n values at
+ * d_qkv + h * head_stride and writes y[h][c][i] (head_dim x n per head, dense).
+ * Needs key_dim % 4 == 0, key_dim <= 64, head_dim % 16 == 0, n % 16 == 0 and n <= 480
+ * (OSH_E_UNSUPPORTED otherwise: run the five-launch sequence); y must not
+ * overlap qkv. */
+OSH_API osh_status osh_attention_f32(int heads, int key_dim, int head_dim, int n, float scale, const float *d_qkv,
+                                     int64_t head_stride, float *d_y, osh_stream s);
+
 /* ----------------------------------------------------------- HIP graphs */
 /* A segment's launches recorded once and replayed per Forward, the role of
  * the Vulkan backend's recorded command buffers (src/OnnxSharp.Vulkan/VkSegment.cs:324-600).

@@ -109,6 +109,7 @@ _SIGS = {
     "osh_resize_nearest_f32": ([_i, _i, _i, _i, _i, _i, _vp, _vp, _i64, _vp], _i),
     "osh_transpose_f32": ([_i, _i, _i, _vp, _i64, _vp, _i64, _vp], _i),
     "osh_softmax_f32": ([_i64, _i, C.c_float, _vp, _vp, _vp], _i),
+    "osh_attention_f32": ([_i, _i, _i, _i, C.c_float, _vp, _i64, _vp, _vp], _i),
     "osh_graph_begin": ([_vp], _i),
     "osh_graph_end": ([_vp, C.POINTER(_vp)], _i),
     "osh_graph_launch": ([_vp, _vp], _i),

@@ -560,14 +560,22 @@ def op_dependencies(ops):
 
 # --------------------------------------------------------------- device side
 
+def attention_fits(key_dim: int, head_dim: int, n: int) -> bool:
+    """The shapes osh_attention_f32 takes: 16-row query tiles, key_dim / 4 <= 16
+    k-steps in registers, 16-channel output blocks, and 16 score rows of n <= 480
+    beside the staged v chunks in 64 KiB of LDS."""
+    return key_dim % 4 == 0 and key_dim <= 64 and head_dim % 16 == 0 and n % 16 == 0 and n <= 480
+
+
 class Frame:
     """Device buffers, packed weights and the launch list of one model, spread
     over `nstreams` streams (fork/join through events) so that independent
     branches -- the detection head's six chains, the P3 head beside the rest
     of the neck -- run side by side."""
 
-    def __init__(self, model: Model, device, nstreams: int = 4, fuse: bool = True):
+    def __init__(self, model: Model, device, nstreams: int = 4, fuse: bool = True, fused_attention: bool = True):
         import torch
+        self.fused_attention = fused_attention
         if fuse:  # conv -> residual Add pairs and SPPF's pools run as single launches
             model = fuse_launches(model)
         self.model = model
@@ -666,6 +674,12 @@ class Frame:
         v = C.c_void_p(base + 4 * 2 * op.key_dim * n)
         qt, sc, st = (C.c_void_p(b.tensor.data_ptr()) for b in (op.qt, op.attn, op.attn_t))
         y = op.y.ptr()
+
+        if self.fused_attention and attention_fits(op.key_dim, op.head_dim, n):
+            def run_fused(stream):
+                N.check(lib.osh_attention_f32(op.heads, op.key_dim, op.head_dim, n, C.c_float(op.scale), q, hs, y,
+                                              stream))
+            return run_fused
 
         def run(stream):
             # q^T per head: [kd, N] -> [N, kd]

@@ -157,3 +157,20 @@ def test_dfl_softmax_shapes():
         DflSoftmaxLayer(16).get_memory_shapes((64, 10))
     st = N.lib().osh_dfl_f32(1, 4, 1, 10, C.c_void_p(1 << 40), 40, C.c_void_p(1 << 41), 40, None)
     assert st == N.OSH_E_INVALID and "bins" in N.last_error()
+
+
+def test_attention_shape_rules_match_the_frame_planner():
+    # y == qkv: every shape the kernel takes stops at the overlap check
+    # (OSH_E_INVALID) before a launch; the rest are OSH_E_UNSUPPORTED, which
+    # the frame planner must predict so that it runs the five-launch sequence
+    from onnxsharp_amd.yolo11n import attention_fits
+    lib = N.lib()
+    base = C.c_void_p(1 << 40)
+    for kd in (4, 28, 30, 32, 64, 68):
+        for hd in (16, 40, 64, 128):
+            for n in (16, 100, 400, 408, 480, 496):
+                st = lib.osh_attention_f32(2, kd, hd, n, C.c_float(0.5), base, (2 * kd + hd) * n, base, None)
+                want = N.OSH_E_INVALID if attention_fits(kd, hd, n) else N.OSH_E_UNSUPPORTED
+                assert st == want, (kd, hd, n, N.last_error())
+    st = lib.osh_attention_f32(1, 32, 64, 400, C.c_float(1.0), base, 128 * 400 - 1, C.c_void_p(1 << 41), None)
+    assert st == N.OSH_E_INVALID and "stride" in N.last_error()

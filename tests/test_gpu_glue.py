@@ -194,3 +194,61 @@ def test_sigmoid_matches_oracle(cuda, oracle):
     x = synth.normal(980, (1, 80, 40, 40), 0, 6)
     y = ActivationLayer("Sigmoid").forward(_dev(x, cuda)).cpu().numpy()
     assert np.array_equal(y, oracle.sigmoid_ref(x))
+
+
+ATTENTION = [(2, 32, 64, 400), (1, 4, 16, 16), (3, 8, 32, 480), (2, 16, 48, 80), (1, 32, 64, 32), (1, 64, 16, 48),
+             (2, 28, 32, 272), (1, 32, 128, 208)]
+
+
+@pytest.mark.parametrize("heads,kd,hd,n", ATTENTION, ids=[f"h{h}_kd{k}_hd{d}_n{n}" for h, k, d, n in ATTENTION])
+def test_fused_attention_is_the_node_sequence(cuda, oracle, heads, kd, hd, n):
+    # one launch against MatMul(q^T, k) -> Mul -> Softmax -> MatMul(v, P^T) as
+    # the oracle restates the nodes, and against the five-launch device path
+    import types
+    import torch
+    from onnxsharp_amd import native as N
+    from oracle import yolo_frame as YO
+    rows = 2 * kd + hd
+    pad = 7 * n  # a head stride above the dense one
+    hs = rows * n + pad
+    qkv = synth.normal(960 + n, (heads, hs), 0, 1)
+    scale = kd ** -0.5
+    dq = _dev(qkv, cuda)
+    y = torch.full((heads * hd * n,), float("nan"), device=cuda)
+    N.call("osh_attention_f32", heads, kd, hd, n, C.c_float(scale), _p(dq), hs, _p(y), None)
+    # five launches: q^T, scores, softmax, P^T, v P^T
+    qt = torch.empty(heads * n * kd, device=cuda)
+    sc = torch.empty(heads * n * n, device=cuda)
+    st = torch.empty_like(sc)
+    y5 = torch.empty_like(y)
+    base = dq.data_ptr()
+    N.call("osh_transpose_f32", heads, kd, n, C.c_void_p(base), hs, _p(qt), n * kd, None)
+    N.call("osh_gemm_f32_batched", heads, n, n, kd, _p(qt), kd, n * kd, C.c_void_p(base + 4 * kd * n), n, hs,
+           None, N.ACT_NONE, _p(sc), n, n * n, None)
+    N.call("osh_softmax_f32", heads * n, n, C.c_float(scale), _p(sc), _p(st), None)
+    N.call("osh_transpose_f32", heads, n, n, _p(st), n * n, _p(sc), n * n, None)
+    N.call("osh_gemm_f32_batched", heads, hd, n, n, C.c_void_p(base + 8 * kd * n), n, hs, _p(sc), n, n * n, None,
+           N.ACT_NONE, _p(y5), n, hd * n, None)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(heads, hd, n)
+    dense = np.ascontiguousarray(qkv[:, :rows * n])
+    op = types.SimpleNamespace(qkv=types.SimpleNamespace(h=1, w=n), key_dim=kd, head_dim=hd, heads=heads,
+                               scale=scale, y=types.SimpleNamespace(c=heads * hd, h=1, w=n))
+    expect = YO.attention(oracle, op, dense).reshape(heads, hd, n)
+    assert np.array_equal(_bits(got), _bits(expect)), f"attention h{heads} kd{kd} hd{hd} n{n} vs oracle"
+    assert np.array_equal(_bits(got), _bits(y5.cpu().numpy().reshape(heads, hd, n))), "fused vs five launches"
+
+
+def test_fused_attention_rejects_what_it_cannot_take(cuda):
+    import torch
+    from onnxsharp_amd import native as N
+    q = torch.zeros(2 * 128 * 1008, device=cuda)
+    y = torch.zeros(64 * 1008, device=cuda)
+    for heads, kd, hd, n in [(1, 32, 64, 1008), (1, 32, 64, 496), (1, 30, 64, 400), (1, 32, 40, 400),
+                             (1, 32, 64, 408), (1, 68, 64, 400)]:
+        rc = N.lib().osh_attention_f32(heads, kd, hd, n, C.c_float(1.0), _p(q), (2 * kd + hd) * n, _p(y), None)
+        assert rc == N.OSH_E_UNSUPPORTED, (heads, kd, hd, n)
+    # y inside qkv
+    rc = N.lib().osh_attention_f32(1, 32, 64, 400, C.c_float(1.0), _p(q), 128 * 400, C.c_void_p(q.data_ptr() + 4),
+                                   None)
+    assert rc == N.OSH_E_INVALID
