@@ -42,7 +42,10 @@ struct C16Chunk {
     float b[3][4][BV];    // per tap and k4 step: the lane's input value of each pixel
 };
 
-template <int TM, int BV, int ACT>
+// WPB waves per workgroup: 4 packs a workgroup's waves onto one CU's SIMDs;
+// 1 spreads the same waves over as many CUs, which for maps with few tiles
+// and deep K leaves each wave a CU's L1 bandwidth for its operand stream.
+template <int TM, int BV, int ACT, int WPB = 4>
 __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const float *__restrict__ x,
                                                      const float *__restrict__ wpk, const float *__restrict__ bias,
                                                      const float *__restrict__ res, float *__restrict__ y,
@@ -50,7 +53,7 @@ __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const fl
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15, g = lane >> 4;
-    const int pt = blockIdx.x * 4 + wave;  // pixel tile
+    const int pt = blockIdx.x * WPB + wave;  // pixel tile
     if (pt >= tiles_p) return;             // whole wave; no barriers below
     const int mt = blockIdx.y;             // output-channel tile of 16*TM
     const int n = blockIdx.z;
@@ -369,17 +372,17 @@ inline osh_status conv16_pack(const osh_conv_params *p, const float *w, void *ou
 // Tile choice: 16*TM output channels x 16*BV pixels per wave.  Prefer the
 // shape whose waves fill the SIMDs in the fewest rounds of the longest chain;
 // larger tiles load fewer operands per MFMA.
-template <int TM, int BV>
+template <int TM, int BV, int WPB = 4>
 inline osh_status conv16_launch_t(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                   const float *res, int act, float *y, hipStream_t st) {
     const int ohw = p->oh * p->ow;
     const int tiles_p = ceil_div(ohw, 16 * BV);
     // output-channel tiles: TM 16-blocks each; the packed weights hold ceil(M/16) blocks
     const int mtiles = ceil_div(ceil_div(p->m, 16), TM);
-    dim3 grid((unsigned)ceil_div(tiles_p, 4), (unsigned)mtiles, (unsigned)p->n);
+    dim3 grid((unsigned)ceil_div(tiles_p, WPB), (unsigned)mtiles, (unsigned)p->n);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16_kernel<TM, BV, ACT>), grid, dim3(256), 0, st, *p, x, w, bias, res, y,
-                                        tiles_p));
+                     hipLaunchKernelGGL((conv16_kernel<TM, BV, ACT, WPB>), grid, dim3(64 * WPB), 0, st, *p, x, w,
+                                        bias, res, y, tiles_p));
     OSH_LAUNCH_CHECK("conv16_kernel");
     return OSH_OK;
 }
@@ -409,6 +412,20 @@ struct C16Variant {
 constexpr C16Variant kC16[] = {{1, 1, 0}, {2, 1, 0}, {4, 1, 0}, {1, 2, 0}, {2, 2, 0}, {4, 2, 0},
                                {1, 1, 1}, {2, 1, 1}, {4, 1, 1}, {1, 2, 1}, {2, 2, 1}, {4, 2, 1}};
 constexpr int kC16Count = sizeof(kC16) / sizeof(kC16[0]);
+
+// The same streamed tiles with one wave per workgroup (WPB = 1).
+constexpr C16Variant kC16w[] = {{1, 1, 0}, {1, 2, 0}, {2, 1, 0}, {2, 2, 0}};
+constexpr int kC16wCount = sizeof(kC16w) / sizeof(kC16w[0]);
+
+inline osh_status conv16w_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                 const float *res, int act, float *y, hipStream_t st, int v) {
+    switch (v) {
+    case 0: return conv16_launch_t<1, 1, 1>(p, x, w, bias, res, act, y, st);
+    case 1: return conv16_launch_t<1, 2, 1>(p, x, w, bias, res, act, y, st);
+    case 2: return conv16_launch_t<2, 1, 1>(p, x, w, bias, res, act, y, st);
+    default: return conv16_launch_t<2, 2, 1>(p, x, w, bias, res, act, y, st);
+    }
+}
 
 // Predicted cost: rounds of waves over the SIMDs times the MFMAs of one wave,
 // inflated by its operand loads per MFMA (TM/4 weight loads and BV input
