@@ -331,11 +331,13 @@ class CopyWorkload(Workload):
 
 def make_workload(name, dev):
     if name == "c2":
-        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "conv16_kernel", 1)
+        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "conv16s_kernel (tuned tile)", 1)
     if name == "c3a":
-        return ConvWorkload(dev, "c3a", (1, 256, 80, 80), (128, 256, 1, 1), 1, "Silu", "gemm16_kernel", 11)
+        return ConvWorkload(dev, "c3a", (1, 256, 80, 80), (128, 256, 1, 1), 1, "Silu", "conv16s_kernel (tuned 1x1 tile)",
+                            11)
     if name == "c3b":
-        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "conv16_kernel", 21)
+        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "conv16s_kernel (tuned tile)",
+                            21)
     if name == "c1":
         return GemmWorkload(dev)
     if name == "c5":

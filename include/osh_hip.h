@@ -90,7 +90,8 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 0..N-1 forces a tile where the shape allows it (6..11:
  *                 weights held in LDS; 12..20: input patch staged in LDS
  *                 and shared by a workgroup's four waves, stride 1 or 2;
- *                 21..N-1: tiles 0, 3, 1, 4 with one wave per workgroup);
+ *                 21..24: tiles 0, 3, 1, 4 with one wave per workgroup;
+ *                 25..N-1: tiles 13, 14, 15 with XCD-banded workgroups);
  *                 -2 = use the weight-stationary 3x3
  *                 kernels instead (summation order differs; within the FP32
  *                 tolerance).  Initial value from ONNXSHARP_HIP_CONV16_VARIANT.

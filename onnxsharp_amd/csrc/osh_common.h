@@ -104,6 +104,17 @@ __device__ __forceinline__ float activate(float x) {
 
 bool exact_silu();
 
+// Workgroups are dealt to the eight XCDs round-robin by linear id, and each
+// XCD has its own L2.  xcd_band(L, G) renumbers workgroup L of a grid of G so
+// that the workgroups of one XCD take one contiguous band of ids: XCD
+// x = L % 8 takes ids [x q + min(x, r), ...) with q = G / 8, r = G % 8 -- a
+// bijection on [0, G).  Neighbouring tiles, which share input lines and
+// weights, then meet in the same L2.
+__device__ __forceinline__ int xcd_band(int L, int G) {
+    const int x = L & 7, k = L >> 3, q = G >> 3, r = G & 7;
+    return x * q + (x < r ? x : r) + k;
+}
+
 // Compute units of the current device (256 on MI355X).
 inline int device_cus() {
     static int cus = 0;

@@ -245,17 +245,20 @@ static bool capturing(hipStream_t st) {
 }
 
 // The 3x3 variant space: ids 0 .. kC16Count-1 are conv16 / conv16l tiles,
-// the next kC16sCount ids the LDS-patch kernel (stride 1 or 2 only), the
-// last kC16wCount conv16 tiles with one wave per workgroup.  All compute the
-// same chain.
-constexpr int kC3Count = kC16Count + kC16sCount + kC16wCount;
+// the next kC16sCount ids the LDS-patch kernel (stride 1 or 2 only), then
+// kC16wCount conv16 tiles with one wave per workgroup, then kC16sxCount
+// LDS-patch tiles with XCD-banded workgroups.  All compute the same chain.
+constexpr int kC3W0 = kC16Count + kC16sCount;
+constexpr int kC3X0 = kC3W0 + kC16wCount;
+constexpr int kC3Count = kC3X0 + kC16sxCount;
 int conv16_variant_count() { return kC3Count; }
 int pointwise_variant_count() { return 1 + kPW16Count; }
 
 static bool c3_fits(const osh_conv_params *p, int v) {
     if (v < kC16Count) return conv16_fits(p, kC16[v]);
-    if (v < kC16Count + kC16sCount) return conv16s_eligible(p);
-    return true;
+    if (v < kC3W0) return conv16s_eligible(p);
+    if (v < kC3X0) return true;
+    return conv16s_eligible(p);
 }
 
 // Predicted cost of an LDS-patch tile: rounds of waves over the SIMDs times
@@ -286,9 +289,10 @@ static osh_status c3_launch(const osh_conv_params *p, const float *x, const floa
                 if (c < bc) v = kC16Count + i, bc = c;
             }
     }
-    if (v >= kC16Count + kC16sCount && v < kC3Count)
-        return conv16w_launch(p, x, w, bias, res, act, y, st, v - kC16Count - kC16sCount);
-    if (v >= kC16Count && v < kC16Count + kC16sCount && conv16s_eligible(p))
+    if (v >= kC3X0 && v < kC3Count && conv16s_eligible(p))
+        return conv16sx_launch(p, x, w, bias, res, act, y, st, v - kC3X0);
+    if (v >= kC3W0 && v < kC3X0) return conv16w_launch(p, x, w, bias, res, act, y, st, v - kC3W0);
+    if (v >= kC16Count && v < kC3W0 && conv16s_eligible(p))
         return conv16s_launch(p, x, w, bias, res, act, y, st, v - kC16Count);
     return conv16_launch(p, x, w, bias, res, act, y, st, v < kC16Count ? v : -1);
 }

@@ -78,7 +78,9 @@ struct C16sGeom {
 
 // VEC: the patch is staged with 16-byte loads of four adjacent columns (a
 // 1x1 stride-1 kernel on a map with W % 4 == 0 and a 16-byte aligned input).
-template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT>
+// XB: workgroups take their tiles XCD-banded (xcd_band), so that the tiles
+// one XCD runs are neighbours whose patches share halo lines in its L2.
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT, bool XB = false>
 __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const float *__restrict__ x,
                                                       const float *__restrict__ wpk, const float *__restrict__ bias,
                                                       const float *__restrict__ res, float *__restrict__ y,
@@ -92,15 +94,21 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
-    const int ty = blockIdx.x / tiles_w, tx = blockIdx.x - ty * tiles_w;
+    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+    if constexpr (XB) {
+        const int wg = xcd_band(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                                gridDim.x * gridDim.y * gridDim.z);
+        bx = wg % gridDim.x, by = (wg / gridDim.x) % gridDim.y, bz = wg / (gridDim.x * gridDim.y);
+    }
+    const int ty = bx / tiles_w, tx = bx - ty * tiles_w;
     const int oy0 = ty * G::TH, ox0 = tx * TWL;
-    const int n = blockIdx.z;
+    const int n = bz;
     const int HW = p.h * p.w, OHW = p.oh * p.ow;
     const int C = p.c, M = p.m;
     const int icbs = C / 16;
     const int kgroups = icbs * G::T;
     const int nchunks = (icbs + CB - 1) / CB;
-    const int mb0 = (blockIdx.y * 4 + wave) * TM;       // first 16-channel output block of this wave
+    const int mb0 = (by * 4 + wave) * TM;               // first 16-channel output block of this wave
     const bool active = mb0 * 16 < M;                    // uniform per wave
     const float *xn = x + (long long)n * C * HW;
     const int iy0 = oy0 * S - p.pt, ix0 = ox0 * S - p.pl;
@@ -277,7 +285,7 @@ inline bool conv16s_eligible(const osh_conv_params *p) {
     return conv16_eligible(p) && p->sh == p->sw && (p->sh == 1 || p->sh == 2);
 }
 
-template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC>
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, bool XB = false>
 inline osh_status conv16s_launch_t(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                    const float *res, int act, float *y, hipStream_t st) {
     using G = C16sGeom<TM, BV, TWL, S, KS, CB, VEC>;
@@ -285,17 +293,17 @@ inline osh_status conv16s_launch_t(const osh_conv_params *p, const float *x, con
     const int mgroups = ceil_div(ceil_div(p->m, 16), 4 * TM);
     dim3 grid((unsigned)(tiles_w * tiles_h), (unsigned)mgroups, (unsigned)p->n);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16s_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT>), grid, dim3(256), 0, st,
-                                        *p, x, w, bias, res, y, tiles_w));
+                     hipLaunchKernelGGL((conv16s_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT, XB>), grid, dim3(256), 0,
+                                        st, *p, x, w, bias, res, y, tiles_w));
     OSH_LAUNCH_CHECK("conv16s_kernel");
     return OSH_OK;
 }
 
-template <int TM, int BV, int TWL>
+template <int TM, int BV, int TWL, bool XB = false>
 inline osh_status conv16s_launch_s(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                    const float *res, int act, float *y, hipStream_t st) {
-    if (p->sh == 1) return conv16s_launch_t<TM, BV, TWL, 1, 3, 1, false>(p, x, w, bias, res, act, y, st);
-    return conv16s_launch_t<TM, BV, TWL, 2, 3, 1, false>(p, x, w, bias, res, act, y, st);
+    if (p->sh == 1) return conv16s_launch_t<TM, BV, TWL, 1, 3, 1, false, XB>(p, x, w, bias, res, act, y, st);
+    return conv16s_launch_t<TM, BV, TWL, 2, 3, 1, false, XB>(p, x, w, bias, res, act, y, st);
 }
 
 inline osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
@@ -310,6 +318,19 @@ inline osh_status conv16s_launch(const osh_conv_params *p, const float *x, const
     case 6: return conv16s_launch_s<2, 2, 8>(p, x, w, bias, res, act, y, st);
     case 7: return conv16s_launch_s<1, 2, 4>(p, x, w, bias, res, act, y, st);
     default: return conv16s_launch_s<1, 4, 4>(p, x, w, bias, res, act, y, st);
+    }
+}
+
+// XCD-banded versions of the 16-column tiles (ids after the one-wave tiles).
+constexpr C16sVariant kC16sx[] = {{1, 2, 16}, {1, 4, 16}, {2, 2, 16}};
+constexpr int kC16sxCount = sizeof(kC16sx) / sizeof(kC16sx[0]);
+
+inline osh_status conv16sx_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                  const float *res, int act, float *y, hipStream_t st, int v) {
+    switch (v) {
+    case 0: return conv16s_launch_s<1, 2, 16, true>(p, x, w, bias, res, act, y, st);
+    case 1: return conv16s_launch_s<1, 4, 16, true>(p, x, w, bias, res, act, y, st);
+    default: return conv16s_launch_s<2, 2, 16, true>(p, x, w, bias, res, act, y, st);
     }
 }
 
