@@ -136,11 +136,12 @@ __global__ __launch_bounds__(256) void residual_add_kernel(long long n, const fl
 //
 // The first layer of an image network (C = 3 colour planes): too little K for
 // MFMA tiles (27 for 3x3) and HBM-bound (it reads the image once and writes M
-// planes).  One thread per output pixel keeps all M accumulators in registers;
-// the weight index is the same for every lane, so the weights come through
-// the scalar cache.  Per output channel the chain is bias, then fmaf over
-// ic -> ky -> kx (the panel order of FirstConv.cs:344-362); padding taps add
-// nothing.
+// planes).  One thread per output pixel keeps MM accumulators in registers
+// (output channels MM * blockIdx.y + 0 .. MM-1: smaller maps split M over
+// the grid's y so that more CUs take part); the weight index is the same for
+// every lane, so the weights come through the scalar cache.  Per output
+// channel the chain is bias, then fmaf over ic -> ky -> kx (the panel order of
+// FirstConv.cs:344-362); padding taps add nothing.
 template <int MM, int CC, int ACT>
 __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, const float *__restrict__ x,
                                                          const float *__restrict__ w,
@@ -154,6 +155,7 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
     const int oy = (int)(t % p.oh);
     const int n = (int)(t / p.oh);
     const int m = p.m;
+    const int oc0 = blockIdx.y * MM;
     // all CC*9 input taps are loaded before the first FMA (independent loads)
     float v[CC][3][3];
     const float *xn = x + (long long)n * CC * p.h * p.w;
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
     const float *rp = res ? res + yo : nullptr;
     // 3x3 taps at compile-time offsets: the weights arrive in wide scalar loads
 #pragma unroll
-    for (int oc = 0; oc < MM; oc++) {  // MM == m (eligibility)
+    for (int oc = oc0; oc < oc0 + MM; oc++) {  // m = MM * gridDim.y (launch)
         float acc = bias ? bias[oc] : 0.f;
         const float *wo = w + oc * CC * 9;
 #pragma unroll
@@ -504,7 +506,13 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
     }
     case ALGO_FIRST: {
         long long total = (long long)p->n * out_hw;
-        dim3 grid((unsigned)((total + 255) / 256));
+        // output channels per thread: all m, halved (down to 4) while the
+        // grid has fewer workgroups than CUs (8 -> 16 at 160x160: 11.0 ->
+        // 6.5 us; the 640x640 stem, already past one per CU, keeps all m)
+        int og = p->m;
+        const long long blocks = (total + 255) / 256;
+        while (og > 4 && blocks * (p->m / og) < device_cus()) og /= 2;
+        dim3 grid((unsigned)blocks, (unsigned)(p->m / og));
 #define OSH_FIRST(MM, CC)                                                                                      \
     OSH_DISPATCH_ACT(act, ACT, hipLaunchKernelGGL((first_conv_kernel<MM, CC, ACT>), grid, dim3(256), 0, stream, \
                                                   *p, d_x, w, d_bias, d_res, d_y))
@@ -518,8 +526,9 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         default: OSH_FIRST(MM, 8); break; \
         }                          \
     } while (0)
-        if (p->m == 8) OSH_FIRST_C(8);
-        else if (p->m == 16) OSH_FIRST_C(16);
+        if (og == 4) OSH_FIRST_C(4);
+        else if (og == 8) OSH_FIRST_C(8);
+        else if (og == 16) OSH_FIRST_C(16);
         else OSH_FIRST_C(32);
 #undef OSH_FIRST_C
 #undef OSH_FIRST
