@@ -220,6 +220,56 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
         }
     };
 
+    // lane (j, g) holds output channels 4g + r of pixel column j of block q
+    float *yn = y + (long long)n * M * OHW;
+    const float *rn = res ? res + (long long)n * M * OHW : nullptr;
+    auto store_block = [&](int q) {
+        const int oy = oy0 + j / TWL + G::THL * q, ox = ox0 + j % TWL;
+        if (oy >= p.oh || ox >= p.ow) return;
+        const int pix = oy * p.ow + ox;
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int oc = (mb0 + tm) * 16 + 4 * g + r;
+                if (oc >= M) continue;
+                float v = activate<ACT>(acc[tm][q][r]);
+                if (rn) v += rn[(long long)oc * OHW + pix];
+                yn[(long long)oc * OHW + pix] = v;
+            }
+    };
+    // For 3x3 tiles with BV <= 2 the last chunk runs the pixel blocks one
+    // after another (one chain issues at the MFMA pipe's own rate) and stores
+    // each block as soon as its chain ends, so the output stores drain under
+    // the other block's MFMAs instead of in one burst after them (128 -> 256
+    // s2 at 80x80: 15.1 -> 14.65 us).  Wider tiles keep their blocks
+    // interleaved (64 -> 64 at 160x160 rose from 23.4 to 25.3 us run block by
+    // block) and store after the loop, as do the pointwise tiles (slower
+    // block by block too).
+    auto compute_last = [&](const float4 (&A)[G::NA][TM], int buf, int chunk) {
+        const float *lb = lds + buf * G::CHUNK + lbase;
+#pragma unroll
+        for (int q = 0; q < BV; q++) {
+#pragma unroll
+            for (int t = 0; t < G::NA; t++) {
+                const int cb = t / G::T, tap = t - cb * G::T;
+                const int ky = tap / KS, kx = tap - KS * (tap / KS);
+                if (CB > 1 && chunk * CB + cb >= icbs) break;
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const float b = lb[(16 * cb + 4 * s) * G::PLANE + (G::THL * q * S + ky) * G::PITCH + kx];
+#pragma unroll
+                    for (int tm = 0; tm < TM; tm++) {
+                        const float4 &a4 = A[t][tm];
+                        const float a = s == 0 ? a4.x : s == 1 ? a4.y : s == 2 ? a4.z : a4.w;
+                        acc[tm][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[tm][q], 0, 0, 0);
+                    }
+                }
+            }
+            store_block(q);
+        }
+    };
+
     // prologue: block 0 in LDS, block 1 in flight, block 0's weights loaded
     const int last = nchunks - 1;
     stage_load(sv0, 0);
@@ -237,7 +287,8 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
         stage_load(sv0, min(icb + 2, last));
         if (active) {
             load_a(A1, min(icb + 1, last));
-            compute(A0, 0, icb);
+            if (BV <= 2 && KS == 3 && icb == last) compute_last(A0, 0, icb);
+            else compute(A0, 0, icb);
         }
         stage_store(sv1, 1);
         __syncthreads();
@@ -245,32 +296,18 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
         stage_load(sv1, min(icb + 3, last));
         if (active) {
             load_a(A0, min(icb + 2, last));
-            compute(A1, 1, icb + 1);
+            if (BV <= 2 && KS == 3 && icb + 1 == last) compute_last(A1, 1, icb + 1);
+            else compute(A1, 1, icb + 1);
         }
         stage_store(sv0, 0);
         __syncthreads();
     }
-    if (!active) return;
-
-    // epilogue: lane (j, g) holds output channels 4g + r of pixel column j
-    float *yn = y + (long long)n * M * OHW;
-    const float *rn = res ? res + (long long)n * M * OHW : nullptr;
+    if constexpr (BV > 2 || KS != 3) {
+        if (!active) return;
 #pragma unroll
-    for (int q = 0; q < BV; q++) {
-        const int oy = oy0 + j / TWL + G::THL * q, ox = ox0 + j % TWL;
-        if (oy >= p.oh || ox >= p.ow) continue;
-        const int pix = oy * p.ow + ox;
-#pragma unroll
-        for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int oc = (mb0 + tm) * 16 + 4 * g + r;
-                if (oc >= M) continue;
-                float v = activate<ACT>(acc[tm][q][r]);
-                if (rn) v += rn[(long long)oc * OHW + pix];
-                yn[(long long)oc * OHW + pix] = v;
-            }
+        for (int q = 0; q < BV; q++) store_block(q);
     }
+    // (otherwise compute_last has stored every block of an active wave)
 }
 
 struct C16sVariant {
