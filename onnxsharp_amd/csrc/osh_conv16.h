@@ -150,13 +150,21 @@ __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const fl
 #pragma unroll
     for (int d = 0; d < D; d++) load(R[d], min(d, last));
     int c = 0;
+    // a chunk's refill loads are issued between its own MFMAs (two MFMAs per
+    // load; each load follows the MFMA that last reads its register), so the
+    // MFMA pipe is not left idle while they issue
+    constexpr int NGR = (12 * TM * BV + 1) / 2;
     for (; c + D <= nch; c += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             __builtin_amdgcn_sched_barrier(0);
             compute(R[d]);
-            __builtin_amdgcn_sched_barrier(0);
             load(R[d], min(c + d + D, last));
+#pragma unroll
+            for (int i = 0; i < NGR; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one VMEM read
+            }
         }
     }
 #pragma unroll
