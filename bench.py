@@ -208,8 +208,9 @@ class FrameWorkload(Workload):
     """A block of ops (yolo11n.Model) per step: the launches recorded once as
     a HIP graph and replayed, inputs resident on the device.
     ONNXSHARP_HIP_FRAME_MODE: "graph" (default, one serial HIP graph),
-    "segments" (per-stream segments as child graphs of one DAG) or "eager"
-    (launches issued from the host on the planned streams)."""
+    "segments" (per-stream segments as child graphs of one DAG), "flat" (the
+    same DAG of plain kernel nodes) or "eager" (launches issued from the host
+    on the planned streams)."""
 
     def __init__(self, dev, name, model, x_np, label):
         from onnxsharp_amd import yolo11n
@@ -222,10 +223,10 @@ class FrameWorkload(Workload):
         self.fr.run()
         self.fr.sync()
         self.mode = os.environ.get("ONNXSHARP_HIP_FRAME_MODE", "graph")
-        if self.mode not in ("graph", "segments", "eager"):
-            raise SystemExit(f"ONNXSHARP_HIP_FRAME_MODE={self.mode!r}: expected graph, segments or eager")
+        if self.mode not in ("graph", "segments", "flat", "eager"):
+            raise SystemExit(f"ONNXSHARP_HIP_FRAME_MODE={self.mode!r}: expected graph, segments, flat or eager")
         if self.mode != "eager":
-            self.fr.capture(parallel=self.mode == "segments")
+            self.fr.capture(parallel=self.mode in ("segments", "flat"), flat=self.mode == "flat")
         self.stream = self.fr.stream
         self.flops = self.model.flops
         # each tensor read or written once per op that touches it

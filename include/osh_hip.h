@@ -398,6 +398,14 @@ typedef void *osh_graph_node;    /* hipGraphNode_t */
 OSH_API osh_status osh_graph_builder_create(osh_graph_builder *b);
 OSH_API osh_status osh_graph_add_captured(osh_graph_builder b, osh_stream s, const osh_graph_node *deps, int ndeps,
                                           osh_graph_node *node);
+/* As osh_graph_add_captured, but the captured launches (a serial chain of
+ * kernels) are added to the builder as kernel nodes of their own, in order,
+ * the first one depending on deps; *first and *last receive the chain's ends
+ * (a dependent segment lists *last).  No child graph: the builder is one flat
+ * DAG of kernel nodes.  OSH_E_UNSUPPORTED (nothing added) when the capture
+ * holds anything but a chain of kernel launches. */
+OSH_API osh_status osh_graph_add_captured_flat(osh_graph_builder b, osh_stream s, const osh_graph_node *deps,
+                                               int ndeps, osh_graph_node *first, osh_graph_node *last);
 OSH_API osh_status osh_graph_instantiate(osh_graph_builder b, osh_graph *g);
 OSH_API osh_status osh_graph_builder_destroy(osh_graph_builder b);
 

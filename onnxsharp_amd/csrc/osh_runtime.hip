@@ -6,6 +6,8 @@
 #include <cstdlib>
 #include <cstring>
 
+#include <vector>
+
 #include "osh_common.h"
 
 namespace osh {
@@ -343,6 +345,64 @@ OSH_API osh_status osh_graph_add_captured(osh_graph_builder b, osh_stream s, con
     (void)hipGraphDestroy(child);  // the node holds its own copy
     if (e != hipSuccess) return fail(OSH_E_DEVICE, "hipGraphAddChildGraphNode failed: %s", hipGetErrorString(e));
     *node = n;
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_graph_add_captured_flat(osh_graph_builder b, osh_stream s, const osh_graph_node *deps,
+                                               int ndeps, osh_graph_node *first, osh_graph_node *last) {
+    if (!b || !s || !first || !last || ndeps < 0 || (ndeps > 0 && !deps)) return fail(OSH_E_INVALID, "bad argument");
+    *first = *last = nullptr;
+    hipGraph_t seg = nullptr;
+    OSH_HIP_CHECK(hipStreamEndCapture(to_stream(s), &seg));
+    // the capture of one stream is a chain: one root, at most one dependent
+    // per node, every node a kernel launch
+    std::vector<hipGraphNode_t> chain;
+    const char *why = nullptr;
+    size_t nroots = 0;
+    if (hipGraphGetRootNodes(seg, nullptr, &nroots) != hipSuccess) why = "hipGraphGetRootNodes failed";
+    else if (nroots > 1) why = "the capture is not one chain";
+    if (!why && nroots == 1) {
+        hipGraphNode_t node = nullptr;
+        size_t one = 1;
+        if (hipGraphGetRootNodes(seg, &node, &one) != hipSuccess) why = "hipGraphGetRootNodes failed";
+        while (!why && node) {
+            hipGraphNodeType t;
+            if (hipGraphNodeGetType(node, &t) != hipSuccess || t != hipGraphNodeTypeKernel) {
+                why = "the capture holds a node that is not a kernel launch";
+                break;
+            }
+            chain.push_back(node);
+            size_t nd = 0;
+            if (hipGraphNodeGetDependentNodes(node, nullptr, &nd) != hipSuccess) why = "dependent query failed";
+            else if (nd > 1) why = "the capture is not one chain";
+            else if (nd == 0) node = nullptr;
+            else if (hipGraphNodeGetDependentNodes(node, &node, &nd) != hipSuccess) why = "dependent query failed";
+        }
+    }
+    if (why) {
+        (void)hipGraphDestroy(seg);
+        return fail(OSH_E_UNSUPPORTED, "flat graph: %s", why);
+    }
+    // copy the kernel nodes (their parameter values are copied at creation)
+    hipGraph_t g = reinterpret_cast<hipGraph_t>(b);
+    hipGraphNode_t prev = nullptr;
+    for (size_t i = 0; i < chain.size(); i++) {
+        hipKernelNodeParams kp{};
+        hipError_t e = hipGraphKernelNodeGetParams(chain[i], &kp);
+        hipGraphNode_t nn = nullptr;
+        if (e == hipSuccess) {
+            if (i == 0) e = hipGraphAddKernelNode(&nn, g, reinterpret_cast<const hipGraphNode_t *>(deps), (size_t)ndeps, &kp);
+            else e = hipGraphAddKernelNode(&nn, g, &prev, 1, &kp);
+        }
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(seg);
+            return fail(OSH_E_DEVICE, "flat graph: kernel node copy failed: %s", hipGetErrorString(e));
+        }
+        if (i == 0) *first = nn;
+        prev = nn;
+    }
+    *last = prev;
+    (void)hipGraphDestroy(seg);
     return OSH_OK;
 }
 

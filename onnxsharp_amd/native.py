@@ -116,6 +116,7 @@ _SIGS = {
     "osh_graph_destroy": ([_vp], _i),
     "osh_graph_builder_create": ([C.POINTER(_vp)], _i),
     "osh_graph_add_captured": ([_vp, _vp, C.POINTER(_vp), _i, C.POINTER(_vp)], _i),
+    "osh_graph_add_captured_flat": ([_vp, _vp, C.POINTER(_vp), _i, C.POINTER(_vp), C.POINTER(_vp)], _i),
     "osh_graph_instantiate": ([_vp, C.POINTER(_vp)], _i),
     "osh_graph_builder_destroy": ([_vp], _i),
 }

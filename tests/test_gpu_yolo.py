@@ -86,8 +86,9 @@ def test_yolo_end_to_end(cuda, oracle, exact_silu):
         fr.close()
 
 
-@pytest.mark.parametrize("parallel", [False, True], ids=["chain", "segments"])
-def test_yolo_graph_replay_matches_eager(cuda, parallel):
+@pytest.mark.parametrize("parallel,flat", [(False, False), (True, False), (True, True)],
+                         ids=["chain", "segments", "flat"])
+def test_yolo_graph_replay_matches_eager(cuda, parallel, flat):
     import torch
     from onnxsharp_amd import native as N
     model, fr = _frame(cuda, 128)
@@ -98,8 +99,8 @@ def test_yolo_graph_replay_matches_eager(cuda, parallel):
         fr.run()
         fr.sync()
         eager = [t.cpu().numpy().copy() for t in fr.outputs()]
-        print(f"capturing {len(model.ops)} ops (parallel={parallel})", flush=True)
-        fr.capture(parallel=parallel)
+        print(f"capturing {len(model.ops)} ops (parallel={parallel}, flat={flat})", flush=True)
+        fr.capture(parallel=parallel, flat=flat)
         print("captured", flush=True)
         for rep in range(3):
             print(f"replay {rep}", flush=True)
