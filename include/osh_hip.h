@@ -106,6 +106,10 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 The -2 settings of "conv16_variant" and "pointwise_variant"
  *                 change the packed weight layout: pack again after changing
  *                 them.
+ *   "dqmm_variant": 0 (default) = osh_dqmm_u8s8 runs a min/max launch and
+ *                 then one launch that quantizes A and multiplies; 1 = min/max,
+ *                 quantize and GEMM as three launches.  Both give identical
+ *                 outputs.  Initial value from ONNXSHARP_HIP_DQMM_VARIANT.
  *   "tune": 1 (default) = the first launch of a 3x3 conv shape on a stream
  *                 that is not capturing times every conv16 tile (they all give
  *                 identical outputs) and keeps the fastest for that shape;

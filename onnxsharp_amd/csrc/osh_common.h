@@ -143,6 +143,10 @@ int conv16_variant_count();
 int pointwise_variant();
 int pointwise_variant_count();
 
+// DynamicQuantizeMatMul pipeline (0 = min/max launch then one fused
+// quantize + GEMM launch, 1 = min/max, quantize and GEMM as three launches).
+int dqmm_variant();
+
 // Whether kernels whose tiles all give identical results may pick their tile
 // by timing it on first use (osh_config "tune", ONNXSHARP_HIP_TUNE; default on).
 bool tuning_enabled();

@@ -5,7 +5,8 @@
 // (QuantizedMatMulOps.cs:280-335) and the zero-point identity of PackedInt8Weights
 // (src/OnnxSharp/Kernels/Int8Gemm.cs:66-70).
 //
-// Pipeline (three launches, all on the caller's stream):
+// Pipeline (three launches, all on the caller's stream; by default 2 and 3
+// run as one launch, dqmm_fused_kernel):
 //   1. dqmm_minmax_kernel   grid-stride min/max of A (0 included, NaN skipped) into per-block
 //                           partials.
 //   2. dqmm_quantize_kernel every block reduces the partials to scale = (max-min)/255 (1 if
@@ -111,16 +112,12 @@ __global__ __launch_bounds__(DQ_THREADS) void dqmm_minmax_kernel(const float *__
 
 // Every consumer block reduces the per-block partials itself (a few hundred
 // floats from L2), so no grid-wide counter is needed and the scratch needs no
-// initialisation.  Block 0 publishes the parameters for later launches.
-__device__ void dq_params(DqScratch *__restrict__ sc, int nparts, int *__restrict__ qparams, float &inv_out,
-                          int &zp_out) {
-    __shared__ float s_inv;
+// initialisation.  One block (`publish`) stores the parameters for later
+// launches and the caller.
+__device__ void dq_finish(DqScratch *__restrict__ sc, float lo, float hi, int *__restrict__ qparams,
+                          bool publish, float &inv_out, int &zp_out, float *scale_out) {
+    __shared__ float s_inv, s_scale;
     __shared__ int s_zp;
-    float lo = 0.f, hi = 0.f;
-    for (int b = threadIdx.x; b < nparts; b += blockDim.x) {
-        lo = __builtin_fminf(lo, sc->partial_min[b]);
-        hi = __builtin_fmaxf(hi, sc->partial_max[b]);
-    }
     block_minmax(lo, hi);
     if (threadIdx.x == 0) {
         // QuantizedMatMulOps.cs:151-155
@@ -131,8 +128,9 @@ __device__ void dq_params(DqScratch *__restrict__ sc, int nparts, int *__restric
         zp = zp < 0 ? 0 : (zp > 255 ? 255 : zp);
         float inv = 1.0f / scale;  // QuantizeAndWiden multiplies by the reciprocal (QuantizedMatMulOps.cs:282)
         s_inv = inv;
+        s_scale = scale;
         s_zp = zp;
-        if (blockIdx.x == 0) {
+        if (publish) {
             sc->scale = scale;
             sc->zp = zp;
             sc->inv = inv;
@@ -146,6 +144,17 @@ __device__ void dq_params(DqScratch *__restrict__ sc, int nparts, int *__restric
     __syncthreads();
     inv_out = s_inv;
     zp_out = s_zp;
+    if (scale_out) *scale_out = s_scale;
+}
+
+__device__ void dq_params(DqScratch *__restrict__ sc, int nparts, int *__restrict__ qparams, bool publish,
+                          float &inv_out, int &zp_out) {
+    float lo = 0.f, hi = 0.f;
+    for (int b = threadIdx.x; b < nparts; b += blockDim.x) {
+        lo = __builtin_fminf(lo, sc->partial_min[b]);
+        hi = __builtin_fmaxf(hi, sc->partial_max[b]);
+    }
+    dq_finish(sc, lo, hi, qparams, publish, inv_out, zp_out, nullptr);
 }
 
 // q = clamp(rne(x * inv) + zp, 0, 255) as QuantizeAndWiden computes it in float.
@@ -199,7 +208,7 @@ __global__ __launch_bounds__(DQ_THREADS) void dqmm_quantize_kernel(const float *
     for (int c = 0; c < DQ_QPRE; c++) pre[c] = load_quad(src, 4 * lane + 256 * c, k, live, vec);
     float inv;
     int zp;
-    dq_params(sc, nparts, qparams, inv, zp);
+    dq_params(sc, nparts, qparams, blockIdx.x == 0, inv, zp);
     if (row >= mpad) return;
     const float zpf = (float)zp;
     int *dst = reinterpret_cast<int *>(apk) + (long long)(row >> 5) * (kpad / 32) * 256 + (row & 31) * 4;
@@ -282,7 +291,7 @@ __global__ __launch_bounds__(DQ_THREADS) void dql_quantize_kernel(const float *_
                                                                    uint8_t *__restrict__ q) {
     float inv;
     int zp;
-    dq_params(sc, nparts, qparams, inv, zp);
+    dq_params(sc, nparts, qparams, blockIdx.x == 0, inv, zp);
     const float zpf = (float)zp;
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long stride = (long long)gridDim.x * blockDim.x;
@@ -411,6 +420,196 @@ __global__ __launch_bounds__(256) void dqmm_gemm_kernel(int m, int k, int n, con
     }
 }
 
+// Quantize + GEMM in one launch (after dqmm_minmax_kernel).  A workgroup owns
+// 32 rows of A and DQF_WAVES column tiles of 32; per chunk of DQF_KS k-steps
+// its 256 threads load the rows' floats (thread -> row tid/8, four consecutive
+// k at 32*i + 4*(tid%8)), quantize them with the parameters every workgroup
+// reduces from the min/max partials, and store a'' = q - 128 in the MFMA
+// A-operand order in LDS; each wave then runs its column tile's
+// v_mfma_i32_32x32x32_i8 chain with B fragments from global memory.  The row
+// sums of a'' and the NaN flags come from the same registers, so nothing but
+// the parameters goes through global scratch.  The partials are loaded first
+// and the first chunk's A and B loads behind them, so the parameter reduction
+// overlaps those loads.  Arithmetic (quantization, zero-point correction,
+// epilogue) is the three-launch pipeline's, so both give identical bits.
+constexpr int DQF_WAVES = 4;
+constexpr int DQF_KS = 16;  // k-steps of 32 per chunk: K = 512 in one chunk
+constexpr int DQF_GM = 4;   // row tiles per group of the tile order
+static_assert(DQ_MINMAX_BLOCKS <= 256, "one min/max partial per thread of a 256-thread workgroup");
+
+__global__ __launch_bounds__(256) void dqmm_fused_kernel(int m, int k, int n, const float *__restrict__ a,
+                                                         DqScratch *__restrict__ sc, int nparts,
+                                                         int *__restrict__ qparams, const int8_t *__restrict__ wpk,
+                                                         const int *__restrict__ colsum,
+                                                         const int *__restrict__ off,
+                                                         const float *__restrict__ wscale, int n_wscale,
+                                                         const float *__restrict__ bias, float *__restrict__ out,
+                                                         int *__restrict__ acc_out) {
+    __shared__ __attribute__((aligned(16))) int lds_a[DQF_KS * 256];  // [kstep][64 lanes][16 bytes]
+    __shared__ int lds_rs[32], lds_rn[32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kpad = pad32(k), ks = kpad / 32, npad = pad32(n);
+    // Tiles: XCD-banded ids, then groups of DQF_GM row tiles x all column
+    // blocks, so one XCD's L2 holds a few row tiles of A and part of W.
+    const int ncb = (npad / 32 + DQF_WAVES - 1) / DQF_WAVES, nmt = pad32(m) / 32;
+    const int id = xcd_band(blockIdx.x, gridDim.x);
+    const int grp = id / (DQF_GM * ncb), gl = id % (DQF_GM * ncb);
+    const int mt0 = grp * DQF_GM;
+    const int gm = nmt - mt0 < DQF_GM ? nmt - mt0 : DQF_GM;
+    const int mt = mt0 + gl % gm;
+    const int nt = (gl / gm) * DQF_WAVES + wave;
+    const bool col_live = nt * 32 < npad;
+    const int r = tid >> 3, c8 = tid & 7;
+    const int row = mt * 32 + r;
+    const bool live = row < m;
+    const float *src = a + (long long)(live ? row : 0) * k;
+    const bool vec = (k & 3) == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+    // all 32 rows live and 16-byte loads: chunks inside k need no per-element checks
+    const bool rows_full = vec && mt * 32 + 32 <= m;
+    const int nchunks = (ks + DQF_KS - 1) / DQF_KS;
+    const i32x4 *B = reinterpret_cast<const i32x4 *>(wpk) + (long long)(col_live ? nt : 0) * ks * 64 + lane;
+
+    // nparts <= 256: one partial per thread (threads past nparts repeat
+    // partial 0), consumed only after the A and B loads are issued
+    const int pidx = tid < nparts ? tid : 0;
+    const float pmin = sc->partial_min[pidx], pmax = sc->partial_max[pidx];
+    Quad x[DQF_KS];
+    i32x4 b[DQF_KS];
+    auto load_chunk = [&](int s0) {
+        if (rows_full && (s0 + DQF_KS) * 32 <= k) {
+#pragma unroll
+            for (int i = 0; i < DQF_KS; i++) {
+                const float4 v = *reinterpret_cast<const float4 *>(src + (s0 + i) * 32 + 4 * c8);
+                x[i].v[0] = v.x; x[i].v[1] = v.y; x[i].v[2] = v.z; x[i].v[3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < DQF_KS; i++) x[i] = load_quad(src, (s0 + i) * 32 + 4 * c8, k, live, vec);
+        }
+    };
+    load_chunk(0);
+    if (col_live) {
+        if (ks >= DQF_KS) {
+#pragma unroll
+            for (int t = 0; t < DQF_KS; t++) b[t] = B[t * 64];
+        } else {
+#pragma unroll
+            for (int t = 0; t < DQF_KS; t++)
+                if (t < ks) b[t] = B[t * 64];
+        }
+    }
+
+    float inv, scale;
+    int zp;
+    dq_finish(sc, __builtin_fminf(0.f, pmin), __builtin_fmaxf(0.f, pmax), qparams, blockIdx.x == 0, inv, zp,
+              &scale);
+    const float zpf = (float)zp;
+
+    int sum = 0;
+    bool nan = false;
+    i32x16 acc = {};
+    int *dst = lds_a + (r + 32 * (c8 >> 2)) * 4 + (c8 & 3);
+    for (int c = 0; c < nchunks; c++) {
+        const int s0 = c * DQF_KS;
+        if (rows_full && (s0 + DQF_KS) * 32 <= k) {
+#pragma unroll
+            for (int i = 0; i < DQF_KS; i++) {
+                unsigned packed = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float p = x[i].v[e] * inv;
+                    nan |= !(p == p);
+                    const int v = quantize_one(x[i].v[e], inv, zpf) - 128;
+                    sum += v;
+                    packed |= (unsigned)(v & 0xff) << (8 * e);
+                }
+                dst[i * 256] = (int)packed;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < DQF_KS; i++) {
+                const int kk = (s0 + i) * 32 + 4 * c8;
+                if (kk < kpad) {
+                    unsigned packed = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        int v = 0;  // padding rows and k carry a'' = 0
+                        if (live && kk + e < k) {
+                            const float p = x[i].v[e] * inv;
+                            nan |= !(p == p);
+                            v = quantize_one(x[i].v[e], inv, zpf) - 128;
+                            sum += v;
+                        }
+                        packed |= (unsigned)(v & 0xff) << (8 * e);
+                    }
+                    dst[i * 256] = (int)packed;
+                }
+            }
+        }
+        __syncthreads();
+        const bool more = c + 1 < nchunks;
+        if (more) load_chunk(s0 + DQF_KS);
+        if (col_live) {
+            const int steps = ks - s0 < DQF_KS ? ks - s0 : DQF_KS;
+            if (steps == DQF_KS) {
+                i32x4 av[DQF_KS];
+#pragma unroll
+                for (int t = 0; t < DQF_KS; t++) av[t] = *reinterpret_cast<const i32x4 *>(lds_a + t * 256 + lane * 4);
+#pragma unroll
+                for (int t = 0; t < DQF_KS; t++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[t], b[t], acc, 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int t = 0; t < DQF_KS; t++) {
+                    if (t < steps) {
+                        const i32x4 av = *reinterpret_cast<const i32x4 *>(lds_a + t * 256 + lane * 4);
+                        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b[t], acc, 0, 0, 0);
+                    }
+                }
+            }
+            if (more) {
+#pragma unroll
+                for (int t = 0; t < DQF_KS; t++)
+                    if (s0 + DQF_KS + t < ks) b[t] = B[(s0 + DQF_KS + t) * 64];
+            }
+        }
+        __syncthreads();
+    }
+    // a row's 8 threads are consecutive lanes of one wave
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+        sum += __shfl_xor(sum, o);
+        const int other = __shfl_xor(nan ? 1 : 0, o);
+        nan = nan || other != 0;
+    }
+    if (c8 == 0) {
+        lds_rs[r] = sum;
+        lds_rn[r] = nan ? 1 : 0;
+    }
+    __syncthreads();
+    const int j = nt * 32 + (lane & 31);
+    if (!col_live || j >= n) return;
+    const unsigned offj = (unsigned)off[j];
+    const unsigned alpha = (unsigned)(128 - zp);
+    const unsigned colterm = alpha * (unsigned)colsum[j] + (unsigned)k * alpha * offj;
+    const float ws = wscale ? (n_wscale == 1 ? wscale[0] : wscale[j]) : 0.0f;
+    const float bj = bias ? bias[j] : 0.0f;
+    const float comb = scale * ws;  // CombinedScale, QuantizedMatMulOps.cs:203-221
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        const int il = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+        const int i = mt * 32 + il;
+        if (i < m) {
+            const int v = (int)((unsigned)acc[q] + offj * (unsigned)lds_rs[il] + colterm);
+            if (acc_out) acc_out[(long long)i * n + j] = v;
+            if (out) {
+                float o = __builtin_fmaf((float)v, comb, bj);
+                if (lds_rn[il]) o = __builtin_nanf("");
+                out[(long long)i * n + j] = o;
+            }
+        }
+    }
+}
+
 static osh_status run_minmax(const float *a, long long count, DqScratch *sc, int *nparts, hipStream_t st) {
     long long blocks = (count / 4 + DQ_THREADS - 1) / DQ_THREADS;
     if (blocks < 1) blocks = 1;
@@ -488,13 +687,20 @@ OSH_API osh_status osh_dqmm_u8s8(int m, int k, int n, const float *d_a, const vo
     int nparts = 0;
     osh_status r = run_minmax(d_a, (long long)m * k, sc, &nparts, st);
     if (r != OSH_OK) return r;
+    const int8_t *frag = static_cast<const int8_t *>(d_wpacked);
+    const int *colsum = reinterpret_cast<const int *>(frag + (size_t)pad32(n) * pad32(k));
+    const int *off = colsum + pad32(n);
+    const long long fblocks = (long long)((pad32(n) / 32 + DQF_WAVES - 1) / DQF_WAVES) * (pad32(m) / 32);
+    if (dqmm_variant() == 0 && fblocks <= 0x7fffffffLL) {
+        hipLaunchKernelGGL(dqmm_fused_kernel, dim3((unsigned)fblocks), dim3(256), 0, st, m, k, n, d_a, sc, nparts, (int *)d_qparams,
+                           frag, colsum, off, d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
+        OSH_LAUNCH_CHECK("dqmm_fused_kernel");
+        return OSH_OK;
+    }
     const int rows_per_block = DQ_THREADS / 64;
     hipLaunchKernelGGL(dqmm_quantize_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
                        dim3(DQ_THREADS), 0, st, d_a, m, k, sc, nparts, (int *)d_qparams, rowsum, apk);
     OSH_LAUNCH_CHECK("dqmm_quantize_kernel");
-    const int8_t *frag = static_cast<const int8_t *>(d_wpacked);
-    const int *colsum = reinterpret_cast<const int *>(frag + (size_t)pad32(n) * pad32(k));
-    const int *off = colsum + pad32(n);
     dim3 grid((pad32(n) / 32 + 1) / 2, (pad32(m) / 32 + 1) / 2);
     hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
                        d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);

@@ -31,6 +31,7 @@ static int g_gemm_variant = -3;  // -3: read ONNXSHARP_HIP_GEMM_VARIANT on first
 static int g_conv16_variant = -3;  // -3: read ONNXSHARP_HIP_CONV16_VARIANT on first use
 static int g_tune = -1;             // -1: read ONNXSHARP_HIP_TUNE on first use
 static int g_pw_variant = -3;       // -3: read ONNXSHARP_HIP_POINTWISE_VARIANT on first use
+static int g_dqmm_variant = -3;     // -3: read ONNXSHARP_HIP_DQMM_VARIANT on first use
 
 bool exact_silu() {
     if (g_exact_silu < 0) {
@@ -70,6 +71,14 @@ int pointwise_variant() {
         g_pw_variant = e ? atoi(e) : -1;
     }
     return g_pw_variant;
+}
+
+int dqmm_variant() {
+    if (g_dqmm_variant == -3) {
+        const char *e = getenv("ONNXSHARP_HIP_DQMM_VARIANT");
+        g_dqmm_variant = (e && atoi(e) == 1) ? 1 : 0;
+    }
+    return g_dqmm_variant;
 }
 
 __global__ void fill_u8_kernel(uint8_t *__restrict__ p, uint8_t v, size_t n) {
@@ -114,6 +123,11 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         g_gemm_variant = value;
         return OSH_OK;
     }
+    if (strcmp(key, "dqmm_variant") == 0) {
+        if (value != 0 && value != 1) return fail(OSH_E_INVALID, "dqmm_variant %d out of range [0, 2)", value);
+        g_dqmm_variant = value;
+        return OSH_OK;
+    }
     return fail(OSH_E_INVALID, "unknown option '%s'", key);
 }
 
@@ -133,6 +147,10 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     }
     if (strcmp(key, "pointwise_variant") == 0) {
         *value = pointwise_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "dqmm_variant") == 0) {
+        *value = dqmm_variant();
         return OSH_OK;
     }
     if (strcmp(key, "pointwise_variants") == 0) {

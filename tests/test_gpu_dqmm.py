@@ -114,3 +114,38 @@ def test_dynamic_quantize_linear_matches_oracle(cuda, oracle):
     eq, es, ez = oracle.dynamic_quantize_linear(x)
     assert (np.float32(s), z) == (es, ez)
     assert np.array_equal(q.cpu().numpy(), eq)
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 512, 2048), (3, 2100, 17), (70, 96, 300), (33, 1040, 130), (1, 7, 3)])
+def test_dqmm_fused_and_three_launch_pipelines_identical(cuda, oracle, m, k, n):
+    """dqmm_variant 0 (quantize inside the GEMM launch, K in chunks of 512) and
+    1 (separate quantize launch) give the same bits, both equal to the oracle."""
+    import ctypes as C
+    from onnxsharp_amd import native as N
+    print(f"dqmm pipelines m={m} k={k} n={n}", flush=True)
+    a = synth.normal(3 * m + k, (m, k))
+    a[m // 2, k // 3] = np.nan  # one NaN row on both pipelines
+    w = synth.randint(m + 2 * n, (k, n), -127, 127, np.int8)
+    ws = synth.uniform(k + 3 * n, (n,), 0.001, 0.02)
+    bias = synth.normal(m + n, (n,), 0, 0.01)
+    old = C.c_int()
+    N.call("osh_config_get", b"dqmm_variant", C.byref(old))
+    got = []
+    try:
+        for v in (0, 1):
+            N.call("osh_config_set", b"dqmm_variant", v)
+            got.append(run_dqmm(cuda, a, w, None, ws, bias))
+    finally:
+        N.call("osh_config_set", b"dqmm_variant", old.value)
+    (o0, a0, s0, z0), (o1, a1, s1, z1) = got
+    assert (s0, z0) == (s1, z1)
+    assert np.array_equal(a0, a1)
+    assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
+    eo, eacc, _, es, ez = oracle.dqmm(a, w, None, ws, bias)
+    assert (s0, z0) == (es, ez)
+    good = np.ones(m, bool)
+    good[m // 2] = False
+    assert np.isnan(o0[m // 2]).all()
+    q = oracle.quantize_u8(a[good], es, ez)
+    assert np.array_equal(a0[good], (q.astype(np.int64) - ez) @ w.astype(np.int64))
+    assert np.array_equal(o0[good], eo[good])
