@@ -84,10 +84,12 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 use the LDS-staged GEMM tile.  Every choice sums k in the
  *                 same order.  Initial value from ONNXSHARP_HIP_GEMM_VARIANT.
  *   "gemm_variants" (get only): N, the number of wave tiles.
- *   "conv16_variant": -1 (default) = 3x3 convolutions with C % 16 == 0 run
- *                 the in-order 16x16x4 MFMA kernel (the reference's NCHWc
- *                 chain, bit for bit) with a wave tile picked per shape;
- *                 0..N-1 forces a tile where the shape allows it (6..11:
+ *   "conv16_variant": -1 (default) = 3x3 convolutions that pass the
+ *                 reference's NCHWc gate (stride 1 or 2, pad 1, C % 16 == 0,
+ *                 M % 32 == 0, batch 1; NchwcConv.cs:100-126) run the in-order
+ *                 16x16x4 MFMA kernel (the reference's NCHWc chain, bit for
+ *                 bit) with a wave tile picked per shape; 0..N-1 forces a tile
+ *                 on any 3x3 shape with C % 16 == 0 it fits (6..11:
  *                 weights held in LDS; 12..20: input patch staged in LDS
  *                 and shared by a workgroup's four waves, stride 1 or 2;
  *                 21..24: tiles 0, 3, 1, 4 with one wave per workgroup;
@@ -110,6 +112,26 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 then one launch that quantizes A and multiplies; 1 = min/max,
  *                 quantize and GEMM as three launches.  Both give identical
  *                 outputs.  Initial value from ONNXSHARP_HIP_DQMM_VARIANT.
+ *   "im2col3x3_variant": -1 (default) = 3x3 stride-1/2 convolutions with
+ *                 C % 16 == 0 that neither the NCHWc nor the Winograd gate
+ *                 takes run the LDS-patch tiles in the reference's im2col
+ *                 order (ConvKernels.cs:554-563), tile picked by first-use
+ *                 timing; 0..N-1 forces a tile.  Initial value from
+ *                 ONNXSHARP_HIP_IM2COL3X3_VARIANT.
+ *   "im2col3x3_variants" (get only): N.
+ *   "winograd": 1 (default) = 3x3 stride-1 convolutions that pass the
+ *                 reference's Winograd gate (Winograd.TryConv3x3,
+ *                 src/OnnxSharp/Kernels/Winograd.cs:58-122) but not its NCHWc
+ *                 gate (NchwcConv.cs:100-126) run Winograd F(2x2,3x3) in the
+ *                 reference's arithmetic -- the reference's own choice on an
+ *                 AVX-512 host; 2 = Winograd for every shape that passes its
+ *                 gate, ahead of the NCHWc kernels (the reference's choice on
+ *                 a host without AVX-512); 0 = never (those shapes take the
+ *                 im2col chain).  Initial value from ONNXSHARP_HIP_WINOGRAD.
+ *                 Changes the packed weight layout: pack again after changing it.
+ *   "winograd_max_pixels": the largest output map (H*W) Winograd takes;
+ *                 initial value from the reference's ONNXSHARP_WINO_MAX, else
+ *                 4096.  Also changes the packed layout.
  *   "tune": 1 (default) = the first launch of a 3x3 conv shape on a stream
  *                 that is not capturing times every conv16 tile (they all give
  *                 identical outputs) and keeps the fastest for that shape;

@@ -143,6 +143,18 @@ int conv16_variant_count();
 int pointwise_variant();
 int pointwise_variant_count();
 
+// Forced LDS-patch tile for the 3x3 convolutions that run in the im2col
+// order (-1 = automatic) and the number of tiles.
+int im2col3x3_variant();
+int im2col3x3_variant_count();
+
+// Winograd F(2x2,3x3) for 3x3 stride-1 convolutions (0 = never, 1 = where
+// the reference's NCHWc kernel does not apply, 2 = ahead of the NCHWc
+// kernels) and the largest output map it takes (H*W; the reference's
+// ONNXSHARP_WINO_MAX, default 4096).
+int winograd_mode();
+long long winograd_max_pixels();
+
 // DynamicQuantizeMatMul pipeline (0 = min/max launch then one fused
 // quantize + GEMM launch, 1 = min/max, quantize and GEMM as three launches).
 int dqmm_variant();

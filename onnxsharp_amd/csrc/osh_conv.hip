@@ -1,23 +1,35 @@
 // osh_conv.hip -- Conv entry points of the C ABI: shape logic of ConvLayer
 // (src/OnnxSharp/Ops/DnnOps.cs:53-89,134-201,379-409) and the kernel choice
-// of ConvLayer.Forward (DnnOps.cs:411-500), re-planned for gfx950.  Every
-// default choice sums in the order the reference's own kernel for that shape
-// uses, so the outputs are its bits:
+// of ConvLayer.Forward (DnnOps.cs:411-500), re-planned for gfx950.  The
+// choice follows the reference's kernel chain on an AVX-512 host --
+// DepthwiseConv, FirstConv, NchwcConv, Winograd, PackedConv, Im2Col, first
+// gate that holds -- and every kernel sums in the order of the reference's
+// kernel for that shape, so the outputs are its bits:
 //
 //   depthwise (group == C == M)         -> dw_conv_kernel (ky -> kx FMA chain, DepthwiseConv.cs)
-//   3x3, C <= 4 or 8, M = 8/16/32, group 1
-//                                       -> first_conv_kernel (the network's first layer,
-//                                          FirstConv.cs, and 8-channel layers: the
-//                                          ic -> ky -> kx FMA chain)
-//   3x3 / dil 1 / any stride, C % 16 == 0
-//                                       -> in-order 16x16x4 MFMA kernels (osh_conv16.h,
+//   3x3, C <= 4, M = 8/16/32, group 1   -> first_conv_kernel (the network's first layer,
+//                                          FirstConv.cs: the ic -> ky -> kx FMA chain)
+//   NchwcConv's gate (3x3, stride 1 or 2, pad 1, C % 16 == 0, M % 32 == 0, batch 1,
+//   NchwcConv.cs:100-126)               -> in-order 16x16x4 MFMA kernels (osh_conv16.h,
 //                                          osh_conv16s.h): the NCHWc chain icb -> ky -> kx -> ic16
+//   Winograd's gate (3x3 s1 p1, C, M >= 8, H*W <= 4096, Winograd.cs:58-122)
+//                                       -> wino_f23_kernel (osh_winograd.h): Winograd.cs's
+//                                          transforms and component GEMMs
+//   other 3x3, stride 1 or 2, C % 16 == 0
+//                                       -> conv16s_kernel<..., I2C> (the LDS-patch tiles with the
+//                                          terms of each 16-channel block in the im2col order)
+//   other 3x3 with C = 8/16/32, M = 8/16/32
+//                                       -> first_conv_kernel (the im2col chain per pixel)
 //   1x1 / stride 1 / pad 0, C % 16 == 0 -> the LDS-tile kernel with one tap, or the GEMM tile,
 //                                          tuned per shape (the GEMM chain over ic)
 //   other 1x1 / stride 1 / pad 0        -> MFMA GEMM over NCHW (W[M,C] x X[C,H*W])
 //   everything else                     -> MFMA implicit GEMM with an im2col gather, k in the
-//                                          im2col order ic -> ky -> kx (ConvKernels.cs)
+//                                          im2col order ic -> ky -> kx (ConvKernels.cs, PackedConv.cs)
 //
+// osh_config "winograd" = 0 leaves Winograd out (those shapes take the im2col
+// chain), 2 puts it ahead of the NCHWc kernels (the reference's choice on a
+// host without AVX-512, for the Winograd-eligible shapes).  A forced
+// "conv16_variant" >= 0 runs the NCHWc-chain kernels on any 3x3 shape they fit.
 // With osh_config_set("conv16_variant", -2) 3x3 shapes take the older
 // weight-stationary / LDS-halo kernels instead (osh_conv3x3_wi.h,
 // osh_conv3x3_ws.h, osh_conv3x3.h), which sum in orders of their own (within
@@ -37,6 +49,7 @@
 #include "osh_conv3x3_ws.h"
 #include "osh_igemm.h"
 #include "osh_launch.h"
+#include "osh_winograd.h"
 
 using namespace osh;
 
@@ -156,9 +169,47 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
     const int n = (int)(t / p.oh);
     const int m = p.m;
     const int oc0 = blockIdx.y * MM;
+    const float *xn = x + (long long)n * CC * p.h * p.w;
+    const long long yo = (long long)n * m * plane + (long long)oy * p.ow + ox;
+    float *yp = y + yo;
+    const float *rp = res ? res + yo : nullptr;
+    if constexpr (CC > 8) {
+        // 16 or 32 channels: MM accumulators, input channels in the outer
+        // loop; each output channel still sums bias, then ic -> ky -> kx
+        float acc[MM];
+#pragma unroll
+        for (int o = 0; o < MM; o++) acc[o] = bias ? bias[oc0 + o] : 0.f;
+        for (int ic = 0; ic < CC; ic++) {
+            float v[3][3];
+#pragma unroll
+            for (int ky = 0; ky < 3; ky++) {
+                const int iy = oy * p.sh - p.pt + ky;
+#pragma unroll
+                for (int kx = 0; kx < 3; kx++) {
+                    const int ix = ox * p.sw - p.pl + kx;
+                    const bool ok = (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
+                    v[ky][kx] = ok ? xn[((long long)ic * p.h + iy) * p.w + ix] : 0.f;
+                }
+            }
+#pragma unroll
+            for (int o = 0; o < MM; o++) {
+                const float *wo = w + ((oc0 + o) * CC + ic) * 9;
+#pragma unroll
+                for (int ky = 0; ky < 3; ky++)
+#pragma unroll
+                    for (int kx = 0; kx < 3; kx++) acc[o] = __builtin_fmaf(wo[ky * 3 + kx], v[ky][kx], acc[o]);
+            }
+        }
+#pragma unroll
+        for (int o = 0; o < MM; o++) {
+            float r = activate<ACT>(acc[o]);
+            if (rp) r += rp[(oc0 + o) * plane];
+            yp[(oc0 + o) * plane] = r;
+        }
+        return;
+    }
     // all CC*9 input taps are loaded before the first FMA (independent loads)
     float v[CC][3][3];
-    const float *xn = x + (long long)n * CC * p.h * p.w;
 #pragma unroll
     for (int ic = 0; ic < CC; ic++)
 #pragma unroll
@@ -171,9 +222,6 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
                 v[ic][ky][kx] = ok ? xn[((long long)ic * p.h + iy) * p.w + ix] : 0.f;
             }
         }
-    const long long yo = (long long)n * m * plane + (long long)oy * p.ow + ox;
-    float *yp = y + yo;
-    const float *rp = res ? res + yo : nullptr;
     // 3x3 taps at compile-time offsets: the weights arrive in wide scalar loads
 #pragma unroll
     for (int oc = oc0; oc < oc0 + MM; oc++) {  // m = MM * gridDim.y (launch)
@@ -196,30 +244,56 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
 // the reference's im2col order for them, and cheaper than a GEMM tile whose
 // M = 16 would idle most of its rows.
 static bool first_conv_eligible(const osh_conv_params *p) {
-    return p->group == 1 && (p->c <= 4 || p->c == 8) && (p->m == 8 || p->m == 16 || p->m == 32) && p->kh == 3 &&
-           p->kw == 3 && p->dh == 1 && p->dw == 1;
+    return p->group == 1 && (p->c <= 4 || p->c == 8 || p->c == 16 || p->c == 32) &&
+           (p->m == 8 || p->m == 16 || p->m == 32) && p->kh == 3 && p->kw == 3 && p->dh == 1 && p->dw == 1;
+}
+
+// NchwcConv.CanUse + Dispatch + TryConv's batch test (NchwcConv.cs:100-126,
+// 166-194): the shapes the reference runs through its NCHWc chain.
+static bool nchwc_gate(const osh_conv_params *p) {
+    const bool s2 = p->sh == 2;
+    return p->group == 1 && p->kh == 3 && p->kw == 3 && p->sh == p->sw && (p->sh == 1 || s2) && p->dh == 1 &&
+           p->dw == 1 && p->pt == 1 && p->pl == 1 && (!s2 || ((p->h & 1) == 0 && (p->w & 1) == 0)) &&
+           p->c % 16 == 0 && p->m % 32 == 0 && p->n == 1 &&
+           (s2 ? p->oh * 2 == p->h && p->ow * 2 == p->w : p->oh == p->h && p->ow == p->w);
 }
 
 enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3, ALGO_WS3X3 = 4, ALGO_WI3X3 = 5,
-                ALGO_FIRST = 6, ALGO_CONV16 = 7, ALGO_PW16 = 8 };
+                ALGO_FIRST = 6, ALGO_CONV16 = 7, ALGO_PW16 = 8, ALGO_WINOGRAD = 9, ALGO_CONV16I = 10 };
+
+static bool is_pointwise(const osh_conv_params *p) {
+    return p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 && p->oh == p->h &&
+           p->ow == p->w;
+}
 
 static ConvAlgo select_algo(const osh_conv_params *p) {
     if (p->group == p->c && p->group == p->m && p->group > 1) return ALGO_DEPTHWISE;
-    if (first_conv_eligible(p)) return ALGO_FIRST;
-    if (conv16_variant() != -2 && conv16_eligible(p)) return ALGO_CONV16;
-    if (pointwise_variant() != -2 && pw16_eligible(p)) return ALGO_PW16;
-    if (p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 && p->oh == p->h &&
-        p->ow == p->w)
-        return ALGO_POINTWISE;
-    // the weight-stationary and LDS-halo 3x3 kernels sum in their own orders:
-    // only on request (conv16_variant -2); by default the remaining shapes
-    // take the implicit-im2col GEMM, whose k order (ic -> ky -> kx) is the
-    // reference's im2col chain
-    if (conv16_variant() == -2) {
+    const int v16 = conv16_variant();
+    if (v16 >= 0 && conv16_eligible(p)) return ALGO_CONV16;  // a forced tile (tuning and tests)
+    if (v16 == -2) {
+        // the weight-stationary and LDS-halo 3x3 kernels, which sum in their
+        // own orders (within the FP32 tolerance): only on request; the direct
+        // kernel keeps the channel counts it took before them (C <= 4 or 8)
+        if (first_conv_eligible(p) && (p->c <= 4 || p->c == 8)) return ALGO_FIRST;
+        if (pointwise_variant() != -2 && pw16_eligible(p)) return ALGO_PW16;
+        if (is_pointwise(p)) return ALGO_POINTWISE;
         if (conv3x3_wi_eligible(p)) return ALGO_WI3X3;
         if (conv3x3_ws_eligible(p)) return ALGO_WS3X3;
         if (conv3x3_eligible(p)) return ALGO_DIRECT3X3;
+        return ALGO_IM2COL;
     }
+    const int wm = winograd_mode();
+    const bool wino = wm != 0 && winograd_eligible(p, winograd_max_pixels());
+    if (p->c <= 4 && first_conv_eligible(p)) return ALGO_FIRST;
+    if (wm == 2 && wino) return ALGO_WINOGRAD;
+    if (nchwc_gate(p) && conv16_eligible(p)) return ALGO_CONV16;
+    if (wino) return ALGO_WINOGRAD;
+    if (conv16s_eligible(p)) return ALGO_CONV16I;  // the LDS-patch tiles in the im2col order
+    if (first_conv_eligible(p)) return ALGO_FIRST;
+    if (pointwise_variant() != -2 && pw16_eligible(p)) return ALGO_PW16;
+    if (is_pointwise(p)) return ALGO_POINTWISE;
+    // the implicit-im2col GEMM: k in the order ic -> ky -> kx, the
+    // reference's im2col and panel chain
     return ALGO_IM2COL;
 }
 
@@ -255,6 +329,7 @@ constexpr int kC3X0 = kC3W0 + kC16wCount;
 constexpr int kC3Count = kC3X0 + kC16sxCount;
 int conv16_variant_count() { return kC3Count; }
 int pointwise_variant_count() { return 1 + kPW16Count; }
+int im2col3x3_variant_count() { return kC16sCount; }
 
 static bool c3_fits(const osh_conv_params *p, int v) {
     if (v < kC16Count) return conv16_fits(p, kC16[v]);
@@ -442,7 +517,9 @@ OSH_API osh_status osh_conv_packed_weight_bytes(const osh_conv_params *p, size_t
     if (!bytes) return fail(OSH_E_INVALID, "bytes is NULL");
     size_t oihw = (size_t)p->m * (p->c / p->group) * p->kh * p->kw * sizeof(float);
     switch (select_algo(p)) {
-    case ALGO_CONV16: *bytes = conv16_packed_bytes(p); break;
+    case ALGO_CONV16:
+    case ALGO_CONV16I: *bytes = conv16_packed_bytes(p); break;
+    case ALGO_WINOGRAD: *bytes = winograd_packed_bytes(p); break;
     case ALGO_PW16: *bytes = conv16_packed_bytes(p) + oihw; break;  // LDS-tile layout, then the raw GEMM operand
     case ALGO_WI3X3: *bytes = conv3x3_wi_packed_bytes(p); break;
     case ALGO_WS3X3: *bytes = conv3x3_ws_packed_bytes(p); break;
@@ -458,6 +535,8 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
     if (st != OSH_OK) return st;
     if (!d_w || !d_packed) return fail(OSH_E_INVALID, "Conv pack: NULL pointer");
     if (select_algo(p) == ALGO_CONV16) return conv16_pack(p, d_w, d_packed, to_stream(s));
+    if (select_algo(p) == ALGO_WINOGRAD) return winograd_pack(p, d_w, d_packed, to_stream(s));
+    if (select_algo(p) == ALGO_CONV16I) return conv16_pack(p, d_w, d_packed, to_stream(s), true);
     if (select_algo(p) == ALGO_PW16) {
         st = conv16_pack(p, d_w, d_packed, to_stream(s));
         if (st != OSH_OK) return st;
@@ -523,6 +602,8 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         case 2: OSH_FIRST(MM, 2); break; \
         case 3: OSH_FIRST(MM, 3); break; \
         case 4: OSH_FIRST(MM, 4); break; \
+        case 16: OSH_FIRST(MM, 16); break; \
+        case 32: OSH_FIRST(MM, 32); break; \
         default: OSH_FIRST(MM, 8); break; \
         }                          \
     } while (0)
@@ -537,6 +618,32 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
     }
     case ALGO_CONV16:
         return conv16_tuned_launch(p, d_x, w, d_bias, d_res, act, d_y, stream);
+    case ALGO_CONV16I:
+        return tuned_launch(
+            p, 4, kC16sCount, im2col3x3_variant(), [](int) { return true; },
+            [&](int v) {
+                if (v < 0) {  // cost model
+                    const int cus = device_cus();
+                    double bc = 0;
+                    for (int i = 0; i < kC16sCount; i++) {
+                        const double c = conv16s_cost(p, kC16s[i], cus);
+                        if (v < 0 || c < bc) v = i, bc = c;
+                    }
+                }
+                return conv16si_launch(p, d_x, w, d_bias, d_res, act, d_y, stream, v);
+            },
+            stream);
+    case ALGO_WINOGRAD: {
+        const long long tiles = (long long)p->n * ((p->h + 1) / 2) * ((p->w + 1) / 2);
+        dim3 grid((unsigned)((p->m + 15) / 16), (unsigned)((tiles + 15) / 16));
+        if (grid.y > 65535) return fail(OSH_E_UNSUPPORTED, "Conv: Winograd grid too large");
+        const float4 *u = reinterpret_cast<const float4 *>(d_wpacked);
+        OSH_DISPATCH_ACT(act, ACT,
+                         hipLaunchKernelGGL(wino_f23_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, u, d_bias,
+                                            d_res, d_y));
+        OSH_LAUNCH_CHECK("wino_f23_kernel");
+        return OSH_OK;
+    }
     case ALGO_WI3X3: {
         osh_status st = conv3x3_wi_launch(p, d_x, w, d_bias, act, d_y, stream, device_cus());
         return st != OSH_OK ? st : residual_add(p, d_res, d_y, stream);
@@ -563,7 +670,7 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
     case ALGO_POINTWISE:
     case ALGO_IM2COL:
         return igemm_conv(p, d_x, w, d_bias, d_res, act, d_y, stream,
-                          select_algo(p) == ALGO_POINTWISE ? B_DENSE : B_IM2COL);
+                          is_pointwise(p) ? B_DENSE : B_IM2COL);
     }
     return fail(OSH_E_INVALID, "Conv: no kernel");
 }

@@ -342,8 +342,11 @@ __global__ __launch_bounds__(256) void conv16l_kernel(osh_conv_params p, const f
 // Pack OIHW weights (T taps per channel) into
 // [ceil(M/16)][C/16 * T k-groups][64 lanes][4 steps]: lane (j, g), step s of
 // k-group (icb, tap) holds w[16 mb + j][16 icb + 4 s + g][tap] (zero for output
-// channels past M).
-__global__ void conv16_pack_kernel(int M, int C, int T, const float *__restrict__ w, float *__restrict__ out) {
+// channels past M).  With i2c (T = 9) the k-groups of a 16-channel block run
+// through its 144 (channel, tap) terms in the im2col order instead: k-group t,
+// step s holds local term 16 t + 4 s + g = 9 ic + tap.
+__global__ void conv16_pack_kernel(int M, int C, int T, const float *__restrict__ w, float *__restrict__ out,
+                                   int i2c) {
     const long long kgroups = (long long)(C / 16) * T;
     const long long total = (long long)((M + 15) / 16) * kgroups * 256;
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -354,8 +357,17 @@ __global__ void conv16_pack_kernel(int M, int C, int T, const float *__restrict_
     const int kg = (int)(t % kgroups);
     const int mb = (int)(t / kgroups);
     const int j = lane & 15, g = lane >> 4;
-    const int icb = kg / T, tap = kg % T;
-    const int oc = mb * 16 + j, ic = icb * 16 + 4 * s + g;
+    const int icb = kg / T;
+    int ic, tap;
+    if (i2c) {
+        const int term = 16 * (kg % T) + 4 * s + g;
+        ic = icb * 16 + term / 9;
+        tap = term % 9;
+    } else {
+        ic = icb * 16 + 4 * s + g;
+        tap = kg % T;
+    }
+    const int oc = mb * 16 + j;
     out[idx] = oc < M ? w[((long long)oc * C + ic) * T + tap] : 0.f;
 }
 
@@ -369,10 +381,11 @@ inline size_t conv16_packed_bytes(const osh_conv_params *p) {
     return (size_t)((p->m + 15) / 16) * (p->c / 16) * p->kh * p->kw * 256 * sizeof(float);
 }
 
-inline osh_status conv16_pack(const osh_conv_params *p, const float *w, void *out, hipStream_t st) {
+inline osh_status conv16_pack(const osh_conv_params *p, const float *w, void *out, hipStream_t st,
+                              bool i2c = false) {
     const long long total = (long long)conv16_packed_bytes(p) / 4;
     hipLaunchKernelGGL(conv16_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p->m, p->c,
-                       p->kh * p->kw, w, static_cast<float *>(out));
+                       p->kh * p->kw, w, static_cast<float *>(out), i2c && p->kh * p->kw == 9 ? 1 : 0);
     OSH_LAUNCH_CHECK("conv16_pack_kernel");
     return OSH_OK;
 }

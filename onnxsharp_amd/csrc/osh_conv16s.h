@@ -19,6 +19,16 @@
 //     conv16_kernel) from global memory with 16-byte loads, one block ahead.
 // Row pitch and channel-plane pitch of the patch are padded so that the 32
 // lanes of each half-wave LDS read fall in distinct banks.
+//
+// I2C runs the same tiles in the im2col order (bias, then ic -> ky -> kx:
+// ConvKernels.Im2Col and PackedConv, src/OnnxSharp/Kernels/ConvKernels.cs:554-563,
+// PackedConv.cs:420-440), the reference's chain for the 3x3 layers its NCHWc
+// gate refuses: a 16-channel block holds 144 consecutive terms of that chain
+// either way, so only the order within a block changes.  Step u of a block
+// gives lane group g the term 4u + g = 9 ic + tap; with u = 9 v + r its channel
+// is 4 v + (4 r + g) / 9, so each lane keeps nine patch offsets (one per r)
+// and the rest of the address is a compile-time constant.  The weights are
+// packed in the same order (conv16_pack with i2c).
 #pragma once
 
 #include "osh_conv16.h"
@@ -80,7 +90,7 @@ struct C16sGeom {
 // 1x1 stride-1 kernel on a map with W % 4 == 0 and a 16-byte aligned input).
 // XB: workgroups take their tiles XCD-banded (xcd_band), so that the tiles
 // one XCD runs are neighbours whose patches share halo lines in its L2.
-template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT, bool XB = false>
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT, bool XB = false, bool I2C = false>
 __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const float *__restrict__ x,
                                                       const float *__restrict__ wpk, const float *__restrict__ bias,
                                                       const float *__restrict__ res, float *__restrict__ y,
@@ -89,6 +99,7 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
     static_assert(16 % TWL == 0, "a lane group covers whole rows of the tile");
     static_assert(!VEC || (KS == 1 && S == 1 && G::PC % 4 == 0 && G::PITCH % 4 == 0 && G::PLANE % 4 == 0),
                   "16-byte staging needs whole, aligned four-column groups");
+    static_assert(!I2C || KS == 3, "the im2col order differs from the NCHWc order only for 3x3 kernels");
     __shared__ __align__(16) float lds[2 * G::CHUNK];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -193,21 +204,40 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
 
     // the lane's pixel (row j / TWL + THL q, column j % TWL) in patch coordinates
     const int lbase = g * G::PLANE + (j / TWL) * S * G::PITCH + (j % TWL) * S;
+    // im2col order: the lane's patch offset of term 4 r + g (r = 0..8) of a
+    // group of four channels
+    int i2c_off[I2C ? 9 : 1];
+    if constexpr (I2C) {
+#pragma unroll
+        for (int r = 0; r < 9; r++) {
+            const int term = 4 * r + g, tap = term % 9;
+            i2c_off[r] = (term / 9) * G::PLANE + (tap / 3) * G::PITCH + tap % 3 + lbase - g * G::PLANE;
+        }
+    }
+    // B operand of k-group t (block cb, tap or term group), step s, pixel block q
+    auto bval = [&](const float *lbuf, int cb, int t, int s, int q) -> float {
+        if constexpr (I2C) {
+            const int u = 4 * (t - cb * G::T) + s, v = u / 9, r = u - 9 * v;
+            return lbuf[(16 * cb + 4 * v) * G::PLANE + G::THL * q * S * G::PITCH + i2c_off[r]];
+        } else {
+            const int tap = t - cb * G::T;
+            const int ky = tap / KS, kx = tap - KS * (tap / KS);
+            return lbuf[lbase + (16 * cb + 4 * s) * G::PLANE + (G::THL * q * S + ky) * G::PITCH + kx];
+        }
+    };
     // a partial last chunk skips its missing channel blocks (no extra terms
     // enter the chain)
     auto compute = [&](const float4 (&A)[G::NA][TM], int buf, int chunk) {
-        const float *lb = lds + buf * G::CHUNK + lbase;
+        const float *lb = lds + buf * G::CHUNK;
 #pragma unroll
         for (int t = 0; t < G::NA; t++) {
-            const int cb = t / G::T, tap = t - cb * G::T;
-            const int ky = tap / KS, kx = tap - KS * (tap / KS);
+            const int cb = t / G::T;
             if (CB > 1 && chunk * CB + cb >= icbs) break;
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 float b[BV];
 #pragma unroll
-                for (int q = 0; q < BV; q++)
-                    b[q] = lb[(16 * cb + 4 * s) * G::PLANE + (G::THL * q * S + ky) * G::PITCH + kx];
+                for (int q = 0; q < BV; q++) b[q] = bval(lb, cb, t, s, q);
 #pragma unroll
                 for (int tm = 0; tm < TM; tm++) {
                     const float4 &a4 = A[t][tm];
@@ -247,17 +277,16 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
     // block) and store after the loop, as do the pointwise tiles (slower
     // block by block too).
     auto compute_last = [&](const float4 (&A)[G::NA][TM], int buf, int chunk) {
-        const float *lb = lds + buf * G::CHUNK + lbase;
+        const float *lb = lds + buf * G::CHUNK;
 #pragma unroll
         for (int q = 0; q < BV; q++) {
 #pragma unroll
             for (int t = 0; t < G::NA; t++) {
-                const int cb = t / G::T, tap = t - cb * G::T;
-                const int ky = tap / KS, kx = tap - KS * (tap / KS);
+                const int cb = t / G::T;
                 if (CB > 1 && chunk * CB + cb >= icbs) break;
 #pragma unroll
                 for (int s = 0; s < 4; s++) {
-                    const float b = lb[(16 * cb + 4 * s) * G::PLANE + (G::THL * q * S + ky) * G::PITCH + kx];
+                    const float b = bval(lb, cb, t, s, q);
 #pragma unroll
                     for (int tm = 0; tm < TM; tm++) {
                         const float4 &a4 = A[t][tm];
@@ -322,7 +351,7 @@ inline bool conv16s_eligible(const osh_conv_params *p) {
     return conv16_eligible(p) && p->sh == p->sw && (p->sh == 1 || p->sh == 2);
 }
 
-template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, bool XB = false>
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, bool XB = false, bool I2C = false>
 inline osh_status conv16s_launch_t(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                    const float *res, int act, float *y, hipStream_t st) {
     using G = C16sGeom<TM, BV, TWL, S, KS, CB, VEC>;
@@ -330,17 +359,33 @@ inline osh_status conv16s_launch_t(const osh_conv_params *p, const float *x, con
     const int mgroups = ceil_div(ceil_div(p->m, 16), 4 * TM);
     dim3 grid((unsigned)(tiles_w * tiles_h), (unsigned)mgroups, (unsigned)p->n);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16s_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT, XB>), grid, dim3(256), 0,
-                                        st, *p, x, w, bias, res, y, tiles_w));
+                     hipLaunchKernelGGL((conv16s_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT, XB, I2C>), grid, dim3(256),
+                                        0, st, *p, x, w, bias, res, y, tiles_w));
     OSH_LAUNCH_CHECK("conv16s_kernel");
     return OSH_OK;
 }
 
-template <int TM, int BV, int TWL, bool XB = false>
+template <int TM, int BV, int TWL, bool XB = false, bool I2C = false>
 inline osh_status conv16s_launch_s(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                    const float *res, int act, float *y, hipStream_t st) {
-    if (p->sh == 1) return conv16s_launch_t<TM, BV, TWL, 1, 3, 1, false, XB>(p, x, w, bias, res, act, y, st);
-    return conv16s_launch_t<TM, BV, TWL, 2, 3, 1, false, XB>(p, x, w, bias, res, act, y, st);
+    if (p->sh == 1) return conv16s_launch_t<TM, BV, TWL, 1, 3, 1, false, XB, I2C>(p, x, w, bias, res, act, y, st);
+    return conv16s_launch_t<TM, BV, TWL, 2, 3, 1, false, XB, I2C>(p, x, w, bias, res, act, y, st);
+}
+
+// The kC16s tiles in the im2col order (weights packed by conv16_pack with i2c).
+inline osh_status conv16si_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                  const float *res, int act, float *y, hipStream_t st, int v) {
+    switch (v) {
+    case 0: return conv16s_launch_s<1, 1, 16, false, true>(p, x, w, bias, res, act, y, st);
+    case 1: return conv16s_launch_s<1, 2, 16, false, true>(p, x, w, bias, res, act, y, st);
+    case 2: return conv16s_launch_s<1, 4, 16, false, true>(p, x, w, bias, res, act, y, st);
+    case 3: return conv16s_launch_s<2, 2, 16, false, true>(p, x, w, bias, res, act, y, st);
+    case 4: return conv16s_launch_s<1, 1, 8, false, true>(p, x, w, bias, res, act, y, st);
+    case 5: return conv16s_launch_s<1, 2, 8, false, true>(p, x, w, bias, res, act, y, st);
+    case 6: return conv16s_launch_s<2, 2, 8, false, true>(p, x, w, bias, res, act, y, st);
+    case 7: return conv16s_launch_s<1, 2, 4, false, true>(p, x, w, bias, res, act, y, st);
+    default: return conv16s_launch_s<1, 4, 4, false, true>(p, x, w, bias, res, act, y, st);
+    }
 }
 
 inline osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,

@@ -32,6 +32,9 @@ static int g_conv16_variant = -3;  // -3: read ONNXSHARP_HIP_CONV16_VARIANT on f
 static int g_tune = -1;             // -1: read ONNXSHARP_HIP_TUNE on first use
 static int g_pw_variant = -3;       // -3: read ONNXSHARP_HIP_POINTWISE_VARIANT on first use
 static int g_dqmm_variant = -3;     // -3: read ONNXSHARP_HIP_DQMM_VARIANT on first use
+static int g_winograd = -3;         // -3: read ONNXSHARP_HIP_WINOGRAD on first use
+static int g_i2c_variant = -3;      // -3: read ONNXSHARP_HIP_IM2COL3X3_VARIANT on first use
+static long long g_wino_max = -3;   // -3: read ONNXSHARP_WINO_MAX on first use
 
 bool exact_silu() {
     if (g_exact_silu < 0) {
@@ -71,6 +74,34 @@ int pointwise_variant() {
         g_pw_variant = e ? atoi(e) : -1;
     }
     return g_pw_variant;
+}
+
+int im2col3x3_variant() {
+    if (g_i2c_variant == -3) {
+        const char *e = getenv("ONNXSHARP_HIP_IM2COL3X3_VARIANT");
+        g_i2c_variant = e ? atoi(e) : -1;
+    }
+    return g_i2c_variant;
+}
+
+int winograd_mode() {
+    if (g_winograd == -3) {
+        const char *e = getenv("ONNXSHARP_HIP_WINOGRAD");
+        const int v = e ? atoi(e) : 1;
+        g_winograd = (v >= 0 && v <= 2) ? v : 1;
+    }
+    return g_winograd;
+}
+
+long long winograd_max_pixels() {
+    if (g_wino_max == -3) {
+        // the reference's own knob (Winograd.cs:38-40): a number, else 4096
+        const char *e = getenv("ONNXSHARP_WINO_MAX");
+        char *end = nullptr;
+        const long long v = e ? strtoll(e, &end, 10) : 0;
+        g_wino_max = (e && end != e && *end == 0) ? v : 4096;
+    }
+    return g_wino_max;
 }
 
 int dqmm_variant() {
@@ -123,6 +154,22 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         g_gemm_variant = value;
         return OSH_OK;
     }
+    if (strcmp(key, "im2col3x3_variant") == 0) {
+        if (value < -1 || value >= im2col3x3_variant_count())
+            return fail(OSH_E_INVALID, "im2col3x3_variant %d out of range [-1, %d)", value,
+                        im2col3x3_variant_count());
+        g_i2c_variant = value;
+        return OSH_OK;
+    }
+    if (strcmp(key, "winograd") == 0) {
+        if (value < 0 || value > 2) return fail(OSH_E_INVALID, "winograd %d out of range [0, 2]", value);
+        g_winograd = value;
+        return OSH_OK;
+    }
+    if (strcmp(key, "winograd_max_pixels") == 0) {
+        g_wino_max = value;
+        return OSH_OK;
+    }
     if (strcmp(key, "dqmm_variant") == 0) {
         if (value != 0 && value != 1) return fail(OSH_E_INVALID, "dqmm_variant %d out of range [0, 2)", value);
         g_dqmm_variant = value;
@@ -147,6 +194,23 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     }
     if (strcmp(key, "pointwise_variant") == 0) {
         *value = pointwise_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "im2col3x3_variant") == 0) {
+        *value = im2col3x3_variant();
+        return OSH_OK;
+    }
+    if (strcmp(key, "im2col3x3_variants") == 0) {
+        *value = im2col3x3_variant_count();
+        return OSH_OK;
+    }
+    if (strcmp(key, "winograd") == 0) {
+        *value = winograd_mode();
+        return OSH_OK;
+    }
+    if (strcmp(key, "winograd_max_pixels") == 0) {
+        const long long v = winograd_max_pixels();
+        *value = v > 2147483647LL ? 2147483647 : (v < -2147483647LL ? -2147483647 : (int)v);
         return OSH_OK;
     }
     if (strcmp(key, "dqmm_variant") == 0) {

@@ -177,6 +177,61 @@ def winograd_f23(x, w, bias):
     return y
 
 
+KERNEL_DEPTHWISE = "depthwise"
+KERNEL_NCHWC = "nchwc"
+KERNEL_WINOGRAD = "winograd"
+KERNEL_IM2COL = "im2col"
+
+
+def conv_reference_kernel(x_shape, w_shape, strides, pads, dilations, group, out_hw, winograd=1,
+                          wino_max=4096):
+    """The kernel ConvLayer.Forward (src/OnnxSharp/Ops/DnnOps.cs:437-482) runs
+    for a 2-D conv on an AVX-512 host, first gate that holds:
+    DepthwiseConv.TryConv (group == C == M, one input channel per group,
+    DepthwiseConv.cs:25-60); FirstConv (C <= 3; its ic -> ky -> kx chain is
+    the im2col order, so it is reported as KERNEL_IM2COL); NchwcConv.TryConv
+    (NchwcConv.cs:100-126,166-194); Winograd.TryConv3x3 (Winograd.cs:58-122);
+    else PackedConv / Im2Col, both the im2col chain.  winograd = 0 leaves
+    Winograd out and 2 puts it ahead of NCHWc, as the backend's option of the
+    same name does.  pads are the begin pads (top, left)."""
+    n, c, h, w = x_shape
+    m, cpg, kh, kw = w_shape
+    sh, sw = strides
+    pt, pl = pads
+    dh, dw = dilations
+    oh, ow = out_hw
+    if group == c and m == c and cpg == 1 and group > 1:
+        return KERNEL_DEPTHWISE
+    if c <= 3 and group == 1:
+        return KERNEL_IM2COL
+    wino = (winograd != 0 and group == 1 and (kh, kw) == (3, 3) and (sh, sw) == (1, 1) and (dh, dw) == (1, 1)
+            and (pt, pl) == (1, 1) and c >= 8 and m >= 8 and (oh, ow) == (h, w) and h >= 6 and w >= 6
+            and h * w <= wino_max and m * c * 16 <= (1 << 24))
+    if winograd == 2 and wino:
+        return KERNEL_WINOGRAD
+    s2 = sh == 2
+    nchwc = (group == 1 and (kh, kw) == (3, 3) and sh == sw and sh in (1, 2) and (dh, dw) == (1, 1)
+             and (pt, pl) == (1, 1) and (not s2 or (h % 2 == 0 and w % 2 == 0)) and c % 16 == 0
+             and m % 32 == 0 and n == 1 and ((oh * 2, ow * 2) == (h, w) if s2 else (oh, ow) == (h, w)))
+    if nchwc:
+        return KERNEL_NCHWC
+    if wino:
+        return KERNEL_WINOGRAD
+    return KERNEL_IM2COL
+
+
+def conv_reference(x, w, bias, strides, pads, dilations, group, out_hw, winograd=1, wino_max=4096):
+    """Conv output (before the fused activation) of the reference kernel
+    conv_reference_kernel picks for the shape."""
+    k = conv_reference_kernel(x.shape, w.shape, strides, pads, dilations, group, out_hw, winograd, wino_max)
+    if k == KERNEL_DEPTHWISE:
+        return conv_dw_f32(x, w, bias, strides, pads, dilations, out_hw)
+    if k == KERNEL_WINOGRAD:
+        return winograd_f23(x, w, bias)
+    return conv2d_f32(x, w, bias, strides, pads, dilations, group, out_hw,
+                      order=ORDER_NCHWC if k == KERNEL_NCHWC else ORDER_IM2COL)
+
+
 # ---------------------------------------------------------------- activations
 
 def _unary(fn, x):

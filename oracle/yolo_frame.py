@@ -4,23 +4,19 @@ TEST INFRASTRUCTURE ONLY: used by tests/ and by bench.py's cpu_baseline leg.
 
 Each op is restated with the oracle's functions in the order the reference's
 AVX-512 dispatch uses for that layer (ConvLayer.Forward,
-src/OnnxSharp/Ops/DnnOps.cs:437-482): depthwise for g == C == M, the NCHWc
-order for 3x3 convolutions whose input channels are a multiple of 16, the
-im2col/pointwise FMA chain otherwise; SiLU is the reference polynomial.  The
+src/OnnxSharp/Ops/DnnOps.cs:437-482, restated by
+oracle.conv_reference_kernel): depthwise for g == C == M, the NCHWc chain
+where NchwcConv's gate holds, Winograd F(2x2,3x3) where Winograd's gate holds,
+the im2col/pointwise FMA chain otherwise; SiLU is the reference polynomial.  The
 attention core uses the GEMM chain for both MatMuls and the oracle softmax.
 """
 import numpy as np
 
 
-def conv(oracle, op, x, res=None):
+def conv(oracle, op, x, res=None, winograd=1):
     k, s, pad = op.k, op.s, op.k // 2
     out_hw = (op.y.h, op.y.w)
-    if op.group > 1 and op.group == op.x.c == op.y.c:
-        y = oracle.conv_dw_f32(x, op.w, op.b, (s, s), (pad, pad), (1, 1), out_hw)
-    else:
-        nchwc = k == 3 and op.group == 1 and op.x.c % 16 == 0
-        y = oracle.conv2d_f32(x, op.w, op.b, (s, s), (pad, pad), (1, 1), op.group, out_hw,
-                              order=oracle.ORDER_NCHWC if nchwc else oracle.ORDER_IM2COL)
+    y = oracle.conv_reference(x, op.w, op.b, (s, s), (pad, pad), (1, 1), op.group, out_hw, winograd=winograd)
     if op.act == "Silu":
         y = oracle.silu_ref(y)
     if res is not None:  # a fused residual Add: one float addition per element

@@ -26,9 +26,15 @@ def run_conv(cuda, x, w, b, act=None, **attrs):
     return y.cpu().numpy(), layer.resolve(x.shape, w.shape)
 
 
-def oracle_conv(oracle, x, w, b, p, act, order=None):
-    o = oracle.ORDER_NCHWC if order is None and (p.c // p.group) % 16 == 0 and p.group == 1 else (order or 0)
-    y = oracle.conv2d_f32(x, w, b, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), p.group, (p.oh, p.ow), order=o)
+def oracle_conv(oracle, x, w, b, p, act, order=None, winograd=1):
+    """The oracle's conv: with order None the kernel the reference's dispatch
+    picks for the shape (depthwise, NCHWc, Winograd or im2col chain), else the
+    given accumulation order."""
+    args = (x, w, b, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), p.group, (p.oh, p.ow))
+    if order is None:
+        y = oracle.conv_reference(*args, winograd=winograd)
+    else:
+        y = oracle.conv2d_f32(*args, order=order)
     if act == "Silu":
         y = oracle.silu_ref(y)
     elif act == "Relu":
@@ -62,10 +68,11 @@ CASES = [
 @pytest.mark.parametrize("name,xs,ws,attrs,act", CASES, ids=[c[0] for c in CASES])
 def test_conv_parity(cuda, oracle, name, xs, ws, attrs, act):
     # Every default kernel sums in the order of the reference's kernel for the
-    # shape: the NCHWc chain for 3x3 with C % 16 == 0 (AVX-512 hosts), the
-    # depthwise chain, else the im2col / GEMM chain.  With the exact SiLU the
-    # output is the oracle's, bit for bit; with the default SiLU it is within
-    # the FP32 bar (and within it of the other ISA order too).
+    # shape on an AVX-512 host: the depthwise chain, the NCHWc chain where
+    # NchwcConv's gate holds, Winograd where Winograd's gate holds, else the
+    # im2col / GEMM chain.  With the exact SiLU the output is the oracle's, bit
+    # for bit; with the default SiLU it is within the FP32 bar (and within it
+    # of the plain im2col order too).
     from onnxsharp_amd import native as N
     print(f"conv {name} x={xs} w={ws} {attrs} act={act}", flush=True)
     seed = sum(xs) * 7 + sum(ws)
@@ -84,11 +91,7 @@ def test_conv_parity(cuda, oracle, name, xs, ws, attrs, act):
         ye, _ = run_conv(cuda, x, w, b, act, **attrs)
     finally:
         N.call("osh_config_set", b"exact_silu", 0)
-    dw = p.group > 1 and p.group == p.c == p.m
-    ref = oracle_conv(oracle, x, w, b, p, act) if not dw else oracle.conv_dw_f32(
-        x, w, b, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), (p.oh, p.ow))
-    if dw and act == "Silu":
-        ref = oracle.silu_ref(ref)
+    ref = oracle_conv(oracle, x, w, b, p, act)
     assert np.array_equal(ye, ref), f"{name}: max |d| {np.abs(ye - ref).max():.3e}"
 
 
@@ -133,10 +136,15 @@ def test_conv_silu_epilogue_on_bias_only_input(cuda, oracle):
     ((1, 1, 9, 11), (8, 1, 3, 3), dict(auto_pad="SAME_UPPER", strides=[2, 2])),
     ((1, 8, 160, 160), (16, 8, 3, 3), dict(pads=[1, 1, 1, 1])),  # YOLO11n's 8 -> 16 bottleneck conv
     ((2, 8, 21, 19), (32, 8, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
-], ids=["stem_640", "c3_m8_s1", "c4_m32_s2_batch2", "c1_m8_same_upper", "c8_m16_160", "c8_m32_s2_batch2"])
+    ((1, 16, 40, 40), (8, 16, 3, 3), dict(strides=[3, 3], pads=[1, 1, 1, 1])),
+    ((1, 32, 30, 31), (16, 32, 3, 3), dict(strides=[1, 2], pads=[1, 1, 1, 1])),
+], ids=["stem_640", "c3_m8_s1", "c4_m32_s2_batch2", "c1_m8_same_upper", "c8_m16_160", "c8_m32_s2_batch2",
+        "c16_m8_s3", "c32_m16_s1x2"])
 def test_first_layer_conv_is_the_fma_chain(cuda, oracle, xs, ws, attrs):
-    # C <= 4 takes the direct first-layer kernel: per output channel the bias,
-    # then fmaf over ic -> ky -> kx, the im2col chain -- bit for bit.
+    # C <= 4, and 3x3 layers with C = 8 (or 16/32 at strides the LDS-patch
+    # tiles do not take) that neither the NCHWc nor the Winograd gate takes,
+    # run the direct per-pixel kernel: per output channel the bias, then fmaf
+    # over ic -> ky -> kx, the im2col chain -- bit for bit.
     from onnxsharp_amd import native as N
     seed = sum(xs) + sum(ws)
     x = synth.uniform(seed, xs)
@@ -165,10 +173,11 @@ CONV16_CASES = [
 
 @pytest.mark.parametrize("name,xs,ws,attrs", CONV16_CASES, ids=[c[0] for c in CONV16_CASES])
 def test_conv16_is_the_nchwc_chain(cuda, oracle, name, xs, ws, attrs):
-    # 3x3 convolutions with C % 16 == 0 run the in-order 16x16x4 kernels: bit
-    # for bit the reference's NCHWc chain (bias, then icb -> ky -> kx -> lane16),
-    # whatever tile is forced -- weights streamed or in LDS, or the input patch
-    # staged in LDS (stride 1 and 2; other strides fall back to the cost model).
+    # A forced tile runs the in-order 16x16x4 kernels on any 3x3 shape with
+    # C % 16 == 0: bit for bit the reference's NCHWc chain (bias, then icb ->
+    # ky -> kx -> lane16), whatever tile -- weights streamed or in LDS, or the
+    # input patch staged in LDS (stride 1 and 2; other strides fall back to the
+    # cost model).  The default dispatch takes them where NchwcConv's gate holds.
     from onnxsharp_amd import native as N
     seed = sum(xs) * 3 + sum(ws)
     x = synth.uniform(seed, xs)
@@ -180,7 +189,7 @@ def test_conv16_is_the_nchwc_chain(cuda, oracle, name, xs, ws, attrs):
     N.call("osh_config_set", b"exact_silu", 1)
     try:
         ref = None
-        for v in [-1] + list(range(nv.value)):
+        for v in range(nv.value):
             print(f"conv16 {name} variant {v}", flush=True)
             N.call("osh_config_set", b"conv16_variant", v)
             y, p = run_conv(cuda, x, w, b, "Silu", **attrs)
@@ -241,6 +250,10 @@ RESIDUAL_CASES = [
     ("depthwise_64_20", (1, 64, 20, 20), (64, 1, 3, 3), dict(group=64, pads=[1, 1, 1, 1]), -1),
     ("first_conv_c3", (1, 3, 64, 64), (16, 3, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
     ("direct_c8_m16_160", (1, 8, 160, 160), (16, 8, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
+    ("im2col_tiles_32to16_80", (1, 32, 80, 80), (16, 32, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
+    ("direct_c32_m16_s1x2", (1, 32, 30, 31), (16, 32, 3, 3), dict(strides=[1, 2], pads=[1, 1, 1, 1]), -1),
+    ("winograd_32to40_18x24", (1, 32, 18, 24), (40, 32, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
+    ("winograd_c24_batch2_odd", (2, 24, 13, 11), (16, 24, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
     ("im2col_dilated_5x5", (1, 5, 23, 21), (7, 5, 5, 5), dict(pads=[4, 4, 4, 4], dilations=[2, 2]), -1),
     ("wave_independent_16", (1, 16, 24, 32), (16, 16, 3, 3), dict(pads=[1, 1, 1, 1]), -2),
     ("weight_stationary_s2", (1, 64, 40, 40), (64, 64, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), -2),
@@ -311,3 +324,100 @@ def test_pointwise_tiles_are_the_gemm_chain(cuda, oracle, name, xs, ws):
     finally:
         N.call("osh_config_set", b"exact_silu", 0)
         N.call("osh_config_set", b"pointwise_variant", -1)
+
+
+WINOGRAD_CASES = [
+    # (name, x, w, act, residual)
+    ("yolo_64to64_20", (1, 64, 20, 20), (64, 64, 3, 3), "Silu", False),
+    ("yolo_deep_256to64_20", (1, 256, 20, 20), (64, 256, 3, 3), "Silu", False),
+    ("yolo_32to32_40", (1, 32, 40, 40), (32, 32, 3, 3), "Silu", True),
+    ("max_map_128to64_64x64", (1, 128, 64, 64), (64, 128, 3, 3), None, False),
+    ("batch2_16to16", (2, 16, 12, 16), (16, 16, 3, 3), "Relu", False),
+    ("odd_24to40_33x45", (1, 24, 33, 45), (40, 24, 3, 3), "Silu", True),
+    ("min_8to8_6x6", (1, 8, 6, 6), (8, 8, 3, 3), None, False),
+    ("partial_40to24_7x9_no_bias", (1, 40, 7, 9), (24, 40, 3, 3), "Silu", False),
+]
+
+
+@pytest.mark.parametrize("name,xs,ws,act,residual", WINOGRAD_CASES, ids=[c[0] for c in WINOGRAD_CASES])
+def test_winograd_is_the_reference_winograd(cuda, oracle, name, xs, ws, act, residual):
+    # winograd = 2 runs every Winograd-eligible shape through wino_f23_kernel:
+    # Winograd.cs's weight, input and output transforms and its k-ascending
+    # component GEMMs, bit for bit against the oracle's restatement (exact SiLU),
+    # within the FP32 bar of the direct conv, and the residual epilogue is the
+    # conv then the Add.
+    import torch
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    print(f"winograd {name} x={xs} w={ws} act={act} residual={residual}", flush=True)
+    seed = sum(xs) * 17 + sum(ws)
+    x = synth.uniform(seed, xs)
+    w = synth.normal(seed + 1, ws, 0, 0.05)
+    b = None if "no_bias" in name else synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    attrs = dict(pads=[1, 1, 1, 1])
+    old = C.c_int()
+    N.call("osh_config_get", b"winograd", C.byref(old))
+    N.call("osh_config_set", b"winograd", 2)
+    N.call("osh_config_set", b"exact_silu", 1)
+    try:
+        layer = ConvLayer(fused_activation=act, **attrs)
+        xt, wt, bt = _t(x, cuda), _t(w, cuda), None if b is None else _t(b, cuda)
+        y = layer.forward(xt, wt, bt)
+        p = layer.resolve(x.shape, w.shape)
+        if residual:
+            r = torch.from_numpy(synth.normal(seed + 3, tuple(y.shape), 0, 1)).to(cuda)
+            yr = layer.forward(xt, wt, bt, residual=r)
+            torch.cuda.synchronize()
+            assert np.array_equal(yr.cpu().numpy(), y.cpu().numpy() + r.cpu().numpy())
+        y = y.cpu().numpy()
+    finally:
+        N.call("osh_config_set", b"winograd", old.value)
+        N.call("osh_config_set", b"exact_silu", 0)
+    assert oracle.conv_reference_kernel(x.shape, w.shape, (1, 1), (1, 1), (1, 1), 1, (p.oh, p.ow),
+                                        winograd=2) == oracle.KERNEL_WINOGRAD
+    ref = oracle_conv(oracle, x, w, b, p, act, winograd=2)
+    assert np.array_equal(y, ref), f"max |d| {np.abs(y - ref).max():.3e} at {np.argwhere(y != ref)[:3]}"
+    direct = oracle_conv(oracle, x, w, b, p, act, order=oracle.ORDER_IM2COL)
+    assert_fp32_close(y, direct, name + " (direct conv)")
+
+
+IM2COL3X3_CASES = [
+    # 3x3 shapes with C % 16 == 0 that the reference runs on its im2col chain
+    ("yolo_32to16_80", (1, 32, 80, 80), (16, 32, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ("yolo_16to8_160", (1, 16, 160, 160), (8, 16, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ("s2_odd_32to72_41x37", (1, 32, 41, 37), (72, 32, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ("s2_batch2_48to40", (2, 48, 20, 22), (40, 48, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ("s1_wide_64to48_70x90", (1, 64, 70, 90), (48, 64, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ("pads_0_2_48to24", (1, 48, 17, 23), (24, 48, 3, 3), dict(pads=[0, 2, 2, 0])),
+]
+
+
+@pytest.mark.parametrize("name,xs,ws,attrs", IM2COL3X3_CASES, ids=[c[0] for c in IM2COL3X3_CASES])
+def test_im2col_order_tiles_are_the_im2col_chain(cuda, oracle, name, xs, ws, attrs):
+    # The LDS-patch tiles with each 16-channel block's terms in the im2col
+    # order: bit for bit the reference's im2col chain (bias, then ic -> ky ->
+    # kx), for every tile, with the default dispatch choosing them.
+    from onnxsharp_amd import native as N
+    seed = sum(xs) * 19 + sum(ws)
+    x = synth.uniform(seed, xs)
+    w = synth.normal(seed + 1, ws, 0, 0.05)
+    b = synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    nv = C.c_int()
+    N.call("osh_config_get", b"im2col3x3_variants", C.byref(nv))
+    assert nv.value >= 9
+    N.call("osh_config_set", b"exact_silu", 1)
+    try:
+        ref = None
+        for v in [-1] + list(range(nv.value)):
+            print(f"im2col3x3 {name} variant {v}", flush=True)
+            N.call("osh_config_set", b"im2col3x3_variant", v)
+            y, p = run_conv(cuda, x, w, b, "Silu", **attrs)
+            if ref is None:
+                k = oracle.conv_reference_kernel(x.shape, w.shape, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw),
+                                                 p.group, (p.oh, p.ow))
+                assert k == oracle.KERNEL_IM2COL, k
+                ref = oracle_conv(oracle, x, w, b, p, "Silu", order=oracle.ORDER_IM2COL)
+            assert np.array_equal(y, ref), f"variant {v}: max |d| {np.abs(y - ref).max():.3e}"
+    finally:
+        N.call("osh_config_set", b"exact_silu", 0)
+        N.call("osh_config_set", b"im2col3x3_variant", -1)

@@ -173,6 +173,70 @@ def test_winograd_matches_direct(oracle, hw):
     assert np.abs(y - ref).max() <= 1e-5
 
 
+def test_winograd_exact_on_integer_data(oracle):
+    # With small integers every Winograd step is exact in float32 (the 1/2
+    # factors of G g G^T give quarters at most), so the result must equal the
+    # direct conv exactly: a wrong sign, index or factor in any of the three
+    # transforms shows up as an integer error.
+    rng = np.random.default_rng(44)
+    for (c, m, h, w) in [(8, 8, 6, 6), (11, 9, 7, 10), (16, 24, 9, 8)]:
+        x = rng.integers(-4, 5, (1, c, h, w)).astype(np.float32)
+        wt = rng.integers(-4, 5, (m, c, 3, 3)).astype(np.float32)
+        b = rng.integers(-8, 9, (m,)).astype(np.float32)
+        ref = oracle.conv2d_f64(x, wt, b, (1, 1), (1, 1), (1, 1), 1, (h, w))
+        assert np.array_equal(oracle.winograd_f23(x, wt, b).astype(np.float64), ref)
+
+
+def _yolo_conv_kernels(oracle, size):
+    from onnxsharp_amd import yolo11n
+    kinds, seen = [], set()
+    for op in yolo11n.build(size).ops:
+        # the C2PSA positional conv runs as one depthwise op per head
+        if isinstance(op, yolo11n.ConvOp) and op.name.split("#")[0] not in seen:
+            seen.add(op.name.split("#")[0])
+            pad = op.k // 2
+            kinds.append((oracle.conv_reference_kernel(
+                (1, op.x.c, op.x.h, op.x.w), (op.y.c, op.x.c // op.group, op.k, op.k), (op.s, op.s),
+                (pad, pad), (1, 1), op.group, (op.y.h, op.y.w)), op.k))
+    return kinds
+
+
+def test_reference_dispatch_of_the_yolo11n_frame(oracle):
+    # ConvLayer.Forward's chain on an AVX-512 host for the 87 convs at 640x640:
+    # 30 NCHWc calls (the reference's profile of this network, bench.md:2330),
+    # 7 depthwise, no Winograd (every small-map 3x3 passes NCHWc's gate), and
+    # the stem, four 3x3 bottleneck convs (16->8, 8->16 at 160, 32->16 at 80,
+    # twice) and the 45 pointwise convs on the im2col / GEMM chain.
+    kinds = _yolo_conv_kernels(oracle, 640)
+    count = lambda k, ks=None: sum(1 for kind, kk in kinds if kind == k and (ks is None or kk == ks))
+    assert len(kinds) == 87
+    assert count(oracle.KERNEL_NCHWC) == 30
+    assert count(oracle.KERNEL_DEPTHWISE) == 7
+    assert count(oracle.KERNEL_WINOGRAD) == 0
+    assert count(oracle.KERNEL_IM2COL, 1) == 45
+    assert count(oracle.KERNEL_IM2COL, 3) == 5
+    # at 128x128 the small maps bring Winograd in for the 3x3 convs NCHWc refuses
+    assert sum(1 for kind, _ in _yolo_conv_kernels(oracle, 128) if kind == oracle.KERNEL_WINOGRAD) >= 4
+
+
+def test_reference_dispatch_gates(oracle):
+    K = oracle.conv_reference_kernel
+    s1, p1, d1 = (1, 1), (1, 1), (1, 1)
+    assert K((1, 64, 20, 20), (64, 64, 3, 3), s1, p1, d1, 1, (20, 20)) == oracle.KERNEL_NCHWC
+    assert K((1, 64, 20, 20), (64, 64, 3, 3), s1, p1, d1, 1, (20, 20), winograd=2) == oracle.KERNEL_WINOGRAD
+    assert K((1, 64, 20, 20), (48, 64, 3, 3), s1, p1, d1, 1, (20, 20)) == oracle.KERNEL_WINOGRAD  # M % 32
+    assert K((2, 64, 20, 20), (64, 64, 3, 3), s1, p1, d1, 1, (20, 20)) == oracle.KERNEL_WINOGRAD  # batch 2
+    assert K((1, 64, 20, 20), (48, 64, 3, 3), s1, p1, d1, 1, (20, 20), winograd=0) == oracle.KERNEL_IM2COL
+    assert K((1, 64, 80, 80), (48, 64, 3, 3), s1, p1, d1, 1, (80, 80)) == oracle.KERNEL_IM2COL  # > 4096 px
+    assert K((1, 64, 80, 80), (48, 64, 3, 3), s1, p1, d1, 1, (80, 80), wino_max=6400) == oracle.KERNEL_WINOGRAD
+    assert K((1, 64, 41, 40), (64, 64, 3, 3), (2, 2), p1, d1, 1, (21, 20)) == oracle.KERNEL_IM2COL  # odd H, s2
+    assert K((1, 64, 40, 40), (64, 64, 3, 3), (2, 2), p1, d1, 1, (20, 20)) == oracle.KERNEL_NCHWC
+    assert K((1, 7, 20, 20), (64, 7, 3, 3), s1, p1, d1, 1, (20, 20)) == oracle.KERNEL_IM2COL  # C < 8
+    assert K((1, 8, 5, 20), (8, 8, 3, 3), s1, p1, d1, 1, (5, 20)) == oracle.KERNEL_IM2COL  # H < 6
+    assert K((1, 32, 20, 20), (32, 1, 3, 3), s1, p1, d1, 32, (20, 20)) == oracle.KERNEL_DEPTHWISE
+    assert K((1, 3, 64, 64), (16, 3, 3, 3), (2, 2), p1, d1, 1, (32, 32)) == oracle.KERNEL_IM2COL
+
+
 # ----------------------------------------------------------- activations
 
 def test_exp_polynomial_accuracy(oracle):
