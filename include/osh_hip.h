@@ -90,10 +90,10 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 16x16x4 MFMA kernel (the reference's NCHWc chain, bit for
  *                 bit) with a wave tile picked per shape; 0..N-1 forces a tile
  *                 on any 3x3 shape with C % 16 == 0 it fits (6..11:
- *                 weights held in LDS; 12..20: input patch staged in LDS
+ *                 weights held in LDS; 12..22: input patch staged in LDS
  *                 and shared by a workgroup's four waves, stride 1 or 2;
- *                 21..24: tiles 0, 3, 1, 4 with one wave per workgroup;
- *                 25..N-1: tiles 13, 14, 15 with XCD-banded workgroups);
+ *                 23..26: tiles 0, 3, 1, 4 with one wave per workgroup;
+ *                 27..N-1: tiles 13, 14, 15 with XCD-banded workgroups);
  *                 -2 = use the weight-stationary 3x3
  *                 kernels instead (summation order differs; within the FP32
  *                 tolerance).  Initial value from ONNXSHARP_HIP_CONV16_VARIANT.

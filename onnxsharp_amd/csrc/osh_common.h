@@ -143,6 +143,10 @@ int conv16_variant_count();
 int pointwise_variant();
 int pointwise_variant_count();
 
+// Drops the record of which kernel a packed conv weight buffer at d_ptr was
+// laid out for (osh_free calls it; the address may be reused).
+void forget_pack(const void *d_ptr);
+
 // Forced LDS-patch tile for the 3x3 convolutions that run in the im2col
 // order (-1 = automatic) and the number of tiles.
 int im2col3x3_variant();

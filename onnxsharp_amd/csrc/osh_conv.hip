@@ -315,6 +315,25 @@ static ConvKey conv_key(const osh_conv_params *p) {
                            p->group);
 }
 
+// Which kernel and shape each packed weight buffer was laid out for.  The
+// layout depends on the kernel choice, which the options "winograd",
+// "winograd_max_pixels", "conv16_variant" -2 and "pointwise_variant" -2 can
+// change between packing and launch; a launch whose buffer was packed for
+// another kernel or shape is refused instead of reading a wrong layout (or
+// past its end).  Buffers this library did not pack are not checked.
+static std::mutex g_packs_mu;
+static std::map<const void *, std::pair<int, ConvKey>> g_packs;
+
+static void record_pack(const osh_conv_params *p, const void *d_packed) {
+    std::lock_guard<std::mutex> lk(g_packs_mu);
+    g_packs[d_packed] = std::make_pair((int)select_algo(p), conv_key(p));
+}
+
+void forget_pack(const void *d_ptr) {
+    std::lock_guard<std::mutex> lk(g_packs_mu);
+    g_packs.erase(d_ptr);
+}
+
 static bool capturing(hipStream_t st) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     return hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
@@ -456,6 +475,10 @@ static osh_status check_params(const osh_conv_params *p) {
 
 }  // namespace osh
 
+namespace osh {
+static osh_status pack_weights(const osh_conv_params *p, const float *d_w, void *d_packed, osh_stream s);
+}  // namespace osh
+
 extern "C" {
 
 OSH_API osh_status osh_conv_infer_shape(const osh_conv_attrs *at, const int64_t x[4], const int64_t w[4],
@@ -534,6 +557,17 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
     osh_status st = check_params(p);
     if (st != OSH_OK) return st;
     if (!d_w || !d_packed) return fail(OSH_E_INVALID, "Conv pack: NULL pointer");
+    st = pack_weights(p, d_w, d_packed, s);
+    if (st == OSH_OK) record_pack(p, d_packed);
+    return st;
+}
+
+}  // extern "C"
+
+namespace osh {
+
+static osh_status pack_weights(const osh_conv_params *p, const float *d_w, void *d_packed, osh_stream s) {
+    osh_status st = OSH_OK;
     if (select_algo(p) == ALGO_CONV16) return conv16_pack(p, d_w, d_packed, to_stream(s));
     if (select_algo(p) == ALGO_WINOGRAD) return winograd_pack(p, d_w, d_packed, to_stream(s));
     if (select_algo(p) == ALGO_CONV16I) return conv16_pack(p, d_w, d_packed, to_stream(s), true);
@@ -553,7 +587,9 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
     return OSH_OK;
 }
 
-}  // extern "C"
+}  // namespace osh
+
+
 
 namespace osh {
 
@@ -715,6 +751,12 @@ static osh_status check_launch(const osh_conv_params *p, const float *d_x, const
     if (st != OSH_OK) return st;
     if (!d_x || !d_wpacked || !d_y) return fail(OSH_E_INVALID, "Conv: NULL tensor pointer");
     if (act < OSH_ACT_NONE || act > OSH_ACT_SILU) return fail(OSH_E_INVALID, "Conv: unknown activation %d", act);
+    std::lock_guard<std::mutex> lk(g_packs_mu);
+    auto it = g_packs.find(d_wpacked);
+    if (it != g_packs.end() && (it->second.first != (int)select_algo(p) || it->second.second != conv_key(p)))
+        return fail(OSH_E_INVALID,
+                    "Conv: the weights were packed for another kernel or shape (pack them again after changing "
+                    "the conv options)");
     return OSH_OK;
 }
 

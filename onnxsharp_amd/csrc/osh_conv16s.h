@@ -342,8 +342,8 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
 struct C16sVariant {
     int tm, bv, twl;
 };
-constexpr C16sVariant kC16s[] = {{1, 1, 16}, {1, 2, 16}, {1, 4, 16}, {2, 2, 16}, {1, 1, 8},
-                                 {1, 2, 8},  {2, 2, 8},  {1, 2, 4},  {1, 4, 4}};
+constexpr C16sVariant kC16s[] = {{1, 1, 16}, {1, 2, 16}, {1, 4, 16}, {2, 2, 16}, {1, 1, 8}, {1, 2, 8},
+                                 {2, 2, 8},  {1, 2, 4},  {1, 4, 4},  {1, 4, 8},  {2, 4, 8}};
 constexpr int kC16sCount = sizeof(kC16s) / sizeof(kC16s[0]);
 
 // Stride 1 or 2 in both directions (the patch geometry is compile-time).
@@ -384,7 +384,9 @@ inline osh_status conv16si_launch(const osh_conv_params *p, const float *x, cons
     case 5: return conv16s_launch_s<1, 2, 8, false, true>(p, x, w, bias, res, act, y, st);
     case 6: return conv16s_launch_s<2, 2, 8, false, true>(p, x, w, bias, res, act, y, st);
     case 7: return conv16s_launch_s<1, 2, 4, false, true>(p, x, w, bias, res, act, y, st);
-    default: return conv16s_launch_s<1, 4, 4, false, true>(p, x, w, bias, res, act, y, st);
+    case 8: return conv16s_launch_s<1, 4, 4, false, true>(p, x, w, bias, res, act, y, st);
+    case 9: return conv16s_launch_s<1, 4, 8, false, true>(p, x, w, bias, res, act, y, st);
+    default: return conv16s_launch_s<2, 4, 8, false, true>(p, x, w, bias, res, act, y, st);
     }
 }
 
@@ -399,7 +401,9 @@ inline osh_status conv16s_launch(const osh_conv_params *p, const float *x, const
     case 5: return conv16s_launch_s<1, 2, 8>(p, x, w, bias, res, act, y, st);
     case 6: return conv16s_launch_s<2, 2, 8>(p, x, w, bias, res, act, y, st);
     case 7: return conv16s_launch_s<1, 2, 4>(p, x, w, bias, res, act, y, st);
-    default: return conv16s_launch_s<1, 4, 4>(p, x, w, bias, res, act, y, st);
+    case 8: return conv16s_launch_s<1, 4, 4>(p, x, w, bias, res, act, y, st);
+    case 9: return conv16s_launch_s<1, 4, 8>(p, x, w, bias, res, act, y, st);
+    default: return conv16s_launch_s<2, 4, 8>(p, x, w, bias, res, act, y, st);
     }
 }
 

@@ -279,6 +279,7 @@ OSH_API osh_status osh_malloc(void **d_ptr, size_t bytes) {
 }
 
 OSH_API osh_status osh_free(void *d_ptr) {
+    if (d_ptr) forget_pack(d_ptr);
     if (d_ptr) OSH_HIP_CHECK(hipFree(d_ptr));
     return OSH_OK;
 }

@@ -421,3 +421,22 @@ def test_im2col_order_tiles_are_the_im2col_chain(cuda, oracle, name, xs, ws, att
     finally:
         N.call("osh_config_set", b"exact_silu", 0)
         N.call("osh_config_set", b"im2col3x3_variant", -1)
+
+
+def test_launch_refuses_weights_packed_for_another_kernel(cuda):
+    # Packed layouts depend on the kernel choice; changing "winograd" between
+    # packing and launch must be refused, not read as the other layout.
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    x = _t(synth.uniform(5, (1, 64, 20, 20)), cuda)
+    w = _t(synth.normal(6, (64, 64, 3, 3), 0, 0.05), cuda)
+    layer = ConvLayer(pads=[1, 1, 1, 1])
+    layer.forward(x, w)  # packed for the NCHWc tiles
+    N.call("osh_config_set", b"winograd", 2)
+    try:
+        with pytest.raises(N.OshError, match="packed for another kernel"):
+            layer.forward(x, w)  # same key: no repack, the launch sees the Winograd choice
+    finally:
+        N.call("osh_config_set", b"winograd", 1)
+    y = layer.forward(x, w)  # the original choice again
+    assert y.shape == (1, 64, 20, 20)
