@@ -233,6 +233,20 @@ OSH_API osh_status osh_conv2d_add_f32(const osh_conv_params *p, const float *d_x
                                       const float *d_bias, int act, const float *d_res, float *d_y,
                                       osh_stream s);
 
+/* Up to 4 independent convs in one launch: conv i is ps[i] on d_xs[i] with
+ * packed weights d_ws[i], bias d_biases[i] (d_biases may be NULL), residual
+ * d_res[i] (d_res may be NULL), output d_ys[i]; one fused activation for all.
+ * No single reference function: it stands for that many ConvLayer.Forward
+ * calls (src/OnnxSharp/Ops/DnnOps.cs:411-500) of layers that do not depend on
+ * each other, e.g. the detection head's three scales.  Outputs are those of
+ * separate osh_conv2d_f32 / osh_conv2d_add_f32 calls, bit for bit.  Convs
+ * that share a kernel family the grouped kernels cover (NCHWc-chain 3x3 of
+ * one stride, pointwise, depthwise) run as one launch; other groups run one
+ * launch per conv. */
+OSH_API osh_status osh_conv2d_group_f32(int count, const osh_conv_params *ps, const float *const *d_xs,
+                                        const void *const *d_ws, const float *const *d_biases, int act,
+                                        const float *const *d_res, float *const *d_ys, osh_stream s);
+
 /* ------------------------------------------------- MatMul + bias (A9, A10) */
 
 /* C[m,n] (row stride ldc) = A[m,k] (lda) * B[k,n] (ldb)

@@ -108,10 +108,9 @@ static osh_status check_attrs(const osh_conv_attrs *at, const int64_t x[4], cons
 // ---------------------------------------------------------------- depthwise
 
 template <int ACT>
-__global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const float *__restrict__ x,
-                                                      const float *__restrict__ w, const float *__restrict__ bias,
-                                                      const float *__restrict__ res, float *__restrict__ y) {
-    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void dw_conv_at(const osh_conv_params &p, const float *__restrict__ x,
+                                           const float *__restrict__ w, const float *__restrict__ bias,
+                                           const float *__restrict__ res, float *__restrict__ y, long long idx) {
     long long total = (long long)p.n * p.m * p.oh * p.ow;
     if (idx >= total) return;
     int ox = (int)(idx % p.ow);
@@ -135,6 +134,24 @@ __global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const f
     float v = activate<ACT>(acc);
     if (res) v += res[idx];
     y[idx] = v;
+}
+
+template <int ACT>
+__global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const float *__restrict__ x,
+                                                      const float *__restrict__ w, const float *__restrict__ bias,
+                                                      const float *__restrict__ res, float *__restrict__ y) {
+    dw_conv_at<ACT>(p, x, w, bias, res, y, (long long)blockIdx.x * blockDim.x + threadIdx.x);
+}
+
+// Several depthwise convs in one launch: workgroup b covers outputs
+// 256 (b - start[i]) .. of conv i (ConvGroup's block table).
+template <int ACT>
+__global__ __launch_bounds__(256) void dw_conv_group_kernel(ConvGroup g) {
+    const int b = blockIdx.x;
+    int i = 0;
+    while (i + 1 < g.count && b >= g.start[i + 1]) i++;
+    dw_conv_at<ACT>(g.p[i], g.x[i], g.w[i], g.bias[i], g.res[i], g.y[i],
+                    (long long)(b - g.start[i]) * 256 + threadIdx.x);
 }
 
 // y += res after a kernel whose epilogue has no residual input: the same two
@@ -713,6 +730,95 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
 
 // The conv as an implicit GEMM over raw OIHW weights: W[M/g][C/g*kh*kw] x
 // (X dense for 1x1 s1 p0, else gathered), per image and group.
+// The convs of a group in one launch when they share a kernel family the
+// grouped kernels cover (LDS-patch 3x3 tiles of one stride, the pointwise
+// LDS tiles, depthwise), else one launch each.  The LDS-patch tile is the one
+// the cost model rates best for the group's slowest conv; every tile gives
+// the same bits.
+static osh_status conv2d_group(int count, const osh_conv_params *ps, const float *const *xs, const void *const *ws,
+                               const float *const *bs, int act, const float *const *rs, float *const *ys,
+                               hipStream_t st) {
+    const ConvAlgo a0 = select_algo(&ps[0]);
+    bool one = count > 1 && (a0 == ALGO_CONV16 || a0 == ALGO_PW16 || a0 == ALGO_DEPTHWISE);
+    bool vec = true;
+    for (int i = 0; i < count && one; i++) {
+        const osh_conv_params &p = ps[i];
+        one = select_algo(&p) == a0 && p.sh == ps[0].sh;
+        if (a0 == ALGO_CONV16) one = one && conv16s_eligible(&p);
+        if (a0 == ALGO_PW16) vec = vec && p.w % 4 == 0 && (reinterpret_cast<uintptr_t>(xs[i]) & 15) == 0;
+    }
+    if (!one) {
+        for (int i = 0; i < count; i++) {
+            osh_status r = conv2d(&ps[i], xs[i], ws[i], bs ? bs[i] : nullptr, act, rs ? rs[i] : nullptr, ys[i], st);
+            if (r != OSH_OK) return r;
+        }
+        return OSH_OK;
+    }
+    ConvGroup g{};
+    g.count = count;
+    for (int i = 0; i < count; i++) {
+        g.p[i] = ps[i];
+        g.x[i] = xs[i];
+        g.w[i] = static_cast<const float *>(ws[i]);
+        g.bias[i] = bs ? bs[i] : nullptr;
+        g.res[i] = rs ? rs[i] : nullptr;
+        g.y[i] = ys[i];
+    }
+    if (a0 == ALGO_DEPTHWISE) {
+        long long total = 0;
+        for (int i = 0; i < count; i++) {
+            g.start[i] = (int)total;
+            total += ((long long)ps[i].n * ps[i].m * ps[i].oh * ps[i].ow + 255) / 256;
+            if (total > 0x7fffffffLL) return fail(OSH_E_UNSUPPORTED, "Conv group: grid too large");
+        }
+        g.start[count] = (int)total;
+        OSH_DISPATCH_ACT(act, ACT,
+                         hipLaunchKernelGGL(dw_conv_group_kernel<ACT>, dim3((unsigned)total), dim3(256), 0, st, g));
+        OSH_LAUNCH_CHECK("dw_conv_group_kernel");
+        return OSH_OK;
+    }
+    if (a0 == ALGO_PW16) {  // the pointwise LDS tiles read the LDS-tile part of the packed weights
+        bool narrow = false;
+        for (int i = 0; i < count; i++) narrow = narrow || ps[i].ow < 16;
+        if (narrow)
+            return vec ? conv16s_group_launch_t<1, 2, 4, 1, 1, PW16_CB, true>(g, act, st)
+                       : conv16s_group_launch_t<1, 2, 4, 1, 1, PW16_CB, false>(g, act, st);
+        return vec ? conv16s_group_launch_t<1, 1, 16, 1, 1, PW16_CB, true>(g, act, st)
+                   : conv16s_group_launch_t<1, 1, 16, 1, 1, PW16_CB, false>(g, act, st);
+    }
+    // The convs run side by side, so the slowest one bounds the launch: pick
+    // the tile with the smallest largest cost (then the smallest total).
+    const int cus = device_cus();
+    int best = 0;
+    double bmax = 0, bsum = 0;
+    for (int v = 0; v < kC16sCount; v++) {
+        double cmax = 0, csum = 0;
+        for (int i = 0; i < count; i++) {
+            const double c = conv16s_cost(&ps[i], kC16s[v], cus);
+            cmax = c > cmax ? c : cmax;
+            csum += c;
+        }
+        if (v == 0 || cmax < bmax || (cmax == bmax && csum < bsum)) best = v, bmax = cmax, bsum = csum;
+    }
+#define OSH_GROUP_TILE(TM, BV, TWL)                                                     \
+    return ps[0].sh == 1 ? conv16s_group_launch_t<TM, BV, TWL, 1, 3, 1, false>(g, act, st) \
+                         : conv16s_group_launch_t<TM, BV, TWL, 2, 3, 1, false>(g, act, st)
+    switch (best) {
+    case 0: OSH_GROUP_TILE(1, 1, 16);
+    case 1: OSH_GROUP_TILE(1, 2, 16);
+    case 2: OSH_GROUP_TILE(1, 4, 16);
+    case 3: OSH_GROUP_TILE(2, 2, 16);
+    case 4: OSH_GROUP_TILE(1, 1, 8);
+    case 5: OSH_GROUP_TILE(1, 2, 8);
+    case 6: OSH_GROUP_TILE(2, 2, 8);
+    case 7: OSH_GROUP_TILE(1, 2, 4);
+    case 8: OSH_GROUP_TILE(1, 4, 4);
+    case 9: OSH_GROUP_TILE(1, 4, 8);
+    default: OSH_GROUP_TILE(2, 4, 8);
+    }
+#undef OSH_GROUP_TILE
+}
+
 static osh_status igemm_conv(const osh_conv_params *p, const float *d_x, const float *w, const float *d_bias,
                              const float *d_res, int act, float *d_y, hipStream_t stream, int bmode) {
     const int cpg = p->c / p->group, opg = p->m / p->group;
@@ -769,6 +875,26 @@ OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, co
     osh_status st = check_launch(p, d_x, d_wpacked, act, d_y);
     if (st != OSH_OK) return st;
     return conv2d(p, d_x, d_wpacked, d_bias, act, nullptr, d_y, to_stream(s));
+}
+
+OSH_API osh_status osh_conv2d_group_f32(int count, const osh_conv_params *ps, const float *const *d_xs,
+                                        const void *const *d_ws, const float *const *d_biases, int act,
+                                        const float *const *d_res, float *const *d_ys, osh_stream s) {
+    if (count < 1 || count > kConvGroupMax) return fail(OSH_E_INVALID, "Conv group: %d convs (1..%d)", count,
+                                                        kConvGroupMax);
+    if (!ps || !d_xs || !d_ws || !d_ys) return fail(OSH_E_INVALID, "Conv group: NULL array");
+    for (int i = 0; i < count; i++) {
+        osh_status st = check_launch(&ps[i], d_xs[i], d_ws[i], act, d_ys[i]);
+        if (st != OSH_OK) return st;
+        const float *r = d_res ? d_res[i] : nullptr;
+        if (r) {
+            const uintptr_t bytes = (uintptr_t)ps[i].n * ps[i].m * ps[i].oh * ps[i].ow * sizeof(float);
+            const uintptr_t r0 = reinterpret_cast<uintptr_t>(r), y0 = reinterpret_cast<uintptr_t>(d_ys[i]);
+            if (r0 < y0 + bytes && y0 < r0 + bytes)
+                return fail(OSH_E_INVALID, "Conv group: a residual overlaps its output");
+        }
+    }
+    return conv2d_group(count, ps, d_xs, d_ws, d_biases, act, d_res, d_ys, to_stream(s));
 }
 
 OSH_API osh_status osh_conv2d_add_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,

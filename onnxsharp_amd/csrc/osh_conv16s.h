@@ -90,11 +90,13 @@ struct C16sGeom {
 // 1x1 stride-1 kernel on a map with W % 4 == 0 and a 16-byte aligned input).
 // XB: workgroups take their tiles XCD-banded (xcd_band), so that the tiles
 // one XCD runs are neighbours whose patches share halo lines in its L2.
-template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT, bool XB = false, bool I2C = false>
-__global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const float *__restrict__ x,
-                                                      const float *__restrict__ wpk, const float *__restrict__ bias,
-                                                      const float *__restrict__ res, float *__restrict__ y,
-                                                      int tiles_w) {
+// One workgroup's tile (bx: pixel tile, by: group of four 16*TM-channel
+// output blocks, bz: image) of the conv p.
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT, bool I2C>
+__device__ __forceinline__ void conv16s_tile(const osh_conv_params &p, const float *__restrict__ x,
+                                             const float *__restrict__ wpk, const float *__restrict__ bias,
+                                             const float *__restrict__ res, float *__restrict__ y, int tiles_w,
+                                             const int bx, const int by, const int bz) {
     using G = C16sGeom<TM, BV, TWL, S, KS, CB, VEC>;
     static_assert(16 % TWL == 0, "a lane group covers whole rows of the tile");
     static_assert(!VEC || (KS == 1 && S == 1 && G::PC % 4 == 0 && G::PITCH % 4 == 0 && G::PLANE % 4 == 0),
@@ -105,12 +107,6 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
-    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
-    if constexpr (XB) {
-        const int wg = xcd_band(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
-                                gridDim.x * gridDim.y * gridDim.z);
-        bx = wg % gridDim.x, by = (wg / gridDim.x) % gridDim.y, bz = wg / (gridDim.x * gridDim.y);
-    }
     const int ty = bx / tiles_w, tx = bx - ty * tiles_w;
     const int oy0 = ty * G::TH, ox0 = tx * TWL;
     const int n = bz;
@@ -337,6 +333,72 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
         for (int q = 0; q < BV; q++) store_block(q);
     }
     // (otherwise compute_last has stored every block of an active wave)
+}
+
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT, bool XB = false, bool I2C = false>
+__global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const float *__restrict__ x,
+                                                      const float *__restrict__ wpk, const float *__restrict__ bias,
+                                                      const float *__restrict__ res, float *__restrict__ y,
+                                                      int tiles_w) {
+    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+    if constexpr (XB) {
+        const int wg = xcd_band(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                                gridDim.x * gridDim.y * gridDim.z);
+        bx = wg % gridDim.x, by = (wg / gridDim.x) % gridDim.y, bz = wg / (gridDim.x * gridDim.y);
+    }
+    conv16s_tile<TM, BV, TWL, S, KS, CB, VEC, ACT, I2C>(p, x, wpk, bias, res, y, tiles_w, bx, by, bz);
+}
+
+// Several independent convs of one tile shape in one launch (e.g. a
+// detection head's three scales): workgroup b runs tile b - start[i] of conv
+// i, start[i] <= b < start[i + 1], with conv i's own sizes and pointers.
+// Every conv keeps its own chain, so the outputs are those of separate
+// launches with the same tile.
+constexpr int kConvGroupMax = 4;
+struct ConvGroup {
+    int count;
+    int start[kConvGroupMax + 1];
+    int tiles_w[kConvGroupMax], tiles[kConvGroupMax], mgroups[kConvGroupMax];
+    osh_conv_params p[kConvGroupMax];
+    const float *x[kConvGroupMax];
+    const float *w[kConvGroupMax];
+    const float *bias[kConvGroupMax];
+    const float *res[kConvGroupMax];
+    float *y[kConvGroupMax];
+};
+
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT>
+__global__ __launch_bounds__(256) void conv16s_group_kernel(ConvGroup g) {
+    const int b = blockIdx.x;
+    int i = 0;
+    while (i + 1 < g.count && b >= g.start[i + 1]) i++;
+    const int local = b - g.start[i];
+    const int bx = local % g.tiles[i], rest = local / g.tiles[i];
+    conv16s_tile<TM, BV, TWL, S, KS, CB, VEC, ACT, false>(g.p[i], g.x[i], g.w[i], g.bias[i], g.res[i], g.y[i],
+                                                          g.tiles_w[i], bx, rest % g.mgroups[i],
+                                                          rest / g.mgroups[i]);
+}
+
+// Fills the block table of g for tile <TM, BV, TWL> and launches it.
+template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC>
+inline osh_status conv16s_group_launch_t(ConvGroup g, int act, hipStream_t st) {
+    using G = C16sGeom<TM, BV, TWL, S, KS, CB, VEC>;
+    long long total = 0;
+    for (int i = 0; i < g.count; i++) {
+        const osh_conv_params &p = g.p[i];
+        g.tiles_w[i] = ceil_div(p.ow, TWL);
+        g.tiles[i] = g.tiles_w[i] * ceil_div(p.oh, G::TH);
+        g.mgroups[i] = ceil_div(ceil_div(p.m, 16), 4 * TM);
+        g.start[i] = (int)total;
+        total += (long long)g.tiles[i] * g.mgroups[i] * p.n;
+    }
+    if (total > 0x7fffffffLL) return fail(OSH_E_UNSUPPORTED, "Conv group: grid too large");
+    g.start[g.count] = (int)total;
+    OSH_DISPATCH_ACT(act, ACT,
+                     hipLaunchKernelGGL((conv16s_group_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT>),
+                                        dim3((unsigned)total), dim3(256), 0, st, g));
+    OSH_LAUNCH_CHECK("conv16s_group_kernel");
+    return OSH_OK;
 }
 
 struct C16sVariant {

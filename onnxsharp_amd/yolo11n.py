@@ -21,6 +21,7 @@ counter-based generator in `synth` with a fixed seed per layer.
 from __future__ import annotations
 
 import ctypes as C
+import re
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -88,6 +89,18 @@ class ConvOp:
     @property
     def flops(self):
         return 2.0 * self.y.c * (self.x.c // self.group) * self.k * self.k * self.y.h * self.y.w
+
+
+@dataclass(eq=False)
+class GroupConvOp:
+    """Independent convs run as one launch (osh_conv2d_group_f32): the same
+    layer of the detection head's three scales."""
+    name: str
+    ops: list
+
+    @property
+    def flops(self):
+        return sum(o.flops for o in self.ops)
 
 
 @dataclass(eq=False)
@@ -171,7 +184,13 @@ class Model:
 
     @property
     def convs(self):
-        return [o for o in self.ops if isinstance(o, ConvOp)]
+        out = []
+        for o in self.ops:
+            if isinstance(o, ConvOp):
+                out.append(o)
+            elif isinstance(o, GroupConvOp):
+                out.extend(o.ops)
+        return out
 
     @property
     def flops(self):
@@ -470,10 +489,33 @@ def fuse_pool_chains(model: Model) -> Model:
     return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
 
 
+def group_head_convs(model: Model) -> Model:
+    """The Detect head runs two conv chains per scale (box: cv2.i.*, class:
+    cv3.i.*), and the three scales' chains are independent of each other.  The
+    same layer of the three scales becomes one GroupConvOp, the groups in
+    layer order where the head's ops were (24 launches -> 8).  Results are
+    unchanged: each conv keeps its own chain."""
+    ops = list(model.ops)
+    idx = [i for i, o in enumerate(ops) if isinstance(o, ConvOp) and o.name.startswith("/model.23/cv")]
+    if not idx or idx != list(range(idx[0], idx[0] + len(idx))):
+        return model
+    layers = {}
+    for i in idx:
+        key = re.sub(r"cv([23])\.(\d)", r"cv\1.#", ops[i].name)
+        layers.setdefault(key, []).append(ops[i])
+    if any(len(v) != 3 or len({o.res is None for o in v}) != 1 or len({o.act for o in v}) != 1
+           for v in layers.values()):
+        return model
+    groups = [GroupConvOp(k, v) for k, v in layers.items()]
+    out = ops[:idx[0]] + groups + ops[idx[-1] + 1:]
+    return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
+
+
 def fuse_launches(model: Model) -> Model:
     """The launch-saving rewrites of the op list (residual Adds into their
-    convs, SPPF's pool chain into one op); results are unchanged."""
-    return fuse_pool_chains(fuse_residual_adds(model))
+    convs, SPPF's pool chain into one op, the head's three scales per layer
+    into one op); results are unchanged."""
+    return group_head_convs(fuse_pool_chains(fuse_residual_adds(model)))
 
 
 def _tiling(c, slices):
@@ -489,6 +531,9 @@ def _tiling(c, slices):
 
 def op_access(op):
     """(reads, writes) of an op as lists of channel slices."""
+    if isinstance(op, GroupConvOp):
+        acc = [op_access(o) for o in op.ops]
+        return [r for a in acc for r in a[0]], [w for a in acc for w in a[1]]
     if isinstance(op, AddOp):
         return [op.a, op.b], [op.y]
     if isinstance(op, ConvOp) and op.res is not None:
@@ -604,26 +649,19 @@ class Frame:
     def _prepare(self, op):
         import torch
         lib = N.lib()
+        if isinstance(op, GroupConvOp):
+            parts = [self._prepare_conv(o) for o in op.ops]
+            n = len(parts)
+            ps = (N.ConvParams * n)(*[pp for pp, _, _ in parts])
+            arr = lambda vals: (C.c_void_p * n)(*vals)
+            xs, ws = arr([o.x.ptr() for o in op.ops]), arr([pk.data_ptr() for _, pk, _ in parts])
+            bs, ys = arr([b.data_ptr() for _, _, b in parts]), arr([o.y.ptr() for o in op.ops])
+            rs = arr([o.res.ptr() if o.res is not None else None for o in op.ops])
+            self._keep += [ps, xs, ws, bs, ys, rs]
+            act = N.ACTIVATIONS[op.ops[0].act]
+            return lambda st: N.check(lib.osh_conv2d_group_f32(n, ps, xs, ws, bs, act, rs, ys, st))
         if isinstance(op, ConvOp):
-            attrs = N.ConvAttrs()
-            attrs.group = op.group
-            attrs.n_kernel_shape, attrs.kernel_shape[0], attrs.kernel_shape[1] = 2, op.k, op.k
-            attrs.n_strides, attrs.strides[0], attrs.strides[1] = 2, op.s, op.s
-            attrs.n_pads = 4
-            for i in range(4):
-                attrs.pads[i] = op.k // 2
-            p = N.ConvParams()
-            N.call("osh_conv_resolve", C.byref(attrs), N.dims64(op.x.shape), N.dims64(op.w.shape), C.byref(p))
-            assert (p.m, p.oh, p.ow) == (op.y.c, op.y.h, op.y.w), op.name
-            nbytes = C.c_size_t()
-            N.call("osh_conv_packed_weight_bytes", C.byref(p), C.byref(nbytes))
-            w = torch.from_numpy(np.ascontiguousarray(op.w)).to(self.device)
-            b = torch.from_numpy(np.ascontiguousarray(op.b)).to(self.device)
-            packed = torch.empty(max(1, nbytes.value // 4), dtype=torch.float32, device=self.device)
-            torch.cuda.synchronize()  # the uploads ran on torch's stream; packing runs on the frame's
-            N.call("osh_conv_pack_weights", C.byref(p), C.c_void_p(w.data_ptr()), C.c_void_p(packed.data_ptr()),
-                   self.stream)
-            self._keep += [p, w, b, packed]
+            p, packed, b = self._prepare_conv(op)
             act = N.ACTIVATIONS[op.act]
             if op.res is not None:
                 return lambda st: N.check(lib.osh_conv2d_add_f32(C.byref(p), op.x.ptr(), C.c_void_p(packed.data_ptr()),
@@ -631,6 +669,34 @@ class Frame:
                                                                  op.y.ptr(), st))
             return lambda st: N.check(lib.osh_conv2d_f32(C.byref(p), op.x.ptr(), C.c_void_p(packed.data_ptr()),
                                                          C.c_void_p(b.data_ptr()), act, op.y.ptr(), st))
+        return self._prepare_other(op)
+
+    def _prepare_conv(self, op):
+        """Resolved params, packed weights and bias of a conv (packed once)."""
+        import torch
+        attrs = N.ConvAttrs()
+        attrs.group = op.group
+        attrs.n_kernel_shape, attrs.kernel_shape[0], attrs.kernel_shape[1] = 2, op.k, op.k
+        attrs.n_strides, attrs.strides[0], attrs.strides[1] = 2, op.s, op.s
+        attrs.n_pads = 4
+        for i in range(4):
+            attrs.pads[i] = op.k // 2
+        p = N.ConvParams()
+        N.call("osh_conv_resolve", C.byref(attrs), N.dims64(op.x.shape), N.dims64(op.w.shape), C.byref(p))
+        assert (p.m, p.oh, p.ow) == (op.y.c, op.y.h, op.y.w), op.name
+        nbytes = C.c_size_t()
+        N.call("osh_conv_packed_weight_bytes", C.byref(p), C.byref(nbytes))
+        w = torch.from_numpy(np.ascontiguousarray(op.w)).to(self.device)
+        b = torch.from_numpy(np.ascontiguousarray(op.b)).to(self.device)
+        packed = torch.empty(max(1, nbytes.value // 4), dtype=torch.float32, device=self.device)
+        torch.cuda.synchronize()  # the uploads ran on torch's stream; packing runs on the frame's
+        N.call("osh_conv_pack_weights", C.byref(p), C.c_void_p(w.data_ptr()), C.c_void_p(packed.data_ptr()),
+               self.stream)
+        self._keep += [p, w, b, packed]
+        return p, packed, b
+
+    def _prepare_other(self, op):
+        lib = N.lib()
         if isinstance(op, AddOp):
             n = op.y.c * op.y.h * op.y.w
             return lambda st: N.check(lib.osh_add_f32(n, op.a.ptr(), op.b.ptr(), op.y.ptr(), st))

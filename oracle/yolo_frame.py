@@ -96,7 +96,9 @@ class Frame:
     def run(self, oracle, x):
         from onnxsharp_amd import yolo11n as Y
         self.put(Y.whole(self.model.input), x)
-        for op in self.model.ops:
-            ins = [np.ascontiguousarray(self.get(s)) for s in op_inputs(op)]
-            self.put(op.y, run_op(oracle, op, ins))
+        for grouped in self.model.ops:
+            # a GroupConvOp's convs are independent: run them one by one
+            for op in getattr(grouped, "ops", [grouped]) if isinstance(grouped, Y.GroupConvOp) else [grouped]:
+                ins = [np.ascontiguousarray(self.get(s)) for s in op_inputs(op)]
+                self.put(op.y, run_op(oracle, op, ins))
         return [self.arrays[id(b)] for b in self.model.outputs]

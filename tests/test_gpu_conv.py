@@ -440,3 +440,52 @@ def test_launch_refuses_weights_packed_for_another_kernel(cuda):
         N.call("osh_config_set", b"winograd", 1)
     y = layer.forward(x, w)  # the original choice again
     assert y.shape == (1, 64, 20, 20)
+
+
+GROUP_CASES = [
+    # (name, [(x shape, w shape, group)], act, residual) -- the head's layer kinds
+    ("head_3x3_nchwc", [((1, 64, 80, 80), (64, 64, 3, 3), 1), ((1, 128, 40, 40), (64, 128, 3, 3), 1),
+                        ((1, 256, 20, 20), (64, 256, 3, 3), 1)], "Silu", False),
+    ("head_depthwise", [((1, 64, 80, 80), (64, 1, 3, 3), 64), ((1, 128, 40, 40), (128, 1, 3, 3), 128),
+                        ((1, 256, 20, 20), (256, 1, 3, 3), 256)], "Silu", False),
+    ("head_pointwise_res", [((1, 64, 80, 80), (80, 64, 1, 1), 1), ((1, 80, 40, 40), (80, 80, 1, 1), 1),
+                            ((1, 80, 20, 20), (80, 80, 1, 1), 1), ((1, 48, 9, 6), (32, 48, 1, 1), 1)], None, True),
+    ("mixed_fallback", [((1, 64, 20, 20), (64, 64, 3, 3), 1), ((1, 32, 20, 20), (32, 1, 3, 3), 32)], "Relu", True),
+]
+
+
+@pytest.mark.parametrize("name,convs,act,residual", GROUP_CASES, ids=[c[0] for c in GROUP_CASES])
+def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
+    # osh_conv2d_group_f32 runs independent convs as one launch (or one per
+    # conv when they do not share a kernel family): the outputs are those of
+    # separate launches, bit for bit.
+    import torch
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    print(f"conv group {name}", flush=True)
+    n = len(convs)
+    layers, xs, ws, bs, rs, ys, ref, ps, packs = [], [], [], [], [], [], [], [], []
+    for k, (xsh, wsh, g) in enumerate(convs):
+        seed = 23 * k + sum(xsh) + sum(wsh)
+        x = _t(synth.uniform(seed, xsh), cuda)
+        w = _t(synth.normal(seed + 1, wsh, 0, 0.05), cuda)
+        b = _t(synth.normal(seed + 2, (wsh[0],), 0, 0.01), cuda)
+        layer = ConvLayer(fused_activation=act, group=g, pads=[1, 1, 1, 1] if wsh[2] == 3 else [0, 0, 0, 0])
+        y0 = layer.forward(x, w, b)
+        r = torch.from_numpy(synth.normal(seed + 3, tuple(y0.shape), 0, 1)).to(cuda) if residual else None
+        if r is not None:
+            y0 = layer.forward(x, w, b, residual=r)
+        torch.cuda.synchronize()
+        ref.append(y0.cpu().numpy())
+        _, p, buf = layer._packed
+        layers.append(layer); xs.append(x); ws.append(buf); bs.append(b); rs.append(r); ps.append(p)
+        ys.append(torch.full(tuple(y0.shape), float("nan"), device=cuda))
+    arr = lambda ts: (C.c_void_p * n)(*[None if t is None else t.data_ptr() for t in ts])
+    pa = (N.ConvParams * n)(*ps)
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    N.check(N.lib().osh_conv2d_group_f32(n, pa, arr(xs), arr(ws), arr(bs), N.ACTIVATIONS[act], arr(rs),
+                                         arr(ys), st))
+    torch.cuda.synchronize()
+    for k in range(n):
+        got = ys[k].cpu().numpy()
+        assert np.array_equal(got, ref[k]), f"conv {k}: max |d| {np.nanmax(np.abs(got - ref[k])):.3e}"

@@ -51,16 +51,19 @@ def test_yolo_per_op_parity(cuda, oracle, exact_silu):
         fr.set_input(synth.uniform(4242, (1, 3, 128, 128)))
         worst = (0.0, "")
         assert len(fr.model.ops) < len(model.ops)  # the residual Adds run inside their convs
-        for i, op in enumerate(fr.model.ops):
-            ins = [_host(s) for s in YO.op_inputs(op)]
+        for i, launch in enumerate(fr.model.ops):
+            # a GroupConvOp is one launch of independent convs: check each
+            members = launch.ops if isinstance(launch, Y.GroupConvOp) else [launch]
+            ins = [[_host(s) for s in YO.op_inputs(op)] for op in members]
             fr._calls[i](fr.stream)
             fr.sync()
-            got = _host(op.y)
-            ref = YO.run_op(oracle, op, ins)
-            what = f"op {i} {type(op).__name__} {op.name}"
-            nbad, dmax = fp32_violations(got, ref)
-            assert_fp32_close(got, ref, what)
-            assert np.array_equal(got, ref), f"{what}: not bit-identical (max |d| {dmax:.3e})"
+            for op, oin in zip(members, ins):
+                got = _host(op.y)
+                ref = YO.run_op(oracle, op, oin)
+                what = f"op {i} {type(op).__name__} {op.name}"
+                nbad, dmax = fp32_violations(got, ref)
+                assert_fp32_close(got, ref, what)
+                assert np.array_equal(got, ref), f"{what}: not bit-identical (max |d| {dmax:.3e})"
         print(f"{len(fr.model.ops)} ops bit-identical", flush=True)
     finally:
         fr.close()

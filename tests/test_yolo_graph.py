@@ -113,7 +113,7 @@ def test_residual_fusion_keeps_a_shared_conv_output():
 
 def test_sppf_pools_become_one_chain(model):
     from onnxsharp_amd import yolo11n as Y
-    f = Y.fuse_launches(model)
+    f = Y.fuse_pool_chains(Y.fuse_residual_adds(model))
     chains = [op for op in f.ops if isinstance(op, Y.PoolChainOp)]
     assert len(chains) == 1 and not any(isinstance(op, Y.MaxPoolOp) for op in f.ops)
     ch = chains[0]
@@ -195,3 +195,26 @@ def test_decode_appends_dfl_and_sigmoid_per_scale():
         assert (d.x.c0, d.x.c, d.y.c0, d.y.c) == (0, 64, 0, 4)
         assert (s_.x.c0, s_.x.c, s_.y.c0, s_.y.c) == (64, 80, 4, 80)
         assert d.y.buf is s_.y.buf
+
+
+def test_head_convs_group_by_layer(model):
+    # The Detect head's 24 convs become 8 groups (one per layer, the three
+    # scales in order), placed where the head was, and the frame drops from
+    # 92 launches to 76.
+    from onnxsharp_amd import yolo11n as Y
+    fused = Y.fuse_launches(model)
+    groups = [o for o in fused.ops if isinstance(o, Y.GroupConvOp)]
+    assert len(groups) == 8 and len(fused.ops) == 76
+    for g in groups:
+        assert [o.name for o in g.ops] == [g.name.replace("#", str(i)) for i in range(3)]
+        assert len({(o.k, o.s, o.group > 1, o.act) for o in g.ops}) == 1
+    assert len(fused.convs) == len(model.convs)
+    head = lambda m: sorted(o.name for o in m.convs if o.name.startswith("/model.23/"))
+    assert head(fused) == head(model)
+    # every op still reads only slices written before it (or the input)
+    written = {id(model.input)}
+    for op in fused.ops:
+        reads, writes = Y.op_access(op)
+        for r in reads:
+            assert id(r.buf) in written, (op.name, r.buf.name)
+        written.update(id(w.buf) for w in writes)
