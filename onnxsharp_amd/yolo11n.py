@@ -511,11 +511,56 @@ def group_head_convs(model: Model) -> Model:
     return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
 
 
+def _conv_kind(op):
+    dw = op.group > 1 and op.group == op.x.c == op.y.c
+    return (op.k, op.s, dw, op.group if not dw else 0, op.act, op.res is None)
+
+
+def _independent(a, b) -> bool:
+    """Whether op b neither reads what a writes nor writes what a reads or writes."""
+    ra, wa = op_access(a)
+    rb, wb = op_access(b)
+    return not any(_overlap(x, y) for x in rb for y in wa) and not any(
+        _overlap(x, y) for x in wb for y in ra + wa)
+
+
+def group_independent_convs(model: Model, window: int = 12) -> Model:
+    """A conv and up to three later convs of the same kind (kernel, stride,
+    depthwise or not, activation, residual or not) that depend on nothing
+    between them, and nothing between them on them, run as one GroupConvOp at
+    the first one's place -- e.g. a C3k block's two 1x1 convs of the same
+    input, or the C2PSA positional conv's two heads.  Results are unchanged."""
+    ops = list(model.ops)
+    out, taken = [], set()
+    for i, a in enumerate(ops):
+        if i in taken:
+            continue
+        if not isinstance(a, ConvOp):
+            out.append(a)
+            continue
+        members, between = [a], []
+        for j in range(i + 1, min(len(ops), i + 1 + window)):
+            if len(members) == 4:
+                break
+            b = ops[j]
+            if j in taken:
+                continue
+            if (isinstance(b, ConvOp) and _conv_kind(b) == _conv_kind(a)
+                    and all(_independent(m, b) and _independent(b, m) for m in members + between)):
+                members.append(b)
+                taken.add(j)
+            else:
+                between.append(b)
+        out.append(a if len(members) == 1 else GroupConvOp("&".join(m.name for m in members), members))
+    return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
+
+
 def fuse_launches(model: Model) -> Model:
     """The launch-saving rewrites of the op list (residual Adds into their
     convs, SPPF's pool chain into one op, the head's three scales per layer
-    into one op); results are unchanged."""
-    return group_head_convs(fuse_pool_chains(fuse_residual_adds(model)))
+    into one op, other independent convs of one kind into one op); results
+    are unchanged."""
+    return group_independent_convs(group_head_convs(fuse_pool_chains(fuse_residual_adds(model))))
 
 
 def _tiling(c, slices):

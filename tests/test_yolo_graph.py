@@ -199,13 +199,18 @@ def test_decode_appends_dfl_and_sigmoid_per_scale():
 
 def test_head_convs_group_by_layer(model):
     # The Detect head's 24 convs become 8 groups (one per layer, the three
-    # scales in order), placed where the head was, and the frame drops from
-    # 92 launches to 76.
+    # scales in order), placed where the head was; with the C3k blocks' paired
+    # 1x1 convs and the positional conv's two heads grouped too, the frame
+    # drops from 92 launches to 72.
     from onnxsharp_amd import yolo11n as Y
     fused = Y.fuse_launches(model)
-    groups = [o for o in fused.ops if isinstance(o, Y.GroupConvOp)]
-    assert len(groups) == 8 and len(fused.ops) == 76
-    for g in groups:
+    head = [o for o in fused.ops if isinstance(o, Y.GroupConvOp) and o.name.startswith("/model.23/cv")]
+    other = [o for o in fused.ops if isinstance(o, Y.GroupConvOp) and o not in head]
+    assert len(head) == 8 and len(other) == 4 and len(fused.ops) == 72
+    for g in other:
+        assert len({Y._conv_kind(o) for o in g.ops}) == 1
+        assert all(Y._independent(a, b) for a in g.ops for b in g.ops if a is not b)
+    for g in head:
         assert [o.name for o in g.ops] == [g.name.replace("#", str(i)) for i in range(3)]
         assert len({(o.k, o.s, o.group > 1, o.act) for o in g.ops}) == 1
     assert len(fused.convs) == len(model.convs)
