@@ -294,10 +294,13 @@ OSH_API osh_status osh_gemm_ex_f32(int trans_a, int trans_b, int m, int n, int k
 OSH_API osh_status osh_dqmm_packed_weight_bytes(int k, int n, size_t *bytes);
 OSH_API osh_status osh_dqmm_scratch_bytes(int m, int k, size_t *bytes);
 
-/* One-time packing of W [k,n] (int8 when w_signed, else uint8) minus its zero
+/* One-time packing of W [k,n] (int8 when w_signed, else uint8) and its zero
  * point(s) (n_wzp = 0: none, 1: per-tensor, n: per-column) into the
- * MFMA-ready layout, with per-column sums.  Fails with OSH_E_UNSUPPORTED if
- * (w - w_zp) leaves [-128, 127].  (Int8F32Gemm.WidenWeights + GemmKernel.Pack,
+ * MFMA-ready layout, with per-column sums and zero-point offsets.  A zero
+ * point has the weights' element type: OSH_E_INVALID outside [-128, 127]
+ * (int8) or [0, 255] (uint8).  OSH_E_UNSUPPORTED when k * 255 * 255 exceeds
+ * INT32_MAX (the int32 accumulator could overflow).
+ * (Int8F32Gemm.WidenWeights + GemmKernel.Pack,
  * src/OnnxSharp/Ops/QuantizedMatMulOps.cs:261-277.) */
 OSH_API osh_status osh_dqmm_pack_weights(int k, int n, const void *d_w, int w_signed, const int32_t *h_wzp,
                                          int n_wzp, void *d_packed, osh_stream s);

@@ -644,9 +644,14 @@ OSH_API osh_status osh_dqmm_pack_weights(int k, int n, const void *d_w, int w_si
     if (n_wzp > 0 && !h_wzp) return fail(OSH_E_INVALID, "DQM pack: w_zero_point is NULL");
     if ((long long)k * 255 * 255 > 2147483647LL)
         return fail(OSH_E_UNSUPPORTED, "DQM: K=%d can overflow the int32 accumulator", k);
+    // a zero point has the weights' element type (ONNX MatMulInteger /
+    // DynamicQuantizeMatMul), so |w - w_zp| <= 255 and K * 255 * 255 bounds
+    // the accumulator (checked above)
+    const int zlo = w_signed ? -128 : 0, zhi = w_signed ? 127 : 255;
     for (int i = 0; i < n_wzp; i++)
-        if (h_wzp[i] < -32768 || h_wzp[i] > 32767)
-            return fail(OSH_E_UNSUPPORTED, "DQM pack: weight zero point %d out of range", h_wzp[i]);
+        if (h_wzp[i] < zlo || h_wzp[i] > zhi)
+            return fail(OSH_E_INVALID, "DQM pack: weight zero point %d outside the %s range [%d, %d]", h_wzp[i],
+                        w_signed ? "int8" : "uint8", zlo, zhi);
     hipStream_t st = to_stream(s);
     int *d_zp = nullptr;
     if (n_wzp > 0) {
@@ -713,7 +718,9 @@ OSH_API osh_status osh_matmul_integer(int m, int k, int n, const void *d_a, int 
     if (m < 0 || k <= 0 || n <= 0) return fail(OSH_E_INVALID, "MatMulInteger: bad size m=%d k=%d n=%d", m, k, n);
     if (m == 0) return OSH_OK;
     if (!d_a || !d_wpacked || !d_c || !d_scratch) return fail(OSH_E_INVALID, "MatMulInteger: NULL pointer");
-    if (a_zp < -32768 || a_zp > 32767) return fail(OSH_E_UNSUPPORTED, "MatMulInteger: a_zero_point %d", a_zp);
+    if (a_zp < (a_signed ? -128 : 0) || a_zp > (a_signed ? 127 : 255))
+        return fail(OSH_E_INVALID, "MatMulInteger: a_zero_point %d outside the %s range", a_zp,
+                    a_signed ? "int8" : "uint8");
     if ((long long)k * 255 * 255 > 2147483647LL)
         return fail(OSH_E_UNSUPPORTED, "MatMulInteger: K=%d can overflow the int32 accumulator", k);
     if (pad32(m) / 32 > 2 * 65535) return fail(OSH_E_UNSUPPORTED, "MatMulInteger: m too large");

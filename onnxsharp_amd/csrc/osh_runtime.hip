@@ -274,7 +274,14 @@ OSH_API osh_status osh_malloc(void **d_ptr, size_t bytes) {
     *d_ptr = nullptr;
     if (bytes == 0) return OSH_OK;
     hipError_t e = hipMalloc(d_ptr, bytes);
-    if (e != hipSuccess) return fail(OSH_E_NOMEM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    if (e != hipSuccess) {
+        // a failed allocation is reported here and nowhere else: clear the
+        // runtime's sticky last error so the caller's next HIP call does not
+        // see it again
+        (void)hipGetLastError();
+        *d_ptr = nullptr;
+        return fail(OSH_E_NOMEM, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    }
     return OSH_OK;
 }
 
@@ -289,7 +296,11 @@ OSH_API osh_status osh_host_alloc(void **h_ptr, size_t bytes) {
     *h_ptr = nullptr;
     if (bytes == 0) return OSH_OK;
     hipError_t e = hipHostMalloc(h_ptr, bytes, hipHostMallocDefault);
-    if (e != hipSuccess) return fail(OSH_E_NOMEM, "hipHostMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *h_ptr = nullptr;
+        return fail(OSH_E_NOMEM, "hipHostMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+    }
     return OSH_OK;
 }
 

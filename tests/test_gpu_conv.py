@@ -489,3 +489,25 @@ def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
     for k in range(n):
         got = ys[k].cpu().numpy()
         assert np.array_equal(got, ref[k]), f"conv {k}: max |d| {np.nanmax(np.abs(got - ref[k])):.3e}"
+
+
+@pytest.mark.parametrize("case", [0, 1, 2])
+@pytest.mark.parametrize("m,chain", [(32, "nchwc"), (16, "im2col"), (64, "nchwc")])
+def test_device_chain_order_pinned_by_planted_magnitudes(cuda, oracle, case, m, chain):
+    """The planted-magnitude inputs of the oracle's order tests (tests/test_oracle.py)
+    through the device dispatch: 32 input channels on a 3x3 map with pad 1, so
+    the centre output pixel sees every planted tap.  M % 32 == 0 passes the
+    reference's NCHWc gate (NchwcConv.cs:100-126) and must give the NCHWc
+    chain's hand-derived value; M = 16 fails it and must give the im2col
+    chain's (ConvKernels.cs:554-563).  Every output channel carries the same
+    planted weights; every output pixel equals the oracle's bit for bit."""
+    from test_oracle import PLANTED, _planted
+    terms, want = PLANTED[case]
+    x, w1 = _planted(terms)
+    w = np.repeat(w1, m, axis=0)
+    b = np.zeros(m, np.float32)
+    print(f"planted case {case}, m={m}: expect the {chain} chain", flush=True)
+    y, p = run_conv(cuda, x, w, b, None, pads=[1, 1, 1, 1])
+    assert (y[0, :, 1, 1] == np.float32(want[chain])).all(), y[0, :, 1, 1]
+    ref = oracle_conv(oracle, x, w, b, p, None)
+    assert np.array_equal(y, ref)

@@ -149,3 +149,44 @@ def test_dqmm_fused_and_three_launch_pipelines_identical(cuda, oracle, m, k, n):
     q = oracle.quantize_u8(a[good], es, ez)
     assert np.array_equal(a0[good], (q.astype(np.int64) - ez) @ w.astype(np.int64))
     assert np.array_equal(o0[good], eo[good])
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 512, 2048), (33, 100, 70)])
+def test_fused_dqmm_equals_the_node_chain_it_replaces(cuda, oracle, m, k, n):
+    """GraphFusion.FuseQuantizedMatMul (src/OnnxSharp/Core/GraphFusion.cs:635-782)
+    replaces DynamicQuantizeLinear -> MatMulInteger -> Cast -> Mul(a_scale *
+    w_scale) -> Add(bias) by one DynamicQuantizeMatMul [A, W, w_zp, w_scale,
+    bias] (:739-744).  On the device the unfused chain (osh_dynamic_quantize_linear,
+    osh_matmul_integer, then the Cast/Mul/Add node outputs) must give the
+    fused op's int32 accumulators bit for bit, and outputs within the one
+    rounding the fused fmaf(acc, s, b) saves over round(round(acc*s) + b)."""
+    import torch
+    from onnxsharp_amd.layers import DynamicQuantizeLinearLayer, MatMulIntegerLayer
+    print(f"DQL -> MatMulInteger -> Cast -> Mul -> Add vs DQM, m={m} k={k} n={n}", flush=True)
+    a = synth.normal(300 + m, (m, k))
+    w = synth.randint(301 + n, (k, n), -127, 127, np.int8)
+    ws = synth.uniform(302 + k, (n,), 0.001, 0.02)
+    bias = synth.normal(303, (n,), 0, 0.01)
+    # the node chain
+    q, a_scale, a_zp = DynamicQuantizeLinearLayer().forward(_t(a, cuda))
+    acc_chain = MatMulIntegerLayer().forward(q, _t(w, cuda), [a_zp], None)
+    comb = torch.tensor([a_scale], dtype=torch.float32, device=cuda) * _t(ws, cuda)  # Mul(a_scale, w_scale)
+    cast = acc_chain.to(torch.float32)                                              # Cast(int32 -> f32)
+    mul = cast * comb                                                               # Mul
+    out_chain = (mul + _t(bias, cuda)).cpu().numpy()                                # Add(bias)
+    # the fused op
+    out, acc, s, z = run_dqmm(cuda, a, w, None, ws, bias)
+    assert (s, z) == (np.float32(a_scale), a_zp)
+    assert np.array_equal(acc, acc_chain.cpu().numpy()), "int32 accumulators"
+    # the fused epilogue differs from the chain by at most the rounding of acc*s
+    comb_h = (np.float32(a_scale) * ws).astype(np.float32)
+    prod = acc.astype(np.float32) * comb_h
+    # |fused - chain| <= ulp(fused)/2 + ulp(acc*s)/2 + ulp(chain)/2
+    bound = 0.5 * (np.abs(np.spacing(out)) + np.abs(np.spacing(prod)) + np.abs(np.spacing(out_chain)))
+    d = np.abs(out.astype(np.float64) - out_chain)
+    assert (d <= bound).all(), f"max |d| {d.max():.3e}"
+    # the chain's own nodes on the host: the oracle's unfused form, bit for bit
+    eo_unfused = (acc.astype(np.float32) * comb_h).astype(np.float32) + bias
+    assert np.array_equal(out_chain, eo_unfused.astype(np.float32))
+    eo, eacc, _, _, _ = oracle.dqmm(a, w, None, ws, bias)
+    assert np.array_equal(out, eo) and np.array_equal(acc, eacc)

@@ -437,3 +437,159 @@ def test_sigmoid_against_float64(oracle):
     ref = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
     assert np.abs(y - ref).max() <= 2e-7
     assert oracle.sigmoid_ref(np.zeros(3, np.float32))[0] == 0.5
+
+
+# ----------------------------------------------------------- summation order, pinned by planted magnitudes
+#
+# A 3x3 conv over a 32-channel 3x3 map (one output pixel, no padding).  Each
+# product term is planted: +2^24 first, -2^24 at a chosen tap, and small powers
+# of two elsewhere.  In float32 a term below 1 added to an accumulator of
+# magnitude 2^24 is lost (the spacing there is 2), and an accumulator of small
+# terms added to 2^24 is lost too, so the output is exactly the sum of the
+# small terms that the chain adds AFTER the -2^24 term.  Which taps those are
+# depends only on the order of the chain, so each order gives a different,
+# hand-derived result.  Orders, as (ic, ky, kx) visiting sequences:
+#   NCHWc  (NchwcConv.Row, src/OnnxSharp/Kernels/NchwcConv.cs:555-605):
+#          channel block ib -> ky -> kx -> lane (ic = 16 ib + lane)
+#   im2col (ConvKernels.cs:554-563; PackedConv.cs:420-440): ic -> ky -> kx
+# and two plausible mistakes that must NOT reproduce the NCHWc result:
+#   lane before kx (ib -> ky -> lane -> kx) and kx before ky (ib -> kx -> ky -> lane).
+
+BIG = np.float32(2.0 ** 24)
+
+
+def _order(kind, cin=32):
+    if kind == "nchwc":
+        return [(16 * ib + l, ky, kx) for ib in range(cin // 16) for ky in range(3) for kx in range(3) for l in range(16)]
+    if kind == "im2col":
+        return [(ic, ky, kx) for ic in range(cin) for ky in range(3) for kx in range(3)]
+    if kind == "lane_before_kx":
+        return [(16 * ib + l, ky, kx) for ib in range(cin // 16) for ky in range(3) for l in range(16) for kx in range(3)]
+    if kind == "kx_before_ky":
+        return [(16 * ib + l, ky, kx) for ib in range(cin // 16) for kx in range(3) for ky in range(3) for l in range(16)]
+    raise ValueError(kind)
+
+
+def _fma32(a, b, c):
+    """float32 fmaf(a, b, c) with one rounding: the exact value is formed in
+    rationals, checked to be exact in float64, then rounded once to float32."""
+    from fractions import Fraction
+    exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    d = float(exact)
+    assert Fraction(d) == exact, "planted values must keep the exact sum inside float64"
+    return np.float32(d)
+
+
+def _planted(terms, cin=32):
+    """x = 1 at every planted tap, w = the term: each product is exactly the term."""
+    x = np.zeros((1, cin, 3, 3), np.float32)
+    w = np.zeros((1, cin, 3, 3), np.float32)
+    for (ic, ky, kx), v in terms.items():
+        x[0, ic, ky, kx] = 1.0
+        w[0, ic, ky, kx] = v
+    return x, w
+
+
+def _chain(kind, x, w, bias):
+    acc = np.float32(bias)
+    for ic, ky, kx in _order(kind, x.shape[1]):
+        acc = _fma32(x[0, ic, ky, kx], w[0, ic, ky, kx], acc)
+    return acc
+
+
+# (planted terms, hand-derived output per order)
+PLANTED = [
+    # -2^24 at (ic 1, ky 0, kx 0): NCHWc visits it 2nd (ib 0, tap 0, lane 1), im2col 10th.
+    # 0.5 at (0, 0, 1) comes after it in NCHWc (tap 1) but before it in im2col and
+    # with lane before kx; 0.25 at (2, 0, 0) and 0.125 at (17, 0, 0) come after in all.
+    ({(0, 0, 0): BIG, (1, 0, 0): -BIG, (0, 0, 1): 0.5, (2, 0, 0): 0.25, (17, 0, 0): 0.125},
+     {"nchwc": 0.875, "im2col": 0.375, "lane_before_kx": 0.375, "kx_before_ky": 0.875}),
+    # -2^24 at (0, 1, 0): NCHWc tap 3, with kx before ky tap 1.  0.5 at (5, 0, 2) is
+    # NCHWc tap 2 (before: lost) but tap 6 with kx before ky (after); im2col
+    # visits ic 5 after ic 0 (kept); lane before kx visits it in row ky 0 (lost).
+    # 0.25 in the second channel block is kept by every order.
+    ({(0, 0, 0): BIG, (0, 1, 0): -BIG, (5, 0, 2): 0.5, (20, 0, 0): 0.25},
+     {"nchwc": 0.25, "im2col": 0.75, "lane_before_kx": 0.25, "kx_before_ky": 0.75}),
+    # the two channel blocks: -2^24 at (16, 2, 2) is the last NCHWc term but one
+    # (lane 0 of the last tap of block 1); only 0.5 at (31, 2, 2) follows it.
+    # im2col reaches (16, 2, 2) at index 152, after which ic 17..31 follow.
+    ({(0, 0, 0): BIG, (16, 2, 2): -BIG, (31, 2, 2): 0.5, (20, 0, 0): 0.25, (15, 2, 2): 0.125},
+     {"nchwc": 0.5, "im2col": 0.75, "lane_before_kx": 0.5, "kx_before_ky": 0.5}),
+]
+
+
+@pytest.mark.parametrize("case", range(len(PLANTED)))
+def test_conv_chain_order_pinned_by_planted_magnitudes(oracle, case):
+    terms, want = PLANTED[case]
+    x, w = _planted(terms)
+    b = np.zeros(1, np.float32)
+    for kind, v in want.items():
+        assert _chain(kind, x, w, 0.0) == np.float32(v), kind  # the hand derivation
+    got_nchwc = oracle.conv2d_f32(x, w, b, (1, 1), (0, 0), (1, 1), 1, (1, 1), order=oracle.ORDER_NCHWC)
+    got_im2col = oracle.conv2d_f32(x, w, b, (1, 1), (0, 0), (1, 1), 1, (1, 1), order=oracle.ORDER_IM2COL)
+    assert got_nchwc[0, 0, 0, 0] == np.float32(want["nchwc"])
+    assert got_im2col[0, 0, 0, 0] == np.float32(want["im2col"])
+    # the order is what the test sees: each case separates NCHWc from at least one wrong order
+    assert any(want[k] != want["nchwc"] for k in ("lane_before_kx", "kx_before_ky", "im2col"))
+
+
+def test_planted_cases_separate_every_wrong_order():
+    # over the three cases, each wrong order differs from NCHWc somewhere
+    for wrong in ("im2col", "lane_before_kx", "kx_before_ky"):
+        assert any(w[wrong] != w["nchwc"] for _, w in PLANTED), wrong
+
+
+def test_conv_chain_starts_at_the_bias(oracle):
+    # bias 2^24, then two terms of 1: bias-first loses each 1 (2^24 + 1 is a tie,
+    # rounded to the even 2^24), bias-last would give 2^24 + 2
+    x, w = _planted({(3, 1, 1): 1.0, (20, 2, 0): 1.0})
+    b = np.array([BIG], np.float32)
+    for order in (oracle.ORDER_NCHWC, oracle.ORDER_IM2COL):
+        y = oracle.conv2d_f32(x, w, b, (1, 1), (0, 0), (1, 1), 1, (1, 1), order=order)
+        assert y[0, 0, 0, 0] == BIG
+    assert _chain("nchwc", x, w, BIG) == BIG
+    assert np.float32(np.float32(2.0) + BIG) == BIG + 2
+
+
+def test_planted_mistake_in_the_order_is_caught(oracle):
+    # the same harness with the oracle's loop order changed (here: the
+    # im2col chain asked to stand in for the NCHWc one) fails case 0
+    terms, want = PLANTED[0]
+    x, w = _planted(terms)
+    wrong = oracle.conv2d_f32(x, w, np.zeros(1, np.float32), (1, 1), (0, 0), (1, 1), 1, (1, 1),
+                              order=oracle.ORDER_IM2COL)
+    assert wrong[0, 0, 0, 0] != np.float32(want["nchwc"])
+
+
+# ----------------------------------------------------------- C2PSA attention core
+
+def _attention_f64(qkv, heads, key_dim, head_dim, n, scale, swap_qk=False):
+    """float64 attention from the definition (ultralytics Attention.forward as
+    exported: attn = softmax(scale * q^T k) over keys, y = v attn^T); with
+    swap_qk the planted mistake k^T q."""
+    q3 = qkv.reshape(heads, 2 * key_dim + head_dim, n).astype(np.float64)
+    out = []
+    for h in range(heads):
+        q, k, v = q3[h, :key_dim], q3[h, key_dim:2 * key_dim], q3[h, 2 * key_dim:]
+        s = (k.T @ q if swap_qk else q.T @ k) * scale
+        e = np.exp(s - s.max(axis=1, keepdims=True))
+        p = e / e.sum(axis=1, keepdims=True)
+        out.append(v @ p.T)
+    return np.concatenate(out, axis=0)
+
+
+def test_attention_matches_float64_and_catches_a_qk_swap(oracle):
+    from types import SimpleNamespace as NS
+    from oracle import yolo_frame
+    heads, key_dim, head_dim, hw = 2, 32, 64, (8, 10)
+    n = hw[0] * hw[1]
+    qkv = synth.normal(51, (1, heads * (2 * key_dim + head_dim), *hw), 0, 1.0)
+    op = NS(qkv=NS(h=hw[0], w=hw[1]), heads=heads, key_dim=key_dim, head_dim=head_dim,
+            scale=key_dim ** -0.5, y=NS(c=heads * head_dim, h=hw[0], w=hw[1]))
+    got = yolo_frame.attention(oracle, op, qkv).reshape(heads * head_dim, n).astype(np.float64)
+    ref = _attention_f64(qkv, heads, key_dim, head_dim, n, op.scale)
+    d = np.abs(got - ref)
+    assert (d <= 1e-5 + 1e-4 * np.abs(ref)).all(), d.max()
+    # the planted mistake: q and k exchanged gives attn^T's softmax, far off
+    bad = _attention_f64(qkv, heads, key_dim, head_dim, n, op.scale, swap_qk=True)
+    assert np.abs(got - bad).max() > 1e-2
