@@ -174,3 +174,14 @@ def test_attention_shape_rules_match_the_frame_planner():
                 assert st == want, (kd, hd, n, N.last_error())
     st = lib.osh_attention_f32(1, 32, 64, 400, C.c_float(1.0), base, 128 * 400 - 1, C.c_void_p(1 << 41), None)
     assert st == N.OSH_E_INVALID and "stride" in N.last_error()
+
+
+@pytest.mark.parametrize("signed,zp", [(0, -1), (0, 256), (1, -129), (1, 128)])
+def test_dqmm_pack_refuses_zero_points_outside_the_weight_type(signed, zp):
+    # checked before any HIP call (this runs without a GPU)
+    import ctypes as C
+    from onnxsharp_amd import native as N
+    z = (C.c_int32 * 1)(zp)
+    fake = C.c_void_p(16)
+    assert N.lib().osh_dqmm_pack_weights(8, 8, fake, signed, z, 1, fake, None) == N.OSH_E_INVALID
+    assert "zero point" in N.last_error()

@@ -47,10 +47,11 @@ def test_matmul_integer_parity(cuda, oracle, m, k, n, adt, azp, bdt, bzp):
     lo, hi, dt = (0, 255, np.uint8) if bdt == "u8" else (-128, 127, np.int8)
     b = synth.randint(seed + 1, (k, n), lo, hi, dt)
     zps = None
+    base = 128 if bdt == "u8" else 0  # a zero point has the weights' element type
     if bzp == "scalar":
-        zps = [int(synth.randint(seed + 2, (1,), -20, 20, np.int32)[0])]
+        zps = [base + int(synth.randint(seed + 2, (1,), -20, 20, np.int32)[0])]
     elif bzp == "column":
-        zps = [int(v) for v in synth.randint(seed + 2, (n,), -20, 20, np.int32)]
+        zps = [base + int(v) for v in synth.randint(seed + 2, (n,), -20, 20, np.int32)]
     y = MatMulIntegerLayer().forward(_t(a, cuda), _t(b, cuda), [azp], zps).cpu().numpy()
     ref = oracle.matmul_integer(a, b, azp, None if zps is None else np.array(zps, np.int32))
     assert y.dtype == np.int32
