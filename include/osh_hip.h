@@ -317,6 +317,19 @@ OSH_API osh_status osh_dqmm_u8s8(int m, int k, int n, const float *d_a, const vo
                                  const float *d_wscale, int n_wscale, const float *d_bias, float *d_out,
                                  int32_t *d_acc, int32_t *d_qparams, void *d_scratch, osh_stream s);
 
+/* osh_dqmm_u8s8 for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): no
+ * counterpart in the reference.  Same arguments, results and kernels as
+ * osh_dqmm_u8s8, minus d_scratch: the scratch is a static 4 MiB array in the
+ * library, one per GPU, held until the process ends, so the call allocates
+ * nothing.  Sizes whose osh_dqmm_scratch_bytes(m, k) exceeds 4 MiB
+ * (e.g. m = k = 2048) fail with OSH_E_UNSUPPORTED.  Every call on one GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (on
+ * different streams or host threads) race and must not be issued. */
+OSH_API osh_status osh_dqmm_u8s8_noalloc(int m, int k, int n, const float *d_a, const void *d_wpacked,
+                                         const float *d_wscale, int n_wscale, const float *d_bias, float *d_out,
+                                         int32_t *d_acc, int32_t *d_qparams, osh_stream s);
+
 /* DynamicQuantizeLinear (src/OnnxSharp/Ops/QuantOps.cs:166-227) on the device:
  * q (u8, n values), scale and zero point into d_qparams {scale bits, zp}. */
 /* MatMulInteger (MatMulIntegerLayer, src/OnnxSharp/Ops/QuantOps.cs:235-428):

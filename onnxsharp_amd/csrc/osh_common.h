@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "osh_hip.h"
@@ -146,6 +147,9 @@ int pointwise_variant_count();
 // Drops the record of which kernel a packed conv weight buffer at d_ptr was
 // laid out for (osh_free calls it; the address may be reused).
 void forget_pack(const void *d_ptr);
+// Device address of the no-allocation DynamicQuantizeMatMul's static scratch
+// on device dev (osh_dqmm.hip), resolved once per device.
+osh_status noalloc_scratch_setup(int dev);
 
 // Forced LDS-patch tile for the 3x3 convolutions that run in the im2col
 // order (-1 = automatic) and the number of tiles.

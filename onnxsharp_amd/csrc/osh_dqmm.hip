@@ -620,6 +620,77 @@ static osh_status run_minmax(const float *a, long long count, DqScratch *sc, int
     return OSH_OK;
 }
 
+static osh_status dqmm_run(int m, int k, int n, const float *d_a, const void *d_wpacked, const float *d_wscale,
+                           int n_wscale, const float *d_bias, float *d_out, int32_t *d_acc, int32_t *d_qparams,
+                           void *d_scratch, hipStream_t st) {
+    DqScratch *sc = static_cast<DqScratch *>(d_scratch);
+    int *rowsum = reinterpret_cast<int *>(sc + 1);
+    int8_t *apk = reinterpret_cast<int8_t *>(rowsum + 2 * pad32(m));
+    int nparts = 0;
+    osh_status r = run_minmax(d_a, (long long)m * k, sc, &nparts, st);
+    if (r != OSH_OK) return r;
+    const int8_t *frag = static_cast<const int8_t *>(d_wpacked);
+    const int *colsum = reinterpret_cast<const int *>(frag + (size_t)pad32(n) * pad32(k));
+    const int *off = colsum + pad32(n);
+    const long long fblocks = (long long)((pad32(n) / 32 + DQF_WAVES - 1) / DQF_WAVES) * (pad32(m) / 32);
+    if (dqmm_variant() == 0 && fblocks <= 0x7fffffffLL) {
+        hipLaunchKernelGGL(dqmm_fused_kernel, dim3((unsigned)fblocks), dim3(256), 0, st, m, k, n, d_a, sc, nparts, (int *)d_qparams,
+                           frag, colsum, off, d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
+        OSH_LAUNCH_CHECK("dqmm_fused_kernel");
+        return OSH_OK;
+    }
+    const int rows_per_block = DQ_THREADS / 64;
+    hipLaunchKernelGGL(dqmm_quantize_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
+                       dim3(DQ_THREADS), 0, st, d_a, m, k, sc, nparts, (int *)d_qparams, rowsum, apk);
+    OSH_LAUNCH_CHECK("dqmm_quantize_kernel");
+    dim3 grid((pad32(n) / 32 + 1) / 2, (pad32(m) / 32 + 1) / 2);
+    hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
+                       d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
+    OSH_LAUNCH_CHECK("dqmm_gemm_kernel");
+    return OSH_OK;
+}
+
+static osh_status dqmm_check(int m, int k, int n, const float *d_a, const void *d_wpacked, const float *d_wscale,
+                             int n_wscale, float *d_out) {
+    if (m < 0 || k <= 0 || n <= 0) return fail(OSH_E_INVALID, "DQM: bad size m=%d k=%d n=%d", m, k, n);
+    if (m == 0) return OSH_OK;
+    if (!d_a || !d_wpacked || !d_wscale || !d_out) return fail(OSH_E_INVALID, "DQM: NULL pointer");
+    if (n_wscale != 1 && n_wscale != n) return fail(OSH_E_INVALID, "DQM: w_scale has %d entries", n_wscale);
+    if ((long long)k * 255 * 255 > 2147483647LL)
+        return fail(OSH_E_UNSUPPORTED, "DQM: K=%d can overflow the int32 accumulator", k);
+    if (pad32(m) / 32 > 2 * 65535) return fail(OSH_E_UNSUPPORTED, "DQM: m too large");
+    return OSH_OK;
+}
+
+// The no-allocation variant's scratch: one array per GPU, held until the
+// process ends.  `scratch` names the host-side stand-in; kernels take the
+// device address hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kNoAllocMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kNoAllocMaxDevices];
+
+// Resolves (once per device, with that device current) the device address of
+// `scratch`; osh_init calls it, and the entry point calls it on its first
+// call on a device that osh_init did not set up.
+osh_status noalloc_scratch_setup(int dev) {
+    if (dev < 0 || dev >= kNoAllocMaxDevices)
+        return fail(OSH_E_UNSUPPORTED, "DQM (no allocation): device %d beyond %d devices", dev, kNoAllocMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return OSH_OK;
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+        (void)hipGetLastError();
+        return fail(OSH_E_DEVICE, "DQM (no allocation): hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                    hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = ptr;
+    return OSH_OK;
+}
+
 }  // namespace osh
 
 extern "C" {
@@ -678,39 +749,37 @@ OSH_API osh_status osh_dqmm_pack_weights(int k, int n, const void *d_w, int w_si
 OSH_API osh_status osh_dqmm_u8s8(int m, int k, int n, const float *d_a, const void *d_wpacked,
                                  const float *d_wscale, int n_wscale, const float *d_bias, float *d_out,
                                  int32_t *d_acc, int32_t *d_qparams, void *d_scratch, osh_stream s) {
-    if (m < 0 || k <= 0 || n <= 0) return fail(OSH_E_INVALID, "DQM: bad size m=%d k=%d n=%d", m, k, n);
-    if (m == 0) return OSH_OK;
-    if (!d_a || !d_wpacked || !d_wscale || !d_out || !d_scratch) return fail(OSH_E_INVALID, "DQM: NULL pointer");
-    if (n_wscale != 1 && n_wscale != n) return fail(OSH_E_INVALID, "DQM: w_scale has %d entries", n_wscale);
-    if ((long long)k * 255 * 255 > 2147483647LL)
-        return fail(OSH_E_UNSUPPORTED, "DQM: K=%d can overflow the int32 accumulator", k);
-    if (pad32(m) / 32 > 2 * 65535) return fail(OSH_E_UNSUPPORTED, "DQM: m too large");
-    hipStream_t st = to_stream(s);
-    DqScratch *sc = static_cast<DqScratch *>(d_scratch);
-    int *rowsum = reinterpret_cast<int *>(sc + 1);
-    int8_t *apk = reinterpret_cast<int8_t *>(rowsum + 2 * pad32(m));
-    int nparts = 0;
-    osh_status r = run_minmax(d_a, (long long)m * k, sc, &nparts, st);
-    if (r != OSH_OK) return r;
-    const int8_t *frag = static_cast<const int8_t *>(d_wpacked);
-    const int *colsum = reinterpret_cast<const int *>(frag + (size_t)pad32(n) * pad32(k));
-    const int *off = colsum + pad32(n);
-    const long long fblocks = (long long)((pad32(n) / 32 + DQF_WAVES - 1) / DQF_WAVES) * (pad32(m) / 32);
-    if (dqmm_variant() == 0 && fblocks <= 0x7fffffffLL) {
-        hipLaunchKernelGGL(dqmm_fused_kernel, dim3((unsigned)fblocks), dim3(256), 0, st, m, k, n, d_a, sc, nparts, (int *)d_qparams,
-                           frag, colsum, off, d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
-        OSH_LAUNCH_CHECK("dqmm_fused_kernel");
-        return OSH_OK;
+    osh_status st = dqmm_check(m, k, n, d_a, d_wpacked, d_wscale, n_wscale, d_out);
+    if (st != OSH_OK || m == 0) return st;
+    if (!d_scratch) return fail(OSH_E_INVALID, "DQM: NULL pointer");
+    return dqmm_run(m, k, n, d_a, d_wpacked, d_wscale, n_wscale, d_bias, d_out, d_acc, d_qparams, d_scratch,
+                    to_stream(s));
+}
+
+OSH_API osh_status osh_dqmm_u8s8_noalloc(int m, int k, int n, const float *d_a, const void *d_wpacked,
+                                         const float *d_wscale, int n_wscale, const float *d_bias, float *d_out,
+                                         int32_t *d_acc, int32_t *d_qparams, osh_stream s) {
+    osh_status st = dqmm_check(m, k, n, d_a, d_wpacked, d_wscale, n_wscale, d_out);
+    if (st != OSH_OK || m == 0) return st;
+    if (scratch_bytes(m, k) > kNoAllocScratchBytes)
+        return fail(OSH_E_UNSUPPORTED,
+                    "DQM (no allocation): m=%d, k=%d need %zu scratch bytes; the static scratch holds %zu", m, k,
+                    scratch_bytes(m, k), kNoAllocScratchBytes);
+    int dev = 0;
+    OSH_HIP_CHECK(hipGetDevice(&dev));
+    void *ptr = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (dev >= 0 && dev < kNoAllocMaxDevices) ptr = g_scratch_ptr[dev];
     }
-    const int rows_per_block = DQ_THREADS / 64;
-    hipLaunchKernelGGL(dqmm_quantize_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
-                       dim3(DQ_THREADS), 0, st, d_a, m, k, sc, nparts, (int *)d_qparams, rowsum, apk);
-    OSH_LAUNCH_CHECK("dqmm_quantize_kernel");
-    dim3 grid((pad32(n) / 32 + 1) / 2, (pad32(m) / 32 + 1) / 2);
-    hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
-                       d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
-    OSH_LAUNCH_CHECK("dqmm_gemm_kernel");
-    return OSH_OK;
+    if (!ptr) {
+        st = noalloc_scratch_setup(dev);
+        if (st != OSH_OK) return st;
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        ptr = g_scratch_ptr[dev];
+    }
+    return dqmm_run(m, k, n, d_a, d_wpacked, d_wscale, n_wscale, d_bias, d_out, d_acc, d_qparams, ptr,
+                    to_stream(s));
 }
 
 OSH_API osh_status osh_matmul_integer(int m, int k, int n, const void *d_a, int a_signed, int a_zp,

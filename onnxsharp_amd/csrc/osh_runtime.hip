@@ -261,7 +261,7 @@ OSH_API osh_status osh_init(int dev, osh_device_info *info) {
             return fail(OSH_E_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only", dev,
                         info->arch);
     }
-    return OSH_OK;
+    return noalloc_scratch_setup(dev);
 }
 
 OSH_API osh_status osh_device_synchronize(void) {

@@ -100,6 +100,7 @@ _SIGS = {
     "osh_dqmm_scratch_bytes": ([_i, _i, C.POINTER(_sz)], _i),
     "osh_dqmm_pack_weights": ([_i, _i, _vp, _i, _vp, _i, _vp, _vp], _i),
     "osh_dqmm_u8s8": ([_i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+    "osh_dqmm_u8s8_noalloc": ([_i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp], _i),
     "osh_matmul_integer": ([_i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _vp], _i),
     "osh_dynamic_quantize_linear": ([_i64, _vp, _vp, _vp, _vp, _vp], _i),
     "osh_activation_f32": ([_i64, _vp, _i, _vp, _vp], _i),

@@ -176,6 +176,19 @@ def test_attention_shape_rules_match_the_frame_planner():
     assert st == N.OSH_E_INVALID and "stride" in N.last_error()
 
 
+def test_noalloc_dqmm_refuses_sizes_beyond_its_scratch_on_the_host():
+    # m = k = 2048 needs more than the 4 MiB static scratch of
+    # osh_dqmm_u8s8_noalloc: refused before any HIP call (this runs without a
+    # GPU), so no pointer is ever read
+    import ctypes as C
+    from onnxsharp_amd import native as N
+    fake = C.c_void_p(16)
+    st = N.lib().osh_dqmm_u8s8_noalloc(2048, 2048, 64, fake, fake, fake, 64, None, fake, None, None, None)
+    assert st == N.OSH_E_UNSUPPORTED
+    assert "scratch" in N.last_error()
+    assert N.lib().osh_dqmm_u8s8_noalloc(0, 512, 64, None, None, None, 64, None, None, None, None, None) == N.OSH_OK
+
+
 @pytest.mark.parametrize("signed,zp", [(0, -1), (0, 256), (1, -129), (1, 128)])
 def test_dqmm_pack_refuses_zero_points_outside_the_weight_type(signed, zp):
     # checked before any HIP call (this runs without a GPU)
