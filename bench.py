@@ -1,27 +1,34 @@
 """Benchmark of the dense-contraction hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all]
 
-A step is one launch of the hot path on resident synthetic inputs.  The
-default workload is the 3x3 stride-1 pad-1 Conv + bias + fused SiLU on
+A step is one pass of the hot path on resident synthetic inputs.  The default
+(--config all) times every workload in one process and prints ONE JSON line:
+the headline is the 3x3 stride-1 pad-1 Conv + bias + fused SiLU on
 X[1,64,160,160] U(0,1), W[64,64,3,3] N(0,0.05), b[64] N(0,0.01) (the shape the
-reference publishes a CPU number for).  Other workloads (--config):
+reference publishes a CPU number for); "configs" holds the others, each with
+its own step time, rate and roofline:
   c1   MatMul + Add(bias) fused: A[1024,768] x B[768,768] + bias[768], U(-1,1)
+  c2   the headline conv
   c3a  1x1 conv 256->128 @ 80x80 + bias + SiLU
   c3b  3x3 stride-2 conv 128->256, 80x80 -> 40x40 + bias + SiLU
   c3c  C2f bottleneck block 128->128 @ 80x80 (1x1, 3x3, 3x3 + residual Add, 1x1; concat/split by slices)
   c4   YOLO11n frame at 640x640 (87 convolutions + C2PSA attention + SPPF/upsample/concat/add glue),
        replayed as one HIP graph; random N(0,0.05) weights, input U(0,1); DFL/NMS stay on the host
   c5   int8 DynamicQuantizeMatMul A f32[512,512] N(0,1), W s8[512,2048], per-column scales, bias
-  copy 64 MiB device-to-device copy (osh_memcpy_d2d): calibrates the HBM byte counters
+--config <name> times one workload alone (profiling runs); --config copy is a
+64 MiB device-to-device copy that calibrates the HBM byte counters.
 
-Prints ONE JSON line.  `value` is whole-job TFLOP/s (TOP/s for c5) from HIP
-events on the launch stream over exactly K back-to-back steps (single-launch
-workloads: the K launches recorded once as a HIP graph after the warm-up and
-replayed, so host launch cost is not in the figure; `ms_per_step_eager` gives
-the same K steps issued one by one; `--eager` makes that the value); `roofline`
-prices the dominant kernel against the MI355X peak; `cpu_baseline` times the
-CPU oracle (a restatement of the reference's CPU kernels) on this host.
+`value` is whole-job TFLOP/s (TOP/s for c5) from HIP events on the launch
+stream over exactly K back-to-back steps (single-launch workloads: the K
+launches recorded once as a HIP graph after the warm-up and replayed, so host
+launch cost is not in the figure; `ms_per_step_eager` gives the same K steps
+issued one by one; `--eager` makes that the value); `roofline` prices the
+dominant kernel against the MI355X peak, with the HBM bytes per launch the
+committed rocprofv3 counter summaries give; `cpu_baseline` times the CPU
+oracle (a C restatement of the reference's CPU kernels, in the order the
+reference's kernel for that shape uses on an AVX-512 host) on this host at 4
+threads and at all available cores.
 """
 from __future__ import annotations
 
@@ -124,10 +131,19 @@ class ConvWorkload(Workload):
             from onnxsharp_amd import native as N
             N.check(st)
 
+    def cpu_order(self, oracle):
+        p = self.p
+        k = oracle.conv_reference_kernel(self.x_np.shape, self.w_np.shape, (p.sh, p.sw), (p.pt, p.pl),
+                                         (p.dh, p.dw), p.group, (p.oh, p.ow))
+        return {oracle.KERNEL_NCHWC: "NchwcConv chain (ib -> ky -> kx -> lane16, NchwcConv.cs:533-605)",
+                oracle.KERNEL_WINOGRAD: "Winograd F(2x2,3x3) (Winograd.cs)",
+                oracle.KERNEL_DEPTHWISE: "DepthwiseConv (ky -> kx)"}.get(
+            k, "im2col / pointwise GEMM chain (ic -> ky -> kx, ConvKernels.cs:464-563)")
+
     def cpu_step(self, oracle):
         p = self.p
-        y = oracle.conv2d_f32(self.x_np, self.w_np, self.b_np, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), p.group,
-                              (p.oh, p.ow), order=oracle.ORDER_IM2COL)
+        y = oracle.conv_reference(self.x_np, self.w_np, self.b_np, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw),
+                                  p.group, (p.oh, p.ow))
         return oracle.silu_ref(y)
 
 
@@ -158,6 +174,9 @@ class GemmWorkload(Workload):
         if st != 0:
             from onnxsharp_amd import native as N
             N.check(st)
+
+    def cpu_order(self, oracle):
+        return "GemmKernel k-ascending FMA chain from the column bias (GemmKernel.cs:1130-1207)"
 
     def cpu_step(self, oracle):
         return oracle.gemm_f32(self.a_np, self.b_np, col_bias=self.bias_np)
@@ -200,6 +219,10 @@ class DqmmWorkload(Workload):
             from onnxsharp_amd import native as N
             N.check(st)
 
+    def cpu_order(self, oracle):
+        return ("Quantizer.MinMax + QuantizeAndWiden, then the F32 GEMM of the widened operands "
+                "(QuantizedMatMulOps.cs:115-201)")
+
     def cpu_step(self, oracle):
         return oracle.dqmm(self.a_np, self.w_np, None, self.ws_np, self.bias_np)[0]
 
@@ -238,6 +261,16 @@ class FrameWorkload(Workload):
             self.fr.run()
         else:
             self.fr.launch()
+
+    def cpu_order(self, oracle):
+        from collections import Counter
+        kinds = Counter()
+        for op in self.model.convs:
+            k = oracle.conv_reference_kernel((1, op.x.c, op.x.h, op.x.w), op.w.shape, (op.s, op.s),
+                                             (op.k // 2, op.k // 2), (1, 1), op.group, (op.y.h, op.y.w))
+            kinds[k] += 1
+        return ("each conv on the kernel ConvLayer.Forward picks on an AVX-512 host (DnnOps.cs:437-482): "
+                + ", ".join(f"{v} {k}" for k, v in sorted(kinds.items())))
 
     def cpu_step(self, oracle):
         from oracle import yolo_frame
@@ -418,21 +451,56 @@ def time_gpu(wl, steps, warmup, graph=True):
     return ms, wall, eager_ms
 
 
+CPU_LABEL = "C++ restatement of OnnxSharp CPU kernels, not the C# binary"
+CPU_IMPL = "oracle/osh_oracle.c: C, gcc -O3 -mavx2 -mfma -ffp-contract=off, explicit fmaf chains, pthreads"
+# CPU seconds per thread count: the headline gets the longest sample
+CPU_BUDGET = {"c2": 10.0, "c3b": 4.0, "c4": 4.0, "c1": 2.0, "c3a": 2.0, "c3c": 2.0, "c5": 2.0}
+CONFIGS = ("c1", "c2", "c3a", "c3b", "c3c", "c4", "c5")
+
+
+def reference_paths(flags) -> dict:
+    """Which reference CPU kernels fire on this host's ISA."""
+    f = set(flags)
+    return {"NchwcConv (needs AVX-512F, NchwcConv.cs:43)": "avx512f" in f,
+            "GemmKernel MR=12 (needs AVX-512VL, GemmKernel.cs:452-454)": "avx512f" in f and "avx512vl" in f,
+            "FirstConv (needs AVX-512F)": "avx512f" in f,
+            "DynamicQuantizeMatMul": "F32 GEMM path on every ISA (QuantizedMatMulOps.cs:170-183)"}
+
+
 def cpu_baseline(wl, threads, budget_s):
+    """(rate, steps, seconds, per-step ms list) of the oracle on this host."""
     from oracle import oracle
     oracle.set_threads(threads)
     wl.cpu_step(oracle)  # warm
-    n, t0 = 0, time.perf_counter()
+    times, t0 = [], time.perf_counter()
     while True:
+        t1 = time.perf_counter()
         wl.cpu_step(oracle)
-        n += 1
+        times.append((time.perf_counter() - t1) * 1e3)
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
-    return wl.flops * n / el / 1e12, n, el
+    return wl.flops * len(times) / el / 1e12, len(times), el, times
 
 
-def read_traffic(kernel, name):
+def cpu_leg(wl, budget_s, hi):
+    from oracle import oracle
+    unit = "TOP/s" if wl.dtype == "int8" else "TFLOP/s"
+    v4, n4, el4, t4 = cpu_baseline(wl, 4, budget_s)
+    cpu = {"value": round(v4, 5), "unit": unit, "cores": 4, "kind": "port",
+           "label": CPU_LABEL, "impl": CPU_IMPL, "order": wl.cpu_order(oracle),
+           "ms_per_step_median": round(float(np.median(t4)), 3), "ms_per_step_min": round(min(t4), 3),
+           "sample": f"{n4} full steps of the same workload in {el4:.1f} s (4 threads)"}
+    allc = int(min(hi.get("affinity_cpus") or 4, hi.get("physical_cores") or 4))
+    if allc != 4:
+        va, na, ela, ta = cpu_baseline(wl, allc, budget_s)
+        cpu["all_cores"] = {"value": round(va, 5), "cores": allc,
+                            "ms_per_step_median": round(float(np.median(ta)), 3),
+                            "ms_per_step_min": round(min(ta), 3), "sample": f"{na} steps in {ela:.1f} s"}
+    return cpu
+
+
+def read_traffic(name):
     """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
     path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
     try:
@@ -442,13 +510,51 @@ def read_traffic(kernel, name):
         return None
 
 
+def measure(wl, args):
+    """GPU figures of one workload: step time, rate and roofline."""
+    ms, wall, eager_ms = time_gpu(wl, args.steps, args.warmup, graph=not args.eager)
+    ms_step = ms / args.steps
+    rate = wl.flops / (ms_step * 1e-3) / 1e12
+    if wl.bound == "hbm":
+        achieved = wl.bytes / (ms_step * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm_gbs"], "unit": "GB/s",
+                "frac": round(achieved / PEAK["hbm_gbs"], 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(rate, 3), "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
+                "frac": round(rate / PEAK["fp32_mfma_tflops"], 4)}
+    roof["traffic"] = read_traffic(wl.name)
+    roof["kernel"] = wl.kernel
+    roof["algorithmic_per_launch"] = {"flops": wl.flops, "bytes": wl.bytes}
+    out = {"value": round(rate, 3), "unit": "TOP/s" if wl.dtype == "int8" else "TFLOP/s",
+           "ms_per_step": round(ms_step, 5), "dtype": wl.dtype, "config": wl.config, "roofline": roof,
+           "wall_s": round(wall, 4)}
+    if wl.dtype == "int8":
+        out["frac_of_int8_mfma_peak"] = round(rate / PEAK["int8_tops"], 4)
+    if eager_ms is not None:
+        out["timing"] = f"HIP events around one HIP graph of the {args.steps} launches (recorded after the warm-up)"
+        out["ms_per_step_eager"] = round(eager_ms / args.steps, 5)
+    elif getattr(wl, "graphable", False):
+        out["timing"] = "HIP events around the launches issued one by one"
+    else:
+        out["timing"] = "HIP events around the frame graph replayed once per step"
+    if wl.name in ("c4", "c3c"):
+        key = "frame" if wl.name == "c4" else "block"
+        out[f"ms_per_{key}"] = round(ms_step, 4)
+        if not args.no_host_copies:
+            out[f"ms_per_{key}_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="c2")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--config", default="all",
+                    help="all (default: every workload, C2 as the headline) or one of "
+                         + ", ".join(CONFIGS) + ", copy")
+    ap.add_argument("--cpu-seconds", type=float, default=None,
+                    help="CPU seconds per thread count (default: per workload, 2-10 s)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-host-copies", action="store_true",
                     help="c3c/c4: skip the extra timing with PCIe copies")
@@ -469,80 +575,61 @@ def main():
     N.call("osh_init", 0, C.byref(info))
     dev = torch.device("cuda", 0)
 
-    wl = make_workload(args.config, dev)
-    ms, wall, eager_ms = time_gpu(wl, args.steps, args.warmup, graph=not args.eager)
-    ms_step = ms / args.steps
-    tflops = wl.flops / (ms_step * 1e-3) / 1e12
-    if wl.name == "copy":
+    if args.config == "copy":
+        wl = make_workload("copy", dev)
+        ms, _, _ = time_gpu(wl, args.steps, args.warmup, graph=not args.eager)
+        ms_step = ms / args.steps
         gbs = wl.bytes / (ms_step * 1e-3) / 1e9
         print(json.dumps({"metric": "device copy GB/s", "value": round(gbs, 1), "unit": "GB/s",
                           "ms_per_step": round(ms_step, 5), "bytes_per_step": wl.bytes}), flush=True)
         return
-    if wl.bound == "hbm":
-        achieved = wl.bytes / (ms_step * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK["hbm_gbs"], "unit": "GB/s",
-                "frac": round(achieved / PEAK["hbm_gbs"], 4)}
-    else:
-        roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
-                "frac": round(tflops / PEAK["fp32_mfma_tflops"], 4)}
-    roof["traffic"] = read_traffic(wl.kernel, wl.name)
-    extra = {}
-    if eager_ms is not None:
-        extra["timing"] = f"HIP events around one HIP graph of the {args.steps} launches (recorded after the warm-up)"
-        extra["ms_per_step_eager"] = round(eager_ms / args.steps, 5)
-    elif getattr(wl, "graphable", False):
-        extra["timing"] = "HIP events around the launches issued one by one"
-    if wl.name == "c4":
-        extra["ms_per_frame"] = round(ms_step, 4)
-        if not args.no_host_copies:
-            extra["ms_per_frame_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
-    if wl.name == "c3c":
-        extra["ms_per_block"] = round(ms_step, 4)
-        if not args.no_host_copies:
-            extra["ms_per_block_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
-    roof["kernel"] = wl.kernel
-    roof["algorithmic_per_launch"] = {"flops": wl.flops, "bytes": wl.bytes}
 
-    cpu = None
-    if not args.no_cpu:
-        hi = host_info()
-        v4, n4, el4 = cpu_baseline(wl, 4, args.cpu_seconds)
-        unit = "TOP/s" if wl.dtype == "int8" else "TFLOP/s"
-        cpu = {"value": round(v4, 5), "unit": unit, "cores": 4, "kind": "port",
-               "sample": f"{n4} full steps of the same workload in {el4:.1f} s (oracle, 4 threads)",
-               "host": hi}
-        if wl.name == "c4":
-            cpu["ms_per_frame"] = round(el4 / n4 * 1e3, 2)
-        if wl.name == "c3c":
-            cpu["ms_per_block"] = round(el4 / n4 * 1e3, 2)
-        allc = hi.get("affinity_cpus") or hi.get("physical_cores") or 4
-        allc = int(min(allc, hi.get("physical_cores", allc), 16))
-        if allc != 4:
-            va, na, ela = cpu_baseline(wl, allc, args.cpu_seconds / 2)
-            cpu["all_cores"] = {"value": round(va, 5), "cores": allc,
-                                "sample": f"{na} steps in {ela:.1f} s"}
+    names = CONFIGS if args.config == "all" else (args.config,)
+    headline = "c2" if args.config == "all" else args.config
+    hi = host_info() if not args.no_cpu else None
+    results = {}
+    for name in names:
+        print(f"bench: {name}", file=sys.stderr, flush=True)
+        wl = make_workload(name, dev)
+        r = measure(wl, args)
+        if not args.no_cpu:
+            budget = args.cpu_seconds if args.cpu_seconds is not None else CPU_BUDGET.get(name, 2.0)
+            r["cpu_baseline"] = cpu_leg(wl, budget, hi)
+        results[name] = r
+        if hasattr(wl, "fr"):
+            wl.fr.close()
+        del wl
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
 
+    h = results[headline]
     out = {
         "metric": METRIC,
-        "value": round(tflops, 3),
-        "unit": "TOP/s" if wl.dtype == "int8" else "TFLOP/s",
+        "value": h["value"],
+        "unit": h["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
+        "ms_per_step": h["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": wl.dtype,
+        "dtype": h["dtype"],
         "data": "synthetic",
-        "config": wl.config,
-        "frac_of_mfma_peak": round(tflops / (PEAK["int8_tops"] if wl.dtype == "int8" else PEAK["fp32_mfma_tflops"]), 4),
-        "wall_s": round(wall, 4),
+        "config": h["config"],
         "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.compute_units},
-        "roofline": roof,
-        "cpu_baseline": cpu,
+        "roofline": h["roofline"],
+        "cpu_baseline": h.get("cpu_baseline"),
     }
-    out.update(extra)
+    for k in ("timing", "ms_per_step_eager", "wall_s", "ms_per_frame", "ms_per_frame_with_host_copies",
+              "ms_per_block", "ms_per_block_with_host_copies", "frac_of_int8_mfma_peak"):
+        if k in h:
+            out[k] = h[k]
+    if hi is not None:
+        out["host"] = hi
+        out["reference_paths"] = reference_paths(hi.get("flags", []))
+    if len(results) > 1:
+        out["configs"] = {k: v for k, v in results.items() if k != headline}
     print(json.dumps(out), flush=True)
 
 

@@ -63,9 +63,10 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Block-level min/max of (lo, hi) into thread 0's return values.
+// Block-level min/max of (lo, hi) into thread 0's return values (NW waves).
+template <int NW = DQ_THREADS / 64>
 __device__ void block_minmax(float &lo, float &hi) {
-    __shared__ float smin[DQ_THREADS / 64], smax[DQ_THREADS / 64];
+    __shared__ float smin[NW], smax[NW];
     lo = wave_min(lo);
     hi = wave_max(hi);
     int w = threadIdx.x >> 6;
@@ -75,7 +76,7 @@ __device__ void block_minmax(float &lo, float &hi) {
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int i = 1; i < DQ_THREADS / 64; i++) {
+        for (int i = 1; i < NW; i++) {
             lo = __builtin_fminf(lo, smin[i]);
             hi = __builtin_fmaxf(hi, smax[i]);
         }
@@ -114,11 +115,12 @@ __global__ __launch_bounds__(DQ_THREADS) void dqmm_minmax_kernel(const float *__
 // floats from L2), so no grid-wide counter is needed and the scratch needs no
 // initialisation.  One block (`publish`) stores the parameters for later
 // launches and the caller.
+template <int NW = DQ_THREADS / 64>
 __device__ void dq_finish(DqScratch *__restrict__ sc, float lo, float hi, int *__restrict__ qparams,
                           bool publish, float &inv_out, int &zp_out, float *scale_out) {
     __shared__ float s_inv, s_scale;
     __shared__ int s_zp;
-    block_minmax(lo, hi);
+    block_minmax<NW>(lo, hi);
     if (threadIdx.x == 0) {
         // QuantizedMatMulOps.cs:151-155
         float scale = (hi - lo) / 255.0f;
@@ -421,33 +423,63 @@ __global__ __launch_bounds__(256) void dqmm_gemm_kernel(int m, int k, int n, con
 }
 
 // Quantize + GEMM in one launch (after dqmm_minmax_kernel).  A workgroup owns
-// 32 rows of A and DQF_WAVES column tiles of 32; per chunk of DQF_KS k-steps
-// its 256 threads load the rows' floats (thread -> row tid/8, four consecutive
-// k at 32*i + 4*(tid%8)), quantize them with the parameters every workgroup
-// reduces from the min/max partials, and store a'' = q - 128 in the MFMA
-// A-operand order in LDS; each wave then runs its column tile's
-// v_mfma_i32_32x32x32_i8 chain with B fragments from global memory.  The row
-// sums of a'' and the NaN flags come from the same registers, so nothing but
-// the parameters goes through global scratch.  The partials are loaded first
-// and the first chunk's A and B loads behind them, so the parameter reduction
-// overlaps those loads.  Arithmetic (quantization, zero-point correction,
-// epilogue) is the three-launch pipeline's, so both give identical bits.
+// 32 rows of A and DQF_WAVES column tiles of 32.  Its 256 threads load the
+// rows' floats (thread -> row tid/8, four consecutive k at 32*i + 4*(tid%8))
+// and each wave its column tile's B fragments for a pass of DQF_KS k-steps,
+// all issued at once behind the min/max partials and the epilogue's column
+// operands.  The threads quantize with the parameters every workgroup
+// reduces from the partials and store a'' = q - 128 in the MFMA A-operand
+// order in LDS; after one barrier each wave runs its v_mfma_i32_32x32x32_i8
+// chain.  The row sums of a'' (v_dot4 over the packed bytes) and the NaN
+// flags come from the same registers; nothing but the parameters goes through
+// global scratch.  Arithmetic (quantization, zero-point correction, epilogue)
+// is the three-launch pipeline's, so both give identical bits.
+//
+// What bounds it (ablations timed with the A loads, the B loads or the
+// quantization removed in turn: each saves only 0.4-0.7 us of ~7 us): the
+// chain of latencies of one pass -- cold operand loads from the Infinity
+// Cache (the L2s start empty after the min/max launch), the parameter
+// reduction, quantization, MFMAs, then 4 MB of output stores -- with one
+// workgroup per CU and nothing to overlap it with.  Splitting K over two or
+// four wave groups per workgroup (more loads in flight per CU) measured
+// slower (10.6, 13.6 us per op against 9.7), as did quantizing and
+// multiplying in four double-buffered chunks (11.2 us).
 constexpr int DQF_WAVES = 4;
-constexpr int DQF_KS = 16;  // k-steps of 32 per chunk: K = 512 in one chunk
+constexpr int DQF_KS = 16;  // k-steps of 32 per pass: K = 512 in one pass
 constexpr int DQF_GM = 4;   // row tiles per group of the tile order
 static_assert(DQ_MINMAX_BLOCKS <= 256, "one min/max partial per thread of a 256-thread workgroup");
 
-__global__ __launch_bounds__(256) void dqmm_fused_kernel(int m, int k, int n, const float *__restrict__ a,
-                                                         DqScratch *__restrict__ sc, int nparts,
-                                                         int *__restrict__ qparams, const int8_t *__restrict__ wpk,
-                                                         const int *__restrict__ colsum,
-                                                         const int *__restrict__ off,
-                                                         const float *__restrict__ wscale, int n_wscale,
-                                                         const float *__restrict__ bias, float *__restrict__ out,
-                                                         int *__restrict__ acc_out) {
+// Four elements of one row, quantized: returns the packed a'' bytes
+// (q - 128 as s8) and adds their sum and NaN flag.  `live_mask` bit e says
+// whether element e is a real element (else its a'' is 0).
+__device__ __forceinline__ unsigned quantize4(const Quad &x, float inv, float zpf, unsigned live_mask, int &sum,
+                                              bool &nan) {
+    unsigned packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float p = x.v[e] * inv;
+        float q = __builtin_rintf(p) + zpf;
+        q = __builtin_fminf(255.0f, __builtin_fmaxf(0.0f, q));  // a NaN product gives 0
+        if (live_mask & (1u << e)) {
+            nan |= !(p == p);
+            packed = __builtin_amdgcn_cvt_pk_u8_f32(q, e, packed);
+        } else {
+            packed |= 128u << (8 * e);  // q = 128 <-> a'' = 0
+        }
+    }
+    packed ^= 0x80808080u;  // q -> q - 128, byte by byte
+    sum = __builtin_amdgcn_sdot4((int)packed, 0x01010101, sum, false);
+    return packed;
+}
+
+__global__ __launch_bounds__(256) void dqmm_fused_kernel(
+    int m, int k, int n, const float *__restrict__ a, DqScratch *__restrict__ sc, int nparts,
+    int *__restrict__ qparams, const int8_t *__restrict__ wpk, const int *__restrict__ colsum,
+    const int *__restrict__ off, const float *__restrict__ wscale, int n_wscale, const float *__restrict__ bias,
+    float *__restrict__ out, int *__restrict__ acc_out) {
     __shared__ __attribute__((aligned(16))) int lds_a[DQF_KS * 256];  // [kstep][64 lanes][16 bytes]
     __shared__ int lds_rs[32], lds_rn[32];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wt = tid >> 6;
     const int kpad = pad32(k), ks = kpad / 32, npad = pad32(n);
     // Tiles: XCD-banded ids, then groups of DQF_GM row tiles x all column
     // blocks, so one XCD's L2 holds a few row tiles of A and part of W.
@@ -457,25 +489,33 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(int m, int k, int n, co
     const int mt0 = grp * DQF_GM;
     const int gm = nmt - mt0 < DQF_GM ? nmt - mt0 : DQF_GM;
     const int mt = mt0 + gl % gm;
-    const int nt = (gl / gm) * DQF_WAVES + wave;
+    const int nt = (gl / gm) * DQF_WAVES + wt;
     const bool col_live = nt * 32 < npad;
     const int r = tid >> 3, c8 = tid & 7;
     const int row = mt * 32 + r;
     const bool live = row < m;
     const float *src = a + (long long)(live ? row : 0) * k;
     const bool vec = (k & 3) == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0;
-    // all 32 rows live and 16-byte loads: chunks inside k need no per-element checks
+    // all 32 rows live and 16-byte loads: passes inside k need no per-element checks
     const bool rows_full = vec && mt * 32 + 32 <= m;
-    const int nchunks = (ks + DQF_KS - 1) / DQF_KS;
+    const int npass = (ks + DQF_KS - 1) / DQF_KS;
     const i32x4 *B = reinterpret_cast<const i32x4 *>(wpk) + (long long)(col_live ? nt : 0) * ks * 64 + lane;
 
     // nparts <= 256: one partial per thread (threads past nparts repeat
-    // partial 0), consumed only after the A and B loads are issued
+    // partial 0), consumed after the loads are issued
     const int pidx = tid < nparts ? tid : 0;
     const float pmin = sc->partial_min[pidx], pmax = sc->partial_max[pidx];
+    // the epilogue's column operands, loaded now so their latency hides under the pass
+    const int j = nt * 32 + (lane & 31);
+    const bool jlive = col_live && j < n;
+    const int offj_raw = jlive ? off[j] : 0;
+    const int csum = jlive ? colsum[j] : 0;
+    const float ws = (jlive && wscale) ? (n_wscale == 1 ? wscale[0] : wscale[j]) : 0.0f;
+    const float bj = (jlive && bias) ? bias[j] : 0.0f;
+
     Quad x[DQF_KS];
     i32x4 b[DQF_KS];
-    auto load_chunk = [&](int s0) {
+    auto load_pass = [&](int s0) {
         if (rows_full && (s0 + DQF_KS) * 32 <= k) {
 #pragma unroll
             for (int i = 0; i < DQF_KS; i++) {
@@ -486,18 +526,13 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(int m, int k, int n, co
 #pragma unroll
             for (int i = 0; i < DQF_KS; i++) x[i] = load_quad(src, (s0 + i) * 32 + 4 * c8, k, live, vec);
         }
-    };
-    load_chunk(0);
-    if (col_live) {
-        if (ks >= DQF_KS) {
-#pragma unroll
-            for (int t = 0; t < DQF_KS; t++) b[t] = B[t * 64];
-        } else {
+        if (col_live) {
 #pragma unroll
             for (int t = 0; t < DQF_KS; t++)
-                if (t < ks) b[t] = B[t * 64];
+                if (s0 + t < ks) b[t] = B[(s0 + t) * 64];
         }
-    }
+    };
+    load_pass(0);
 
     float inv, scale;
     int zp;
@@ -509,70 +544,46 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(int m, int k, int n, co
     bool nan = false;
     i32x16 acc = {};
     int *dst = lds_a + (r + 32 * (c8 >> 2)) * 4 + (c8 & 3);
-    for (int c = 0; c < nchunks; c++) {
-        const int s0 = c * DQF_KS;
+    for (int ps = 0; ps < npass; ps++) {
+        const int s0 = ps * DQF_KS;
         if (rows_full && (s0 + DQF_KS) * 32 <= k) {
 #pragma unroll
-            for (int i = 0; i < DQF_KS; i++) {
-                unsigned packed = 0;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float p = x[i].v[e] * inv;
-                    nan |= !(p == p);
-                    const int v = quantize_one(x[i].v[e], inv, zpf) - 128;
-                    sum += v;
-                    packed |= (unsigned)(v & 0xff) << (8 * e);
-                }
-                dst[i * 256] = (int)packed;
-            }
+            for (int i = 0; i < DQF_KS; i++) dst[i * 256] = (int)quantize4(x[i], inv, zpf, 0xfu, sum, nan);
         } else {
 #pragma unroll
             for (int i = 0; i < DQF_KS; i++) {
                 const int kk = (s0 + i) * 32 + 4 * c8;
                 if (kk < kpad) {
-                    unsigned packed = 0;
+                    unsigned lm = 0;
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        int v = 0;  // padding rows and k carry a'' = 0
-                        if (live && kk + e < k) {
-                            const float p = x[i].v[e] * inv;
-                            nan |= !(p == p);
-                            v = quantize_one(x[i].v[e], inv, zpf) - 128;
-                            sum += v;
-                        }
-                        packed |= (unsigned)(v & 0xff) << (8 * e);
-                    }
-                    dst[i * 256] = (int)packed;
+                    for (int e = 0; e < 4; e++) lm |= (live && kk + e < k) ? (1u << e) : 0u;
+                    dst[i * 256] = (int)quantize4(x[i], inv, zpf, lm, sum, nan);
                 }
             }
         }
         __syncthreads();
-        const bool more = c + 1 < nchunks;
-        if (more) load_chunk(s0 + DQF_KS);
         if (col_live) {
-            const int steps = ks - s0 < DQF_KS ? ks - s0 : DQF_KS;
-            if (steps == DQF_KS) {
+            const int *srcl = lds_a + lane * 4;
+            if (s0 + DQF_KS <= ks) {
                 i32x4 av[DQF_KS];
 #pragma unroll
-                for (int t = 0; t < DQF_KS; t++) av[t] = *reinterpret_cast<const i32x4 *>(lds_a + t * 256 + lane * 4);
+                for (int t = 0; t < DQF_KS; t++) av[t] = *reinterpret_cast<const i32x4 *>(srcl + t * 256);
 #pragma unroll
                 for (int t = 0; t < DQF_KS; t++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[t], b[t], acc, 0, 0, 0);
             } else {
 #pragma unroll
                 for (int t = 0; t < DQF_KS; t++) {
-                    if (t < steps) {
-                        const i32x4 av = *reinterpret_cast<const i32x4 *>(lds_a + t * 256 + lane * 4);
+                    if (s0 + t < ks) {
+                        const i32x4 av = *reinterpret_cast<const i32x4 *>(srcl + t * 256);
                         acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b[t], acc, 0, 0, 0);
                     }
                 }
             }
-            if (more) {
-#pragma unroll
-                for (int t = 0; t < DQF_KS; t++)
-                    if (s0 + DQF_KS + t < ks) b[t] = B[(s0 + DQF_KS + t) * 64];
-            }
         }
-        __syncthreads();
+        if (ps + 1 < npass) {
+            load_pass(s0 + DQF_KS);  // x and b are free: the pass is quantized and multiplied
+            __syncthreads();         // every wave's MFMAs have read the pass before it is rewritten
+        }
     }
     // a row's 8 threads are consecutive lanes of one wave
 #pragma unroll
@@ -586,24 +597,22 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(int m, int k, int n, co
         lds_rn[r] = nan ? 1 : 0;
     }
     __syncthreads();
-    const int j = nt * 32 + (lane & 31);
-    if (!col_live || j >= n) return;
-    const unsigned offj = (unsigned)off[j];
+    if (!jlive) return;
+    const unsigned offj = (unsigned)offj_raw;
     const unsigned alpha = (unsigned)(128 - zp);
-    const unsigned colterm = alpha * (unsigned)colsum[j] + (unsigned)k * alpha * offj;
-    const float ws = wscale ? (n_wscale == 1 ? wscale[0] : wscale[j]) : 0.0f;
-    const float bj = bias ? bias[j] : 0.0f;
+    const unsigned colterm = alpha * (unsigned)csum + (unsigned)k * alpha * offj;
     const float comb = scale * ws;  // CombinedScale, QuantizedMatMulOps.cs:203-221
 #pragma unroll
     for (int q = 0; q < 16; q++) {
         const int il = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
         const int i = mt * 32 + il;
         if (i < m) {
-            const int v = (int)((unsigned)acc[q] + offj * (unsigned)lds_rs[il] + colterm);
+            const int rs = lds_rs[il], rn = lds_rn[il];
+            const int v = (int)((unsigned)acc[q] + offj * (unsigned)rs + colterm);
             if (acc_out) acc_out[(long long)i * n + j] = v;
             if (out) {
                 float o = __builtin_fmaf((float)v, comb, bj);
-                if (lds_rn[il]) o = __builtin_nanf("");
+                if (rn) o = __builtin_nanf("");
                 out[(long long)i * n + j] = o;
             }
         }
@@ -634,8 +643,8 @@ static osh_status dqmm_run(int m, int k, int n, const float *d_a, const void *d_
     const int *off = colsum + pad32(n);
     const long long fblocks = (long long)((pad32(n) / 32 + DQF_WAVES - 1) / DQF_WAVES) * (pad32(m) / 32);
     if (dqmm_variant() == 0 && fblocks <= 0x7fffffffLL) {
-        hipLaunchKernelGGL(dqmm_fused_kernel, dim3((unsigned)fblocks), dim3(256), 0, st, m, k, n, d_a, sc, nparts, (int *)d_qparams,
-                           frag, colsum, off, d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
+        hipLaunchKernelGGL(dqmm_fused_kernel, dim3((unsigned)fblocks), dim3(256), 0, st, m, k, n, d_a, sc, nparts,
+                           (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
         OSH_LAUNCH_CHECK("dqmm_fused_kernel");
         return OSH_OK;
     }
