@@ -112,6 +112,8 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 then one launch that quantizes A and multiplies; 1 = min/max,
  *                 quantize and GEMM as three launches.  Both give identical
  *                 outputs.  Initial value from ONNXSHARP_HIP_DQMM_VARIANT.
+ *   "dqmm_launches" (get only): kernel launches (2 or 3) of the calling
+ *                 thread's last osh_dqmm_u8s8 / osh_dqmm_u8s8_noalloc call.
  *   "im2col3x3_variant": -1 (default) = 3x3 stride-1/2 convolutions with
  *                 C % 16 == 0 that neither the NCHWc nor the Winograd gate
  *                 takes run the LDS-patch tiles in the reference's im2col

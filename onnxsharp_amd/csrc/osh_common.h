@@ -166,6 +166,8 @@ long long winograd_max_pixels();
 // DynamicQuantizeMatMul pipeline (0 = min/max launch then one fused
 // quantize + GEMM launch, 1 = min/max, quantize and GEMM as three launches).
 int dqmm_variant();
+// Kernel launches of the calling thread's last DynamicQuantizeMatMul (2 or 3).
+int dqmm_last_launches();
 
 // Whether kernels whose tiles all give identical results may pick their tile
 // by timing it on first use (osh_config "tune", ONNXSHARP_HIP_TUNE; default on).

@@ -111,6 +111,31 @@ __global__ __launch_bounds__(DQ_THREADS) void dqmm_minmax_kernel(const float *__
     }
 }
 
+// scale = (max-min)/255 (1 if not > 0), zp = clamp(rne(-min/scale)),
+// inv = 1/scale: single IEEE ops, no contraction (QuantizedMatMulOps.cs:151-155;
+// QuantizeAndWiden multiplies by the reciprocal, :282).
+__device__ __forceinline__ void dq_param_values(float lo, float hi, float &scale, int &zp, float &inv) {
+    scale = (hi - lo) / 255.0f;
+    if (!(scale > 0.0f)) scale = 1.0f;
+    const float zf = __builtin_rintf(-lo / scale);
+    zp = (int)zf;
+    zp = zp < 0 ? 0 : (zp > 255 ? 255 : zp);
+    inv = 1.0f / scale;
+}
+
+// The parameters for later launches and the caller.
+__device__ __forceinline__ void dq_publish_params(DqScratch *__restrict__ sc, int *__restrict__ qparams, float scale,
+                                                  int zp, float inv) {
+    sc->scale = scale;
+    sc->zp = zp;
+    sc->inv = inv;
+    sc->alpha = 128 - zp;
+    if (qparams) {
+        qparams[0] = __float_as_int(scale);
+        qparams[1] = zp;
+    }
+}
+
 // Every consumer block reduces the per-block partials itself (a few hundred
 // floats from L2), so no grid-wide counter is needed and the scratch needs no
 // initialisation.  One block (`publish`) stores the parameters for later
@@ -122,26 +147,13 @@ __device__ void dq_finish(DqScratch *__restrict__ sc, float lo, float hi, int *_
     __shared__ int s_zp;
     block_minmax<NW>(lo, hi);
     if (threadIdx.x == 0) {
-        // QuantizedMatMulOps.cs:151-155
-        float scale = (hi - lo) / 255.0f;
-        if (!(scale > 0.0f)) scale = 1.0f;
-        float zf = __builtin_rintf(-lo / scale);
-        int zp = (int)zf;
-        zp = zp < 0 ? 0 : (zp > 255 ? 255 : zp);
-        float inv = 1.0f / scale;  // QuantizeAndWiden multiplies by the reciprocal (QuantizedMatMulOps.cs:282)
+        float scale, inv;
+        int zp;
+        dq_param_values(lo, hi, scale, zp, inv);
         s_inv = inv;
         s_scale = scale;
         s_zp = zp;
-        if (publish) {
-            sc->scale = scale;
-            sc->zp = zp;
-            sc->inv = inv;
-            sc->alpha = 128 - zp;
-            if (qparams) {
-                qparams[0] = __float_as_int(scale);
-                qparams[1] = zp;
-            }
-        }
+        if (publish) dq_publish_params(sc, qparams, scale, zp, inv);
     }
     __syncthreads();
     inv_out = s_inv;
@@ -422,28 +434,24 @@ __global__ __launch_bounds__(256) void dqmm_gemm_kernel(int m, int k, int n, con
     }
 }
 
-// Quantize + GEMM in one launch (after dqmm_minmax_kernel).  A workgroup owns
+// Quantize + GEMM in one launch, after dqmm_minmax_kernel.  A workgroup owns
 // 32 rows of A and DQF_WAVES column tiles of 32.  Its 256 threads load the
 // rows' floats (thread -> row tid/8, four consecutive k at 32*i + 4*(tid%8))
 // and each wave its column tile's B fragments for a pass of DQF_KS k-steps,
 // all issued at once behind the min/max partials and the epilogue's column
-// operands.  The threads quantize with the parameters every workgroup
-// reduces from the partials and store a'' = q - 128 in the MFMA A-operand
-// order in LDS; after one barrier each wave runs its v_mfma_i32_32x32x32_i8
-// chain.  The row sums of a'' (v_dot4 over the packed bytes) and the NaN
-// flags come from the same registers; nothing but the parameters goes through
-// global scratch.  Arithmetic (quantization, zero-point correction, epilogue)
-// is the three-launch pipeline's, so both give identical bits.
+// operands.  The threads quantize with the parameters every workgroup reduces
+// from the partials and store a'' = q - 128 in the MFMA A-operand order in
+// LDS; after one barrier each wave runs its v_mfma_i32_32x32x32_i8 chain.  The
+// row sums of a'' (v_dot4 over the packed bytes) and the NaN flags come from
+// the same registers; nothing but the parameters goes through global scratch.
+// Arithmetic (quantization, zero-point correction, epilogue) is the
+// three-launch pipeline's, so both give identical bits.
 //
-// What bounds it (ablations timed with the A loads, the B loads or the
-// quantization removed in turn: each saves only 0.4-0.7 us of ~7 us): the
-// chain of latencies of one pass -- cold operand loads from the Infinity
-// Cache (the L2s start empty after the min/max launch), the parameter
-// reduction, quantization, MFMAs, then 4 MB of output stores -- with one
-// workgroup per CU and nothing to overlap it with.  Splitting K over two or
-// four wave groups per workgroup (more loads in flight per CU) measured
-// slower (10.6, 13.6 us per op against 9.7), as did quantizing and
-// multiplying in four double-buffered chunks (11.2 us).
+// Time line of one launch at C5's size (512 x 512 x 2048; per-workgroup
+// s_memrealtime stamps in a copy of the kernel, medians): workgroups start
+// over 0.7 us; the first loads return after ~2 us (a cold first load takes
+// that long even with nothing else in flight); quantization 0.9 us; the MFMA
+// chain 1.0 us; the output stores 1.2 us, near the HBM write rate for 4 MB.
 constexpr int DQF_WAVES = 4;
 constexpr int DQF_KS = 16;  // k-steps of 32 per pass: K = 512 in one pass
 constexpr int DQF_GM = 4;   // row tiles per group of the tile order
@@ -451,15 +459,19 @@ static_assert(DQ_MINMAX_BLOCKS <= 256, "one min/max partial per thread of a 256-
 
 // Four elements of one row, quantized: returns the packed a'' bytes
 // (q - 128 as s8) and adds their sum and NaN flag.  `live_mask` bit e says
-// whether element e is a real element (else its a'' is 0).
+// whether element e is a real element (else its a'' is 0).  v_cvt_pk_u8_f32
+// converts with round-to-nearest-even and saturates to [0, 255] (a NaN gives
+// 0), so on the integer-valued q = rne(x * inv) + zp it is the clamp of
+// QuantizeAndWiden; both facts were checked on the device for every integer
+// from -1000 to 1300, the .25/.5/.75 fractions, +-inf and NaN, and the
+// pipelines' bit equality is tested.
 __device__ __forceinline__ unsigned quantize4(const Quad &x, float inv, float zpf, unsigned live_mask, int &sum,
                                               bool &nan) {
     unsigned packed = 0;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const float p = x.v[e] * inv;
-        float q = __builtin_rintf(p) + zpf;
-        q = __builtin_fminf(255.0f, __builtin_fmaxf(0.0f, q));  // a NaN product gives 0
+        const float q = __builtin_rintf(p) + zpf;
         if (live_mask & (1u << e)) {
             nan |= !(p == p);
             packed = __builtin_amdgcn_cvt_pk_u8_f32(q, e, packed);
@@ -472,14 +484,25 @@ __device__ __forceinline__ unsigned quantize4(const Quad &x, float inv, float zp
     return packed;
 }
 
-__global__ __launch_bounds__(256) void dqmm_fused_kernel(
-    int m, int k, int n, const float *__restrict__ a, DqScratch *__restrict__ sc, int nparts,
-    int *__restrict__ qparams, const int8_t *__restrict__ wpk, const int *__restrict__ colsum,
-    const int *__restrict__ off, const float *__restrict__ wscale, int n_wscale, const float *__restrict__ bias,
-    float *__restrict__ out, int *__restrict__ acc_out) {
+// FULL: m % 32 == 0, n % 128 == 0, k % 512 == 0 and A 16-byte aligned, so
+// every row, column and k-step is live and no load or store needs a check.
+// The host picks it whenever it applies; the kernel then has no divergent
+// paths, so the compiler issues all operand loads before the first wait
+// (with the checks, the registers of the two load paths are merged by copies
+// that wait for every A load before any B load is issued).
+//
+// A and W are not declared __restrict__: the operand loads must stay ahead of
+// the barriers that follow them (the compiler may otherwise sink loads of
+// restrict read-only memory to their first use).
+template <bool FULL>
+__global__ __launch_bounds__(64 * DQF_WAVES) void dqmm_fused_kernel(
+    int m, int k, int n, const float *a, DqScratch *__restrict__ sc, int nparts, int *__restrict__ qparams,
+    const int8_t *wpk, const int *__restrict__ colsum, const int *__restrict__ off,
+    const float *__restrict__ wscale, int n_wscale, const float *__restrict__ bias, float *__restrict__ out,
+    int *__restrict__ acc_out) {
     __shared__ __attribute__((aligned(16))) int lds_a[DQF_KS * 256];  // [kstep][64 lanes][16 bytes]
     __shared__ int lds_rs[32], lds_rn[32];
-    const int tid = threadIdx.x, lane = tid & 63, wt = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wt = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kpad = pad32(k), ks = kpad / 32, npad = pad32(n);
     // Tiles: XCD-banded ids, then groups of DQF_GM row tiles x all column
     // blocks, so one XCD's L2 holds a few row tiles of A and part of W.
@@ -490,33 +513,33 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(
     const int gm = nmt - mt0 < DQF_GM ? nmt - mt0 : DQF_GM;
     const int mt = mt0 + gl % gm;
     const int nt = (gl / gm) * DQF_WAVES + wt;
-    const bool col_live = nt * 32 < npad;
+    const bool col_live = FULL || nt * 32 < npad;
     const int r = tid >> 3, c8 = tid & 7;
     const int row = mt * 32 + r;
-    const bool live = row < m;
+    const bool live = FULL || row < m;
     const float *src = a + (long long)(live ? row : 0) * k;
-    const bool vec = (k & 3) == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0;
+    const bool vec = FULL || ((k & 3) == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0);
     // all 32 rows live and 16-byte loads: passes inside k need no per-element checks
-    const bool rows_full = vec && mt * 32 + 32 <= m;
+    const bool rows_full = FULL || (vec && mt * 32 + 32 <= m);
     const int npass = (ks + DQF_KS - 1) / DQF_KS;
     const i32x4 *B = reinterpret_cast<const i32x4 *>(wpk) + (long long)(col_live ? nt : 0) * ks * 64 + lane;
 
     // nparts <= 256: one partial per thread (threads past nparts repeat
-    // partial 0), consumed after the loads are issued
+    // partial 0), consumed after the operand loads are issued
     const int pidx = tid < nparts ? tid : 0;
     const float pmin = sc->partial_min[pidx], pmax = sc->partial_max[pidx];
     // the epilogue's column operands, loaded now so their latency hides under the pass
     const int j = nt * 32 + (lane & 31);
-    const bool jlive = col_live && j < n;
+    const bool jlive = col_live && (FULL || j < n);
     const int offj_raw = jlive ? off[j] : 0;
     const int csum = jlive ? colsum[j] : 0;
-    const float ws = (jlive && wscale) ? (n_wscale == 1 ? wscale[0] : wscale[j]) : 0.0f;
+    const float ws = jlive ? (n_wscale == 1 ? wscale[0] : wscale[j]) : 0.0f;
     const float bj = (jlive && bias) ? bias[j] : 0.0f;
 
     Quad x[DQF_KS];
     i32x4 b[DQF_KS];
     auto load_pass = [&](int s0) {
-        if (rows_full && (s0 + DQF_KS) * 32 <= k) {
+        if (FULL || (rows_full && (s0 + DQF_KS) * 32 <= k)) {
 #pragma unroll
             for (int i = 0; i < DQF_KS; i++) {
                 const float4 v = *reinterpret_cast<const float4 *>(src + (s0 + i) * 32 + 4 * c8);
@@ -526,13 +549,19 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(
 #pragma unroll
             for (int i = 0; i < DQF_KS; i++) x[i] = load_quad(src, (s0 + i) * 32 + 4 * c8, k, live, vec);
         }
-        if (col_live) {
+        if (FULL) {
+#pragma unroll
+            for (int t = 0; t < DQF_KS; t++) b[t] = B[(s0 + t) * 64];
+        } else if (col_live) {
 #pragma unroll
             for (int t = 0; t < DQF_KS; t++)
                 if (s0 + t < ks) b[t] = B[(s0 + t) * 64];
         }
     };
     load_pass(0);
+    // nothing below moves above this point: every load is out before the
+    // first wait
+    __builtin_amdgcn_sched_barrier(0);
 
     float inv, scale;
     int zp;
@@ -540,13 +569,15 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(
               &scale);
     const float zpf = (float)zp;
 
+    // The MFMA chain runs as two interleaved chains (even and odd k-steps)
+    // summed at the end; int32 sums are exact in any order.
     int sum = 0;
     bool nan = false;
-    i32x16 acc = {};
+    i32x16 acc0 = {}, acc1 = {};
     int *dst = lds_a + (r + 32 * (c8 >> 2)) * 4 + (c8 & 3);
     for (int ps = 0; ps < npass; ps++) {
         const int s0 = ps * DQF_KS;
-        if (rows_full && (s0 + DQF_KS) * 32 <= k) {
+        if (FULL || (rows_full && (s0 + DQF_KS) * 32 <= k)) {
 #pragma unroll
             for (int i = 0; i < DQF_KS; i++) dst[i * 256] = (int)quantize4(x[i], inv, zpf, 0xfu, sum, nan);
         } else {
@@ -564,27 +595,35 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(
         __syncthreads();
         if (col_live) {
             const int *srcl = lds_a + lane * 4;
-            if (s0 + DQF_KS <= ks) {
+            if (FULL || s0 + DQF_KS <= ks) {
                 i32x4 av[DQF_KS];
 #pragma unroll
                 for (int t = 0; t < DQF_KS; t++) av[t] = *reinterpret_cast<const i32x4 *>(srcl + t * 256);
 #pragma unroll
-                for (int t = 0; t < DQF_KS; t++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[t], b[t], acc, 0, 0, 0);
+                for (int t = 0; t < DQF_KS; t += 2) {
+                    acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[t], b[t], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[t + 1], b[t + 1], acc1, 0, 0, 0);
+                }
             } else {
 #pragma unroll
                 for (int t = 0; t < DQF_KS; t++) {
                     if (s0 + t < ks) {
                         const i32x4 av = *reinterpret_cast<const i32x4 *>(srcl + t * 256);
-                        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b[t], acc, 0, 0, 0);
+                        if (t & 1) acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b[t], acc1, 0, 0, 0);
+                        else acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b[t], acc0, 0, 0, 0);
                     }
                 }
             }
         }
         if (ps + 1 < npass) {
+            // the next pass's loads go out after this pass's MFMAs, whose b
+            // registers they reuse
+            __builtin_amdgcn_sched_barrier(0);
             load_pass(s0 + DQF_KS);  // x and b are free: the pass is quantized and multiplied
             __syncthreads();         // every wave's MFMAs have read the pass before it is rewritten
         }
     }
+    const i32x16 acc = acc0 + acc1;
     // a row's 8 threads are consecutive lanes of one wave
 #pragma unroll
     for (int o = 1; o < 8; o <<= 1) {
@@ -606,7 +645,7 @@ __global__ __launch_bounds__(256) void dqmm_fused_kernel(
     for (int q = 0; q < 16; q++) {
         const int il = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
         const int i = mt * 32 + il;
-        if (i < m) {
+        if (FULL || i < m) {
             const int rs = lds_rs[il], rn = lds_rn[il];
             const int v = (int)((unsigned)acc[q] + offj * (unsigned)rs + colterm);
             if (acc_out) acc_out[(long long)i * n + j] = v;
@@ -629,23 +668,36 @@ static osh_status run_minmax(const float *a, long long count, DqScratch *sc, int
     return OSH_OK;
 }
 
+static thread_local int t_dqmm_launches = 0;
+int dqmm_last_launches() { return t_dqmm_launches; }
+
 static osh_status dqmm_run(int m, int k, int n, const float *d_a, const void *d_wpacked, const float *d_wscale,
                            int n_wscale, const float *d_bias, float *d_out, int32_t *d_acc, int32_t *d_qparams,
                            void *d_scratch, hipStream_t st) {
     DqScratch *sc = static_cast<DqScratch *>(d_scratch);
     int *rowsum = reinterpret_cast<int *>(sc + 1);
     int8_t *apk = reinterpret_cast<int8_t *>(rowsum + 2 * pad32(m));
-    int nparts = 0;
-    osh_status r = run_minmax(d_a, (long long)m * k, sc, &nparts, st);
-    if (r != OSH_OK) return r;
     const int8_t *frag = static_cast<const int8_t *>(d_wpacked);
     const int *colsum = reinterpret_cast<const int *>(frag + (size_t)pad32(n) * pad32(k));
     const int *off = colsum + pad32(n);
     const long long fblocks = (long long)((pad32(n) / 32 + DQF_WAVES - 1) / DQF_WAVES) * (pad32(m) / 32);
+    const long long total = (long long)m * k;
+    int nparts = 0;
+    osh_status r = run_minmax(d_a, total, sc, &nparts, st);
+    if (r != OSH_OK) return r;
+    const bool full = m % 32 == 0 && n % 128 == 0 && k % (32 * DQF_KS) == 0 &&
+                      (reinterpret_cast<uintptr_t>(d_a) & 15) == 0;
     if (dqmm_variant() == 0 && fblocks <= 0x7fffffffLL) {
-        hipLaunchKernelGGL(dqmm_fused_kernel, dim3((unsigned)fblocks), dim3(256), 0, st, m, k, n, d_a, sc, nparts,
-                           (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
+        if (full)
+            hipLaunchKernelGGL(dqmm_fused_kernel<true>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k, n,
+                               d_a, sc, nparts, (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias, d_out,
+                               (int *)d_acc);
+        else
+            hipLaunchKernelGGL(dqmm_fused_kernel<false>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k,
+                               n, d_a, sc, nparts, (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias,
+                               d_out, (int *)d_acc);
         OSH_LAUNCH_CHECK("dqmm_fused_kernel");
+        t_dqmm_launches = 2;
         return OSH_OK;
     }
     const int rows_per_block = DQ_THREADS / 64;
@@ -656,6 +708,7 @@ static osh_status dqmm_run(int m, int k, int n, const float *d_a, const void *d_
     hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
                        d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
     OSH_LAUNCH_CHECK("dqmm_gemm_kernel");
+    t_dqmm_launches = 3;
     return OSH_OK;
 }
 

@@ -217,6 +217,10 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
         *value = dqmm_variant();
         return OSH_OK;
     }
+    if (strcmp(key, "dqmm_launches") == 0) {
+        *value = dqmm_last_launches();
+        return OSH_OK;
+    }
     if (strcmp(key, "pointwise_variants") == 0) {
         *value = pointwise_variant_count();
         return OSH_OK;

@@ -116,10 +116,13 @@ def test_dynamic_quantize_linear_matches_oracle(cuda, oracle):
     assert np.array_equal(q.cpu().numpy(), eq)
 
 
-@pytest.mark.parametrize("m,k,n", [(512, 512, 2048), (3, 2100, 17), (70, 96, 300), (33, 1040, 130), (1, 7, 3)])
+@pytest.mark.parametrize("m,k,n", [(512, 512, 2048), (3, 2100, 17), (70, 96, 300), (33, 1040, 130), (1, 7, 3),
+                                   (64, 1024, 256), (128, 512, 512), (256, 1024, 1024)])
 def test_dqmm_fused_and_three_launch_pipelines_identical(cuda, oracle, m, k, n):
-    """dqmm_variant 0 (quantize inside the GEMM launch, K in chunks of 512) and
-    1 (separate quantize launch) give the same bits, both equal to the oracle."""
+    """dqmm_variant 0 (min/max launch, then quantize inside the GEMM launch, K
+    in chunks of 512; the branch-free kernel where every tile is full) and 1
+    (min/max, quantize and GEMM launches) give the same bits, both equal to
+    the oracle."""
     import ctypes as C
     from onnxsharp_amd import native as N
     print(f"dqmm pipelines m={m} k={k} n={n}", flush=True)
@@ -130,13 +133,17 @@ def test_dqmm_fused_and_three_launch_pipelines_identical(cuda, oracle, m, k, n):
     bias = synth.normal(m + n, (n,), 0, 0.01)
     old = C.c_int()
     N.call("osh_config_get", b"dqmm_variant", C.byref(old))
-    got = []
+    got, launches = [], []
     try:
         for v in (0, 1):
             N.call("osh_config_set", b"dqmm_variant", v)
             got.append(run_dqmm(cuda, a, w, None, ws, bias))
+            nl = C.c_int()
+            N.call("osh_config_get", b"dqmm_launches", C.byref(nl))
+            launches.append(nl.value)
     finally:
         N.call("osh_config_set", b"dqmm_variant", old.value)
+    assert launches == [2, 3], launches
     (o0, a0, s0, z0), (o1, a1, s1, z1) = got
     assert (s0, z0) == (s1, z1)
     assert np.array_equal(a0, a1)
@@ -190,3 +197,103 @@ def test_fused_dqmm_equals_the_node_chain_it_replaces(cuda, oracle, m, k, n):
     assert np.array_equal(out_chain, eo_unfused.astype(np.float32))
     eo, eacc, _, _, _ = oracle.dqmm(a, w, None, ws, bias)
     assert np.array_equal(out, eo) and np.array_equal(acc, eacc)
+
+
+def _packed(cuda, w):
+    import ctypes as C
+    import torch
+    from onnxsharp_amd import native as N
+    k, n = w.shape
+    nb = C.c_size_t()
+    N.call("osh_dqmm_packed_weight_bytes", k, n, C.byref(nb))
+    packed = torch.empty(nb.value, dtype=torch.uint8, device=cuda)
+    dw = _t(w, cuda)
+    N.call("osh_dqmm_pack_weights", k, n, C.c_void_p(dw.data_ptr()), 1, None, 0, C.c_void_p(packed.data_ptr()),
+           None)
+    return packed
+
+
+def test_dqmm_calls_in_a_row_over_changing_inputs_and_dirty_scratch(cuda, oracle):
+    """Calls in a row on one scratch buffer whose A ranges differ (a stale
+    min/max partial would change the scale), starting from a scratch full of
+    arbitrary bytes, each equal the oracle bit for bit."""
+    import ctypes as C
+    import torch
+    from onnxsharp_amd import native as N
+    m, k, n = 512, 512, 2048
+    w = synth.randint(900, (k, n), -127, 127, np.int8)
+    ws = synth.uniform(901, (n,), 0.001, 0.02)
+    bias = synth.normal(902, (n,), 0, 0.01)
+    packed = _packed(cuda, w)
+    sb = C.c_size_t()
+    N.call("osh_dqmm_scratch_bytes", m, k, C.byref(sb))
+    for fill in (0xFF, None):
+        scratch = torch.empty(sb.value, dtype=torch.uint8, device=cuda)
+        if fill is None:
+            scratch.copy_(torch.from_numpy(synth.randint(903, (sb.value,), 0, 255, np.uint8)))
+        else:
+            scratch.fill_(fill)
+        for call, (seed, scale_a) in enumerate(((910, 1.0), (911, 7.5), (910, 1.0), (912, 0.01))):
+            print(f"DQM calls in a row: scratch fill {fill}, call {call}, A seed {seed} x {scale_a}", flush=True)
+            a = (synth.normal(seed, (m, k)) * np.float32(scale_a)).astype(np.float32)
+            da, dws, db = _t(a, cuda), _t(ws, cuda), _t(bias, cuda)
+            out = torch.empty((m, n), dtype=torch.float32, device=cuda)
+            acc = torch.empty((m, n), dtype=torch.int32, device=cuda)
+            qp = torch.empty(2, dtype=torch.int32, device=cuda)
+            p = lambda x: C.c_void_p(x.data_ptr())
+            N.call("osh_dqmm_u8s8", m, k, n, p(da), p(packed), p(dws), n, p(db), p(out), p(acc), p(qp), p(scratch),
+                   None)
+            torch.cuda.synchronize()
+            eo, eacc, _, es, ez = oracle.dqmm(a, w, None, ws, bias)
+            q = qp.cpu().numpy()
+            assert (np.float32(q[0:1].view(np.float32)[0]), int(q[1])) == (es, ez)
+            assert np.array_equal(acc.cpu().numpy(), eacc)
+            assert np.array_equal(out.cpu().numpy(), eo)
+
+
+def test_dqmm_graph_replays_see_new_inputs(cuda, oracle):
+    """A HIP graph holding one DynamicQuantizeMatMul (min/max launch, then the
+    fused launch) replays with frozen kernel arguments; each replay after new
+    data is copied into A quantizes with that data's own min/max."""
+    import ctypes as C
+    import torch
+    from onnxsharp_amd import native as N
+    m, k, n = 512, 512, 2048
+    w = synth.randint(920, (k, n), -127, 127, np.int8)
+    ws = synth.uniform(921, (n,), 0.001, 0.02)
+    bias = synth.normal(922, (n,), 0, 0.01)
+    packed = _packed(cuda, w)
+    sb = C.c_size_t()
+    N.call("osh_dqmm_scratch_bytes", m, k, C.byref(sb))
+    scratch = torch.empty(sb.value, dtype=torch.uint8, device=cuda)
+    da = torch.empty((m, k), dtype=torch.float32, device=cuda)
+    dws, db = _t(ws, cuda), _t(bias, cuda)
+    out = torch.empty((m, n), dtype=torch.float32, device=cuda)
+    acc = torch.empty((m, n), dtype=torch.int32, device=cuda)
+    st = C.c_void_p()
+    N.call("osh_stream_create", C.byref(st))
+    g = C.c_void_p()
+    p = lambda x: C.c_void_p(x.data_ptr())
+    try:
+        da.copy_(_t(synth.normal(930, (m, k)), cuda))
+        torch.cuda.synchronize()
+        N.call("osh_graph_begin", st)
+        try:
+            N.call("osh_dqmm_u8s8", m, k, n, p(da), p(packed), p(dws), n, p(db), p(out), p(acc), None, p(scratch),
+                   st)
+        finally:
+            N.call("osh_graph_end", st, C.byref(g))
+        for rep, (seed, scale_a) in enumerate(((931, 1.0), (932, 20.0), (931, 1.0), (933, 0.05))):
+            print(f"DQM graph replay {rep}: A seed {seed} x {scale_a}", flush=True)
+            a = (synth.normal(seed, (m, k)) * np.float32(scale_a)).astype(np.float32)
+            da.copy_(_t(a, cuda))
+            torch.cuda.synchronize()
+            N.call("osh_graph_launch", g, st)
+            N.call("osh_stream_sync", st)
+            eo, eacc, _, _, _ = oracle.dqmm(a, w, None, ws, bias)
+            assert np.array_equal(acc.cpu().numpy(), eacc), f"replay {rep}: accumulators"
+            assert np.array_equal(out.cpu().numpy(), eo), f"replay {rep}: outputs"
+    finally:
+        if g.value:
+            N.call("osh_graph_destroy", g)
+        N.call("osh_stream_destroy", st)
