@@ -93,10 +93,8 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 weights held in LDS; 12..22: input patch staged in LDS
  *                 and shared by a workgroup's four waves, stride 1 or 2;
  *                 23..26: tiles 0, 3, 1, 4 with one wave per workgroup;
- *                 27..N-1: tiles 13, 14, 15 with XCD-banded workgroups);
- *                 -2 = use the weight-stationary 3x3
- *                 kernels instead (summation order differs; within the FP32
- *                 tolerance).  Initial value from ONNXSHARP_HIP_CONV16_VARIANT.
+ *                 27..N-1: tiles 13, 14, 15 with XCD-banded workgroups).
+ *                 Initial value from ONNXSHARP_HIP_CONV16_VARIANT.
  *   "conv16_variants" (get only): N, the number of 3x3 tiles.
  *   "pointwise_variant": -1 (default) = 1x1 stride-1 convolutions with
  *                 C % 16 == 0 pick, by the same first-use timing, between the
@@ -105,9 +103,8 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 GEMM path only.  Initial value from
  *                 ONNXSHARP_HIP_POINTWISE_VARIANT.
  *   "pointwise_variants" (get only): N.
- *                 The -2 settings of "conv16_variant" and "pointwise_variant"
- *                 change the packed weight layout: pack again after changing
- *                 them.
+ *                 The -2 setting of "pointwise_variant" changes the packed
+ *                 weight layout: pack again after changing it.
  *   "dqmm_variant": 0 (default) = osh_dqmm_u8s8 runs a min/max launch and
  *                 then one launch that quantizes A and multiplies; 1 = min/max,
  *                 quantize and GEMM as three launches.  Both give identical

@@ -30,10 +30,6 @@
 // chain), 2 puts it ahead of the NCHWc kernels (the reference's choice on a
 // host without AVX-512, for the Winograd-eligible shapes).  A forced
 // "conv16_variant" >= 0 runs the NCHWc-chain kernels on any 3x3 shape they fit.
-// With osh_config_set("conv16_variant", -2) 3x3 shapes take the older
-// weight-stationary / LDS-halo kernels instead (osh_conv3x3_wi.h,
-// osh_conv3x3_ws.h, osh_conv3x3.h), which sum in orders of their own (within
-// the FP32 tolerance).
 //
 // Bias and the fused activation (Relu / SiLU, GraphFusion.cs:1713-1718) are
 // applied in registers before the single store, then an optional residual.
@@ -44,9 +40,6 @@
 
 #include "osh_conv16.h"
 #include "osh_conv16s.h"
-#include "osh_conv3x3.h"
-#include "osh_conv3x3_wi.h"
-#include "osh_conv3x3_ws.h"
 #include "osh_igemm.h"
 #include "osh_launch.h"
 #include "osh_winograd.h"
@@ -152,14 +145,6 @@ __global__ __launch_bounds__(256) void dw_conv_group_kernel(ConvGroup g) {
     while (i + 1 < g.count && b >= g.start[i + 1]) i++;
     dw_conv_at<ACT>(g.p[i], g.x[i], g.w[i], g.bias[i], g.res[i], g.y[i],
                     (long long)(b - g.start[i]) * 256 + threadIdx.x);
-}
-
-// y += res after a kernel whose epilogue has no residual input: the same two
-// roundings (activation output, then the sum) as the fused epilogues.
-__global__ __launch_bounds__(256) void residual_add_kernel(long long n, const float *__restrict__ res,
-                                                           float *__restrict__ y) {
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = y[i] + res[i];
 }
 
 // ------------------------------------------------------- small-C first layer
@@ -275,8 +260,8 @@ static bool nchwc_gate(const osh_conv_params *p) {
            (s2 ? p->oh * 2 == p->h && p->ow * 2 == p->w : p->oh == p->h && p->ow == p->w);
 }
 
-enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_DIRECT3X3 = 2, ALGO_IM2COL = 3, ALGO_WS3X3 = 4, ALGO_WI3X3 = 5,
-                ALGO_FIRST = 6, ALGO_CONV16 = 7, ALGO_PW16 = 8, ALGO_WINOGRAD = 9, ALGO_CONV16I = 10 };
+enum ConvAlgo { ALGO_DEPTHWISE = 0, ALGO_POINTWISE = 1, ALGO_IM2COL = 3, ALGO_FIRST = 6, ALGO_CONV16 = 7, ALGO_PW16 = 8,
+                ALGO_WINOGRAD = 9, ALGO_CONV16I = 10 };
 
 static bool is_pointwise(const osh_conv_params *p) {
     return p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->pt == 0 && p->pl == 0 && p->oh == p->h &&
@@ -287,18 +272,6 @@ static ConvAlgo select_algo(const osh_conv_params *p) {
     if (p->group == p->c && p->group == p->m && p->group > 1) return ALGO_DEPTHWISE;
     const int v16 = conv16_variant();
     if (v16 >= 0 && conv16_eligible(p)) return ALGO_CONV16;  // a forced tile (tuning and tests)
-    if (v16 == -2) {
-        // the weight-stationary and LDS-halo 3x3 kernels, which sum in their
-        // own orders (within the FP32 tolerance): only on request; the direct
-        // kernel keeps the channel counts it took before them (C <= 4 or 8)
-        if (first_conv_eligible(p) && (p->c <= 4 || p->c == 8)) return ALGO_FIRST;
-        if (pointwise_variant() != -2 && pw16_eligible(p)) return ALGO_PW16;
-        if (is_pointwise(p)) return ALGO_POINTWISE;
-        if (conv3x3_wi_eligible(p)) return ALGO_WI3X3;
-        if (conv3x3_ws_eligible(p)) return ALGO_WS3X3;
-        if (conv3x3_eligible(p)) return ALGO_DIRECT3X3;
-        return ALGO_IM2COL;
-    }
     const int wm = winograd_mode();
     const bool wino = wm != 0 && winograd_eligible(p, winograd_max_pixels());
     if (p->c <= 4 && first_conv_eligible(p)) return ALGO_FIRST;
@@ -334,7 +307,7 @@ static ConvKey conv_key(const osh_conv_params *p) {
 
 // Which kernel and shape each packed weight buffer was laid out for.  The
 // layout depends on the kernel choice, which the options "winograd",
-// "winograd_max_pixels", "conv16_variant" -2 and "pointwise_variant" -2 can
+// "winograd_max_pixels" and "pointwise_variant" -2 can
 // change between packing and launch; a launch whose buffer was packed for
 // another kernel or shape is refused instead of reading a wrong layout (or
 // past its end).  Buffers this library did not pack are not checked.
@@ -467,14 +440,6 @@ static osh_status conv16_tuned_launch(const osh_conv_params *p, const float *x, 
         [&](int v) { return c3_launch(p, x, w, bias, res, act, y, st, v); }, st);
 }
 
-static osh_status residual_add(const osh_conv_params *p, const float *res, float *y, hipStream_t st) {
-    if (!res) return OSH_OK;
-    const long long n = (long long)p->n * p->m * p->oh * p->ow;
-    hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, n, res, y);
-    OSH_LAUNCH_CHECK("residual_add_kernel");
-    return OSH_OK;
-}
-
 static osh_status check_params(const osh_conv_params *p) {
     if (!p) return fail(OSH_E_INVALID, "Conv: params is NULL");
     if (p->n <= 0 || p->c <= 0 || p->h <= 0 || p->w <= 0 || p->m <= 0 || p->kh <= 0 || p->kw <= 0 ||
@@ -561,9 +526,6 @@ OSH_API osh_status osh_conv_packed_weight_bytes(const osh_conv_params *p, size_t
     case ALGO_CONV16I: *bytes = conv16_packed_bytes(p); break;
     case ALGO_WINOGRAD: *bytes = winograd_packed_bytes(p); break;
     case ALGO_PW16: *bytes = conv16_packed_bytes(p) + oihw; break;  // LDS-tile layout, then the raw GEMM operand
-    case ALGO_WI3X3: *bytes = conv3x3_wi_packed_bytes(p); break;
-    case ALGO_WS3X3: *bytes = conv3x3_ws_packed_bytes(p); break;
-    case ALGO_DIRECT3X3: *bytes = conv3x3_packed_bytes(p); break;
     default: *bytes = oihw;
     }
     return OSH_OK;
@@ -596,9 +558,6 @@ static osh_status pack_weights(const osh_conv_params *p, const float *d_w, void 
                                      hipMemcpyDeviceToDevice, to_stream(s)));
         return OSH_OK;
     }
-    if (select_algo(p) == ALGO_WI3X3) return conv3x3_wi_pack(p, d_w, d_packed, to_stream(s));
-    if (select_algo(p) == ALGO_WS3X3) return conv3x3_ws_pack(p, d_w, d_packed, to_stream(s));
-    if (select_algo(p) == ALGO_DIRECT3X3) return conv3x3_pack(p, d_w, d_packed, to_stream(s));
     size_t oihw = (size_t)p->m * (p->c / p->group) * p->kh * p->kw * sizeof(float);
     OSH_HIP_CHECK(hipMemcpyAsync(d_packed, d_w, oihw, hipMemcpyDeviceToDevice, to_stream(s)));
     return OSH_OK;
@@ -697,16 +656,6 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         OSH_LAUNCH_CHECK("wino_f23_kernel");
         return OSH_OK;
     }
-    case ALGO_WI3X3: {
-        osh_status st = conv3x3_wi_launch(p, d_x, w, d_bias, act, d_y, stream, device_cus());
-        return st != OSH_OK ? st : residual_add(p, d_res, d_y, stream);
-    }
-    case ALGO_WS3X3: {
-        osh_status st = conv3x3_ws_launch(p, d_x, w, d_bias, act, d_y, stream);
-        return st != OSH_OK ? st : residual_add(p, d_res, d_y, stream);
-    }
-    case ALGO_DIRECT3X3:
-        return conv3x3_launch(p, d_x, w, d_bias, d_res, act, d_y, stream);
     case ALGO_PW16: {
         // 0: the GEMM tile over the raw weights; 1..: the LDS-tile kernel
         const float *wraw = reinterpret_cast<const float *>(static_cast<const char *>(d_wpacked) +
@@ -780,11 +729,7 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
     if (a0 == ALGO_PW16) {  // the pointwise LDS tiles read the LDS-tile part of the packed weights
         bool narrow = false;
         for (int i = 0; i < count; i++) narrow = narrow || ps[i].ow < 16;
-        if (narrow)
-            return vec ? conv16s_group_launch_t<1, 2, 4, 1, 1, PW16_CB, true>(g, act, st)
-                       : conv16s_group_launch_t<1, 2, 4, 1, 1, PW16_CB, false>(g, act, st);
-        return vec ? conv16s_group_launch_t<1, 1, 16, 1, 1, PW16_CB, true>(g, act, st)
-                   : conv16s_group_launch_t<1, 1, 16, 1, 1, PW16_CB, false>(g, act, st);
+        return pw16_group_launch(g, act, st, narrow, vec);
     }
     // The convs run side by side, so the slowest one bounds the launch: pick
     // the tile with the smallest largest cost (then the smallest total).
@@ -800,23 +745,7 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
         }
         if (v == 0 || cmax < bmax || (cmax == bmax && csum < bsum)) best = v, bmax = cmax, bsum = csum;
     }
-#define OSH_GROUP_TILE(TM, BV, TWL)                                                     \
-    return ps[0].sh == 1 ? conv16s_group_launch_t<TM, BV, TWL, 1, 3, 1, false>(g, act, st) \
-                         : conv16s_group_launch_t<TM, BV, TWL, 2, 3, 1, false>(g, act, st)
-    switch (best) {
-    case 0: OSH_GROUP_TILE(1, 1, 16);
-    case 1: OSH_GROUP_TILE(1, 2, 16);
-    case 2: OSH_GROUP_TILE(1, 4, 16);
-    case 3: OSH_GROUP_TILE(2, 2, 16);
-    case 4: OSH_GROUP_TILE(1, 1, 8);
-    case 5: OSH_GROUP_TILE(1, 2, 8);
-    case 6: OSH_GROUP_TILE(2, 2, 8);
-    case 7: OSH_GROUP_TILE(1, 2, 4);
-    case 8: OSH_GROUP_TILE(1, 4, 4);
-    case 9: OSH_GROUP_TILE(1, 4, 8);
-    default: OSH_GROUP_TILE(2, 4, 8);
-    }
-#undef OSH_GROUP_TILE
+    return conv16s_group_launch(g, act, st, best, ps[0].sh);
 }
 
 static osh_status igemm_conv(const osh_conv_params *p, const float *d_x, const float *w, const float *d_bias,

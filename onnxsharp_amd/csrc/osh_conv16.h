@@ -345,8 +345,8 @@ __global__ __launch_bounds__(256) void conv16l_kernel(osh_conv_params p, const f
 // channels past M).  With i2c (T = 9) the k-groups of a 16-channel block run
 // through its 144 (channel, tap) terms in the im2col order instead: k-group t,
 // step s holds local term 16 t + 4 s + g = 9 ic + tap.
-__global__ void conv16_pack_kernel(int M, int C, int T, const float *__restrict__ w, float *__restrict__ out,
-                                   int i2c) {
+static __global__ void conv16_pack_kernel(int M, int C, int T, const float *__restrict__ w, float *__restrict__ out,
+                                          int i2c) {
     const long long kgroups = (long long)(C / 16) * T;
     const long long total = (long long)((M + 15) / 16) * kgroups * 256;
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -438,15 +438,8 @@ constexpr int kC16Count = sizeof(kC16) / sizeof(kC16[0]);
 constexpr C16Variant kC16w[] = {{1, 1, 0}, {1, 2, 0}, {2, 1, 0}, {2, 2, 0}};
 constexpr int kC16wCount = sizeof(kC16w) / sizeof(kC16w[0]);
 
-inline osh_status conv16w_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                 const float *res, int act, float *y, hipStream_t st, int v) {
-    switch (v) {
-    case 0: return conv16_launch_t<1, 1, 1>(p, x, w, bias, res, act, y, st);
-    case 1: return conv16_launch_t<1, 2, 1>(p, x, w, bias, res, act, y, st);
-    case 2: return conv16_launch_t<2, 1, 1>(p, x, w, bias, res, act, y, st);
-    default: return conv16_launch_t<2, 2, 1>(p, x, w, bias, res, act, y, st);
-    }
-}
+osh_status conv16w_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                          const float *res, int act, float *y, hipStream_t st, int v);
 
 // Predicted cost: rounds of waves over the SIMDs times the MFMAs of one wave,
 // inflated by its operand loads per MFMA (TM/4 weight loads and BV input
@@ -466,35 +459,7 @@ inline double conv16_cost(const osh_conv_params *p, const C16Variant &v, int cus
     return rounds * u * (9.0 * p->c / 4) * (1.0 + 0.6 * loads / u);
 }
 
-inline osh_status conv16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                const float *res, int act, float *y, hipStream_t st, int forced) {
-    int best = -1;
-    if (forced >= 0 && forced < kC16Count) {
-        best = forced;
-    } else {
-        double bc = 0;
-        const int cus = device_cus();
-        for (int i = 0; i < kC16Count; i++) {
-            if (!conv16_fits(p, kC16[i])) continue;
-            const double c = conv16_cost(p, kC16[i], cus);
-            if (best < 0 || c < bc) best = i, bc = c;
-        }
-    }
-    if (!conv16_fits(p, kC16[best])) best -= 6;  // forced LDS tile too large: same tile from L2
-    switch (best) {
-    case 0: return conv16_launch_t<1, 1>(p, x, w, bias, res, act, y, st);
-    case 1: return conv16_launch_t<2, 1>(p, x, w, bias, res, act, y, st);
-    case 2: return conv16_launch_t<4, 1>(p, x, w, bias, res, act, y, st);
-    case 3: return conv16_launch_t<1, 2>(p, x, w, bias, res, act, y, st);
-    case 4: return conv16_launch_t<2, 2>(p, x, w, bias, res, act, y, st);
-    case 5: return conv16_launch_t<4, 2>(p, x, w, bias, res, act, y, st);
-    case 6: return conv16l_launch_t<1, 1>(p, x, w, bias, res, act, y, st);
-    case 7: return conv16l_launch_t<2, 1>(p, x, w, bias, res, act, y, st);
-    case 8: return conv16l_launch_t<4, 1>(p, x, w, bias, res, act, y, st);
-    case 9: return conv16l_launch_t<1, 2>(p, x, w, bias, res, act, y, st);
-    case 10: return conv16l_launch_t<2, 2>(p, x, w, bias, res, act, y, st);
-    default: return conv16l_launch_t<4, 2>(p, x, w, bias, res, act, y, st);
-    }
-}
+osh_status conv16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                         const float *res, int act, float *y, hipStream_t st, int forced);
 
 }  // namespace osh

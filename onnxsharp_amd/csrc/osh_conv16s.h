@@ -435,52 +435,18 @@ inline osh_status conv16s_launch_s(const osh_conv_params *p, const float *x, con
 }
 
 // The kC16s tiles in the im2col order (weights packed by conv16_pack with i2c).
-inline osh_status conv16si_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                  const float *res, int act, float *y, hipStream_t st, int v) {
-    switch (v) {
-    case 0: return conv16s_launch_s<1, 1, 16, false, true>(p, x, w, bias, res, act, y, st);
-    case 1: return conv16s_launch_s<1, 2, 16, false, true>(p, x, w, bias, res, act, y, st);
-    case 2: return conv16s_launch_s<1, 4, 16, false, true>(p, x, w, bias, res, act, y, st);
-    case 3: return conv16s_launch_s<2, 2, 16, false, true>(p, x, w, bias, res, act, y, st);
-    case 4: return conv16s_launch_s<1, 1, 8, false, true>(p, x, w, bias, res, act, y, st);
-    case 5: return conv16s_launch_s<1, 2, 8, false, true>(p, x, w, bias, res, act, y, st);
-    case 6: return conv16s_launch_s<2, 2, 8, false, true>(p, x, w, bias, res, act, y, st);
-    case 7: return conv16s_launch_s<1, 2, 4, false, true>(p, x, w, bias, res, act, y, st);
-    case 8: return conv16s_launch_s<1, 4, 4, false, true>(p, x, w, bias, res, act, y, st);
-    case 9: return conv16s_launch_s<1, 4, 8, false, true>(p, x, w, bias, res, act, y, st);
-    default: return conv16s_launch_s<2, 4, 8, false, true>(p, x, w, bias, res, act, y, st);
-    }
-}
+osh_status conv16si_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                           const float *res, int act, float *y, hipStream_t st, int v);
 
-inline osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                 const float *res, int act, float *y, hipStream_t st, int v) {
-    switch (v) {
-    case 0: return conv16s_launch_s<1, 1, 16>(p, x, w, bias, res, act, y, st);
-    case 1: return conv16s_launch_s<1, 2, 16>(p, x, w, bias, res, act, y, st);
-    case 2: return conv16s_launch_s<1, 4, 16>(p, x, w, bias, res, act, y, st);
-    case 3: return conv16s_launch_s<2, 2, 16>(p, x, w, bias, res, act, y, st);
-    case 4: return conv16s_launch_s<1, 1, 8>(p, x, w, bias, res, act, y, st);
-    case 5: return conv16s_launch_s<1, 2, 8>(p, x, w, bias, res, act, y, st);
-    case 6: return conv16s_launch_s<2, 2, 8>(p, x, w, bias, res, act, y, st);
-    case 7: return conv16s_launch_s<1, 2, 4>(p, x, w, bias, res, act, y, st);
-    case 8: return conv16s_launch_s<1, 4, 4>(p, x, w, bias, res, act, y, st);
-    case 9: return conv16s_launch_s<1, 4, 8>(p, x, w, bias, res, act, y, st);
-    default: return conv16s_launch_s<2, 4, 8>(p, x, w, bias, res, act, y, st);
-    }
-}
+osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                          const float *res, int act, float *y, hipStream_t st, int v);
 
 // XCD-banded versions of the 16-column tiles (ids after the one-wave tiles).
 constexpr C16sVariant kC16sx[] = {{1, 2, 16}, {1, 4, 16}, {2, 2, 16}};
 constexpr int kC16sxCount = sizeof(kC16sx) / sizeof(kC16sx[0]);
 
-inline osh_status conv16sx_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                  const float *res, int act, float *y, hipStream_t st, int v) {
-    switch (v) {
-    case 0: return conv16s_launch_s<1, 2, 16, true>(p, x, w, bias, res, act, y, st);
-    case 1: return conv16s_launch_s<1, 4, 16, true>(p, x, w, bias, res, act, y, st);
-    default: return conv16s_launch_s<2, 2, 16, true>(p, x, w, bias, res, act, y, st);
-    }
-}
+osh_status conv16sx_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                           const float *res, int act, float *y, hipStream_t st, int v);
 
 // ---- pointwise (1x1, stride 1, no pads): the same kernel with KS = 1 and
 // four 16-channel blocks per staged chunk; the chain is the GEMM chain over
@@ -497,26 +463,14 @@ inline bool pw16_eligible(const osh_conv_params *p) {
            (long long)((p->m + 15) / 16) * (p->c / 16) * 1024 < (1LL << 31) && p->n <= 65535;
 }
 
-template <int TM, int BV, int TWL>
-inline osh_status pw16_launch_v(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                                const float *res, int act, float *y, hipStream_t st) {
-    const bool vec = p->w % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    if (vec) return conv16s_launch_t<TM, BV, TWL, 1, 1, PW16_CB, true>(p, x, w, bias, res, act, y, st);
-    return conv16s_launch_t<TM, BV, TWL, 1, 1, PW16_CB, false>(p, x, w, bias, res, act, y, st);
-}
 
-inline osh_status pw16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
-                              const float *res, int act, float *y, hipStream_t st, int v) {
-    switch (v) {
-    case 0: return pw16_launch_v<1, 1, 16>(p, x, w, bias, res, act, y, st);
-    case 1: return pw16_launch_v<1, 2, 16>(p, x, w, bias, res, act, y, st);
-    case 2: return pw16_launch_v<1, 4, 16>(p, x, w, bias, res, act, y, st);
-    case 3: return pw16_launch_v<2, 2, 16>(p, x, w, bias, res, act, y, st);
-    case 4: return pw16_launch_v<2, 4, 16>(p, x, w, bias, res, act, y, st);
-    case 5: return pw16_launch_v<1, 2, 4>(p, x, w, bias, res, act, y, st);
-    case 6: return pw16_launch_v<1, 4, 4>(p, x, w, bias, res, act, y, st);
-    default: return pw16_launch_v<2, 4, 4>(p, x, w, bias, res, act, y, st);
-    }
-}
+osh_status pw16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                       const float *res, int act, float *y, hipStream_t st, int v);
+
+// The grouped launches (osh_conv2d_group_f32): the LDS-patch 3x3 tile `tile`
+// (an index into kC16s) at stride s, or the pointwise LDS tile (16 or, with
+// `narrow`, 4 columns wide; `vec`: 16-byte input loads).
+osh_status conv16s_group_launch(ConvGroup g, int act, hipStream_t st, int tile, int s);
+osh_status pw16_group_launch(ConvGroup g, int act, hipStream_t st, bool narrow, bool vec);
 
 }  // namespace osh

@@ -1,0 +1,39 @@
+// osh_conv_pw.hip -- launches of the pointwise LDS tiles (conv16s_kernel with KS = 1), alone and grouped.
+//
+// Tile instantiations live in translation units of their own so that the
+// library's sources compile in parallel; the kernels are in the headers.
+#include "osh_conv16s.h"
+
+namespace osh {
+
+template <int TM, int BV, int TWL>
+inline osh_status pw16_launch_v(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                                const float *res, int act, float *y, hipStream_t st) {
+    const bool vec = p->w % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (vec) return conv16s_launch_t<TM, BV, TWL, 1, 1, PW16_CB, true>(p, x, w, bias, res, act, y, st);
+    return conv16s_launch_t<TM, BV, TWL, 1, 1, PW16_CB, false>(p, x, w, bias, res, act, y, st);
+}
+
+osh_status pw16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                       const float *res, int act, float *y, hipStream_t st, int v) {
+    switch (v) {
+    case 0: return pw16_launch_v<1, 1, 16>(p, x, w, bias, res, act, y, st);
+    case 1: return pw16_launch_v<1, 2, 16>(p, x, w, bias, res, act, y, st);
+    case 2: return pw16_launch_v<1, 4, 16>(p, x, w, bias, res, act, y, st);
+    case 3: return pw16_launch_v<2, 2, 16>(p, x, w, bias, res, act, y, st);
+    case 4: return pw16_launch_v<2, 4, 16>(p, x, w, bias, res, act, y, st);
+    case 5: return pw16_launch_v<1, 2, 4>(p, x, w, bias, res, act, y, st);
+    case 6: return pw16_launch_v<1, 4, 4>(p, x, w, bias, res, act, y, st);
+    default: return pw16_launch_v<2, 4, 4>(p, x, w, bias, res, act, y, st);
+    }
+}
+
+osh_status pw16_group_launch(ConvGroup g, int act, hipStream_t st, bool narrow, bool vec) {
+    if (narrow)
+        return vec ? conv16s_group_launch_t<1, 2, 4, 1, 1, PW16_CB, true>(g, act, st)
+                   : conv16s_group_launch_t<1, 2, 4, 1, 1, PW16_CB, false>(g, act, st);
+    return vec ? conv16s_group_launch_t<1, 1, 16, 1, 1, PW16_CB, true>(g, act, st)
+               : conv16s_group_launch_t<1, 1, 16, 1, 1, PW16_CB, false>(g, act, st);
+}
+
+}  // namespace osh

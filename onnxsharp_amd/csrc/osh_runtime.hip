@@ -137,8 +137,8 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         return OSH_OK;
     }
     if (strcmp(key, "conv16_variant") == 0) {
-        if (value < -2 || value >= conv16_variant_count())
-            return fail(OSH_E_INVALID, "conv16_variant %d out of range [-2, %d)", value, conv16_variant_count());
+        if (value < -1 || value >= conv16_variant_count())
+            return fail(OSH_E_INVALID, "conv16_variant %d out of range [-1, %d)", value, conv16_variant_count());
         g_conv16_variant = value;
         return OSH_OK;
     }

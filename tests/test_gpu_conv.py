@@ -201,39 +201,6 @@ def test_conv16_is_the_nchwc_chain(cuda, oracle, name, xs, ws, attrs):
         N.call("osh_config_set", b"conv16_variant", -1)
 
 
-WS_CASES = [
-    ("wi_c2_64to64_160", (1, 64, 160, 160), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1]), True),
-    ("wi_32to40_partial", (1, 32, 18, 24), (40, 32, 3, 3), dict(pads=[1, 1, 1, 1]), True),
-    ("wi_16to16_batch2", (2, 16, 12, 16), (16, 16, 3, 3), dict(pads=[1, 1, 1, 1]), True),
-    ("ws_c3b_128to256_s2", (1, 128, 80, 80), (256, 128, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), False),
-    ("ws_64to64_s2", (1, 64, 80, 80), (64, 64, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), False),
-]
-
-
-@pytest.mark.parametrize("name,xs,ws,attrs,exact", WS_CASES, ids=[c[0] for c in WS_CASES])
-def test_weight_stationary_kernels(cuda, oracle, name, xs, ws, attrs, exact):
-    # conv16_variant = -2 routes 3x3 convolutions to the weight-stationary
-    # kernels: the wave-independent one (stride 1, C = 16/32/64) adds in the
-    # NCHWc order and must match that chain bit for bit; the split-K one
-    # (stride 2) sums 16-channel partials and stays within the FP32 bar.
-    from onnxsharp_amd import native as N
-    seed = sum(xs) * 5 + sum(ws)
-    x = synth.uniform(seed, xs)
-    w = synth.normal(seed + 1, ws, 0, 0.05)
-    b = synth.normal(seed + 2, (ws[0],), 0, 0.01)
-    N.call("osh_config_set", b"exact_silu", 1)
-    N.call("osh_config_set", b"conv16_variant", -2)
-    try:
-        y, p = run_conv(cuda, x, w, b, "Silu", **attrs)
-    finally:
-        N.call("osh_config_set", b"exact_silu", 0)
-        N.call("osh_config_set", b"conv16_variant", -1)
-    ref = oracle_conv(oracle, x, w, b, p, "Silu", order=oracle.ORDER_NCHWC)
-    assert_fp32_close(y, ref, name)
-    if exact:
-        assert np.array_equal(y, ref), f"{name}: max |d| {np.abs(y - ref).max():.3e}"
-
-
 RESIDUAL_CASES = [
     # (name, x, w, attrs, conv16_variant) -- one per kernel family of the dispatch
     ("conv16_3x3_64to64_40", (1, 64, 40, 40), (64, 64, 3, 3), dict(pads=[1, 1, 1, 1]), 4),
@@ -255,8 +222,6 @@ RESIDUAL_CASES = [
     ("winograd_32to40_18x24", (1, 32, 18, 24), (40, 32, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
     ("winograd_c24_batch2_odd", (2, 24, 13, 11), (16, 24, 3, 3), dict(pads=[1, 1, 1, 1]), -1),
     ("im2col_dilated_5x5", (1, 5, 23, 21), (7, 5, 5, 5), dict(pads=[4, 4, 4, 4], dilations=[2, 2]), -1),
-    ("wave_independent_16", (1, 16, 24, 32), (16, 16, 3, 3), dict(pads=[1, 1, 1, 1]), -2),
-    ("weight_stationary_s2", (1, 64, 40, 40), (64, 64, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1]), -2),
 ]
 
 
