@@ -105,6 +105,10 @@ OSH_API osh_status osh_device_synchronize(void);
  *   "pointwise_variants" (get only): N.
  *                 The -2 setting of "pointwise_variant" changes the packed
  *                 weight layout: pack again after changing it.
+ *   Environment: ONNXSHARP_HIP_TUNE_DB=<path> keeps the first-use tile
+ *                 choices in a text file: read on first use, each new choice
+ *                 appended, so later processes choose the same tiles without
+ *                 timing them.
  *   "dqmm_variant": 0 (default) = osh_dqmm_u8s8 runs a min/max launch and
  *                 then one launch that quantizes A and multiplies; 1 = min/max,
  *                 quantize and GEMM as three launches.  Both give identical

@@ -33,7 +33,10 @@
 //
 // Bias and the fused activation (Relu / SiLU, GraphFusion.cs:1713-1718) are
 // applied in registers before the single store, then an optional residual.
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <string>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -296,13 +299,78 @@ static ConvAlgo select_algo(const osh_conv_params *p) {
 // the tiles, writing the real output every time) and remembers the winner
 // per shape.  Launches recorded
 // into a graph before that use the cost model.
+//
+// With ONNXSHARP_HIP_TUNE_DB=<path> the choices persist: the table is read
+// from that text file on first use and every new choice is appended to it,
+// so a later process (a deployment, a profiler run) makes the same choices
+// without timing.  The first line names the format and the size of each tile
+// family; a file written for other families is started afresh.  A recorded
+// tile that does not fit its shape is tuned again.
 static std::mutex g_tune_mu;
 using ConvKey = std::tuple<int, int, int, int, int, int, int, int, int, int, int, int, int, int>;
 static std::map<std::tuple<int, ConvKey>, int> g_tuned;
+static bool g_tune_db_read = false;
 
 static ConvKey conv_key(const osh_conv_params *p) {
     return std::make_tuple(p->n, p->c, p->h, p->w, p->m, p->kh, p->kw, p->sh, p->sw, p->pt, p->pl, p->oh, p->ow,
                            p->group);
+}
+
+static std::string tune_db_header() {
+    char h[128];
+    snprintf(h, sizeof(h), "onnxsharp-hip tune v1 conv3x3=%d pointwise=%d im2col3x3=%d", conv16_variant_count(),
+             pointwise_variant_count(), im2col3x3_variant_count());
+    return h;
+}
+
+static const char *tune_db_path() {
+    const char *e = getenv("ONNXSHARP_HIP_TUNE_DB");
+    return (e && *e) ? e : nullptr;
+}
+
+// Reads the database once (g_tune_mu held).
+static void tune_db_read_locked() {
+    if (g_tune_db_read) return;
+    g_tune_db_read = true;
+    const char *path = tune_db_path();
+    if (!path) return;
+    FILE *f = fopen(path, "r");
+    if (!f) return;
+    char line[512];
+    const std::string want = tune_db_header();
+    bool ok = fgets(line, sizeof(line), f) && std::string(line).substr(0, want.size()) == want;
+    int v[16];
+    while (ok && fgets(line, sizeof(line), f)) {
+        if (sscanf(line, "%d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d", &v[0], &v[1], &v[2], &v[3], &v[4], &v[5],
+                   &v[6], &v[7], &v[8], &v[9], &v[10], &v[11], &v[12], &v[13], &v[14], &v[15]) != 16)
+            continue;
+        g_tuned[std::make_tuple(v[0], std::make_tuple(v[1], v[2], v[3], v[4], v[5], v[6], v[7], v[8], v[9], v[10],
+                                                      v[11], v[12], v[13], v[14]))] = v[15];
+    }
+    fclose(f);
+    if (!ok) {  // another format: start the file afresh
+        FILE *w = fopen(path, "w");
+        if (w) {
+            fprintf(w, "%s\n", want.c_str());
+            fclose(w);
+        }
+    }
+}
+
+// Appends one choice (g_tune_mu held).
+static void tune_db_append_locked(int tag, const ConvKey &k, int v) {
+    const char *path = tune_db_path();
+    if (!path) return;
+    FILE *probe = fopen(path, "r");
+    const bool fresh = probe == nullptr;
+    if (probe) fclose(probe);
+    FILE *f = fopen(path, "a");
+    if (!f) return;
+    if (fresh) fprintf(f, "%s\n", tune_db_header().c_str());
+    fprintf(f, "%d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d\n", tag, std::get<0>(k), std::get<1>(k),
+            std::get<2>(k), std::get<3>(k), std::get<4>(k), std::get<5>(k), std::get<6>(k), std::get<7>(k),
+            std::get<8>(k), std::get<9>(k), std::get<10>(k), std::get<11>(k), std::get<12>(k), std::get<13>(k), v);
+    fclose(f);
 }
 
 // Which kernel and shape each packed weight buffer was laid out for.  The
@@ -392,8 +460,10 @@ static osh_status tuned_launch(const osh_conv_params *p, int tag, int count, int
     const auto key = std::make_tuple(tag, conv_key(p));
     {
         std::lock_guard<std::mutex> lk(g_tune_mu);
+        tune_db_read_locked();
         auto it = g_tuned.find(key);
-        if (it != g_tuned.end()) return launch(it->second);
+        if (it != g_tuned.end() && it->second >= 0 && it->second < count && fits(it->second))
+            return launch(it->second);
     }
     if (capturing(st)) return launch(-1);
     hipEvent_t e0, e1;
@@ -429,6 +499,7 @@ static osh_status tuned_launch(const osh_conv_params *p, int tag, int count, int
     {
         std::lock_guard<std::mutex> lk(g_tune_mu);
         g_tuned[key] = best;
+        tune_db_append_locked(tag, std::get<1>(key), best);
     }
     return OSH_OK;  // y already holds the result (every tile computes the same values)
 }
