@@ -93,7 +93,8 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 weights held in LDS; 12..22: input patch staged in LDS
  *                 and shared by a workgroup's four waves, stride 1 or 2;
  *                 23..26: tiles 0, 3, 1, 4 with one wave per workgroup;
- *                 27..N-1: tiles 13, 14, 15 with XCD-banded workgroups).
+ *                 27..N-1: XCD-banded 16-column tiles, TM x BV = 1x2, 1x4,
+ *                 2x2, 1x7, 1x8).
  *                 Initial value from ONNXSHARP_HIP_CONV16_VARIANT.
  *   "conv16_variants" (get only): N, the number of 3x3 tiles.
  *   "pointwise_variant": -1 (default) = 1x1 stride-1 convolutions with
@@ -220,9 +221,18 @@ OSH_API osh_status osh_conv_packed_weight_bytes(const osh_conv_params *p, size_t
 OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *d_w, void *d_packed,
                                          osh_stream s);
 
+/* The library remembers which kernel and shape each packed buffer was laid out
+ * for and refuses a launch with a mismatching one.  A caller that releases or
+ * reuses memory it allocated itself (not through osh_malloc, whose osh_free
+ * does this) calls osh_conv_forget_pack on the range so that the record does
+ * not outlive the buffer.  No counterpart in the reference (its packed weights
+ * are managed objects). */
+OSH_API osh_status osh_conv_forget_pack(const void *d_packed, size_t bytes);
+
 /* Conv forward, NCHW f32 in and out, bias (length m) optional, fused
  * activation act (ConvLayer.Forward, src/OnnxSharp/Ops/DnnOps.cs:411-500).
- * d_wpacked is the output of osh_conv_pack_weights for the same p. */
+ * d_wpacked is the output of osh_conv_pack_weights for the same p.  The
+ * output must not overlap the input (OSH_E_INVALID). */
 OSH_API osh_status osh_conv2d_f32(const osh_conv_params *p, const float *d_x, const void *d_wpacked,
                                   const float *d_bias, int act, float *d_y, osh_stream s);
 

@@ -378,18 +378,49 @@ static void tune_db_append_locked(int tag, const ConvKey &k, int v) {
 // "winograd_max_pixels" and "pointwise_variant" -2 can
 // change between packing and launch; a launch whose buffer was packed for
 // another kernel or shape is refused instead of reading a wrong layout (or
-// past its end).  Buffers this library did not pack are not checked.
+// past its end).  Buffers this library did not pack are not checked.  An
+// entry covers [address, address + bytes): packing into a range drops every
+// entry it overlaps (memory reused for new weights), and osh_free /
+// osh_conv_forget_pack drop the entries of a range the caller releases.
+struct PackTag {
+    int algo;
+    ConvKey key;
+    size_t bytes;
+};
 static std::mutex g_packs_mu;
-static std::map<const void *, std::pair<int, ConvKey>> g_packs;
+static std::map<uintptr_t, PackTag> g_packs;  // by start address
 
-static void record_pack(const osh_conv_params *p, const void *d_packed) {
-    std::lock_guard<std::mutex> lk(g_packs_mu);
-    g_packs[d_packed] = std::make_pair((int)select_algo(p), conv_key(p));
+// Erases the entries overlapping [a, a + bytes) (g_packs_mu held).
+static void forget_range_locked(uintptr_t a, size_t bytes) {
+    auto it = g_packs.lower_bound(a);
+    if (it != g_packs.begin()) {
+        auto prev = std::prev(it);
+        if (prev->first + prev->second.bytes > a) it = prev;
+    }
+    while (it != g_packs.end() && it->first < a + (bytes ? bytes : 1)) it = g_packs.erase(it);
 }
 
+static void record_pack(const osh_conv_params *p, const void *d_packed, size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_packs_mu);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(d_packed);
+    forget_range_locked(a, bytes);
+    g_packs[a] = PackTag{(int)select_algo(p), conv_key(p), bytes ? bytes : 1};
+}
+
+// Drops the entry that starts at d_ptr and every entry inside the
+// allocation it starts (osh_free passes the allocation base).
 void forget_pack(const void *d_ptr) {
     std::lock_guard<std::mutex> lk(g_packs_mu);
-    g_packs.erase(d_ptr);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(d_ptr);
+    size_t span = 1;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, const_cast<void *>(d_ptr)) == hipSuccess &&
+        reinterpret_cast<uintptr_t>(base) == a)
+        span = size;
+    else
+        (void)hipGetLastError();
+    forget_range_locked(a, span);
 }
 
 static bool capturing(hipStream_t st) {
@@ -608,8 +639,19 @@ OSH_API osh_status osh_conv_pack_weights(const osh_conv_params *p, const float *
     if (st != OSH_OK) return st;
     if (!d_w || !d_packed) return fail(OSH_E_INVALID, "Conv pack: NULL pointer");
     st = pack_weights(p, d_w, d_packed, s);
-    if (st == OSH_OK) record_pack(p, d_packed);
+    if (st == OSH_OK) {
+        size_t bytes = 0;
+        if (osh_conv_packed_weight_bytes(p, &bytes) != OSH_OK) bytes = 1;
+        record_pack(p, d_packed, bytes);
+    }
     return st;
+}
+
+OSH_API osh_status osh_conv_forget_pack(const void *d_packed, size_t bytes) {
+    if (!d_packed) return fail(OSH_E_INVALID, "Conv forget pack: NULL pointer");
+    std::lock_guard<std::mutex> lk(g_packs_mu);
+    forget_range_locked(reinterpret_cast<uintptr_t>(d_packed), bytes);
+    return OSH_OK;
 }
 
 }  // extern "C"
@@ -851,15 +893,25 @@ static osh_status igemm_conv(const osh_conv_params *p, const float *d_x, const f
     }
 }
 
+static size_t x_bytes(const osh_conv_params *p) { return (size_t)p->n * p->c * p->h * p->w * sizeof(float); }
+static size_t y_bytes(const osh_conv_params *p) { return (size_t)p->n * p->m * p->oh * p->ow * sizeof(float); }
+static bool ranges_overlap(const void *a, size_t na, const void *b, size_t nb) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a && b && a0 < b0 + nb && b0 < a0 + na;
+}
+
 static osh_status check_launch(const osh_conv_params *p, const float *d_x, const void *d_wpacked, int act,
                                 float *d_y) {
     osh_status st = check_params(p);
     if (st != OSH_OK) return st;
     if (!d_x || !d_wpacked || !d_y) return fail(OSH_E_INVALID, "Conv: NULL tensor pointer");
     if (act < OSH_ACT_NONE || act > OSH_ACT_SILU) return fail(OSH_E_INVALID, "Conv: unknown activation %d", act);
+    // in place is refused: the tiles read input halos other workgroups write
+    if (ranges_overlap(d_x, x_bytes(p), d_y, y_bytes(p)))
+        return fail(OSH_E_INVALID, "Conv: the output overlaps the input");
     std::lock_guard<std::mutex> lk(g_packs_mu);
-    auto it = g_packs.find(d_wpacked);
-    if (it != g_packs.end() && (it->second.first != (int)select_algo(p) || it->second.second != conv_key(p)))
+    auto it = g_packs.find(reinterpret_cast<uintptr_t>(d_wpacked));
+    if (it != g_packs.end() && (it->second.algo != (int)select_algo(p) || it->second.key != conv_key(p)))
         return fail(OSH_E_INVALID,
                     "Conv: the weights were packed for another kernel or shape (pack them again after changing "
                     "the conv options)");
@@ -886,14 +938,18 @@ OSH_API osh_status osh_conv2d_group_f32(int count, const osh_conv_params *ps, co
     for (int i = 0; i < count; i++) {
         osh_status st = check_launch(&ps[i], d_xs[i], d_ws[i], act, d_ys[i]);
         if (st != OSH_OK) return st;
-        const float *r = d_res ? d_res[i] : nullptr;
-        if (r) {
-            const uintptr_t bytes = (uintptr_t)ps[i].n * ps[i].m * ps[i].oh * ps[i].ow * sizeof(float);
-            const uintptr_t r0 = reinterpret_cast<uintptr_t>(r), y0 = reinterpret_cast<uintptr_t>(d_ys[i]);
-            if (r0 < y0 + bytes && y0 < r0 + bytes)
-                return fail(OSH_E_INVALID, "Conv group: a residual overlaps its output");
-        }
     }
+    // The members run side by side in one launch: no output may overlap any
+    // member's input, residual or output (the own input is checked above).
+    for (int i = 0; i < count; i++)
+        for (int j = 0; j < count; j++) {
+            const float *rj = d_res ? d_res[j] : nullptr;
+            if (ranges_overlap(d_ys[i], y_bytes(&ps[i]), rj, y_bytes(&ps[j])))
+                return fail(OSH_E_INVALID, "Conv group: output %d overlaps the residual of conv %d", i, j);
+            if (i != j && (ranges_overlap(d_ys[i], y_bytes(&ps[i]), d_xs[j], x_bytes(&ps[j])) ||
+                           ranges_overlap(d_ys[i], y_bytes(&ps[i]), d_ys[j], y_bytes(&ps[j]))))
+                return fail(OSH_E_INVALID, "Conv group: output %d overlaps the input or output of conv %d", i, j);
+        }
     return conv2d_group(count, ps, d_xs, d_ws, d_biases, act, d_res, d_ys, to_stream(s));
 }
 
@@ -902,9 +958,7 @@ OSH_API osh_status osh_conv2d_add_f32(const osh_conv_params *p, const float *d_x
     osh_status st = check_launch(p, d_x, d_wpacked, act, d_y);
     if (st != OSH_OK) return st;
     if (!d_res) return fail(OSH_E_INVALID, "Conv+Add: residual is NULL");
-    const uintptr_t bytes = (uintptr_t)p->n * p->m * p->oh * p->ow * sizeof(float);
-    const uintptr_t r0 = reinterpret_cast<uintptr_t>(d_res), y0 = reinterpret_cast<uintptr_t>(d_y);
-    if (r0 < y0 + bytes && y0 < r0 + bytes)
+    if (ranges_overlap(d_res, y_bytes(p), d_y, y_bytes(p)))
         return fail(OSH_E_INVALID, "Conv+Add: the residual overlaps the output");
     return conv2d(p, d_x, d_wpacked, d_bias, act, d_res, d_y, to_stream(s));
 }

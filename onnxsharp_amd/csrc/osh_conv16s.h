@@ -442,7 +442,10 @@ osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float 
                           const float *res, int act, float *y, hipStream_t st, int v);
 
 // XCD-banded versions of the 16-column tiles (ids after the one-wave tiles).
-constexpr C16sVariant kC16sx[] = {{1, 2, 16}, {1, 4, 16}, {2, 2, 16}};
+// BV = 7 and 8: taller tiles that spread a large map's 16x16 blocks evenly
+// over the SIMDs (64 -> 64 at 160x160: 230 workgroups, one wave per SIMD with
+// seven blocks, instead of 400 with four, two waves on 576 SIMDs).
+constexpr C16sVariant kC16sx[] = {{1, 2, 16}, {1, 4, 16}, {2, 2, 16}, {1, 7, 16}, {1, 8, 16}};
 constexpr int kC16sxCount = sizeof(kC16sx) / sizeof(kC16sx[0]);
 
 osh_status conv16sx_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,

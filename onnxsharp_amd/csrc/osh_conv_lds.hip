@@ -28,7 +28,9 @@ osh_status conv16sx_launch(const osh_conv_params *p, const float *x, const float
     switch (v) {
     case 0: return conv16s_launch_s<1, 2, 16, true>(p, x, w, bias, res, act, y, st);
     case 1: return conv16s_launch_s<1, 4, 16, true>(p, x, w, bias, res, act, y, st);
-    default: return conv16s_launch_s<2, 2, 16, true>(p, x, w, bias, res, act, y, st);
+    case 2: return conv16s_launch_s<2, 2, 16, true>(p, x, w, bias, res, act, y, st);
+    case 3: return conv16s_launch_s<1, 7, 16, true>(p, x, w, bias, res, act, y, st);
+    default: return conv16s_launch_s<1, 8, 16, true>(p, x, w, bias, res, act, y, st);
     }
 }
 

@@ -96,8 +96,23 @@ class ConvLayer:
         N.call("osh_conv_packed_weight_bytes", C.byref(p), C.byref(nbytes))
         buf = torch.empty(max(1, nbytes.value), dtype=torch.uint8, device=w.device)
         N.call("osh_conv_pack_weights", C.byref(p), _ptr(w), _ptr(buf), C.c_void_p(_stream()))
+        self._release_pack()
         self._packed = ((w.data_ptr(), tuple(w.shape), tuple(x_shape), w._version), p, buf)
         return p, buf
+
+    def _release_pack(self):
+        """Drop the library's record of the packed buffer this layer is about
+        to let go (torch may hand its memory to another tensor)."""
+        if self._packed is not None:
+            buf = self._packed[2]
+            N.lib().osh_conv_forget_pack(_ptr(buf), buf.numel())
+            self._packed = None
+
+    def __del__(self):
+        try:
+            self._release_pack()
+        except Exception:  # interpreter shutdown: nothing left to keep consistent
+            pass
 
     def forward(self, x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -88,6 +88,7 @@ _SIGS = {
     "osh_conv_resolve": ([C.POINTER(ConvAttrs), _i64p, _i64p, C.POINTER(ConvParams)], _i),
     "osh_conv_packed_weight_bytes": ([C.POINTER(ConvParams), C.POINTER(_sz)], _i),
     "osh_conv_pack_weights": ([C.POINTER(ConvParams), _vp, _vp, _vp], _i),
+    "osh_conv_forget_pack": ([_vp, _sz], _i),
     "osh_conv2d_f32": ([C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp], _i),
     "osh_conv2d_add_f32": ([C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp, _vp], _i),
     "osh_conv2d_group_f32": ([_i, C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp, _vp], _i),

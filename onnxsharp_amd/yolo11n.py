@@ -687,6 +687,7 @@ class Frame:
         self.graph = None
         self._calls = []
         self._keep = []
+        self._packs = []  # packed conv weights: their records are dropped in close()
         for op in model.ops:
             self._calls.append(self._prepare(op))
         torch.cuda.synchronize()
@@ -738,6 +739,7 @@ class Frame:
         N.call("osh_conv_pack_weights", C.byref(p), C.c_void_p(w.data_ptr()), C.c_void_p(packed.data_ptr()),
                self.stream)
         self._keep += [p, w, b, packed]
+        self._packs.append(packed)
         return p, packed, b
 
     def _prepare_other(self, op):
@@ -943,6 +945,9 @@ class Frame:
         if self.graph is not None:
             N.call("osh_graph_destroy", self.graph)
             self.graph = None
+        for buf in self._packs:
+            N.call("osh_conv_forget_pack", C.c_void_p(buf.data_ptr()), buf.numel() * buf.element_size())
+        self._packs = []
         for ev in self.events.values():
             N.call("osh_event_destroy", ev)
         self.events = {}

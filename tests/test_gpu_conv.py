@@ -407,6 +407,88 @@ def test_launch_refuses_weights_packed_for_another_kernel(cuda):
     assert y.shape == (1, 64, 20, 20)
 
 
+def test_pack_record_follows_the_memory(cuda):
+    """Packing into memory drops the records of whatever it overlaps, and
+    osh_conv_forget_pack drops a released range: a buffer reused for another
+    shape's weights is not refused for its old layout."""
+    import torch
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    x1 = _t(synth.uniform(51, (1, 64, 20, 20)), cuda)
+    w1 = _t(synth.normal(52, (64, 64, 3, 3), 0, 0.05), cuda)
+    x2 = _t(synth.uniform(53, (1, 32, 16, 16)), cuda)
+    w2 = _t(synth.normal(54, (48, 32, 1, 1), 0, 0.05), cuda)
+    l1, l2 = ConvLayer(pads=[1, 1, 1, 1]), ConvLayer()
+    p1 = l1.resolve(tuple(x1.shape), tuple(w1.shape))
+    p2 = l2.resolve(tuple(x2.shape), tuple(w2.shape))
+    n1, n2 = C.c_size_t(), C.c_size_t()
+    N.call("osh_conv_packed_weight_bytes", C.byref(p1), C.byref(n1))
+    N.call("osh_conv_packed_weight_bytes", C.byref(p2), C.byref(n2))
+    arena = torch.empty(max(n1.value, n2.value) + 4096, dtype=torch.uint8, device=cuda)
+    ptr = C.c_void_p(arena.data_ptr())
+    y1 = torch.empty((1, 64, 20, 20), device=cuda)
+    y2 = torch.empty((1, 48, 16, 16), device=cuda)
+    N.call("osh_conv_pack_weights", C.byref(p1), C.c_void_p(w1.data_ptr()), ptr, None)
+    N.call("osh_conv2d_f32", C.byref(p1), C.c_void_p(x1.data_ptr()), ptr, None, N.ACT_NONE,
+           C.c_void_p(y1.data_ptr()), None)
+    with pytest.raises(N.OshError, match="packed for another kernel"):  # still conv 1's layout
+        N.call("osh_conv2d_f32", C.byref(p2), C.c_void_p(x2.data_ptr()), ptr, None, N.ACT_NONE,
+               C.c_void_p(y2.data_ptr()), None)
+    # packing conv 2 into the same memory replaces the record
+    N.call("osh_conv_pack_weights", C.byref(p2), C.c_void_p(w2.data_ptr()), ptr, None)
+    N.call("osh_conv2d_f32", C.byref(p2), C.c_void_p(x2.data_ptr()), ptr, None, N.ACT_NONE,
+           C.c_void_p(y2.data_ptr()), None)
+    ref2 = l2.forward(x2, w2)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, ref2)
+    # a forgotten range is unchecked memory again (the caller owns its contents)
+    N.call("osh_conv_pack_weights", C.byref(p1), C.c_void_p(w1.data_ptr()), ptr, None)
+    N.call("osh_conv_forget_pack", ptr, arena.numel())
+    N.call("osh_conv_pack_weights", C.byref(p2), C.c_void_p(w2.data_ptr()), ptr, None)
+    N.call("osh_conv2d_f32", C.byref(p2), C.c_void_p(x2.data_ptr()), ptr, None, N.ACT_NONE,
+           C.c_void_p(y2.data_ptr()), None)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, ref2)
+
+
+def test_conv_refuses_overlapping_outputs(cuda):
+    """A conv writing over its own input, and a group whose member's output
+    overlaps another member's input, residual or output, are refused (the
+    tiles of one launch run side by side); disjoint slices of one buffer are
+    accepted and equal separate launches."""
+    import torch
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    x = _t(synth.uniform(61, (1, 64, 20, 20)), cuda)
+    w = _t(synth.normal(62, (64, 64, 1, 1), 0, 0.05), cuda)
+    layer = ConvLayer()
+    y = layer.forward(x, w)
+    _, p, buf = layer._packed
+    big = torch.zeros((1, 256, 20, 20), device=cuda)
+    sl = lambda c0: C.c_void_p(big[:, c0:c0 + 64].data_ptr())
+    with pytest.raises(N.OshError, match="overlaps the input"):  # in place
+        N.call("osh_conv2d_f32", C.byref(p), sl(0), C.c_void_p(buf.data_ptr()), None, N.ACT_NONE, sl(32), None)
+    pa = (N.ConvParams * 2)(p, p)
+    arr = lambda *ps: (C.c_void_p * 2)(*[v.value if isinstance(v, C.c_void_p) else v for v in ps])
+    wb = C.c_void_p(buf.data_ptr())
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    cases = [  # channel ranges: x0, x1 -> y0, y1 (64 channels each)
+        ("output 0 over input 1", arr(sl(0), sl(128)), arr(sl(96), sl(192)), None),
+        ("output 0 is input 1", arr(sl(0), sl(128)), arr(sl(128), sl(192)), None),
+        ("outputs overlap", arr(sl(0), sl(64)), arr(sl(128), sl(160)), None),
+        ("output 1 over residual 0", arr(sl(0), sl(64)), arr(sl(128), sl(192)), arr(sl(192), None)),
+    ]
+    for what, xs, ys, rs in cases:
+        with pytest.raises(N.OshError, match="overlaps"):
+            N.check(N.lib().osh_conv2d_group_f32(2, pa, xs, arr(wb, wb), None, N.ACT_NONE, rs, ys, st))
+    big[:, 0:64] = x
+    big[:, 64:128] = x
+    N.check(N.lib().osh_conv2d_group_f32(2, pa, arr(sl(0), sl(64)), arr(wb, wb), None, N.ACT_NONE, None,
+                                         arr(sl(128), sl(192)), st))
+    torch.cuda.synchronize()
+    assert torch.equal(big[:, 128:192], y) and torch.equal(big[:, 192:256], y)
+
+
 GROUP_CASES = [
     # (name, [(x shape, w shape, group)], act, residual) -- the head's layer kinds
     ("head_3x3_nchwc", [((1, 64, 80, 80), (64, 64, 3, 3), 1), ((1, 128, 40, 40), (64, 128, 3, 3), 1),
