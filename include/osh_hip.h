@@ -300,6 +300,62 @@ OSH_API osh_status osh_gemm_ex_f32(int trans_a, int trans_b, int m, int n, int k
                                    const float *d_b, float beta, const float *d_c, int64_t c_len, float *d_y,
                                    void *d_workspace, osh_stream s);
 
+/* ------------------------------------------------ pointwise conv chains */
+
+/* A chain of convolutions over the same H x W map run as one launch, each
+ * workgroup taking 16 consecutive pixels through every stage: stage k is a
+ * 1x1 conv (stride 1, no pads, group 1) whose input channels are the concat,
+ * in order, of up to OSH_PW_MAX_SRC parts -- tensors in memory or outputs of
+ * earlier stages -- or, as stage 0 only, a 3x3 depthwise conv (stride 1,
+ * pad 1).  Every stage computes exactly what osh_conv2d_f32 / osh_conv2d_add_f32
+ * compute for it (same chain, activation, residual), writes its whole output
+ * to y, and keeps its pixels on chip for the later stages, so a chain gives
+ * the bits of its convs launched one after another with one launch instead
+ * of several.  This is a launch fusion with no counterpart in the reference,
+ * for the frame executor (OnnxSharp's graph keeps the nodes; the backend
+ * fuses their launches).
+ *
+ * Conditions (OSH_E_INVALID otherwise): batch 1; a 1x1 stage's weights packed
+ * by osh_conv_pack_weights for that conv (the pointwise LDS-tile layout, so
+ * C % 16 == 0), m % 16 == 0 and every part's channel count a multiple of 16;
+ * a depthwise stage's weights are the raw [m][1][3][3] of a conv with m == c;
+ * every y non-NULL; no y overlaps another y.  A 1x1 stage reads and writes
+ * only its own 16 pixels and a tile runs its stages in order, so within one
+ * chain a stage's y may overlap a tensor the same or an earlier stage reads
+ * from memory (at whole channel planes: e.g. writing over the shortcut a
+ * previous stage added); any other overlap of a y with a tensor the launch
+ * reads -- another chain's, a later stage's, a depthwise stage's input -- is
+ * refused. */
+#define OSH_PW_MAX_SRC 3
+#define OSH_PW_MAX_STAGES 5
+#define OSH_PW_MAX_CHAINS 3
+enum { OSH_PW_1X1 = 0, OSH_PW_DW3X3 = 1 };
+
+typedef struct {
+    int kind;                             /* OSH_PW_1X1 or OSH_PW_DW3X3 */
+    int m;                                /* output channels */
+    int act;                              /* OSH_ACT_NONE / RELU / SILU */
+    int nsrc;                             /* input parts, concat order */
+    int src_stage[OSH_PW_MAX_SRC];        /* -1: the tensor src[i]; k >= 0: stage k's output */
+    const float *src[OSH_PW_MAX_SRC];     /* [c_i, H, W] when src_stage[i] == -1; for k >= 0 NULL (the
+                                             whole output) or a pointer into stage k's y at a channel */
+    int src_c[OSH_PW_MAX_SRC];            /* channels of part i */
+    const void *w;                        /* packed weights (1x1) or raw [m][1][3][3] (depthwise) */
+    const float *bias;                    /* [m] or NULL */
+    int res_stage;                        /* -1: res (may be NULL); k >= 0: stage k's output */
+    const float *res;                     /* [m, H, W] added after the activation */
+    float *y;                             /* [m, H, W] */
+} osh_pw_stage;
+
+typedef struct {
+    int h, w;                             /* map size (batch 1) */
+    int nstages;
+    osh_pw_stage stage[OSH_PW_MAX_STAGES];
+} osh_pw_chain;
+
+/* Runs `count` independent chains (1..OSH_PW_MAX_CHAINS) in one launch. */
+OSH_API osh_status osh_pw_chain_f32(int count, const osh_pw_chain *chains, osh_stream s);
+
 /* ------------------------------------------- DynamicQuantizeMatMul (A13-A15) */
 
 /* Bytes of the packed int8 weight buffer and of the scratch buffer that

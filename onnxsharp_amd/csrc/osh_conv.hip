@@ -40,6 +40,7 @@
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <utility>
 
 #include "osh_conv16.h"
 #include "osh_conv16s.h"
@@ -316,6 +317,18 @@ static ConvKey conv_key(const osh_conv_params *p) {
                            p->group);
 }
 
+// One key for a group of convs: each field of the first member's key mixed
+// with the others' (a collision could only pick a different, equally exact
+// tile).
+template <size_t... I>
+static ConvKey mix_key_impl(const ConvKey &a, const ConvKey &b, std::index_sequence<I...>) {
+    return std::make_tuple((int)((unsigned)std::get<I>(a) * 1000003u ^ (unsigned)std::get<I>(b))...);
+}
+static ConvKey mix_key(const ConvKey &a, const ConvKey &b) {
+    return mix_key_impl(a, b, std::make_index_sequence<std::tuple_size<ConvKey>::value>{});
+}
+constexpr int kGroupTuneTag = 20;  // tuning-table tags of grouped launches (3x3, +1 pointwise)
+
 static std::string tune_db_header() {
     char h[128];
     snprintf(h, sizeof(h), "onnxsharp-hip tune v1 conv3x3=%d pointwise=%d im2col3x3=%d", conv16_variant_count(),
@@ -398,6 +411,16 @@ static void forget_range_locked(uintptr_t a, size_t bytes) {
         if (prev->first + prev->second.bytes > a) it = prev;
     }
     while (it != g_packs.end() && it->first < a + (bytes ? bytes : 1)) it = g_packs.erase(it);
+}
+
+// Whether d_w holds weights this library packed for p with the pointwise
+// LDS-tile layout (conv16 layout first), the layout the pointwise-chain
+// kernel reads.
+bool packed_for_pointwise_tiles(const osh_conv_params *p, const void *d_w) {
+    if (select_algo(p) != ALGO_PW16) return false;
+    std::lock_guard<std::mutex> lk(g_packs_mu);
+    auto it = g_packs.find(reinterpret_cast<uintptr_t>(d_w));
+    return it != g_packs.end() && it->second.algo == (int)ALGO_PW16 && it->second.key == conv_key(p);
 }
 
 static void record_pack(const osh_conv_params *p, const void *d_packed, size_t bytes) {
@@ -485,10 +508,19 @@ static osh_status c3_launch(const osh_conv_params *p, const float *x, const floa
 // Launches variant v (0 .. count-1) of a tile family, or the family's
 // cost-model pick for v < 0.  Tag separates families in the tuning table.
 template <class Fits, class Launch>
+static osh_status tuned_launch_key(const std::tuple<int, ConvKey> &key, int count, int forced, Fits fits,
+                                   Launch launch, hipStream_t st);
+
+template <class Fits, class Launch>
 static osh_status tuned_launch(const osh_conv_params *p, int tag, int count, int forced, Fits fits, Launch launch,
                                hipStream_t st) {
+    return tuned_launch_key(std::make_tuple(tag, conv_key(p)), count, forced, fits, launch, st);
+}
+
+template <class Fits, class Launch>
+static osh_status tuned_launch_key(const std::tuple<int, ConvKey> &key, int count, int forced, Fits fits,
+                                   Launch launch, hipStream_t st) {
     if (forced >= 0 || !tuning_enabled()) return launch(forced >= 0 && forced < count && fits(forced) ? forced : -1);
-    const auto key = std::make_tuple(tag, conv_key(p));
     {
         std::lock_guard<std::mutex> lk(g_tune_mu);
         tune_db_read_locked();
@@ -530,7 +562,7 @@ static osh_status tuned_launch(const osh_conv_params *p, int tag, int count, int
     {
         std::lock_guard<std::mutex> lk(g_tune_mu);
         g_tuned[key] = best;
-        tune_db_append_locked(tag, std::get<1>(key), best);
+        tune_db_append_locked(std::get<0>(key), std::get<1>(key), best);
     }
     return OSH_OK;  // y already holds the result (every tile computes the same values)
 }
@@ -839,13 +871,22 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
         OSH_LAUNCH_CHECK("dw_conv_group_kernel");
         return OSH_OK;
     }
+    // The tile is chosen like a single conv's, by first-use timing of the
+    // whole group (every tile gives every member the same bits), keyed by all
+    // members' shapes; launches recorded into a graph before that use the
+    // default below.
+    ConvKey gk = conv_key(&ps[0]);
+    for (int i = 1; i < count; i++) gk = mix_key(gk, conv_key(&ps[i]));
     if (a0 == ALGO_PW16) {  // the pointwise LDS tiles read the LDS-tile part of the packed weights
         bool narrow = false;
         for (int i = 0; i < count; i++) narrow = narrow || ps[i].ow < 16;
-        return pw16_group_launch(g, act, st, narrow, vec);
+        const int dflt = narrow ? 5 : 0;  // {1, 2, 4} on narrow maps, else {1, 1, 16}
+        return tuned_launch_key(
+            std::make_tuple(kGroupTuneTag + 1, gk), kPW16Count, -1, [](int) { return true; },
+            [&](int v) { return pw16_group_launch(g, act, st, v < 0 ? dflt : v, vec); }, st);
     }
-    // The convs run side by side, so the slowest one bounds the launch: pick
-    // the tile with the smallest largest cost (then the smallest total).
+    // Default: the convs run side by side, so the slowest one bounds the
+    // launch: the tile with the smallest largest cost (then the smallest total).
     const int cus = device_cus();
     int best = 0;
     double bmax = 0, bsum = 0;
@@ -858,7 +899,9 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
         }
         if (v == 0 || cmax < bmax || (cmax == bmax && csum < bsum)) best = v, bmax = cmax, bsum = csum;
     }
-    return conv16s_group_launch(g, act, st, best, ps[0].sh);
+    return tuned_launch_key(
+        std::make_tuple(kGroupTuneTag, gk), kC16sCount, -1, [](int) { return true; },
+        [&](int v) { return conv16s_group_launch(g, act, st, v < 0 ? best : v, ps[0].sh); }, st);
 }
 
 static osh_status igemm_conv(const osh_conv_params *p, const float *d_x, const float *w, const float *d_bias,

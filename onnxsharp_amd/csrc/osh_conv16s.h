@@ -471,9 +471,9 @@ osh_status pw16_launch(const osh_conv_params *p, const float *x, const float *w,
                        const float *res, int act, float *y, hipStream_t st, int v);
 
 // The grouped launches (osh_conv2d_group_f32): the LDS-patch 3x3 tile `tile`
-// (an index into kC16s) at stride s, or the pointwise LDS tile (16 or, with
-// `narrow`, 4 columns wide; `vec`: 16-byte input loads).
+// (an index into kC16s) at stride s, or the pointwise LDS tile `tile` (an
+// index into kPW16; `vec`: 16-byte input loads).
 osh_status conv16s_group_launch(ConvGroup g, int act, hipStream_t st, int tile, int s);
-osh_status pw16_group_launch(ConvGroup g, int act, hipStream_t st, bool narrow, bool vec);
+osh_status pw16_group_launch(ConvGroup g, int act, hipStream_t st, int tile, bool vec);
 
 }  // namespace osh

@@ -28,12 +28,23 @@ osh_status pw16_launch(const osh_conv_params *p, const float *x, const float *w,
     }
 }
 
-osh_status pw16_group_launch(ConvGroup g, int act, hipStream_t st, bool narrow, bool vec) {
-    if (narrow)
-        return vec ? conv16s_group_launch_t<1, 2, 4, 1, 1, PW16_CB, true>(g, act, st)
-                   : conv16s_group_launch_t<1, 2, 4, 1, 1, PW16_CB, false>(g, act, st);
-    return vec ? conv16s_group_launch_t<1, 1, 16, 1, 1, PW16_CB, true>(g, act, st)
-               : conv16s_group_launch_t<1, 1, 16, 1, 1, PW16_CB, false>(g, act, st);
+template <int TM, int BV, int TWL>
+static osh_status pw16_group_v(ConvGroup g, int act, hipStream_t st, bool vec) {
+    return vec ? conv16s_group_launch_t<TM, BV, TWL, 1, 1, PW16_CB, true>(g, act, st)
+               : conv16s_group_launch_t<TM, BV, TWL, 1, 1, PW16_CB, false>(g, act, st);
+}
+
+osh_status pw16_group_launch(ConvGroup g, int act, hipStream_t st, int tile, bool vec) {
+    switch (tile) {
+    case 0: return pw16_group_v<1, 1, 16>(g, act, st, vec);
+    case 1: return pw16_group_v<1, 2, 16>(g, act, st, vec);
+    case 2: return pw16_group_v<1, 4, 16>(g, act, st, vec);
+    case 3: return pw16_group_v<2, 2, 16>(g, act, st, vec);
+    case 4: return pw16_group_v<2, 4, 16>(g, act, st, vec);
+    case 5: return pw16_group_v<1, 2, 4>(g, act, st, vec);
+    case 6: return pw16_group_v<1, 4, 4>(g, act, st, vec);
+    default: return pw16_group_v<2, 4, 4>(g, act, st, vec);
+    }
 }
 
 }  // namespace osh

@@ -54,6 +54,23 @@ class ConvParams(C.Structure):
                                        "pt", "pl", "pb", "pr", "oh", "ow")]
 
 
+PW_1X1, PW_DW3X3 = 0, 1
+PW_MAX_SRC, PW_MAX_STAGES, PW_MAX_CHAINS = 3, 5, 3
+
+
+class PwStage(C.Structure):
+    """osh_pw_stage: one stage of a pointwise chain (include/osh_hip.h)."""
+    _fields_ = [("kind", C.c_int), ("m", C.c_int), ("act", C.c_int), ("nsrc", C.c_int),
+                ("src_stage", C.c_int * PW_MAX_SRC), ("src", C.c_void_p * PW_MAX_SRC), ("src_c", C.c_int * PW_MAX_SRC),
+                ("w", C.c_void_p), ("bias", C.c_void_p), ("res_stage", C.c_int), ("res", C.c_void_p),
+                ("y", C.c_void_p)]
+
+
+class PwChain(C.Structure):
+    """osh_pw_chain: stages over one H x W map."""
+    _fields_ = [("h", C.c_int), ("w", C.c_int), ("nstages", C.c_int), ("stage", PwStage * PW_MAX_STAGES)]
+
+
 class PoolParams(C.Structure):
     _fields_ = [(f, C.c_int) for f in ("n", "c", "h", "w", "kh", "kw", "sh", "sw", "pt", "pl", "oh", "ow")]
 
@@ -89,6 +106,7 @@ _SIGS = {
     "osh_conv_packed_weight_bytes": ([C.POINTER(ConvParams), C.POINTER(_sz)], _i),
     "osh_conv_pack_weights": ([C.POINTER(ConvParams), _vp, _vp, _vp], _i),
     "osh_conv_forget_pack": ([_vp, _sz], _i),
+    "osh_pw_chain_f32": ([_i, C.POINTER(PwChain), _vp], _i),
     "osh_conv2d_f32": ([C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp], _i),
     "osh_conv2d_add_f32": ([C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp, _vp], _i),
     "osh_conv2d_group_f32": ([_i, C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp, _vp], _i),

@@ -198,3 +198,33 @@ def test_dqmm_pack_refuses_zero_points_outside_the_weight_type(signed, zp):
     fake = C.c_void_p(16)
     assert N.lib().osh_dqmm_pack_weights(8, 8, fake, signed, z, 1, fake, None) == N.OSH_E_INVALID
     assert "zero point" in N.last_error()
+
+
+def test_ctypes_structs_match_the_c_header(tmp_path):
+    """The ctypes mirrors of the header's structs have the C layout (sizes and
+    field offsets as gcc lays them out from include/osh_hip.h)."""
+    import ctypes as C
+    import os
+    import shutil
+    import subprocess
+    from onnxsharp_amd import native as N
+    if not shutil.which("gcc"):
+        pytest.skip("no gcc")
+    structs = {"osh_conv_params": N.ConvParams, "osh_conv_attrs": N.ConvAttrs, "osh_pw_stage": N.PwStage,
+               "osh_pw_chain": N.PwChain}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "osh_hip.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'  printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", inc, str(src), "-o", str(exe)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n") if l)
+    for cname, py in structs.items():
+        assert int(got[cname]) == C.sizeof(py), cname
+        for f, _ in py._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(py, f).offset, f"{cname}.{f}"
