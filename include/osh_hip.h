@@ -319,13 +319,17 @@ OSH_API osh_status osh_gemm_ex_f32(int trans_a, int trans_b, int m, int n, int k
  * by osh_conv_pack_weights for that conv (the pointwise LDS-tile layout, so
  * C % 16 == 0), m % 16 == 0 and every part's channel count a multiple of 16;
  * a depthwise stage's weights are the raw [m][1][3][3] of a conv with m == c;
- * every y non-NULL; no y overlaps another y.  A 1x1 stage reads and writes
- * only its own 16 pixels and a tile runs its stages in order, so within one
- * chain a stage's y may overlap a tensor the same or an earlier stage reads
- * from memory (at whole channel planes: e.g. writing over the shortcut a
- * previous stage added); any other overlap of a y with a tensor the launch
- * reads -- another chain's, a later stage's, a depthwise stage's input -- is
- * refused. */
+ * every y non-NULL; no y overlaps another y.  A workgroup reads everything it
+ * reads from memory before any stage writes, and a 1x1 stage reads and
+ * writes only its own 16 pixels, so within one chain a stage's y may overlap
+ * a tensor the same or an earlier stage reads from memory (at whole channel
+ * planes: e.g. writing over the shortcut a previous stage added); any other
+ * overlap of a y with a tensor the launch reads -- another chain's, a later
+ * stage's, a depthwise stage's input -- is refused.  OSH_E_UNSUPPORTED: H*W
+ * not a multiple of 4, a 1x1 stage of more than 512 channels, a part in
+ * memory of more than 512 channels, a depthwise stage of more than 256, more
+ * than 8 tensors a chain reads from memory, or a chain whose 1x1 weights,
+ * staged tensors and kept outputs exceed 160 KB of LDS. */
 #define OSH_PW_MAX_SRC 3
 #define OSH_PW_MAX_STAGES 5
 #define OSH_PW_MAX_CHAINS 3

@@ -104,6 +104,25 @@ class GroupConvOp:
 
 
 @dataclass(eq=False)
+class ChainOp:
+    """Up to three independent chains of convs over one map each -- 1x1 convs,
+    the first one may be a 3x3 depthwise -- run as one launch
+    (osh_pw_chain_f32): a stage reads earlier stages' outputs on chip, and
+    every stage still writes its whole output, so readers outside the chain
+    see what the convs one by one would have written."""
+    name: str
+    chains: list  # per chain: its ConvOps in stage order
+
+    @property
+    def ops(self):
+        return [o for ch in self.chains for o in ch]
+
+    @property
+    def flops(self):
+        return sum(o.flops for o in self.ops)
+
+
+@dataclass(eq=False)
 class AddOp:
     name: str
     a: Slice
@@ -188,7 +207,7 @@ class Model:
         for o in self.ops:
             if isinstance(o, ConvOp):
                 out.append(o)
-            elif isinstance(o, GroupConvOp):
+            elif isinstance(o, (GroupConvOp, ChainOp)):
                 out.extend(o.ops)
         return out
 
@@ -555,12 +574,174 @@ def group_independent_convs(model: Model, window: int = 12) -> Model:
     return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
 
 
-def fuse_launches(model: Model) -> Model:
+def _is_depthwise3x3(op) -> bool:
+    return op.k == 3 and op.s == 1 and op.group > 1 and op.group == op.x.c == op.y.c
+
+
+def chain_parts(x: Slice, stages) -> list:
+    """The channels of x as the concat parts of a chain stage: (k, slice) where
+    earlier stage k wrote them, (-1, slice) where they come from memory."""
+    parts, c, end = [], x.c0, x.c0 + x.c
+    while c < end:
+        hit = [k for k, s in enumerate(stages) if s.y.buf is x.buf and s.y.c0 <= c < s.y.c0 + s.y.c]
+        if hit:
+            k = hit[-1]
+            n = min(end, stages[k].y.c0 + stages[k].y.c) - c
+        else:
+            k = -1
+            n = min([s.y.c0 for s in stages if s.y.buf is x.buf and c < s.y.c0 < end] + [end]) - c
+        parts.append((k, Slice(x.buf, c, n)))
+        c += n
+    return parts
+
+
+def chain_res_stage(op, stages) -> int:
+    """The earlier stage whose output is exactly op's residual, -1 if the
+    residual (or its absence) is in memory, -2 if it overlaps a stage's output
+    only in part."""
+    if op.res is None:
+        return -1
+    for k, s in enumerate(stages):
+        if _overlap(op.res, s.y):
+            return k if (op.res.buf, op.res.c0, op.res.c) == (s.y.buf, s.y.c0, s.y.c) else -2
+    return -1
+
+
+def _chain_launch(convs):
+    """The chains one osh_pw_chain_f32 launch runs for `convs` (the convs of
+    consecutive ops, in program order), or None if the launch cannot take
+    them: a conv joins the chain whose outputs it reads (it may read only
+    one chain's), otherwise it starts a chain.  The checks are the launch's
+    own (include/osh_hip.h): 1x1 convs over multiples of 16 channels, a 3x3
+    depthwise only as stage 0, parts and residuals the stages can take, no
+    output over another or over a depthwise stage's input, independent
+    chains, and the LDS the launch needs."""
+    chains = []
+    for op in convs:
+        reads = [op.x] + ([op.res] if op.res is not None else [])
+        owners = {ci for ci, ch in enumerate(chains) for s in ch if any(_overlap(r, s.y) for r in reads)}
+        if len(owners) > 1 or op.act not in N.ACTIVATIONS:
+            return None
+        ci = owners.pop() if owners else len(chains)
+        if ci == len(chains):
+            chains.append([])
+        ch = chains[ci]
+        if _is_depthwise3x3(op):
+            if ch or op.y.c > 256:
+                return None
+        elif not (op.k == 1 and op.s == 1 and op.group == 1 and op.x.c % 16 == 0 and op.y.c % 16 == 0):
+            return None
+        if ch and (op.y.h, op.y.w) != (ch[0].y.h, ch[0].y.w):
+            return None
+        ch.append(op)
+    if len(chains) > N.PW_MAX_CHAINS or any(len(ch) > N.PW_MAX_STAGES for ch in chains):
+        return None
+    outs = [o.y for o in convs]
+    if any(_overlap(a, b) for i, a in enumerate(outs) for b in outs[:i]):
+        return None
+    for a, ca in enumerate(chains):
+        for cb in chains[a + 1:]:
+            if not all(_independent(x, y) and _independent(y, x) for x in ca for y in cb):
+                return None
+    for ch in chains:
+        if (ch[0].y.h * ch[0].y.w) % 4:
+            return None
+        if _is_depthwise3x3(ch[0]) and any(_overlap(ch[0].x, y) for y in outs):
+            return None
+        floats, kept, segs = 0, set(), 0
+        for k, op in enumerate(ch):
+            parts = chain_parts(op.x, ch[:k])
+            rs = chain_res_stage(op, ch[:k])
+            if rs == -2 or (rs >= 0 and ch[rs].y.c != op.y.c):
+                return None
+            if rs >= 0:
+                kept.add(rs)
+            kept.update(s for s, _ in parts if s >= 0)
+            if k == 0 and _is_depthwise3x3(op):
+                continue
+            if len(parts) > N.PW_MAX_SRC or any(p.c % 16 for _, p in parts) or op.y.c > 512:
+                return None
+            if any(p.c > 512 for s, p in parts if s < 0):
+                return None
+            # LDS: the packed weights, the bias, the parts and residual in memory
+            mem = [p.c for s, p in parts if s < 0] + ([op.y.c] if op.res is not None and rs < 0 else [])
+            segs += len(mem)
+            floats += op.y.c * op.x.c + (op.y.c + 3) // 4 * 4 + 16 * sum(mem)
+        floats += 16 * sum(ch[k].y.c for k in kept)
+        if segs > 8 or 4 * floats > 160 * 1024:
+            return None
+    return chains
+
+
+# Launch floor of one kernel in a serial graph on one MI355X (dispatch, cold
+# first loads), and the issue interval of a dependent 16x16x4 FP32 MFMA chain
+# (13.7 ns: 32.8 cycles at the ~2.4 GHz clock).
+_LAUNCH_US = 3.5
+_MFMA_STEP_US = 0.0137
+
+
+def _chain_gain_us(chains, nops) -> float:
+    """Modelled time a chain launch saves over its `nops` launches: the launch
+    floors it drops, less the serialisation it adds -- a chain workgroup runs
+    all M/16 output blocks of a stage on its CU's four SIMDs, C/4 dependent
+    MFMAs each, where the stage alone would spread them over the chip."""
+    def extra(op):
+        if op.k != 1:
+            return 0.0
+        return ((op.y.c // 16 + 3) // 4 - 1) * (op.x.c / 4) * _MFMA_STEP_US
+    return _LAUNCH_US * (nops - 1) - max(sum(extra(o) for o in ch) for ch in chains)
+
+
+def chain_pointwise_convs(model: Model, max_ops: int = 6, min_gain_us: float = 0.5) -> Model:
+    """Runs of consecutive conv ops that one osh_pw_chain_f32 launch can take
+    (see _chain_launch) become one ChainOp where the cost model says the
+    launch pays: C3k2's cv1 with the paired 1x1 convs after it, C3k's cv3
+    with the block's cv2, C2PSA's proj / ffn / cv2 tail, the class branch of
+    the head (depthwise -> 1x1 [-> 1x1]) at its three scales.  Each start
+    takes the window of highest modelled gain.  Results are unchanged."""
+    ops = list(model.ops)
+    out, i = [], 0
+    while i < len(ops):
+        best, convs = None, []
+        for j in range(i, min(len(ops), i + max_ops)):
+            o = ops[j]
+            if isinstance(o, ConvOp):
+                convs.append(o)
+            elif isinstance(o, GroupConvOp):
+                convs.extend(o.ops)
+            else:
+                break
+            if j == i:
+                continue
+            chains = _chain_launch(convs)
+            if chains is None:
+                continue
+            gain = _chain_gain_us(chains, j - i + 1)
+            if gain >= min_gain_us and (best is None or gain > best[0]):
+                best = (gain, j, chains)
+        if best is None:
+            out.append(ops[i])
+            i += 1
+            continue
+        _, j, chains = best
+        name = " | ".join(" > ".join(o.name for o in ch) for ch in chains)
+        out.append(ChainOp(name, chains))
+        i = j + 1
+    return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
+
+
+def fuse_launches(model: Model, chains: bool = False) -> Model:
     """The launch-saving rewrites of the op list (residual Adds into their
     convs, SPPF's pool chain into one op, the head's three scales per layer
-    into one op, other independent convs of one kind into one op); results
-    are unchanged."""
-    return group_independent_convs(group_head_convs(fuse_pool_chains(fuse_residual_adds(model))))
+    into one op, other independent convs of one kind into one op, and with
+    chains=True runs of pointwise convs into chain launches); results are
+    unchanged.  Chains are off by default: on one MI355X every chain the
+    pass picks in the 640 frame ran slower than its separate launches (a
+    chain workgroup runs its stages one after another with one dependent
+    MFMA accumulator per wave, while separate launches spread each stage over
+    the chip), 0.493 against 0.465 ms per frame."""
+    m = group_independent_convs(group_head_convs(fuse_pool_chains(fuse_residual_adds(model))))
+    return chain_pointwise_convs(m) if chains else m
 
 
 def _tiling(c, slices):
@@ -576,7 +757,7 @@ def _tiling(c, slices):
 
 def op_access(op):
     """(reads, writes) of an op as lists of channel slices."""
-    if isinstance(op, GroupConvOp):
+    if isinstance(op, (GroupConvOp, ChainOp)):
         acc = [op_access(o) for o in op.ops]
         return [r for a in acc for r in a[0]], [w for a in acc for w in a[1]]
     if isinstance(op, AddOp):
@@ -663,11 +844,12 @@ class Frame:
     branches -- the detection head's six chains, the P3 head beside the rest
     of the neck -- run side by side."""
 
-    def __init__(self, model: Model, device, nstreams: int = 4, fuse: bool = True, fused_attention: bool = True):
+    def __init__(self, model: Model, device, nstreams: int = 4, fuse: bool = True, fused_attention: bool = True,
+                 chains: bool = False):
         import torch
         self.fused_attention = fused_attention
-        if fuse:  # conv -> residual Add pairs and SPPF's pools run as single launches
-            model = fuse_launches(model)
+        if fuse:  # conv -> residual Add pairs, SPPF's pools, grouped and chained convs run as single launches
+            model = fuse_launches(model, chains=chains)
         self.model = model
         self.device = device
         for b in model.bufs:
@@ -706,6 +888,8 @@ class Frame:
             self._keep += [ps, xs, ws, bs, ys, rs]
             act = N.ACTIVATIONS[op.ops[0].act]
             return lambda st: N.check(lib.osh_conv2d_group_f32(n, ps, xs, ws, bs, act, rs, ys, st))
+        if isinstance(op, ChainOp):
+            return self._prepare_chain(op)
         if isinstance(op, ConvOp):
             p, packed, b = self._prepare_conv(op)
             act = N.ACTIVATIONS[op.act]
@@ -741,6 +925,34 @@ class Frame:
         self._keep += [p, w, b, packed]
         self._packs.append(packed)
         return p, packed, b
+
+    def _prepare_chain(self, op: ChainOp):
+        """osh_pw_chain_f32 descriptors of a ChainOp: stage parts that an
+        earlier stage wrote point into that stage's output, the rest into
+        memory; a residual that is an earlier stage's output comes from chip."""
+        lib = N.lib()
+        arr = (N.PwChain * len(op.chains))()
+        for ci, ch in enumerate(op.chains):
+            d = arr[ci]
+            d.h, d.w, d.nstages = ch[0].y.h, ch[0].y.w, len(ch)
+            for k, cv in enumerate(ch):
+                _, packed, b = self._prepare_conv(cv)
+                st = d.stage[k]
+                st.kind = N.PW_DW3X3 if _is_depthwise3x3(cv) else N.PW_1X1
+                st.m, st.act = cv.y.c, N.ACTIVATIONS[cv.act]
+                parts = chain_parts(cv.x, ch[:k])
+                st.nsrc = len(parts)
+                for i, (s, sl) in enumerate(parts):
+                    st.src_stage[i], st.src[i], st.src_c[i] = s, sl.ptr().value, sl.c
+                st.w, st.bias = packed.data_ptr(), b.data_ptr()
+                rs = chain_res_stage(cv, ch[:k])
+                assert rs >= -1, cv.name
+                st.res_stage = rs
+                st.res = cv.res.ptr().value if cv.res is not None and rs < 0 else None
+                st.y = cv.y.ptr().value
+        self._keep.append(arr)
+        n = len(op.chains)
+        return lambda s: N.check(lib.osh_pw_chain_f32(n, arr, s))
 
     def _prepare_other(self, op):
         lib = N.lib()

@@ -53,38 +53,40 @@ def _stage(conv, x_shape, kind, parts, res_stage=-1, res=None, y=None):
     return st
 
 
-def _psa_chain(cuda, hw, seed):
-    """C2PSA's tail: proj (+ shortcut) -> ffn.0 -> ffn.1 (+ proj's output) ->
-    cv2 over the concat of cv1's first half and ffn.1's output."""
+def _psa_chain(cuda, hw, seed, c=32):
+    """C2PSA's tail with c channels (128 in YOLO11n; its weights do not fit
+    in LDS at 128, so the frame keeps those convs apart): proj (+ shortcut)
+    -> ffn.0 -> ffn.1 (+ proj's output) -> cv2 over the concat of cv1's first
+    half and ffn.1's output."""
     import torch
     from onnxsharp_amd import native as N
     h, w = hw
-    s1 = _t(synth.uniform(seed, (1, 128, h, w), -1, 1), cuda)
-    b = _t(synth.uniform(seed + 1, (1, 128, h, w), -1, 1), cuda)
-    cat = torch.empty((1, 256, h, w), device=cuda)
-    cat[:, :128] = _t(synth.uniform(seed + 2, (1, 128, h, w), -1, 1), cuda)
-    proj = _Conv(cuda, seed + 10, 128, 128, 1, None)
-    f0 = _Conv(cuda, seed + 20, 128, 256, 1, "Silu")
-    f1 = _Conv(cuda, seed + 30, 256, 128, 1, None)
-    cv2 = _Conv(cuda, seed + 40, 256, 256, 1, "Silu")
+    s1 = _t(synth.uniform(seed, (1, c, h, w), -1, 1), cuda)
+    b = _t(synth.uniform(seed + 1, (1, c, h, w), -1, 1), cuda)
+    cat = torch.empty((1, 2 * c, h, w), device=cuda)
+    cat[:, :c] = _t(synth.uniform(seed + 2, (1, c, h, w), -1, 1), cuda)
+    proj = _Conv(cuda, seed + 10, c, c, 1, None)
+    f0 = _Conv(cuda, seed + 20, c, 2 * c, 1, "Silu")
+    f1 = _Conv(cuda, seed + 30, 2 * c, c, 1, None)
+    cv2 = _Conv(cuda, seed + 40, 2 * c, 2 * c, 1, "Silu")
     # one by one
     r_b1 = proj.run(s1, res=b)
     r_f0 = f0.run(r_b1)
     r_f1 = f1.run(r_f0, res=r_b1)
     cat_ref = cat.clone()
-    cat_ref[:, 128:] = r_f1
+    cat_ref[:, c:] = r_f1
     r_y = cv2.run(cat_ref)
     # as one chain
     y_b1 = torch.full_like(r_b1, float("nan"))
     y_f0 = torch.full_like(r_f0, float("nan"))
     y_y = torch.full_like(r_y, float("nan"))
-    cat_out = cat[:, 128:]  # ffn.1 writes the concat's second half
+    cat_out = cat[:, c:]  # ffn.1 writes the concat's second half
     ch = N.PwChain()
     ch.h, ch.w, ch.nstages = h, w, 4
-    ch.stage[0] = _stage(proj, (1, 128, h, w), N.PW_1X1, [(-1, s1, 128)], res=b, y=y_b1)
-    ch.stage[1] = _stage(f0, (1, 128, h, w), N.PW_1X1, [(0, None, 128)], y=y_f0)
-    ch.stage[2] = _stage(f1, (1, 256, h, w), N.PW_1X1, [(1, None, 256)], res_stage=0, y=cat_out)
-    ch.stage[3] = _stage(cv2, (1, 256, h, w), N.PW_1X1, [(-1, cat[:, :128], 128), (2, None, 128)], y=y_y)
+    ch.stage[0] = _stage(proj, (1, c, h, w), N.PW_1X1, [(-1, s1, c)], res=b, y=y_b1)
+    ch.stage[1] = _stage(f0, (1, c, h, w), N.PW_1X1, [(0, None, c)], y=y_f0)
+    ch.stage[2] = _stage(f1, (1, 2 * c, h, w), N.PW_1X1, [(1, None, 2 * c)], res_stage=0, y=cat_out)
+    ch.stage[3] = _stage(cv2, (1, 2 * c, h, w), N.PW_1X1, [(-1, cat[:, :c], c), (2, None, c)], y=y_y)
     refs = [(y_b1, r_b1), (y_f0, r_f0), (cat_out, r_f1), (y_y, r_y)]
     return ch, refs, [s1, b, cat, proj, f0, f1, cv2]
 
@@ -136,39 +138,67 @@ def test_psa_tail_chain_equals_separate_convs(cuda, exact, hw):
 
 def test_chain_stage_may_overwrite_what_it_read_earlier(cuda):
     """C2PSA's ffn.1 writes the concat half whose old contents (the block's
-    shortcut) proj added as its residual two stages earlier: per tile the read
-    comes first, so the chain equals the convs one by one; and a stage part
-    may take some channels of an earlier stage's output (C3k's two 1x1 convs
-    over the second half of cv1's output)."""
+    shortcut) proj added as its residual two stages earlier: a tile reads
+    everything first, so the chain equals the convs one by one; and a stage
+    part may take some channels of an earlier stage's output (C3k's two 1x1
+    convs over the second half of cv1's output)."""
     import torch
     from onnxsharp_amd import native as N
     h = w = 20
-    cat = torch.empty((1, 256, h, w), device=cuda)
-    cat[:] = _t(synth.uniform(77, (1, 256, h, w), -1, 1), cuda)
-    s1 = _t(synth.uniform(78, (1, 128, h, w), -1, 1), cuda)
-    proj = _Conv(cuda, 80, 128, 128, 1, None)
-    f0 = _Conv(cuda, 90, 128, 256, 1, "Silu")
-    f1 = _Conv(cuda, 100, 256, 128, 1, None)
-    cv2 = _Conv(cuda, 110, 256, 256, 1, "Silu")
-    half = _Conv(cuda, 120, 128, 64, 1, "Silu")
+    c = 32
+    cat = torch.empty((1, 2 * c, h, w), device=cuda)
+    cat[:] = _t(synth.uniform(77, (1, 2 * c, h, w), -1, 1), cuda)
+    s1 = _t(synth.uniform(78, (1, c, h, w), -1, 1), cuda)
+    proj = _Conv(cuda, 80, c, c, 1, None)
+    f0 = _Conv(cuda, 90, c, 2 * c, 1, "Silu")
+    f1 = _Conv(cuda, 100, 2 * c, c, 1, None)
+    cv2 = _Conv(cuda, 110, 2 * c, 2 * c, 1, "Silu")
+    half = _Conv(cuda, 120, c, 16, 1, "Silu")
     ref_cat = cat.clone()
-    r_b1 = proj.run(s1, res=ref_cat[:, 128:].contiguous())
+    r_b1 = proj.run(s1, res=ref_cat[:, c:].contiguous())
     r_f0 = f0.run(r_b1)
-    ref_cat[:, 128:] = f1.run(r_f0, res=r_b1)
+    ref_cat[:, c:] = f1.run(r_f0, res=r_b1)
     r_y = cv2.run(ref_cat)
-    r_h = half.run(r_f0[:, 128:].contiguous())
+    r_h = half.run(r_f0[:, c:].contiguous())
     y_b1, y_f0, y_y, y_h = (torch.empty_like(t) for t in (r_b1, r_f0, r_y, r_h))
     ch = N.PwChain()
     ch.h, ch.w, ch.nstages = h, w, 5
-    ch.stage[0] = _stage(proj, (1, 128, h, w), N.PW_1X1, [(-1, s1, 128)], res=cat[:, 128:], y=y_b1)
-    ch.stage[1] = _stage(f0, (1, 128, h, w), N.PW_1X1, [(0, None, 128)], y=y_f0)
-    ch.stage[2] = _stage(f1, (1, 256, h, w), N.PW_1X1, [(1, None, 256)], res_stage=0, y=cat[:, 128:])
-    ch.stage[3] = _stage(cv2, (1, 256, h, w), N.PW_1X1, [(-1, cat[:, :128], 128), (2, None, 128)], y=y_y)
-    ch.stage[4] = _stage(half, (1, 128, h, w), N.PW_1X1, [(1, y_f0[:, 128:], 128)], y=y_h)
+    ch.stage[0] = _stage(proj, (1, c, h, w), N.PW_1X1, [(-1, s1, c)], res=cat[:, c:], y=y_b1)
+    ch.stage[1] = _stage(f0, (1, c, h, w), N.PW_1X1, [(0, None, c)], y=y_f0)
+    ch.stage[2] = _stage(f1, (1, 2 * c, h, w), N.PW_1X1, [(1, None, 2 * c)], res_stage=0, y=cat[:, c:])
+    ch.stage[3] = _stage(cv2, (1, 2 * c, h, w), N.PW_1X1, [(-1, cat[:, :c], c), (2, None, c)], y=y_y)
+    ch.stage[4] = _stage(half, (1, c, h, w), N.PW_1X1, [(1, y_f0[:, c:], c)], y=y_h)
     _run([ch])
-    for name, got, ref in (("proj", y_b1, r_b1), ("ffn.0", y_f0, r_f0), ("ffn.1", cat[:, 128:], ref_cat[:, 128:]),
+    for name, got, ref in (("proj", y_b1, r_b1), ("ffn.0", y_f0, r_f0), ("ffn.1", cat[:, c:], ref_cat[:, c:]),
                            ("cv2", y_y, r_y), ("half", y_h, r_h)):
         assert np.array_equal(got.cpu().numpy(), ref.cpu().numpy()), name
+
+
+def test_chain_with_three_parts_and_a_wide_stage(cuda):
+    """A stage over three parts (memory, an earlier stage, memory) and a
+    stage of 512 channels: parts start inside an unrolled group of input
+    blocks, and the wide stage takes two bias values a thread and eight
+    output blocks a wave."""
+    import torch
+    from onnxsharp_amd import native as N
+    h, w = 8, 12
+    a = _t(synth.uniform(501, (1, 48, h, w), -1, 1), cuda)
+    m = _t(synth.uniform(502, (1, 80, h, w), -1, 1), cuda)
+    c0 = _Conv(cuda, 510, 48, 64, 1, "Silu")
+    c1 = _Conv(cuda, 520, 48 + 64 + 80, 32, 1, None)
+    c2 = _Conv(cuda, 530, 32, 512, 1, "Silu")
+    r0 = c0.run(a)
+    r1 = c1.run(torch.cat([a, r0, m], dim=1))
+    r2 = c2.run(r1)
+    y0, y1, y2 = (torch.full_like(t, float("nan")) for t in (r0, r1, r2))
+    ch = N.PwChain()
+    ch.h, ch.w, ch.nstages = h, w, 3
+    ch.stage[0] = _stage(c0, (1, 48, h, w), N.PW_1X1, [(-1, a, 48)], y=y0)
+    ch.stage[1] = _stage(c1, (1, 192, h, w), N.PW_1X1, [(-1, a, 48), (0, None, 64), (-1, m, 80)], y=y1)
+    ch.stage[2] = _stage(c2, (1, 32, h, w), N.PW_1X1, [(1, None, 32)], y=y2)
+    _run([ch])
+    for k, (got, ref) in enumerate(((y0, r0), (y1, r1), (y2, r2))):
+        assert np.array_equal(got.cpu().numpy(), ref.cpu().numpy()), f"stage {k}"
 
 
 @pytest.mark.parametrize("exact", [0, 1])
@@ -188,14 +218,15 @@ def test_head_tails_of_three_scales_in_one_launch(cuda, exact):
 
 def test_chain_refusals(cuda):
     """An output over a tensor a later stage reads from memory, an output over
-    a depthwise stage's input, weights not packed for the stage, and a
-    depthwise stage after stage 0 are refused."""
+    a depthwise stage's input, weights not packed for the stage, a depthwise
+    stage after stage 0, and a chain whose weights do not fit in LDS are
+    refused."""
     import torch
     from onnxsharp_amd import native as N
     ch, refs, keep = _psa_chain(cuda, (20, 20), 7)
     cat = keep[2]
     bad = N.PwChain.from_buffer_copy(ch)
-    bad.stage[0].y = cat[:, :128].data_ptr()  # proj over the part cv2 reads later
+    bad.stage[0].y = cat[:, :32].data_ptr()  # proj over the part cv2 reads later
     with pytest.raises(N.OshError, match="overlaps"):
         _run([bad])
     hch0, _, hkeep0 = _head_chain(cuda, 80, (20, 20), 8)
@@ -212,4 +243,7 @@ def test_chain_refusals(cuda):
     bad.stage[1], bad.stage[0] = hch.stage[0], hch.stage[1]
     with pytest.raises(N.OshError):
         _run([bad])
+    big, _, _ = _psa_chain(cuda, (20, 20), 10, c=128)  # 576 KB of weights
+    with pytest.raises(N.OshError, match="LDS"):
+        _run([big])
     torch.cuda.synchronize()

@@ -31,10 +31,10 @@ def exact_silu():
     N.call("osh_config_set", b"exact_silu", 0)
 
 
-def _frame(cuda, size, decode=False):
+def _frame(cuda, size, decode=False, chains=False):
     from onnxsharp_amd import yolo11n
     model = yolo11n.build(size, decode=decode)
-    return model, yolo11n.Frame(model, cuda)
+    return model, yolo11n.Frame(model, cuda, chains=chains)
 
 
 def _host(sl):
@@ -43,28 +43,37 @@ def _host(sl):
     return np.ascontiguousarray(sl.buf.tensor[:, sl.c0:sl.c0 + sl.c].cpu().numpy())
 
 
-@pytest.mark.parametrize("size", [128, 640])
-def test_yolo_per_op_parity(cuda, oracle, exact_silu, size):
+@pytest.mark.parametrize("size,chains", [(128, False), (640, False), (640, True)])
+def test_yolo_per_op_parity(cuda, oracle, exact_silu, size, chains):
     # 640 is the benchmarked frame: map-size-tuned tiles at 80/40/20, the
     # grouped head launches over three scales and the one-launch C2PSA
     # attention at n = 400 (at 128 the attention takes the five-launch path)
     from oracle import yolo_frame as YO
     from onnxsharp_amd import yolo11n as Y
-    model, fr = _frame(cuda, size, decode=True)
+    model, fr = _frame(cuda, size, decode=True, chains=chains)
     try:
-        print(f"per-op parity at {size}x{size}: {len(fr.model.ops)} launches", flush=True)
+        print(f"per-op parity at {size}x{size}, chains={chains}: {len(fr.model.ops)} launches", flush=True)
         fr.set_input(synth.uniform(4242, (1, 3, size, size)))
         worst = (0.0, "")
         assert len(fr.model.ops) < len(model.ops)  # the residual Adds run inside their convs
         for i, launch in enumerate(fr.model.ops):
-            # a GroupConvOp is one launch of independent convs: check each
-            members = launch.ops if isinstance(launch, Y.GroupConvOp) else [launch]
-            ins = [[_host(s) for s in YO.op_inputs(op)] for op in members]
+            # a GroupConvOp is one launch of independent convs, a ChainOp one
+            # launch of convs in chains: check each conv against the oracle
+            # run one by one over host copies of the buffers the launch
+            # touches, taken before it (later stages read earlier outputs)
+            members = launch.ops if isinstance(launch, (Y.GroupConvOp, Y.ChainOp)) else [launch]
+            reads, writes = Y.op_access(launch)
+            host = {}
+            for sl in reads + writes:
+                if id(sl.buf) not in host:
+                    host[id(sl.buf)] = _host(Y.whole(sl.buf)).copy()
             fr._calls[i](fr.stream)
             fr.sync()
-            for op, oin in zip(members, ins):
+            for op in members:
+                oin = [np.ascontiguousarray(host[id(s.buf)][:, s.c0:s.c0 + s.c]) for s in YO.op_inputs(op)]
                 got = _host(op.y)
                 ref = YO.run_op(oracle, op, oin)
+                host[id(op.y.buf)][:, op.y.c0:op.y.c0 + op.y.c] = ref
                 what = f"op {i} {type(op).__name__} {op.name}"
                 nbad, dmax = fp32_violations(got, ref)
                 assert_fp32_close(got, ref, what)
@@ -74,6 +83,7 @@ def test_yolo_per_op_parity(cuda, oracle, exact_silu, size):
         if size == 640:  # the launches that only the 640 frame takes were checked
             assert any(isinstance(l, Y.AttentionOp) for l in fr.model.ops)
             assert any(isinstance(l, Y.GroupConvOp) for l in fr.model.ops)
+            assert any(isinstance(l, Y.ChainOp) for l in fr.model.ops) == chains
     finally:
         fr.close()
 

@@ -201,9 +201,9 @@ def test_head_convs_group_by_layer(model):
     # The Detect head's 24 convs become 8 groups (one per layer, the three
     # scales in order), placed where the head was; with the C3k blocks' paired
     # 1x1 convs and the positional conv's two heads grouped too, the frame
-    # drops from 92 launches to 72.
+    # drops from 92 launches to 72 (before the pointwise chains).
     from onnxsharp_amd import yolo11n as Y
-    fused = Y.fuse_launches(model)
+    fused = Y.fuse_launches(model, chains=False)
     head = [o for o in fused.ops if isinstance(o, Y.GroupConvOp) and o.name.startswith("/model.23/cv")]
     other = [o for o in fused.ops if isinstance(o, Y.GroupConvOp) and o not in head]
     assert len(head) == 8 and len(other) == 4 and len(fused.ops) == 72
@@ -223,3 +223,66 @@ def test_head_convs_group_by_layer(model):
         for r in reads:
             assert id(r.buf) in written, (op.name, r.buf.name)
         written.update(id(w.buf) for w in writes)
+
+
+def test_pointwise_chains_of_the_640_frame(model):
+    # With chains on, runs of pointwise convs whose weights fit in LDS become
+    # chain launches where the cost model says they pay: C3k2's cv1 with the
+    # C3k's paired 1x1 convs and C3k's cv3 with C3k2's cv2 (model.6 at 40x40),
+    # and the head's class branch in two launches of three scales: 72
+    # launches become 67.  (The C2PSA tail's 576 KB of weights do not fit.)
+    from onnxsharp_amd import yolo11n as Y
+    fused = Y.fuse_launches(model, chains=True)
+    chains = [o for o in fused.ops if isinstance(o, Y.ChainOp)]
+    assert len(fused.ops) == 67 and len(chains) == 4
+    assert len(Y.fuse_launches(model).ops) == 72  # off by default
+    unchained = Y.fuse_launches(model, chains=False)
+    assert sorted(o.name for o in fused.convs) == sorted(o.name for o in unchained.convs)
+    shapes = [[[(o.x.c, o.y.c, o.y.h) for o in ch] for ch in c.chains] for c in chains]
+    assert [[(128, 128, 40), (64, 32, 40), (64, 32, 40)]] in shapes  # model.6 cv1 -> C3k cv1, cv2
+    head = [c for c in chains if c.name.startswith("/model.23/")]
+    assert len(head) == 2 and all(len(c.chains) == 3 for c in head)
+    assert all(Y._is_depthwise3x3(ch[0]) for c in head for ch in c.chains)
+    # the C2PSA tail: ffn.1 would add proj's output from chip, proj the shortcut from memory
+    ops = [o for o in unchained.ops if isinstance(o, Y.ConvOp) and "/model.10/m/m.0/" in o.name and o.k == 1][1:]
+    assert Y.chain_res_stage(ops[2], ops[:2]) == 0 and Y.chain_res_stage(ops[0], []) == -1
+    assert Y._chain_launch(ops + [next(o for o in unchained.ops if o.name == "/model.10/cv2/conv/Conv")]) is None
+    for c in chains:
+        assert Y._chain_launch(c.ops) is not None
+        for ch in c.chains:
+            assert len({(o.y.h, o.y.w) for o in ch}) == 1
+            for k, op in enumerate(ch):
+                parts = Y.chain_parts(op.x, ch[:k])
+                assert [p.c0 for _, p in parts] == [op.x.c0] + [op.x.c0 + sum(q.c for _, q in parts[:i])
+                                                               for i in range(1, len(parts))]
+                assert sum(p.c for _, p in parts) == op.x.c
+                for st, p in parts:
+                    if st >= 0:  # inside the stage's output
+                        y = ch[st].y
+                        assert p.buf is y.buf and y.c0 <= p.c0 and p.c0 + p.c <= y.c0 + y.c
+                    else:  # written by no earlier stage
+                        assert not any(Y._overlap(p, e.y) for e in ch[:k])
+    # C3k's cv3 -> C3k2's cv2 over [C3k2's cv1 output, cv3's output]
+    c6 = next(c for c in chains if c.name.startswith("/model.6/m.0/cv3")).chains[0]
+    assert [(s, p.c0, p.c) for s, p in Y.chain_parts(c6[1].x, c6[:1])] == [(-1, 0, 128), (0, 128, 64)]
+
+
+def test_chain_launch_refusals(model):
+    from onnxsharp_amd import yolo11n as Y
+    fused = Y.fuse_launches(model, chains=False)
+    ops = {o.name: o for o in fused.convs}
+    g = lambda n: ops[n]
+    dw = g("/model.23/cv3.0/cv3.0.1/cv3.0.1.0/conv/Conv")
+    pw = g("/model.23/cv3.0/cv3.0.0/cv3.0.0.1/conv/Conv")
+    assert Y._chain_launch([pw, dw]) is None  # a depthwise conv only as stage 0
+    assert Y._chain_launch([g("/model.6/m.0/m/m.0/cv1/conv/Conv")]) is None  # a dense 3x3 conv
+    # four independent chains: one more than a launch takes
+    four = [g(f"/model.23/cv3.{i}/cv3.{i}.0/cv3.{i}.0.0/conv/Conv") for i in range(3)] + [dw]
+    assert Y._chain_launch(four) is None
+    # maps of different sizes in one chain
+    a = g("/model.13/cv2/conv/Conv")  # 1x1 at 40x40
+    b = g("/model.16/cv1/conv/Conv")  # 1x1 at 80x80
+    assert Y._chain_launch([a, b]) is not None  # independent: two chains
+    import dataclasses
+    b2 = dataclasses.replace(b, x=a.y)
+    assert Y._chain_launch([a, b2]) is None  # b2 reads a's output on another map
