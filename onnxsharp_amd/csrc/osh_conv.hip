@@ -806,7 +806,7 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         const float *wraw = reinterpret_cast<const float *>(static_cast<const char *>(d_wpacked) +
                                                             conv16_packed_bytes(p));
         return tuned_launch(
-            p, 1, 1 + kPW16Count, pointwise_variant(), [](int) { return true; },
+            p, 1, 1 + kPW16Count, pointwise_variant(), [p](int v) { return v == 0 || pw16_fits(p, v - 1); },
             [&](int v) {
                 if (v == 0) return igemm_conv(p, d_x, wraw, d_bias, d_res, act, d_y, stream, B_DENSE);
                 if (v < 0) v = 1 + pw16_pick(p);
@@ -881,8 +881,13 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
         bool narrow = false;
         for (int i = 0; i < count; i++) narrow = narrow || ps[i].ow < 16;
         const int dflt = narrow ? 5 : 0;  // {1, 2, 4} on narrow maps, else {1, 1, 16}
+        auto fits = [&](int v) {
+            for (int i = 0; i < count; i++)
+                if (!pw16_fits(&ps[i], v)) return false;
+            return true;
+        };
         return tuned_launch_key(
-            std::make_tuple(kGroupTuneTag + 1, gk), kPW16Count, -1, [](int) { return true; },
+            std::make_tuple(kGroupTuneTag + 1, gk), kPW16Count, -1, fits,
             [&](int v) { return pw16_group_launch(g, act, st, v < 0 ? dflt : v, vec); }, st);
     }
     // Default: the convs run side by side, so the slowest one bounds the

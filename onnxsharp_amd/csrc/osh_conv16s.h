@@ -295,6 +295,20 @@ __device__ __forceinline__ void conv16s_tile(const osh_conv_params &p, const flo
         }
     };
 
+    if constexpr (KS == 1 && CB >= 8) {
+        // a pointwise tile with CB >= 8 takes all of C in one chunk (the
+        // launch checks C <= 16 CB): the patch and every weight block are in
+        // flight together, one barrier, then the whole chain
+        stage_load(sv0, 0);
+        if (active) load_a(A0, 0);
+        stage_store(sv0, 0);
+        __syncthreads();
+        if (!active) return;
+        compute(A0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < BV; q++) store_block(q);
+        return;
+    }
     // prologue: block 0 in LDS, block 1 in flight, block 0's weights loaded
     const int last = nchunks - 1;
     stage_load(sv0, 0);
@@ -452,12 +466,23 @@ osh_status conv16sx_launch(const osh_conv_params *p, const float *x, const float
                            const float *res, int act, float *y, hipStream_t st, int v);
 
 // ---- pointwise (1x1, stride 1, no pads): the same kernel with KS = 1 and
-// four 16-channel blocks per staged chunk; the chain is the GEMM chain over
+// CB 16-channel blocks per staged chunk; the chain is the GEMM chain over
 // input channels (bias, then ic ascending), as GemmKernel.Multiply sums it.
-constexpr int PW16_CB = 4;
-constexpr C16sVariant kPW16[] = {{1, 1, 16}, {1, 2, 16}, {1, 4, 16}, {2, 2, 16},
-                                 {2, 4, 16}, {1, 2, 4},  {1, 4, 4},  {2, 4, 4}};
+// CB = 8 and 16 take all of C (at most 128 or 256 channels) in one chunk:
+// the patch and every weight block of the wave are in flight at once and
+// there is one barrier (256 -> 128 at 80x80: one chunk instead of four).
+struct PW16Variant {
+    int tm, bv, twl, cb;
+};
+constexpr PW16Variant kPW16[] = {{1, 1, 16, 4}, {1, 2, 16, 4}, {1, 4, 16, 4}, {2, 2, 16, 4}, {2, 4, 16, 4},
+                                 {1, 2, 4, 4},  {1, 4, 4, 4},  {2, 4, 4, 4},  {1, 1, 16, 8}, {1, 1, 16, 16},
+                                 {1, 2, 16, 8}, {1, 2, 16, 16}};
 constexpr int kPW16Count = sizeof(kPW16) / sizeof(kPW16[0]);
+
+// Whether pointwise tile `tile` takes a conv of p's input channels.
+inline bool pw16_fits(const osh_conv_params *p, int tile) {
+    return tile >= 0 && tile < kPW16Count && (kPW16[tile].cb < 8 || p->c <= 16 * kPW16[tile].cb);
+}
 
 inline bool pw16_eligible(const osh_conv_params *p) {
     return p->group == 1 && p->kh == 1 && p->kw == 1 && p->sh == 1 && p->sw == 1 && p->dh == 1 && p->dw == 1 &&

@@ -6,12 +6,12 @@
 
 namespace osh {
 
-template <int TM, int BV, int TWL>
+template <int TM, int BV, int TWL, int CB = 4>
 inline osh_status pw16_launch_v(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                 const float *res, int act, float *y, hipStream_t st) {
     const bool vec = p->w % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    if (vec) return conv16s_launch_t<TM, BV, TWL, 1, 1, PW16_CB, true>(p, x, w, bias, res, act, y, st);
-    return conv16s_launch_t<TM, BV, TWL, 1, 1, PW16_CB, false>(p, x, w, bias, res, act, y, st);
+    if (vec) return conv16s_launch_t<TM, BV, TWL, 1, 1, CB, true>(p, x, w, bias, res, act, y, st);
+    return conv16s_launch_t<TM, BV, TWL, 1, 1, CB, false>(p, x, w, bias, res, act, y, st);
 }
 
 osh_status pw16_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
@@ -24,14 +24,18 @@ osh_status pw16_launch(const osh_conv_params *p, const float *x, const float *w,
     case 4: return pw16_launch_v<2, 4, 16>(p, x, w, bias, res, act, y, st);
     case 5: return pw16_launch_v<1, 2, 4>(p, x, w, bias, res, act, y, st);
     case 6: return pw16_launch_v<1, 4, 4>(p, x, w, bias, res, act, y, st);
-    default: return pw16_launch_v<2, 4, 4>(p, x, w, bias, res, act, y, st);
+    case 7: return pw16_launch_v<2, 4, 4>(p, x, w, bias, res, act, y, st);
+    case 8: return pw16_launch_v<1, 1, 16, 8>(p, x, w, bias, res, act, y, st);
+    case 9: return pw16_launch_v<1, 1, 16, 16>(p, x, w, bias, res, act, y, st);
+    case 10: return pw16_launch_v<1, 2, 16, 8>(p, x, w, bias, res, act, y, st);
+    default: return pw16_launch_v<1, 2, 16, 16>(p, x, w, bias, res, act, y, st);
     }
 }
 
-template <int TM, int BV, int TWL>
+template <int TM, int BV, int TWL, int CB = 4>
 static osh_status pw16_group_v(ConvGroup g, int act, hipStream_t st, bool vec) {
-    return vec ? conv16s_group_launch_t<TM, BV, TWL, 1, 1, PW16_CB, true>(g, act, st)
-               : conv16s_group_launch_t<TM, BV, TWL, 1, 1, PW16_CB, false>(g, act, st);
+    return vec ? conv16s_group_launch_t<TM, BV, TWL, 1, 1, CB, true>(g, act, st)
+               : conv16s_group_launch_t<TM, BV, TWL, 1, 1, CB, false>(g, act, st);
 }
 
 osh_status pw16_group_launch(ConvGroup g, int act, hipStream_t st, int tile, bool vec) {
@@ -43,7 +47,11 @@ osh_status pw16_group_launch(ConvGroup g, int act, hipStream_t st, int tile, boo
     case 4: return pw16_group_v<2, 4, 16>(g, act, st, vec);
     case 5: return pw16_group_v<1, 2, 4>(g, act, st, vec);
     case 6: return pw16_group_v<1, 4, 4>(g, act, st, vec);
-    default: return pw16_group_v<2, 4, 4>(g, act, st, vec);
+    case 7: return pw16_group_v<2, 4, 4>(g, act, st, vec);
+    case 8: return pw16_group_v<1, 1, 16, 8>(g, act, st, vec);
+    case 9: return pw16_group_v<1, 1, 16, 16>(g, act, st, vec);
+    case 10: return pw16_group_v<1, 2, 16, 8>(g, act, st, vec);
+    default: return pw16_group_v<1, 2, 16, 16>(g, act, st, vec);
     }
 }
 
