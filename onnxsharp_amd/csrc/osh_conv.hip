@@ -848,15 +848,25 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
         }
         return OSH_OK;
     }
+    // Members are laid out longest chain first (most MFMA steps a wave, C/g
+    // * kh * kw): workgroups start in block order, so the deep-K member's
+    // chains (the head's 256 -> 64 at 20x20: 576 dependent steps) start at
+    // once and the shorter members' workgroups fill the SIMDs around them.
+    int order[kConvGroupMax];
+    for (int i = 0; i < count; i++) order[i] = i;
+    auto steps = [&](int i) { return (long long)ps[i].c / ps[i].group * ps[i].kh * ps[i].kw; };
+    for (int i = 1; i < count; i++)  // stable insertion sort, descending
+        for (int k = i; k > 0 && steps(order[k]) > steps(order[k - 1]); k--) std::swap(order[k], order[k - 1]);
     ConvGroup g{};
     g.count = count;
-    for (int i = 0; i < count; i++) {
-        g.p[i] = ps[i];
-        g.x[i] = xs[i];
-        g.w[i] = static_cast<const float *>(ws[i]);
-        g.bias[i] = bs ? bs[i] : nullptr;
-        g.res[i] = rs ? rs[i] : nullptr;
-        g.y[i] = ys[i];
+    for (int k = 0; k < count; k++) {
+        const int i = order[k];
+        g.p[k] = ps[i];
+        g.x[k] = xs[i];
+        g.w[k] = static_cast<const float *>(ws[i]);
+        g.bias[k] = bs ? bs[i] : nullptr;
+        g.res[k] = rs ? rs[i] : nullptr;
+        g.y[k] = ys[i];
     }
     if (a0 == ALGO_DEPTHWISE) {
         long long total = 0;
