@@ -133,6 +133,49 @@ __device__ __forceinline__ void dw_conv_at(const osh_conv_params &p, const float
     y[idx] = v;
 }
 
+// The 3x3 stride-S, dilation-1 case of dw_conv_at (every depthwise layer of
+// YOLO11n): 32-bit indices, and the nine weights and the in-map taps loaded
+// before the chain starts, so the loads are in flight together; taps off the
+// map are skipped, as in dw_conv_at (an fma with a zero tap could turn a -0
+// accumulator into +0).
+inline bool dw3_eligible(const osh_conv_params *p) {
+    return p->kh == 3 && p->kw == 3 && p->dh == 1 && p->dw == 1 && p->sh == p->sw && (p->sh == 1 || p->sh == 2) &&
+           (long long)p->n * p->m * p->oh * p->ow < (1LL << 31) && (long long)p->n * p->c * p->h * p->w < (1LL << 31);
+}
+
+template <int ACT, int S>
+__device__ __forceinline__ void dw3_conv_at(const osh_conv_params &p, const float *__restrict__ x,
+                                            const float *__restrict__ w, const float *__restrict__ bias,
+                                            const float *__restrict__ res, float *__restrict__ y, int idx) {
+    const int total = p.n * p.m * p.oh * p.ow;
+    if (idx >= total) return;
+    const int ox = idx % p.ow;
+    int t = idx / p.ow;
+    const int oy = t % p.oh;
+    t /= p.oh;
+    const int c = t % p.m, n = t / p.m;
+    const float *xc = x + (n * p.c + c) * p.h * p.w;
+    const float *wc = w + c * 9;
+    const int iy0 = oy * S - p.pt, ix0 = ox * S - p.pl;
+    float wv[9], tap[9];
+    unsigned in = 0;
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+        const int iy = iy0 + k / 3, ix = ix0 + k % 3;
+        const bool ok = (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
+        in |= ok ? 1u << k : 0u;
+        wv[k] = wc[k];
+        tap[k] = ok ? xc[iy * p.w + ix] : 0.f;
+    }
+    float acc = bias ? bias[c] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 9; k++)
+        if (in & (1u << k)) acc = __builtin_fmaf(wv[k], tap[k], acc);
+    float v = activate<ACT>(acc);
+    if (res) v += res[idx];
+    y[idx] = v;
+}
+
 template <int ACT>
 __global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const float *__restrict__ x,
                                                       const float *__restrict__ w, const float *__restrict__ bias,
@@ -140,15 +183,26 @@ __global__ __launch_bounds__(256) void dw_conv_kernel(osh_conv_params p, const f
     dw_conv_at<ACT>(p, x, w, bias, res, y, (long long)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
+template <int ACT, int S>
+__global__ __launch_bounds__(256) void dw3_conv_kernel(osh_conv_params p, const float *__restrict__ x,
+                                                       const float *__restrict__ w, const float *__restrict__ bias,
+                                                       const float *__restrict__ res, float *__restrict__ y) {
+    dw3_conv_at<ACT, S>(p, x, w, bias, res, y, blockIdx.x * 256 + threadIdx.x);
+}
+
 // Several depthwise convs in one launch: workgroup b covers outputs
-// 256 (b - start[i]) .. of conv i (ConvGroup's block table).
-template <int ACT>
+// 256 (b - start[i]) .. of conv i (ConvGroup's block table).  S > 0: every
+// member is a 3x3 stride-S conv (dw3_eligible).
+template <int ACT, int S>
 __global__ __launch_bounds__(256) void dw_conv_group_kernel(ConvGroup g) {
     const int b = blockIdx.x;
     int i = 0;
     while (i + 1 < g.count && b >= g.start[i + 1]) i++;
-    dw_conv_at<ACT>(g.p[i], g.x[i], g.w[i], g.bias[i], g.res[i], g.y[i],
-                    (long long)(b - g.start[i]) * 256 + threadIdx.x);
+    if constexpr (S > 0)
+        dw3_conv_at<ACT, S>(g.p[i], g.x[i], g.w[i], g.bias[i], g.res[i], g.y[i], (b - g.start[i]) * 256 + threadIdx.x);
+    else
+        dw_conv_at<ACT>(g.p[i], g.x[i], g.w[i], g.bias[i], g.res[i], g.y[i],
+                        (long long)(b - g.start[i]) * 256 + threadIdx.x);
 }
 
 // ------------------------------------------------------- small-C first layer
@@ -734,6 +788,19 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
     case ALGO_DEPTHWISE: {
         long long total = (long long)p->n * p->m * out_hw;
         dim3 grid((unsigned)((total + 255) / 256));
+        if (dw3_eligible(p)) {
+            if (p->sh == 1) {
+                OSH_DISPATCH_ACT(act, ACT,
+                                 hipLaunchKernelGGL((dw3_conv_kernel<ACT, 1>), grid, dim3(256), 0, stream, *p, d_x, w,
+                                                    d_bias, d_res, d_y));
+            } else {
+                OSH_DISPATCH_ACT(act, ACT,
+                                 hipLaunchKernelGGL((dw3_conv_kernel<ACT, 2>), grid, dim3(256), 0, stream, *p, d_x, w,
+                                                    d_bias, d_res, d_y));
+            }
+            OSH_LAUNCH_CHECK("dw3_conv_kernel");
+            return OSH_OK;
+        }
         OSH_DISPATCH_ACT(act, ACT,
                          hipLaunchKernelGGL(dw_conv_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, w, d_bias, d_res,
                                             d_y));
@@ -876,8 +943,22 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
             if (total > 0x7fffffffLL) return fail(OSH_E_UNSUPPORTED, "Conv group: grid too large");
         }
         g.start[count] = (int)total;
-        OSH_DISPATCH_ACT(act, ACT,
-                         hipLaunchKernelGGL(dw_conv_group_kernel<ACT>, dim3((unsigned)total), dim3(256), 0, st, g));
+        int s3 = dw3_eligible(&ps[0]) ? ps[0].sh : 0;  // every member 3x3 at one stride: the 3x3 path
+        for (int i = 1; i < count; i++)
+            if (!dw3_eligible(&ps[i]) || ps[i].sh != s3) s3 = 0;
+        if (s3 == 1) {
+            OSH_DISPATCH_ACT(act, ACT,
+                             hipLaunchKernelGGL((dw_conv_group_kernel<ACT, 1>), dim3((unsigned)total), dim3(256), 0, st,
+                                                g));
+        } else if (s3 == 2) {
+            OSH_DISPATCH_ACT(act, ACT,
+                             hipLaunchKernelGGL((dw_conv_group_kernel<ACT, 2>), dim3((unsigned)total), dim3(256), 0, st,
+                                                g));
+        } else {
+            OSH_DISPATCH_ACT(act, ACT,
+                             hipLaunchKernelGGL((dw_conv_group_kernel<ACT, 0>), dim3((unsigned)total), dim3(256), 0, st,
+                                                g));
+        }
         OSH_LAUNCH_CHECK("dw_conv_group_kernel");
         return OSH_OK;
     }

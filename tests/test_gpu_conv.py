@@ -60,6 +60,10 @@ CASES = [
     ("dilated_5x5", (1, 5, 23, 21), (7, 5, 5, 5), dict(pads=[4, 4, 4, 4], dilations=[2, 2]), None),
     ("depthwise_3x3", (1, 32, 20, 20), (32, 1, 3, 3), dict(group=32, pads=[1, 1, 1, 1]), None),
     ("depthwise_3x3_s2", (1, 24, 19, 18), (24, 1, 3, 3), dict(group=24, strides=[2, 2], pads=[1, 1, 1, 1]), "Silu"),
+    ("depthwise_3x3_batch2_pad0", (2, 16, 11, 13), (16, 1, 3, 3), dict(group=16), "Relu"),
+    ("depthwise_5x5_generic", (1, 12, 15, 17), (12, 1, 5, 5), dict(group=12, pads=[2, 2, 2, 2]), "Silu"),
+    ("depthwise_3x3_dilated_generic", (1, 8, 14, 16), (8, 1, 3, 3), dict(group=8, pads=[2, 2, 2, 2], dilations=[2, 2]),
+     None),
     ("same_upper_s2", (1, 1, 9, 11), (1, 1, 3, 3), dict(auto_pad="SAME_UPPER", strides=[2, 2]), None),
     ("valid_1x3", (1, 6, 10, 12), (4, 6, 1, 3), dict(auto_pad="VALID"), None),
 ]
