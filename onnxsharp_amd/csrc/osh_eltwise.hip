@@ -206,6 +206,26 @@ __global__ __launch_bounds__(256) void resize_nearest_kernel(int c, int h, int w
     y[n * y_batch_stride + ((long long)ch * oh + oy) * ow + ox] = v;
 }
 
+// The 2x case with an even input width: a thread reads two neighbouring
+// input pixels (8 bytes) and writes the four output pixels of each of its two
+// output rows as one 16-byte store, with 32-bit indices.
+__global__ __launch_bounds__(256) void resize2x_kernel(int c, int h, int w2, const float2 *__restrict__ x,
+                                                       float *__restrict__ y, long long y_batch_stride, int total) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int ix = idx % w2;  // pair of input columns 2 ix, 2 ix + 1
+    int t = idx / w2;
+    const int iy = t % h;
+    t /= h;
+    const int ch = t % c, n = t / c;
+    const float2 v = x[idx];
+    const int ow = 4 * w2;
+    float *row = y + n * y_batch_stride + ((long long)ch * 2 * h + 2 * iy) * ow + 4 * ix;
+    const float4 o = make_float4(v.x, v.x, v.y, v.y);
+    *reinterpret_cast<float4 *>(row) = o;
+    *reinterpret_cast<float4 *>(row + ow) = o;
+}
+
 // 32 x 32 tiles through LDS so that both the read and the write are coalesced.
 __global__ __launch_bounds__(256) void transpose_kernel(int rows, int cols, const float *__restrict__ x,
                                                          long long xs, float *__restrict__ y, long long ys) {
@@ -374,6 +394,14 @@ OSH_API osh_status osh_resize_nearest_f32(int n, int c, int h, int w, int fh, in
     const long long plane = (long long)c * h * fh * w * fw;
     if (y_batch_stride < plane) return fail(OSH_E_INVALID, "Resize: output batch stride below c*oh*ow");
     const long long total = (long long)n * plane;
+    const long long pairs = (long long)n * c * h * w / 2;
+    if (fh == 2 && fw == 2 && w % 2 == 0 && pairs < (1LL << 31) && y_batch_stride % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(d_x) & 7) == 0 && (reinterpret_cast<uintptr_t>(d_y) & 15) == 0) {
+        hipLaunchKernelGGL(resize2x_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, to_stream(s), c, h,
+                           w / 2, reinterpret_cast<const float2 *>(d_x), d_y, (long long)y_batch_stride, (int)pairs);
+        OSH_LAUNCH_CHECK("resize2x_kernel");
+        return OSH_OK;
+    }
     hipLaunchKernelGGL(resize_nearest_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), c,
                        h, w, fh, fw, d_x, d_y, (long long)y_batch_stride, total);
     OSH_LAUNCH_CHECK("resize_nearest_kernel");

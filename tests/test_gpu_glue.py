@@ -108,8 +108,11 @@ def test_pool_chain_is_three_pools(cuda, oracle, shape, k):
         assert np.array_equal(_bits(part), _bits(ref)), f"pool {i + 1} vs oracle"
 
 
-@pytest.mark.parametrize("shape,f", [((1, 256, 20, 20), 2), ((2, 3, 7, 5), 3)])
+@pytest.mark.parametrize("shape,f", [((1, 256, 20, 20), 2), ((2, 3, 7, 5), 3), ((2, 5, 6, 8), 2), ((1, 4, 5, 7), 2)],
+                         ids=["yolo_2x", "3x", "batch2_2x", "odd_width_2x"])
 def test_resize_nearest_into_a_channel_slice(cuda, oracle, shape, f):
+    # 2x with an even width takes the paired kernel (16-byte stores), other
+    # shapes the per-element one; both into a channel slice of a wider buffer
     import torch
     from onnxsharp_amd import native as N
     n, c, h, w = shape
