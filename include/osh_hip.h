@@ -103,6 +103,11 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 tiles (1..N-1); all sum in the GEMM chain's order.  -2 = the
  *                 GEMM path only.  Initial value from
  *                 ONNXSHARP_HIP_POINTWISE_VARIANT.
+ *   "group3x3_tile": -1 (default) = grouped 3x3 launches
+ *                 (osh_conv2d_group_f32) pick their tile by first-use timing
+ *                 of the whole group; 0..N-1 forces one of the LDS-patch
+ *                 tiles; all give the same bits.
+ *   "group3x3_tiles" (get only): N.
  *   "pointwise_variants" (get only): N.
  *                 The -2 setting of "pointwise_variant" changes the packed
  *                 weight layout: pack again after changing it.

@@ -156,6 +156,11 @@ osh_status noalloc_scratch_setup(int dev);
 int im2col3x3_variant();
 int im2col3x3_variant_count();
 
+// Forced tile of the grouped 3x3 launches (-1 = first-use timing) and the
+// number of tiles (the LDS-patch tiles).
+int group3x3_tile();
+int group3x3_tile_count();
+
 // Winograd F(2x2,3x3) for 3x3 stride-1 convolutions (0 = never, 1 = where
 // the reference's NCHWc kernel does not apply, 2 = ahead of the NCHWc
 // kernels) and the largest output map it takes (H*W; the reference's

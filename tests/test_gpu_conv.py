@@ -505,6 +505,16 @@ GROUP_CASES = [
 ]
 
 
+def _group_tiles():
+    from onnxsharp_amd import native as N
+    try:
+        nt = C.c_int()
+        N.call("osh_config_get", b"group3x3_tiles", C.byref(nt))
+        return nt.value
+    except Exception:
+        return 0
+
+
 @pytest.mark.parametrize("name,convs,act,residual", GROUP_CASES, ids=[c[0] for c in GROUP_CASES])
 def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
     # osh_conv2d_group_f32 runs independent convs as one launch (or one per
@@ -534,12 +544,24 @@ def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
     arr = lambda ts: (C.c_void_p * n)(*[None if t is None else t.data_ptr() for t in ts])
     pa = (N.ConvParams * n)(*ps)
     st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    N.check(N.lib().osh_conv2d_group_f32(n, pa, arr(xs), arr(ws), arr(bs), N.ACTIVATIONS[act], arr(rs),
-                                         arr(ys), st))
-    torch.cuda.synchronize()
-    for k in range(n):
-        got = ys[k].cpu().numpy()
-        assert np.array_equal(got, ref[k]), f"conv {k}: max |d| {np.nanmax(np.abs(got - ref[k])):.3e}"
+    # the 3x3 group: every tile forced in turn (the first-use timing would keep
+    # only the last tile's output), then the automatic choice
+    tiles = list(range(_group_tiles())) if name == "head_3x3_nchwc" else []
+    try:
+        for tile in tiles + [-1]:
+            N.call("osh_config_set", b"group3x3_tile", tile) if tiles else None
+            for y in ys:
+                y.fill_(float("nan"))
+            N.check(N.lib().osh_conv2d_group_f32(n, pa, arr(xs), arr(ws), arr(bs), N.ACTIVATIONS[act], arr(rs),
+                                                 arr(ys), st))
+            torch.cuda.synchronize()
+            for k in range(n):
+                got = ys[k].cpu().numpy()
+                assert np.array_equal(got, ref[k]), \
+                    f"tile {tile} conv {k}: max |d| {np.nanmax(np.abs(got - ref[k])):.3e}"
+    finally:
+        if tiles:
+            N.call("osh_config_set", b"group3x3_tile", -1)
 
 
 @pytest.mark.parametrize("case", [0, 1, 2])
