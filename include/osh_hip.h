@@ -108,6 +108,9 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 of the whole group; 0..N-1 forces one of the LDS-patch
  *                 tiles; all give the same bits.
  *   "group3x3_tiles" (get only): N.
+ *   "group_pointwise_tile", "group_pointwise_tiles": the same for grouped
+ *                 pointwise launches (the pointwise LDS tiles that fit every
+ *                 member; a forced tile that does not fit takes the default).
  *   "pointwise_variants" (get only): N.
  *                 The -2 setting of "pointwise_variant" changes the packed
  *                 weight layout: pack again after changing it.

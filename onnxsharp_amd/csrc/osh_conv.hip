@@ -516,6 +516,7 @@ int conv16_variant_count() { return kC3Count; }
 int pointwise_variant_count() { return 1 + kPW16Count; }
 int im2col3x3_variant_count() { return kC16sCount; }
 int group3x3_tile_count() { return kC16sCount; }
+int group_pointwise_tile_count() { return kPW16Count; }
 
 static bool c3_fits(const osh_conv_params *p, int v) {
     if (v < kC16Count) return conv16_fits(p, kC16[v]);
@@ -979,7 +980,7 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
             return true;
         };
         return tuned_launch_key(
-            std::make_tuple(kGroupTuneTag + 1, gk), kPW16Count, -1, fits,
+            std::make_tuple(kGroupTuneTag + 1, gk), kPW16Count, group_pointwise_tile(), fits,
             [&](int v) { return pw16_group_launch(g, act, st, v < 0 ? dflt : v, vec); }, st);
     }
     // Default: the convs run side by side, so the slowest one bounds the

@@ -35,6 +35,7 @@ static int g_dqmm_variant = -3;     // -3: read ONNXSHARP_HIP_DQMM_VARIANT on fi
 static int g_winograd = -3;         // -3: read ONNXSHARP_HIP_WINOGRAD on first use
 static int g_i2c_variant = -3;      // -3: read ONNXSHARP_HIP_IM2COL3X3_VARIANT on first use
 static int g_group3x3_tile = -1;    // forced tile of grouped 3x3 launches (-1: first-use timing)
+static int g_group_pw_tile = -1;    // forced tile of grouped pointwise launches (-1: first-use timing)
 static long long g_wino_max = -3;   // -3: read ONNXSHARP_WINO_MAX on first use
 
 bool exact_silu() {
@@ -86,6 +87,7 @@ int im2col3x3_variant() {
 }
 
 int group3x3_tile() { return g_group3x3_tile; }
+int group_pointwise_tile() { return g_group_pw_tile; }
 
 int winograd_mode() {
     if (g_winograd == -3) {
@@ -170,6 +172,13 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         g_group3x3_tile = value;
         return OSH_OK;
     }
+    if (strcmp(key, "group_pointwise_tile") == 0) {
+        if (value < -1 || value >= group_pointwise_tile_count())
+            return fail(OSH_E_INVALID, "group_pointwise_tile %d out of range [-1, %d)", value,
+                        group_pointwise_tile_count());
+        g_group_pw_tile = value;
+        return OSH_OK;
+    }
     if (strcmp(key, "winograd") == 0) {
         if (value < 0 || value > 2) return fail(OSH_E_INVALID, "winograd %d out of range [0, 2]", value);
         g_winograd = value;
@@ -219,6 +228,14 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     }
     if (strcmp(key, "group3x3_tiles") == 0) {
         *value = group3x3_tile_count();
+        return OSH_OK;
+    }
+    if (strcmp(key, "group_pointwise_tile") == 0) {
+        *value = group_pointwise_tile();
+        return OSH_OK;
+    }
+    if (strcmp(key, "group_pointwise_tiles") == 0) {
+        *value = group_pointwise_tile_count();
         return OSH_OK;
     }
     if (strcmp(key, "winograd") == 0) {

@@ -505,14 +505,11 @@ GROUP_CASES = [
 ]
 
 
-def _group_tiles():
+def _group_tiles(key):
     from onnxsharp_amd import native as N
-    try:
-        nt = C.c_int()
-        N.call("osh_config_get", b"group3x3_tiles", C.byref(nt))
-        return nt.value
-    except Exception:
-        return 0
+    nt = C.c_int()
+    N.call("osh_config_get", key + b"s", C.byref(nt))
+    return nt.value
 
 
 @pytest.mark.parametrize("name,convs,act,residual", GROUP_CASES, ids=[c[0] for c in GROUP_CASES])
@@ -544,12 +541,14 @@ def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
     arr = lambda ts: (C.c_void_p * n)(*[None if t is None else t.data_ptr() for t in ts])
     pa = (N.ConvParams * n)(*ps)
     st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    # the 3x3 group: every tile forced in turn (the first-use timing would keep
-    # only the last tile's output), then the automatic choice
-    tiles = list(range(_group_tiles())) if name == "head_3x3_nchwc" else []
+    # the 3x3 and pointwise groups: every tile forced in turn (the first-use
+    # timing would keep only the last tile's output), then the automatic choice
+    key = {"head_3x3_nchwc": b"group3x3_tile", "head_pointwise_res": b"group_pointwise_tile"}.get(name)
+    tiles = list(range(_group_tiles(key))) if key else []
     try:
         for tile in tiles + [-1]:
-            N.call("osh_config_set", b"group3x3_tile", tile) if tiles else None
+            if key:
+                N.call("osh_config_set", key, tile)
             for y in ys:
                 y.fill_(float("nan"))
             N.check(N.lib().osh_conv2d_group_f32(n, pa, arr(xs), arr(ws), arr(bs), N.ACTIVATIONS[act], arr(rs),
@@ -560,8 +559,8 @@ def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
                 assert np.array_equal(got, ref[k]), \
                     f"tile {tile} conv {k}: max |d| {np.nanmax(np.abs(got - ref[k])):.3e}"
     finally:
-        if tiles:
-            N.call("osh_config_set", b"group3x3_tile", -1)
+        if key:
+            N.call("osh_config_set", key, -1)
 
 
 @pytest.mark.parametrize("case", [0, 1, 2])
