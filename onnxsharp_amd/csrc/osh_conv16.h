@@ -101,75 +101,145 @@ __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const fl
         }
     }
 
-    // chunk c = icb * 3 + ky: taps (ky, 0..2) of channel block icb
-    auto load = [&](C16Chunk<TM, BV> &R, int c) {
+    if constexpr (TM * BV <= 2) {
+        // One chunk = one 16-channel input block: its nine taps (ky, kx) x four
+        // k4 steps, with every register index known at compile time.  Two
+        // chunks are in flight in fixed registers (R0 holds the even blocks, R1
+        // the odd ones): each tap's refill loads for the block two ahead are
+        // issued right after the tap's MFMAs, and the last two blocks issue no
+        // refills, so nothing is loaded that is not used and the loop carries
+        // no register copies that would wait for every load.
+        struct Blk {
+            float4 a[9][TM];    // per tap: the lane's 4 k4-step weights of each output block
+            float b[9][4][BV];  // per tap and k4 step: the lane's input value of each pixel
+        };
         __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)xn, (short)0, bytes_x, 0x00020000);
         __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)wpk, (short)0, bytes_w, 0x00020000);
-        const int icb = c / 3, ky = c - icb * 3;
-#pragma unroll
-        for (int kx = 0; kx < 3; kx++) {
-            const int kg = icb * 9 + ky * 3 + kx;
+        auto ld = [&](Blk &R, int icb, int t) {
 #pragma unroll
             for (int tm = 0; tm < TM; tm++) {
-                auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, voa[tm], kg * 1024, 0);
-                R.a[kx][tm] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
-                                          __uint_as_float(v[3]));
+                auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, voa[tm], (icb * 9 + t) * 1024, 0);
+                R.a[t][tm] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                                         __uint_as_float(v[3]));
             }
 #pragma unroll
-            for (int s = 0; s < 4; s++)
+            for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
                 for (int q = 0; q < BV; q++)
-                    R.b[kx][s][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                        rx, off[q][ky * 3 + kx], (icb * 16 + 4 * s) * HW * 4, 0));
-        }
-    };
-    auto compute = [&](const C16Chunk<TM, BV> &R) {
+                    R.b[t][s4][q] = __uint_as_float(
+                        __builtin_amdgcn_raw_buffer_load_b32(rx, off[q][t], (icb * 16 + 4 * s4) * HW * 4, 0));
+        };
+        auto mm = [&](const Blk &R, int t) {
 #pragma unroll
-        for (int kx = 0; kx < 3; kx++)
-#pragma unroll
-            for (int s = 0; s < 4; s++)
+            for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
                 for (int tm = 0; tm < TM; tm++) {
-                    const float4 &a4 = R.a[kx][tm];
-                    const float a = s == 0 ? a4.x : s == 1 ? a4.y : s == 2 ? a4.z : a4.w;
+                    const float4 &a4 = R.a[t][tm];
+                    const float a = s4 == 0 ? a4.x : s4 == 1 ? a4.y : s4 == 2 ? a4.z : a4.w;
 #pragma unroll
                     for (int q = 0; q < BV; q++)
-                        acc[tm][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, R.b[kx][s][q], acc[tm][q], 0, 0, 0);
+                        acc[tm][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, R.b[t][s4][q], acc[tm][q], 0, 0, 0);
                 }
-    };
-
-    // D chunks in flight (their loads fit the 63 outstanding vector loads a
-    // wave can count); the ring is unrolled so each chunk has fixed registers,
-    // and prefetch indices are clamped to the last chunk (a reload, in bounds)
-    // so the steady-state body has no branches.
-    constexpr int L = 3 * (TM + 4 * BV);
-    constexpr int D = 60 / L < 2 ? 2 : (60 / L > 4 ? 4 : 60 / L);
-    const int nch = icbs * 3;
-    const int last = nch - 1;
-    C16Chunk<TM, BV> R[D];
+        };
+        Blk R0, R1;
 #pragma unroll
-    for (int d = 0; d < D; d++) load(R[d], min(d, last));
-    int c = 0;
-    // a chunk's refill loads are issued between its own MFMAs (two MFMAs per
-    // load; each load follows the MFMA that last reads its register), so the
-    // MFMA pipe is not left idle while they issue
-    constexpr int NGR = (12 * TM * BV + 1) / 2;
-    for (; c + D <= nch; c += D) {
+        for (int t = 0; t < 9; t++) ld(R0, 0, t);
+        if (icbs > 1) {
 #pragma unroll
-        for (int d = 0; d < D; d++) {
-            __builtin_amdgcn_sched_barrier(0);
-            compute(R[d]);
-            load(R[d], min(c + d + D, last));
+            for (int t = 0; t < 9; t++) ld(R1, 1, t);
+        }
+        int icb = 0;
+        for (; icb + 2 <= icbs; icb += 2) {
+            if (icb + 2 < icbs) {
 #pragma unroll
-            for (int i = 0; i < NGR; i++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one VMEM read
+                for (int t = 0; t < 9; t++) mm(R0, t), ld(R0, icb + 2, t);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 9; t++) mm(R0, t);
+            }
+            if (icb + 3 < icbs) {
+#pragma unroll
+                for (int t = 0; t < 9; t++) mm(R1, t), ld(R1, icb + 3, t);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 9; t++) mm(R1, t);
             }
         }
-    }
+        if (icb < icbs) {
 #pragma unroll
-    for (int d = 0; d < D; d++)
-        if (c + d < nch) compute(R[d]);
+            for (int t = 0; t < 9; t++) mm(R0, t);
+        }
+    } else {
+        // chunk c = icb * 3 + ky: taps (ky, 0..2) of channel block icb
+        auto load = [&](C16Chunk<TM, BV> &R, int c) {
+            __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)xn, (short)0, bytes_x, 0x00020000);
+            __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)wpk, (short)0, bytes_w, 0x00020000);
+            const int icb = c / 3, ky = c - icb * 3;
+    #pragma unroll
+            for (int kx = 0; kx < 3; kx++) {
+                const int kg = icb * 9 + ky * 3 + kx;
+    #pragma unroll
+                for (int tm = 0; tm < TM; tm++) {
+                    auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, voa[tm], kg * 1024, 0);
+                    R.a[kx][tm] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                                              __uint_as_float(v[3]));
+                }
+    #pragma unroll
+                for (int s = 0; s < 4; s++)
+    #pragma unroll
+                    for (int q = 0; q < BV; q++)
+                        R.b[kx][s][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                            rx, off[q][ky * 3 + kx], (icb * 16 + 4 * s) * HW * 4, 0));
+            }
+        };
+        auto compute = [&](const C16Chunk<TM, BV> &R) {
+    #pragma unroll
+            for (int kx = 0; kx < 3; kx++)
+    #pragma unroll
+                for (int s = 0; s < 4; s++)
+    #pragma unroll
+                    for (int tm = 0; tm < TM; tm++) {
+                        const float4 &a4 = R.a[kx][tm];
+                        const float a = s == 0 ? a4.x : s == 1 ? a4.y : s == 2 ? a4.z : a4.w;
+    #pragma unroll
+                        for (int q = 0; q < BV; q++)
+                            acc[tm][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, R.b[kx][s][q], acc[tm][q], 0, 0, 0);
+                    }
+        };
+
+        // D chunks in flight (their loads fit the 63 outstanding vector loads a
+        // wave can count); the ring is unrolled so each chunk has fixed registers,
+        // and prefetch indices are clamped to the last chunk (a reload, in bounds)
+        // so the steady-state body has no branches.
+        constexpr int L = 3 * (TM + 4 * BV);
+        constexpr int D = 60 / L < 2 ? 2 : (60 / L > 4 ? 4 : 60 / L);
+        const int nch = icbs * 3;
+        const int last = nch - 1;
+        C16Chunk<TM, BV> R[D];
+    #pragma unroll
+        for (int d = 0; d < D; d++) load(R[d], min(d, last));
+        int c = 0;
+        // a chunk's refill loads are issued between its own MFMAs (two MFMAs per
+        // load; each load follows the MFMA that last reads its register), so the
+        // MFMA pipe is not left idle while they issue
+        constexpr int NGR = (12 * TM * BV + 1) / 2;
+        for (; c + D <= nch; c += D) {
+    #pragma unroll
+            for (int d = 0; d < D; d++) {
+                __builtin_amdgcn_sched_barrier(0);
+                compute(R[d]);
+                load(R[d], min(c + d + D, last));
+    #pragma unroll
+                for (int i = 0; i < NGR; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one VMEM read
+                }
+            }
+        }
+    #pragma unroll
+        for (int d = 0; d < D; d++)
+            if (c + d < nch) compute(R[d]);
+    }
 
     // ---- epilogue: activation, stores (16 lanes = 16 consecutive pixels per channel row)
 #pragma unroll
