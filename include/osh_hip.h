@@ -106,7 +106,9 @@ OSH_API osh_status osh_device_synchronize(void);
  *   "group3x3_tile": -1 (default) = grouped 3x3 launches
  *                 (osh_conv2d_group_f32) pick their tile by first-use timing
  *                 of the whole group; 0..N-1 forces one of the LDS-patch
- *                 tiles; all give the same bits.
+ *                 tiles (N/2..N-1: tile i - N/2 with one workgroup per CU,
+ *                 which leaves a long member's chain its SIMDs alone); all
+ *                 give the same bits.
  *   "group3x3_tiles" (get only): N.
  *   "group_pointwise_tile", "group_pointwise_tiles": the same for grouped
  *                 pointwise launches (the pointwise LDS tiles that fit every

@@ -515,7 +515,7 @@ constexpr int kC3Count = kC3X0 + kC16sxCount;
 int conv16_variant_count() { return kC3Count; }
 int pointwise_variant_count() { return 1 + kPW16Count; }
 int im2col3x3_variant_count() { return kC16sCount; }
-int group3x3_tile_count() { return kC16sCount; }
+int group3x3_tile_count() { return 2 * kC16sCount; }  // each tile shared, then one workgroup per CU
 int group_pointwise_tile_count() { return kPW16Count; }
 
 static bool c3_fits(const osh_conv_params *p, int v) {
@@ -998,7 +998,7 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
         if (v == 0 || cmax < bmax || (cmax == bmax && csum < bsum)) best = v, bmax = cmax, bsum = csum;
     }
     return tuned_launch_key(
-        std::make_tuple(kGroupTuneTag, gk), kC16sCount, group3x3_tile(), [](int) { return true; },
+        std::make_tuple(kGroupTuneTag, gk), group3x3_tile_count(), group3x3_tile(), [](int) { return true; },
         [&](int v) { return conv16s_group_launch(g, act, st, v < 0 ? best : v, ps[0].sh); }, st);
 }
 

@@ -393,9 +393,14 @@ __global__ __launch_bounds__(256) void conv16s_group_kernel(ConvGroup g) {
                                                           rest / g.mgroups[i]);
 }
 
-// Fills the block table of g for tile <TM, BV, TWL> and launches it.
+// Fills the block table of g for tile <TM, BV, TWL> and launches it.  With
+// `exclusive`, every workgroup also reserves more than half of a CU's LDS, so
+// no two workgroups share a CU: a member with a long chain then keeps its
+// SIMDs' MFMA pipes to itself instead of sharing them with the waves of
+// other members that would otherwise be placed on the same CU.
+constexpr int kConvGroupExclusiveLds = 84 * 1024;  // > 160 KB / 2 with any tile's own LDS
 template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC>
-inline osh_status conv16s_group_launch_t(ConvGroup g, int act, hipStream_t st) {
+inline osh_status conv16s_group_launch_t(ConvGroup g, int act, hipStream_t st, bool exclusive = false) {
     using G = C16sGeom<TM, BV, TWL, S, KS, CB, VEC>;
     long long total = 0;
     for (int i = 0; i < g.count; i++) {
@@ -410,7 +415,8 @@ inline osh_status conv16s_group_launch_t(ConvGroup g, int act, hipStream_t st) {
     g.start[g.count] = (int)total;
     OSH_DISPATCH_ACT(act, ACT,
                      hipLaunchKernelGGL((conv16s_group_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT>),
-                                        dim3((unsigned)total), dim3(256), 0, st, g));
+                                        dim3((unsigned)total), dim3(256), exclusive ? kConvGroupExclusiveLds : 0,
+                                        st, g));
     OSH_LAUNCH_CHECK("conv16s_group_kernel");
     return OSH_OK;
 }

@@ -6,10 +6,13 @@
 
 namespace osh {
 
+// Tiles kC16sCount and up are the same tiles, one workgroup per CU.
 osh_status conv16s_group_launch(ConvGroup g, int act, hipStream_t st, int tile, int s) {
-#define OSH_GROUP_TILE(TM, BV, TWL)                                                     \
-    return s == 1 ? conv16s_group_launch_t<TM, BV, TWL, 1, 3, 1, false>(g, act, st) \
-                  : conv16s_group_launch_t<TM, BV, TWL, 2, 3, 1, false>(g, act, st)
+    const bool ex = tile >= kC16sCount;
+    if (ex) tile -= kC16sCount;
+#define OSH_GROUP_TILE(TM, BV, TWL)                                                         \
+    return s == 1 ? conv16s_group_launch_t<TM, BV, TWL, 1, 3, 1, false>(g, act, st, ex) \
+                  : conv16s_group_launch_t<TM, BV, TWL, 2, 3, 1, false>(g, act, st, ex)
     switch (tile) {
     case 0: OSH_GROUP_TILE(1, 1, 16);
     case 1: OSH_GROUP_TILE(1, 2, 16);
