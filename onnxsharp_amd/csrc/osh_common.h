@@ -163,6 +163,8 @@ int group3x3_tile_count();
 // The same for grouped pointwise launches (the pointwise LDS tiles).
 int group_pointwise_tile();
 int group_pointwise_tile_count();
+// Forced tile of the fused 3x3 pair (-1 = first-use timing).
+int pair_tile();
 
 // Winograd F(2x2,3x3) for 3x3 stride-1 convolutions (0 = never, 1 = where
 // the reference's NCHWc kernel does not apply, 2 = ahead of the NCHWc

@@ -44,6 +44,7 @@
 
 #include "osh_conv16.h"
 #include "osh_conv16s.h"
+#include "osh_conv_pair.h"
 #include "osh_igemm.h"
 #include "osh_launch.h"
 #include "osh_winograd.h"
@@ -1059,6 +1060,41 @@ static osh_status check_launch(const osh_conv_params *p, const float *d_x, const
     return OSH_OK;
 }
 
+// ---- two chained 3x3 convs in one launch (osh_conv_pair.hip)
+
+constexpr int kPairTuneTag = 30;  // tuning-table tag of the fused pair
+
+// Why a pair cannot run fused, or nullptr: both convs 3x3 stride 1 pad 1 over
+// one 1 x C x H x W map, the second reading the first's output, 16/32/64
+// channels out of each, SiLU, and the single-conv dispatch taking for each
+// the chain the pair computes (NCHWc for 32 and 64 outputs, im2col for 16).
+static const char *pair_refusal(const osh_conv_params *pa, const osh_conv_params *pb, int act) {
+    auto same_map_3x3 = [](const osh_conv_params *p) {
+        return p->group == 1 && p->kh == 3 && p->kw == 3 && p->sh == 1 && p->sw == 1 && p->dh == 1 &&
+               p->dw == 1 && p->pt == 1 && p->pl == 1 && p->oh == p->h && p->ow == p->w;
+    };
+    if (!same_map_3x3(pa) || !same_map_3x3(pb)) return "both convs must be 3x3, stride 1, pad 1 on one map";
+    if (pa->n != 1 || pb->n != 1) return "batch 1 only";
+    if (pb->c != pa->m || pb->h != pa->h || pb->w != pa->w) return "the second conv must read the first one's output";
+    if (pa->c % 16 != 0 || pa->c > 64) return "the first conv must have 16, 32, 48 or 64 input channels";
+    auto cb_ok = [](int m) { return m == 16 || m == 32 || m == 64; };
+    if (!cb_ok(pa->m) || !cb_ok(pb->m)) return "each conv must have 16, 32 or 64 output channels";
+    if (act != OSH_ACT_SILU) return "the fused pair takes SiLU convs";
+    if ((long long)pa->c * pa->h * pa->w * 4 >= (1LL << 31)) return "input too large";
+    if (select_algo(pa) != (pa->m == 16 ? ALGO_CONV16I : ALGO_CONV16) ||
+        select_algo(pb) != (pb->m == 16 ? ALGO_CONV16I : ALGO_CONV16))
+        return "the single-conv dispatch takes another chain for one of the convs";
+    return nullptr;
+}
+
+static osh_status check_pack(const void *d_wpacked, const osh_conv_params *p) {
+    std::lock_guard<std::mutex> lk(g_packs_mu);
+    auto it = g_packs.find(reinterpret_cast<uintptr_t>(d_wpacked));
+    if (it != g_packs.end() && (it->second.algo != (int)select_algo(p) || it->second.key != conv_key(p)))
+        return fail(OSH_E_INVALID, "Conv pair: weights packed for another kernel or shape");
+    return OSH_OK;
+}
+
 }  // namespace osh
 
 extern "C" {
@@ -1102,6 +1138,55 @@ OSH_API osh_status osh_conv2d_add_f32(const osh_conv_params *p, const float *d_x
     if (ranges_overlap(d_res, y_bytes(p), d_y, y_bytes(p)))
         return fail(OSH_E_INVALID, "Conv+Add: the residual overlaps the output");
     return conv2d(p, d_x, d_wpacked, d_bias, act, d_res, d_y, to_stream(s));
+}
+
+OSH_API osh_status osh_conv2d_pair_check(const osh_conv_params *pa, const osh_conv_params *pb, int act) {
+    if (!pa || !pb) return fail(OSH_E_INVALID, "Conv pair: params is NULL");
+    osh_status st = check_params(pa);
+    if (st == OSH_OK) st = check_params(pb);
+    if (st != OSH_OK) return st;
+    if (const char *why = pair_refusal(pa, pb, act)) return fail(OSH_E_UNSUPPORTED, "Conv pair: %s", why);
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv_params *pb, const float *d_x,
+                                       const void *d_wa, const float *d_bias_a, const void *d_wb,
+                                       const float *d_bias_b, int act, const float *d_res, float *d_ya, float *d_y,
+                                       osh_stream s) {
+    osh_status st = osh_conv2d_pair_check(pa, pb, act);
+    if (st != OSH_OK) return st;
+    if (!d_x || !d_wa || !d_wb || !d_y) return fail(OSH_E_INVALID, "Conv pair: NULL tensor pointer");
+    if ((st = check_pack(d_wa, pa)) != OSH_OK || (st = check_pack(d_wb, pb)) != OSH_OK) return st;
+    // every workgroup reads input rows that neighbouring workgroups' outputs
+    // would cover if they overlapped; the residual is read only where the same
+    // thread then writes the output (so it may be the output itself)
+    const size_t xb = x_bytes(pa), yab = y_bytes(pa), yb = y_bytes(pb);
+    if (ranges_overlap(d_y, yb, d_x, xb) || (d_ya && ranges_overlap(d_ya, yab, d_x, xb)) ||
+        (d_ya && ranges_overlap(d_ya, yab, d_y, yb)))
+        return fail(OSH_E_INVALID, "Conv pair: an output overlaps the input or the other output");
+    if (d_res && d_res != d_y && ranges_overlap(d_res, yb, d_y, yb))
+        return fail(OSH_E_INVALID, "Conv pair: the residual partly overlaps the output");
+    if (d_res && d_ya && ranges_overlap(d_res, yb, d_ya, yab))
+        return fail(OSH_E_INVALID, "Conv pair: the residual overlaps the intermediate");
+    PairArgs a{};
+    a.h = pa->h;
+    a.w = pa->w;
+    a.c0 = pa->c;
+    a.x = d_x;
+    a.wa = static_cast<const float *>(d_wa);
+    a.ba = d_bias_a;
+    a.wb = static_cast<const float *>(d_wb);
+    a.bb = d_bias_b;
+    a.res = d_res;
+    a.ya = d_ya;
+    a.y = d_y;
+    const int cb1 = pa->m / 16, cb2 = pb->m / 16;
+    hipStream_t stream = to_stream(s);
+    const auto key = std::make_tuple(kPairTuneTag, mix_key(conv_key(pa), conv_key(pb)));
+    return tuned_launch_key(
+        key, conv_pair_tile_count(), pair_tile(), [](int) { return true; },
+        [&](int v) { return conv_pair_launch(a, cb1, cb2, stream, v < 0 ? (pa->h * pa->w >= 6400 ? 2 : 1) : v); },
+        stream);
 }
 
 }  // extern "C"

@@ -42,21 +42,16 @@ struct C16Chunk {
     float b[3][4][BV];    // per tap and k4 step: the lane's input value of each pixel
 };
 
-// WPB waves per workgroup: 4 packs a workgroup's waves onto one CU's SIMDs;
-// 1 spreads the same waves over as many CUs, which for maps with few tiles
-// and deep K leaves each wave a CU's L1 bandwidth for its operand stream.
-template <int TM, int BV, int ACT, int WPB = 4>
-__global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const float *__restrict__ x,
-                                                     const float *__restrict__ wpk, const float *__restrict__ bias,
-                                                     const float *__restrict__ res, float *__restrict__ y,
-                                                     int tiles_p) {
+// One wave's tile: pixel tile pt (16*BV output pixels), output-channel tile
+// mt (16*TM channels) of image n.  No barriers: any subset of a workgroup's
+// waves may run it.
+template <int TM, int BV, int ACT>
+__device__ __forceinline__ void conv16_wave(const osh_conv_params &p, const float *__restrict__ x,
+                                            const float *__restrict__ wpk, const float *__restrict__ bias,
+                                            const float *__restrict__ res, float *__restrict__ y, const int pt,
+                                            const int mt, const int n) {
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15, g = lane >> 4;
-    const int pt = blockIdx.x * WPB + wave;  // pixel tile
-    if (pt >= tiles_p) return;             // whole wave; no barriers below
-    const int mt = blockIdx.y;             // output-channel tile of 16*TM
-    const int n = blockIdx.z;
     const int HW = p.h * p.w, OHW = p.oh * p.ow;
     const int C = p.c, M = p.m;
     const int icbs = C / 16;
@@ -258,6 +253,20 @@ __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const fl
                 }
             }
         }
+}
+
+// WPB waves per workgroup: 4 packs a workgroup's waves onto one CU's SIMDs;
+// 1 spreads the same waves over as many CUs, which for maps with few tiles
+// and deep K leaves each wave a CU's L1 bandwidth for its operand stream.
+template <int TM, int BV, int ACT, int WPB = 4>
+__global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const float *__restrict__ x,
+                                                     const float *__restrict__ wpk, const float *__restrict__ bias,
+                                                     const float *__restrict__ res, float *__restrict__ y,
+                                                     int tiles_p) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int pt = blockIdx.x * WPB + wave;  // pixel tile
+    if (pt >= tiles_p) return;             // whole wave; no barriers in the tile
+    conv16_wave<TM, BV, ACT>(p, x, wpk, bias, res, y, pt, blockIdx.y, blockIdx.z);
 }
 
 // Same chain with the workgroup's weights resident in LDS: the four waves of

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "osh_common.h"
+#include "osh_conv_pair.h"
 
 namespace osh {
 
@@ -36,6 +37,7 @@ static int g_winograd = -3;         // -3: read ONNXSHARP_HIP_WINOGRAD on first 
 static int g_i2c_variant = -3;      // -3: read ONNXSHARP_HIP_IM2COL3X3_VARIANT on first use
 static int g_group3x3_tile = -1;    // forced tile of grouped 3x3 launches (-1: first-use timing)
 static int g_group_pw_tile = -1;    // forced tile of grouped pointwise launches (-1: first-use timing)
+static int g_pair_tile = -1;        // forced tile of the fused 3x3 pair (-1: first-use timing)
 static long long g_wino_max = -3;   // -3: read ONNXSHARP_WINO_MAX on first use
 
 bool exact_silu() {
@@ -88,6 +90,7 @@ int im2col3x3_variant() {
 
 int group3x3_tile() { return g_group3x3_tile; }
 int group_pointwise_tile() { return g_group_pw_tile; }
+int pair_tile() { return g_pair_tile; }
 
 int winograd_mode() {
     if (g_winograd == -3) {
@@ -172,6 +175,12 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         g_group3x3_tile = value;
         return OSH_OK;
     }
+    if (strcmp(key, "pair_tile") == 0) {
+        if (value < -1 || value >= conv_pair_tile_count())
+            return fail(OSH_E_INVALID, "pair_tile %d out of range [-1, %d)", value, conv_pair_tile_count());
+        g_pair_tile = value;
+        return OSH_OK;
+    }
     if (strcmp(key, "group_pointwise_tile") == 0) {
         if (value < -1 || value >= group_pointwise_tile_count())
             return fail(OSH_E_INVALID, "group_pointwise_tile %d out of range [-1, %d)", value,
@@ -232,6 +241,14 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     }
     if (strcmp(key, "group_pointwise_tile") == 0) {
         *value = group_pointwise_tile();
+        return OSH_OK;
+    }
+    if (strcmp(key, "pair_tile") == 0) {
+        *value = pair_tile();
+        return OSH_OK;
+    }
+    if (strcmp(key, "pair_tiles") == 0) {
+        *value = conv_pair_tile_count();
         return OSH_OK;
     }
     if (strcmp(key, "group_pointwise_tiles") == 0) {

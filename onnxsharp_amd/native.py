@@ -110,6 +110,9 @@ _SIGS = {
     "osh_conv2d_f32": ([C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp], _i),
     "osh_conv2d_add_f32": ([C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp, _vp], _i),
     "osh_conv2d_group_f32": ([_i, C.POINTER(ConvParams), _vp, _vp, _vp, _i, _vp, _vp, _vp], _i),
+    "osh_conv2d_pair_f32": ([C.POINTER(ConvParams), C.POINTER(ConvParams), _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp,
+                             _vp, _vp], _i),
+    "osh_conv2d_pair_check": ([C.POINTER(ConvParams), C.POINTER(ConvParams), _i], _i),
     "osh_gemm_f32": ([_i, _i, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _vp], _i),
     "osh_gemm_f32_batched": ([_i, _i, _i, _i, _vp, _i, _i64, _vp, _i, _i64, _vp, _i, _vp, _i, _i64, _vp], _i),
     "osh_matmul_infer_shape": ([_i64p, _i, _i64p, _i, _i64p, C.POINTER(C.c_int)], _i),

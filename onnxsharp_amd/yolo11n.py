@@ -123,6 +123,24 @@ class ChainOp:
 
 
 @dataclass(eq=False)
+class PairOp:
+    """Two chained 3x3 SiLU convs over one map -- a bottleneck's cv1 -> cv2,
+    b reading a's output -- run as one launch (osh_conv2d_pair_f32): a's
+    output stays on chip for b and is still written to a.y."""
+    name: str
+    a: ConvOp
+    b: ConvOp
+
+    @property
+    def ops(self):
+        return [self.a, self.b]
+
+    @property
+    def flops(self):
+        return self.a.flops + self.b.flops
+
+
+@dataclass(eq=False)
 class AddOp:
     name: str
     a: Slice
@@ -207,7 +225,7 @@ class Model:
         for o in self.ops:
             if isinstance(o, ConvOp):
                 out.append(o)
-            elif isinstance(o, (GroupConvOp, ChainOp)):
+            elif isinstance(o, (GroupConvOp, ChainOp, PairOp)):
                 out.extend(o.ops)
         return out
 
@@ -730,7 +748,65 @@ def chain_pointwise_convs(model: Model, max_ops: int = 6, min_gain_us: float = 0
     return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
 
 
-def fuse_launches(model: Model, chains: bool = False) -> Model:
+def pair_bottleneck_convs(model: Model, takes=None, min_pixels: int = 6400) -> Model:
+    """Adjacent 3x3 SiLU convs where the second reads exactly the first's
+    output and nothing else touches that buffer (a bottleneck's cv1 -> cv2)
+    become one PairOp, on maps of at least `min_pixels`, where `takes(a, b)`
+    (default: the library's osh_conv2d_pair_check on the resolved params)
+    accepts them.
+
+    A pair saves a launch and the intermediate's round trip, but each
+    workgroup also computes the first conv over a one-pixel ring around its
+    tile, on its own CU's four MFMA pipes: one 16x16x4 FP32 MFMA keeps a
+    pipe busy for its full 32 cycles, so the ring's extra blocks cost time
+    one for one.  On the 640 frame's 80x80 pairs (32 -> 16 -> 32) the pair
+    ran 7.2 us against 8.9 us as two launches; on the 40x40 and 20x20 pairs
+    it ran 8.0-15.1 us against 8.1-10.6 us."""
+    takes = takes or pair_supported
+    ops = list(model.ops)
+    users = {}
+    for o in ops:
+        r, w = op_access(o)
+        for sl in r + w:
+            users.setdefault(id(sl.buf), set()).add(id(o))
+    out, i = [], 0
+    while i < len(ops):
+        a = ops[i]
+        b = ops[i + 1] if i + 1 < len(ops) else None
+        if (isinstance(a, ConvOp) and isinstance(b, ConvOp) and a.res is None and
+                all(c.k == 3 and c.s == 1 and c.group == 1 and c.act == "Silu" for c in (a, b)) and
+                a.y.h * a.y.w >= min_pixels and
+                b.x.buf is a.y.buf and b.x.c0 == a.y.c0 and b.x.c == a.y.c == a.y.buf.c and
+                users.get(id(a.y.buf)) == {id(a), id(b)} and takes(a, b)):
+            out.append(PairOp(a.name.rsplit("/", 3)[0] + "#pair", a, b))
+            i += 2
+            continue
+        out.append(a)
+        i += 1
+    m = Model(model.size, model.bufs, out, model.input, model.outputs)
+    return m
+
+
+def _conv_params(op: ConvOp) -> N.ConvParams:
+    attrs = N.ConvAttrs()
+    attrs.group = op.group
+    attrs.n_kernel_shape, attrs.kernel_shape[0], attrs.kernel_shape[1] = 2, op.k, op.k
+    attrs.n_strides, attrs.strides[0], attrs.strides[1] = 2, op.s, op.s
+    attrs.n_pads = 4
+    for i in range(4):
+        attrs.pads[i] = op.k // 2
+    p = N.ConvParams()
+    N.call("osh_conv_resolve", C.byref(attrs), N.dims64(op.x.shape), N.dims64(op.w.shape), C.byref(p))
+    return p
+
+
+def pair_supported(a: ConvOp, b: ConvOp) -> bool:
+    """Whether osh_conv2d_pair_f32 takes conv a followed by conv b (a host-side check)."""
+    pa, pb = _conv_params(a), _conv_params(b)
+    return N.lib().osh_conv2d_pair_check(C.byref(pa), C.byref(pb), N.ACTIVATIONS[a.act]) == 0
+
+
+def fuse_launches(model: Model, chains: bool = False, pairs: bool = True) -> Model:
     """The launch-saving rewrites of the op list (residual Adds into their
     convs, SPPF's pool chain into one op, the head's three scales per layer
     into one op, other independent convs of one kind into one op, and with
@@ -741,6 +817,8 @@ def fuse_launches(model: Model, chains: bool = False) -> Model:
     MFMA accumulator per wave, while separate launches spread each stage over
     the chip), 0.493 against 0.465 ms per frame."""
     m = group_independent_convs(group_head_convs(fuse_pool_chains(fuse_residual_adds(model))))
+    if pairs:
+        m = pair_bottleneck_convs(m)
     return chain_pointwise_convs(m) if chains else m
 
 
@@ -757,7 +835,7 @@ def _tiling(c, slices):
 
 def op_access(op):
     """(reads, writes) of an op as lists of channel slices."""
-    if isinstance(op, (GroupConvOp, ChainOp)):
+    if isinstance(op, (GroupConvOp, ChainOp, PairOp)):
         acc = [op_access(o) for o in op.ops]
         return [r for a in acc for r in a[0]], [w for a in acc for w in a[1]]
     if isinstance(op, AddOp):
@@ -845,11 +923,11 @@ class Frame:
     of the neck -- run side by side."""
 
     def __init__(self, model: Model, device, nstreams: int = 4, fuse: bool = True, fused_attention: bool = True,
-                 chains: bool = False):
+                 chains: bool = False, pairs: bool = True):
         import torch
         self.fused_attention = fused_attention
-        if fuse:  # conv -> residual Add pairs, SPPF's pools, grouped and chained convs run as single launches
-            model = fuse_launches(model, chains=chains)
+        if fuse:  # conv -> residual Add pairs, SPPF's pools, grouped, paired and chained convs as single launches
+            model = fuse_launches(model, chains=chains, pairs=pairs)
         self.model = model
         self.device = device
         for b in model.bufs:
@@ -890,6 +968,14 @@ class Frame:
             return lambda st: N.check(lib.osh_conv2d_group_f32(n, ps, xs, ws, bs, act, rs, ys, st))
         if isinstance(op, ChainOp):
             return self._prepare_chain(op)
+        if isinstance(op, PairOp):
+            pa, wa, ba = self._prepare_conv(op.a)
+            pb, wb, bb = self._prepare_conv(op.b)
+            act = N.ACTIVATIONS[op.a.act]
+            res = op.b.res.ptr() if op.b.res is not None else None
+            return lambda st: N.check(lib.osh_conv2d_pair_f32(
+                C.byref(pa), C.byref(pb), op.a.x.ptr(), C.c_void_p(wa.data_ptr()), C.c_void_p(ba.data_ptr()),
+                C.c_void_p(wb.data_ptr()), C.c_void_p(bb.data_ptr()), act, res, op.a.y.ptr(), op.b.y.ptr(), st))
         if isinstance(op, ConvOp):
             p, packed, b = self._prepare_conv(op)
             act = N.ACTIVATIONS[op.act]
@@ -904,15 +990,7 @@ class Frame:
     def _prepare_conv(self, op):
         """Resolved params, packed weights and bias of a conv (packed once)."""
         import torch
-        attrs = N.ConvAttrs()
-        attrs.group = op.group
-        attrs.n_kernel_shape, attrs.kernel_shape[0], attrs.kernel_shape[1] = 2, op.k, op.k
-        attrs.n_strides, attrs.strides[0], attrs.strides[1] = 2, op.s, op.s
-        attrs.n_pads = 4
-        for i in range(4):
-            attrs.pads[i] = op.k // 2
-        p = N.ConvParams()
-        N.call("osh_conv_resolve", C.byref(attrs), N.dims64(op.x.shape), N.dims64(op.w.shape), C.byref(p))
+        p = _conv_params(op)
         assert (p.m, p.oh, p.ow) == (op.y.c, op.y.h, op.y.w), op.name
         nbytes = C.c_size_t()
         N.call("osh_conv_packed_weight_bytes", C.byref(p), C.byref(nbytes))

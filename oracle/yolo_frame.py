@@ -97,9 +97,10 @@ class Frame:
         from onnxsharp_amd import yolo11n as Y
         self.put(Y.whole(self.model.input), x)
         for grouped in self.model.ops:
-            # a GroupConvOp's convs are independent and a ChainOp's chains
-            # are, with stages in order: run the convs one by one
-            for op in grouped.ops if isinstance(grouped, (Y.GroupConvOp, Y.ChainOp)) else [grouped]:
+            # a GroupConvOp's convs are independent, a ChainOp's chains are
+            # (stages in order) and a PairOp is two convs in order: run the
+            # convs one by one
+            for op in grouped.ops if isinstance(grouped, (Y.GroupConvOp, Y.ChainOp, Y.PairOp)) else [grouped]:
                 ins = [np.ascontiguousarray(self.get(s)) for s in op_inputs(op)]
                 self.put(op.y, run_op(oracle, op, ins))
         return [self.arrays[id(b)] for b in self.model.outputs]

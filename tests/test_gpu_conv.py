@@ -502,6 +502,9 @@ GROUP_CASES = [
     ("head_pointwise_res", [((1, 64, 80, 80), (80, 64, 1, 1), 1), ((1, 80, 40, 40), (80, 80, 1, 1), 1),
                             ((1, 80, 20, 20), (80, 80, 1, 1), 1), ((1, 48, 9, 6), (32, 48, 1, 1), 1)], None, True),
     ("mixed_fallback", [((1, 64, 20, 20), (64, 64, 3, 3), 1), ((1, 32, 20, 20), (32, 1, 3, 3), 32)], "Relu", True),
+    # stride 2, odd maps, a deep member first (the streamed one-wave member of the mixed tiles)
+    ("strided_3x3", [((1, 32, 41, 39), (48, 32, 3, 3), 1, 2), ((1, 128, 11, 13), (32, 128, 3, 3), 1, 2)],
+     "Silu", True),
 ]
 
 
@@ -523,12 +526,15 @@ def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
     print(f"conv group {name}", flush=True)
     n = len(convs)
     layers, xs, ws, bs, rs, ys, ref, ps, packs = [], [], [], [], [], [], [], [], []
-    for k, (xsh, wsh, g) in enumerate(convs):
+    for k, conv in enumerate(convs):
+        xsh, wsh, g = conv[:3]
+        stride = conv[3] if len(conv) > 3 else 1
         seed = 23 * k + sum(xsh) + sum(wsh)
         x = _t(synth.uniform(seed, xsh), cuda)
         w = _t(synth.normal(seed + 1, wsh, 0, 0.05), cuda)
         b = _t(synth.normal(seed + 2, (wsh[0],), 0, 0.01), cuda)
-        layer = ConvLayer(fused_activation=act, group=g, pads=[1, 1, 1, 1] if wsh[2] == 3 else [0, 0, 0, 0])
+        layer = ConvLayer(fused_activation=act, group=g, pads=[1, 1, 1, 1] if wsh[2] == 3 else [0, 0, 0, 0],
+                          strides=[stride, stride])
         y0 = layer.forward(x, w, b)
         r = torch.from_numpy(synth.normal(seed + 3, tuple(y0.shape), 0, 1)).to(cuda) if residual else None
         if r is not None:
@@ -543,7 +549,8 @@ def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
     st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     # the 3x3 and pointwise groups: every tile forced in turn (the first-use
     # timing would keep only the last tile's output), then the automatic choice
-    key = {"head_3x3_nchwc": b"group3x3_tile", "head_pointwise_res": b"group_pointwise_tile"}.get(name)
+    key = {"head_3x3_nchwc": b"group3x3_tile", "strided_3x3": b"group3x3_tile",
+           "head_pointwise_res": b"group_pointwise_tile"}.get(name)
     tiles = list(range(_group_tiles(key))) if key else []
     try:
         for tile in tiles + [-1]:
@@ -583,3 +590,109 @@ def test_device_chain_order_pinned_by_planted_magnitudes(cuda, oracle, case, m, 
     assert (y[0, :, 1, 1] == np.float32(want[chain])).all(), y[0, :, 1, 1]
     ref = oracle_conv(oracle, x, w, b, p, None)
     assert np.array_equal(y, ref)
+
+
+PAIR_CASES = [
+    # (name, x shape, c1, c2, residual, options) -- a bottleneck's cv1 -> cv2
+    ("c3k2_80", (1, 32, 80, 80), 16, 32, True, {}),          # im2col chain, then NCHWc
+    ("c3k_40", (1, 32, 40, 40), 32, 32, True, {}),
+    ("c3k2_neck_40", (1, 64, 40, 40), 32, 64, False, {}),
+    ("c3k_20", (1, 64, 20, 20), 64, 64, True, {}),
+    ("odd_map", (1, 32, 13, 11), 16, 32, True, {"winograd": 0}),
+    ("deep_ragged", (1, 48, 7, 9), 64, 16, True, {"winograd": 0}),  # 3 input chunks, im2col second conv
+    ("exact_silu", (1, 64, 20, 20), 32, 32, False, {"exact_silu": 1}),
+]
+
+
+@pytest.mark.parametrize("name,xs,c1,c2,residual,opts", PAIR_CASES, ids=[c[0] for c in PAIR_CASES])
+def test_conv_pair_equals_two_launches(cuda, name, xs, c1, c2, residual, opts):
+    # osh_conv2d_pair_f32 runs a bottleneck's two 3x3 convs in one launch with
+    # the intermediate on chip: its outputs (and the intermediate it still
+    # stores) are those of the two separate launches, bit for bit, under every
+    # tile and under the first-use choice.
+    import torch
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    print(f"conv pair {name}", flush=True)
+    saved = {}
+    for k, v in opts.items():
+        cur = C.c_int(); N.call("osh_config_get", k.encode(), C.byref(cur)); saved[k] = cur.value
+        N.call("osh_config_set", k.encode(), v)
+    try:
+        seed = sum(xs) + 7 * c1 + c2
+        x = _t(synth.uniform(seed, xs), cuda)
+        wa = _t(synth.normal(seed + 1, (c1, xs[1], 3, 3), 0, 0.05), cuda)
+        ba = _t(synth.normal(seed + 2, (c1,), 0, 0.01), cuda)
+        wb = _t(synth.normal(seed + 3, (c2, c1, 3, 3), 0, 0.05), cuda)
+        bb = _t(synth.normal(seed + 4, (c2,), 0, 0.01), cuda)
+        la = ConvLayer(pads=[1, 1, 1, 1], fused_activation="Silu")
+        lb = ConvLayer(pads=[1, 1, 1, 1], fused_activation="Silu")
+        t_ref = la.forward(x, wa, ba)
+        r = _t(synth.normal(seed + 5, (1, c2, xs[2], xs[3]), 0, 1), cuda) if residual else None
+        y_ref = lb.forward(t_ref, wb, bb, residual=r)
+        torch.cuda.synchronize()
+        t_ref, y_ref = t_ref.cpu().numpy(), y_ref.cpu().numpy()
+        _, pa, bufa = la._packed
+        _, pb, bufb = lb._packed
+        st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        N.call("osh_conv2d_pair_check", C.byref(pa), C.byref(pb), N.ACT_SILU)
+        nt = C.c_int(); N.call("osh_config_get", b"pair_tiles", C.byref(nt))
+        ptr = lambda t: C.c_void_p(t.data_ptr()) if t is not None else None
+        try:
+            for tile in list(range(nt.value)) + [-1]:
+                N.call("osh_config_set", b"pair_tile", tile)
+                ya = torch.full((1, c1, xs[2], xs[3]), float("nan"), device=cuda)
+                y = torch.full((1, c2, xs[2], xs[3]), float("nan"), device=cuda)
+                N.call("osh_conv2d_pair_f32", C.byref(pa), C.byref(pb), ptr(x), ptr(bufa), ptr(ba), ptr(bufb),
+                       ptr(bb), N.ACT_SILU, ptr(r), ptr(ya), ptr(y), st)
+                torch.cuda.synchronize()
+                assert np.array_equal(ya.cpu().numpy(), t_ref), f"{name}: intermediate differs under tile {tile}"
+                assert np.array_equal(y.cpu().numpy(), y_ref), f"{name}: output differs under tile {tile}"
+        finally:
+            N.call("osh_config_set", b"pair_tile", -1)
+        # the intermediate may be left unstored; the residual may be the output itself
+        y2 = torch.from_numpy(synth.normal(seed + 5, (1, c2, xs[2], xs[3]), 0, 1)).to(cuda) if residual else \
+            torch.empty((1, c2, xs[2], xs[3]), device=cuda)
+        N.call("osh_conv2d_pair_f32", C.byref(pa), C.byref(pb), ptr(x), ptr(bufa), ptr(ba), ptr(bufb), ptr(bb),
+               N.ACT_SILU, ptr(y2) if residual else None, None, ptr(y2), st)
+        torch.cuda.synchronize()
+        assert np.array_equal(y2.cpu().numpy(), y_ref)
+    finally:
+        for k, v in saved.items():
+            N.call("osh_config_set", k.encode(), v)
+
+
+def test_conv_pair_refusals(cuda):
+    import torch
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+
+    def params(xs, m, k=3, s=1, pads=(1, 1, 1, 1)):
+        return ConvLayer(pads=list(pads), strides=[s, s]).resolve(xs, (m, xs[1], k, k))
+
+    ok = (params((1, 32, 40, 40), 32), params((1, 32, 40, 40), 64))
+    N.call("osh_conv2d_pair_check", C.byref(ok[0]), C.byref(ok[1]), N.ACT_SILU)
+    bad = [
+        ("stride 2", params((1, 32, 40, 40), 32, s=2), ok[1], N.ACT_SILU),
+        ("1x1", params((1, 32, 40, 40), 32, k=1, pads=(0, 0, 0, 0)), ok[1], N.ACT_SILU),
+        ("48 outputs", params((1, 32, 40, 40), 48), params((1, 48, 40, 40), 32), N.ACT_SILU),
+        ("8 input channels", params((1, 8, 40, 40), 32), ok[1], N.ACT_SILU),
+        ("not chained", ok[0], params((1, 16, 40, 40), 32), N.ACT_SILU),
+        ("relu", ok[0], ok[1], N.ACT_RELU),
+        ("winograd chain", params((1, 32, 40, 40), 16), params((1, 16, 40, 40), 32), N.ACT_SILU),
+    ]
+    for what, pa, pb, act in bad:
+        with pytest.raises(N.OshError) as e:
+            N.call("osh_conv2d_pair_check", C.byref(pa), C.byref(pb), act)
+        assert e.value.status == N.OSH_E_UNSUPPORTED, what
+    # outputs may not overlap the input
+    la, lb = ConvLayer(pads=[1, 1, 1, 1]), ConvLayer(pads=[1, 1, 1, 1])
+    buf = torch.zeros((1, 128, 40, 40), device=cuda)
+    wa, wb = torch.zeros((32, 32, 3, 3), device=cuda), torch.zeros((64, 32, 3, 3), device=cuda)
+    pa, bufa = la.prepack_weights((1, 32, 40, 40), wa)
+    pb, bufb = lb.prepack_weights((1, 32, 40, 40), wb)
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sl = lambda c0: C.c_void_p(buf.data_ptr() + 4 * c0 * 1600)
+    with pytest.raises(N.OshError, match="overlaps"):
+        N.call("osh_conv2d_pair_f32", C.byref(pa), C.byref(pb), sl(0), C.c_void_p(bufa.data_ptr()), None,
+               C.c_void_p(bufb.data_ptr()), None, N.ACT_SILU, None, None, sl(16), st)

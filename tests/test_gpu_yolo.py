@@ -61,7 +61,7 @@ def test_yolo_per_op_parity(cuda, oracle, exact_silu, size, chains):
             # launch of convs in chains: check each conv against the oracle
             # run one by one over host copies of the buffers the launch
             # touches, taken before it (later stages read earlier outputs)
-            members = launch.ops if isinstance(launch, (Y.GroupConvOp, Y.ChainOp)) else [launch]
+            members = launch.ops if isinstance(launch, (Y.GroupConvOp, Y.ChainOp, Y.PairOp)) else [launch]
             reads, writes = Y.op_access(launch)
             host = {}
             for sl in reads + writes:

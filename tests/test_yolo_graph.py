@@ -179,9 +179,35 @@ def test_c2f_block_structure():
     assert len(add) == 1 and (add[0].y.c0, add[0].y.c, add[0].y.buf.c) == (128, 64, 192)
     assert add[0].a.buf is add[0].y.buf and add[0].a.c0 == 64  # the shortcut is the split's second half
     assert abs(sum(o.flops for o in m.convs) / 1e9 - 1.4680064) < 1e-9
-    f = Y.fuse_launches(m)
+    f = Y.fuse_launches(m, pairs=False)
     assert len(f.ops) == 4 and f.ops[2].res is not None and f.ops[2].res.c0 == 64
+    # by default the bottleneck's two 3x3 convs run as one pair launch
+    f = Y.fuse_launches(m)
+    assert len(f.ops) == 3 and isinstance(f.ops[1], Y.PairOp)
+    pair = f.ops[1]
+    assert pair.b.x.buf is pair.a.y.buf and pair.b.res.c0 == 64 and pair.a.x.c0 == 64
     assert [(b.c, b.h, b.w) for b in m.outputs] == [(128, 80, 80)]
+
+
+def test_pairs_of_the_640_frame():
+    # the bottleneck pairs the frame fuses: the two 80x80 ones (the pair
+    # kernel's ring recompute makes it slower than two launches on the
+    # 40x40 and 20x20 maps); the library's own check decides what it takes
+    from onnxsharp_amd import yolo11n as Y
+    m = Y.build(640)
+    f = Y.fuse_launches(m)
+    pairs = [o for o in f.ops if isinstance(o, Y.PairOp)]
+    assert [(p.a.x.c, p.a.y.c, p.b.y.c, p.a.x.h) for p in pairs] == [(32, 16, 32, 80), (32, 16, 32, 80)]
+    assert all(p.b.res is not None and p.b.res.buf is p.a.x.buf for p in pairs)
+    assert len(f.ops) == len(Y.fuse_launches(m, pairs=False).ops) - 2
+    # without the map-size floor every bottleneck pair the library takes fuses
+    g = Y.pair_bottleneck_convs(Y.fuse_launches(m, pairs=False), min_pixels=0)
+    assert len([o for o in g.ops if isinstance(o, Y.PairOp)]) == 10
+    # the 160x160 pair (16 -> 8 -> 16) has an 8-channel intermediate: refused
+    assert not any(p.a.x.h == 160 for p in (o for o in g.ops if isinstance(o, Y.PairOp)))
+    # a refusal from the library keeps the convs separate
+    h = Y.pair_bottleneck_convs(Y.fuse_launches(m, pairs=False), takes=lambda a, b: False, min_pixels=0)
+    assert not any(isinstance(o, Y.PairOp) for o in h.ops)
 
 
 def test_decode_appends_dfl_and_sigmoid_per_scale():
@@ -201,9 +227,10 @@ def test_head_convs_group_by_layer(model):
     # The Detect head's 24 convs become 8 groups (one per layer, the three
     # scales in order), placed where the head was; with the C3k blocks' paired
     # 1x1 convs and the positional conv's two heads grouped too, the frame
-    # drops from 92 launches to 72 (before the pointwise chains).
+    # drops from 92 launches to 72 (before the bottleneck pairs and the
+    # pointwise chains).
     from onnxsharp_amd import yolo11n as Y
-    fused = Y.fuse_launches(model, chains=False)
+    fused = Y.fuse_launches(model, chains=False, pairs=False)
     head = [o for o in fused.ops if isinstance(o, Y.GroupConvOp) and o.name.startswith("/model.23/cv")]
     other = [o for o in fused.ops if isinstance(o, Y.GroupConvOp) and o not in head]
     assert len(head) == 8 and len(other) == 4 and len(fused.ops) == 72
@@ -232,11 +259,11 @@ def test_pointwise_chains_of_the_640_frame(model):
     # and the head's class branch in two launches of three scales: 72
     # launches become 67.  (The C2PSA tail's 576 KB of weights do not fit.)
     from onnxsharp_amd import yolo11n as Y
-    fused = Y.fuse_launches(model, chains=True)
+    fused = Y.fuse_launches(model, chains=True, pairs=False)
     chains = [o for o in fused.ops if isinstance(o, Y.ChainOp)]
     assert len(fused.ops) == 67 and len(chains) == 4
-    assert len(Y.fuse_launches(model).ops) == 72  # off by default
-    unchained = Y.fuse_launches(model, chains=False)
+    assert len(Y.fuse_launches(model, pairs=False).ops) == 72  # off by default
+    unchained = Y.fuse_launches(model, chains=False, pairs=False)
     assert sorted(o.name for o in fused.convs) == sorted(o.name for o in unchained.convs)
     shapes = [[[(o.x.c, o.y.c, o.y.h) for o in ch] for ch in c.chains] for c in chains]
     assert [[(128, 128, 40), (64, 32, 40), (64, 32, 40)]] in shapes  # model.6 cv1 -> C3k cv1, cv2
