@@ -113,8 +113,9 @@ OSH_API osh_status osh_device_synchronize(void);
  *   "group_pointwise_tile", "group_pointwise_tiles": the same for grouped
  *                 pointwise launches (the pointwise LDS tiles that fit every
  *                 member; a forced tile that does not fit takes the default).
- *   "pair_tile", "pair_tiles": the same for osh_conv2d_pair_f32 (its output
- *                 tiles, 4x4, 4x8, 8x8).
+ *   "pair_tile", "pair_tiles": the same for osh_conv2d_pair_f32: its
+ *                 output tiles (4x4, 4x8, 8x8), then N-1 = the two convs as
+ *                 separate launches (only with an intermediate buffer).
  *   "pointwise_variants" (get only): N.
  *                 The -2 setting of "pointwise_variant" changes the packed
  *                 weight layout: pack again after changing it.
@@ -278,13 +279,15 @@ OSH_API osh_status osh_conv2d_group_f32(int count, const osh_conv_params *ps, co
  * C3k2 / C3k blocks of YOLO11n).  d_wa / d_wb are each conv's weights packed
  * by osh_conv_pack_weights; the result is that of osh_conv2d_f32(pa) into
  * d_ya followed by osh_conv2d_f32 / osh_conv2d_add_f32(pb) into d_y (with the
- * residual d_res, which may be NULL or d_y itself), bit for bit: each conv
+ * residual d_res, which may be NULL), bit for bit: each conv
  * keeps its chain, and the intermediate stays on chip (it is still written to
- * d_ya unless d_ya is NULL).  Takes 3x3 stride-1 pad-1 SiLU convs on one
+ * d_ya unless d_ya is NULL).  First-use timing chooses between the fused
+ * kernel's tiles and, when d_ya is given, two separate launches, whichever
+ * is faster for the shapes.  Takes 3x3 stride-1 pad-1 SiLU convs on one
  * 1 x C x H x W map, C = 16 / 32 / 48 / 64, 16 / 32 / 64 output channels each, in the
  * chain orders the single-conv dispatch takes for them; anything else returns
  * OSH_E_UNSUPPORTED (run the two convs separately).  No output may overlap
- * d_x or the other output. */
+ * d_x or the other output, and the residual may not overlap d_y. */
 OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv_params *pb, const float *d_x,
                                        const void *d_wa, const float *d_bias_a, const void *d_wb,
                                        const float *d_bias_b, int act, const float *d_res, float *d_ya, float *d_y,

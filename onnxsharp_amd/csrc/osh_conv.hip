@@ -578,13 +578,16 @@ template <class Fits, class Launch>
 static osh_status tuned_launch_key(const std::tuple<int, ConvKey> &key, int count, int forced, Fits fits,
                                    Launch launch, hipStream_t st) {
     if (forced >= 0 || !tuning_enabled()) return launch(forced >= 0 && forced < count && fits(forced) ? forced : -1);
+    int chosen = -1;
     {
         std::lock_guard<std::mutex> lk(g_tune_mu);
         tune_db_read_locked();
         auto it = g_tuned.find(key);
-        if (it != g_tuned.end() && it->second >= 0 && it->second < count && fits(it->second))
-            return launch(it->second);
+        if (it != g_tuned.end()) chosen = it->second;
     }
+    // launched outside the lock: a launch may itself be a tuned launch (the
+    // conv pair's two-launch form runs each conv through its own choice)
+    if (chosen >= 0 && chosen < count && fits(chosen)) return launch(chosen);
     if (capturing(st)) return launch(-1);
     hipEvent_t e0, e1;
     OSH_HIP_CHECK(hipEventCreate(&e0));
@@ -1062,7 +1065,7 @@ static osh_status check_launch(const osh_conv_params *p, const float *d_x, const
 
 // ---- two chained 3x3 convs in one launch (osh_conv_pair.hip)
 
-constexpr int kPairTuneTag = 30;  // tuning-table tag of the fused pair
+constexpr int kPairTuneTag = 30;  // tuning-table tags of the fused pair (+1 without an intermediate buffer)
 
 // Why a pair cannot run fused, or nullptr: both convs 3x3 stride 1 pad 1 over
 // one 1 x C x H x W map, the second reading the first's output, 16/32/64
@@ -1158,14 +1161,14 @@ OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv
     if (!d_x || !d_wa || !d_wb || !d_y) return fail(OSH_E_INVALID, "Conv pair: NULL tensor pointer");
     if ((st = check_pack(d_wa, pa)) != OSH_OK || (st = check_pack(d_wb, pb)) != OSH_OK) return st;
     // every workgroup reads input rows that neighbouring workgroups' outputs
-    // would cover if they overlapped; the residual is read only where the same
-    // thread then writes the output (so it may be the output itself)
+    // would cover if they overlapped; a residual inside the output would be
+    // added again by every launch of first-use timing
     const size_t xb = x_bytes(pa), yab = y_bytes(pa), yb = y_bytes(pb);
     if (ranges_overlap(d_y, yb, d_x, xb) || (d_ya && ranges_overlap(d_ya, yab, d_x, xb)) ||
         (d_ya && ranges_overlap(d_ya, yab, d_y, yb)))
         return fail(OSH_E_INVALID, "Conv pair: an output overlaps the input or the other output");
-    if (d_res && d_res != d_y && ranges_overlap(d_res, yb, d_y, yb))
-        return fail(OSH_E_INVALID, "Conv pair: the residual partly overlaps the output");
+    if (d_res && ranges_overlap(d_res, yb, d_y, yb))
+        return fail(OSH_E_INVALID, "Conv pair: the residual overlaps the output");
     if (d_res && d_ya && ranges_overlap(d_res, yb, d_ya, yab))
         return fail(OSH_E_INVALID, "Conv pair: the residual overlaps the intermediate");
     PairArgs a{};
@@ -1182,10 +1185,24 @@ OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv
     a.y = d_y;
     const int cb1 = pa->m / 16, cb2 = pb->m / 16;
     hipStream_t stream = to_stream(s);
-    const auto key = std::make_tuple(kPairTuneTag, mix_key(conv_key(pa), conv_key(pb)));
+    // Variants: the pair kernel's tiles, then (when the intermediate has a
+    // buffer) the two convs as separate launches -- the pair's ring
+    // recompute runs on one CU's four MFMA pipes, which loses to two
+    // launches on small maps and wide intermediates.  First-use timing picks;
+    // before it (graph capture) the pair runs on maps of 80x80 and more with
+    // at most 32 intermediate channels.
+    const int ntile = conv_pair_tile_count();
+    const auto key = std::make_tuple(kPairTuneTag + (d_ya ? 0 : 1), mix_key(conv_key(pa), conv_key(pb)));
     return tuned_launch_key(
-        key, conv_pair_tile_count(), pair_tile(), [](int) { return true; },
-        [&](int v) { return conv_pair_launch(a, cb1, cb2, stream, v < 0 ? (pa->h * pa->w >= 6400 ? 2 : 1) : v); },
+        key, ntile + 1, pair_tile(), [&](int v) { return v < ntile || d_ya != nullptr; },
+        [&](int v) {
+            if (v < 0) v = (pa->h * pa->w >= 6400 && pa->m <= 32) || !d_ya ? 2 : ntile;
+            if (v == ntile) {
+                osh_status st = conv2d(pa, d_x, d_wa, d_bias_a, act, nullptr, d_ya, stream);
+                return st != OSH_OK ? st : conv2d(pb, d_ya, d_wb, d_bias_b, act, d_res, d_y, stream);
+            }
+            return conv_pair_launch(a, cb1, cb2, stream, v);
+        },
         stream);
 }
 

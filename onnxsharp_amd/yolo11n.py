@@ -748,20 +748,21 @@ def chain_pointwise_convs(model: Model, max_ops: int = 6, min_gain_us: float = 0
     return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
 
 
-def pair_bottleneck_convs(model: Model, takes=None, min_pixels: int = 6400) -> Model:
+def pair_bottleneck_convs(model: Model, takes=None, min_pixels: int = 0) -> Model:
     """Adjacent 3x3 SiLU convs where the second reads exactly the first's
     output and nothing else touches that buffer (a bottleneck's cv1 -> cv2)
     become one PairOp, on maps of at least `min_pixels`, where `takes(a, b)`
     (default: the library's osh_conv2d_pair_check on the resolved params)
     accepts them.
 
-    A pair saves a launch and the intermediate's round trip, but each
+    A fused pair saves a launch and the intermediate's round trip, but each
     workgroup also computes the first conv over a one-pixel ring around its
     tile, on its own CU's four MFMA pipes: one 16x16x4 FP32 MFMA keeps a
     pipe busy for its full 32 cycles, so the ring's extra blocks cost time
-    one for one.  On the 640 frame's 80x80 pairs (32 -> 16 -> 32) the pair
-    ran 7.2 us against 8.9 us as two launches; on the 40x40 and 20x20 pairs
-    it ran 8.0-15.1 us against 8.1-10.6 us."""
+    one for one.  On the 640 frame's 80x80 pairs (32 -> 16 -> 32) the fused
+    kernel ran 7.2 us against 8.9 us as two launches; on the 40x40 and 20x20
+    pairs 8.0-15.1 us against 8.1-10.6 us.  osh_conv2d_pair_f32 times both
+    forms on first use and keeps the faster one."""
     takes = takes or pair_supported
     ops = list(model.ops)
     users = {}

@@ -650,13 +650,17 @@ def test_conv_pair_equals_two_launches(cuda, name, xs, c1, c2, residual, opts):
                 assert np.array_equal(y.cpu().numpy(), y_ref), f"{name}: output differs under tile {tile}"
         finally:
             N.call("osh_config_set", b"pair_tile", -1)
-        # the intermediate may be left unstored; the residual may be the output itself
-        y2 = torch.from_numpy(synth.normal(seed + 5, (1, c2, xs[2], xs[3]), 0, 1)).to(cuda) if residual else \
-            torch.empty((1, c2, xs[2], xs[3]), device=cuda)
+        # the intermediate may be left unstored (first-use timing then only
+        # chooses among the fused tiles)
+        y2 = torch.full((1, c2, xs[2], xs[3]), float("nan"), device=cuda)
         N.call("osh_conv2d_pair_f32", C.byref(pa), C.byref(pb), ptr(x), ptr(bufa), ptr(ba), ptr(bufb), ptr(bb),
-               N.ACT_SILU, ptr(y2) if residual else None, None, ptr(y2), st)
+               N.ACT_SILU, ptr(r), None, ptr(y2), st)
         torch.cuda.synchronize()
         assert np.array_equal(y2.cpu().numpy(), y_ref)
+        if residual:  # a residual inside the output is refused
+            with pytest.raises(N.OshError, match="residual overlaps"):
+                N.call("osh_conv2d_pair_f32", C.byref(pa), C.byref(pb), ptr(x), ptr(bufa), ptr(ba), ptr(bufb),
+                       ptr(bb), N.ACT_SILU, ptr(y2), None, ptr(y2), st)
     finally:
         for k, v in saved.items():
             N.call("osh_config_set", k.encode(), v)

@@ -190,23 +190,23 @@ def test_c2f_block_structure():
 
 
 def test_pairs_of_the_640_frame():
-    # the bottleneck pairs the frame fuses: the two 80x80 ones (the pair
-    # kernel's ring recompute makes it slower than two launches on the
-    # 40x40 and 20x20 maps); the library's own check decides what it takes
+    # every bottleneck pair the library takes becomes one PairOp (which then
+    # times the fused kernel against two launches on first use): all of the
+    # frame's but the 160x160 one, whose intermediate has 8 channels
     from onnxsharp_amd import yolo11n as Y
     m = Y.build(640)
     f = Y.fuse_launches(m)
     pairs = [o for o in f.ops if isinstance(o, Y.PairOp)]
-    assert [(p.a.x.c, p.a.y.c, p.b.y.c, p.a.x.h) for p in pairs] == [(32, 16, 32, 80), (32, 16, 32, 80)]
+    assert sorted((p.a.x.c, p.a.y.c, p.b.y.c, p.a.x.h) for p in pairs) == sorted(
+        [(32, 16, 32, 80)] * 2 + [(32, 32, 32, 40)] * 2 + [(64, 32, 64, 40)] * 2 + [(64, 64, 64, 20)] * 4)
     assert all(p.b.res is not None and p.b.res.buf is p.a.x.buf for p in pairs)
-    assert len(f.ops) == len(Y.fuse_launches(m, pairs=False).ops) - 2
-    # without the map-size floor every bottleneck pair the library takes fuses
-    g = Y.pair_bottleneck_convs(Y.fuse_launches(m, pairs=False), min_pixels=0)
-    assert len([o for o in g.ops if isinstance(o, Y.PairOp)]) == 10
-    # the 160x160 pair (16 -> 8 -> 16) has an 8-channel intermediate: refused
-    assert not any(p.a.x.h == 160 for p in (o for o in g.ops if isinstance(o, Y.PairOp)))
+    assert len(f.ops) == len(Y.fuse_launches(m, pairs=False).ops) - 10
+    assert not any(p.a.x.h == 160 for p in pairs)
+    # a map-size floor keeps the smaller maps' convs apart
+    g = Y.pair_bottleneck_convs(Y.fuse_launches(m, pairs=False), min_pixels=6400)
+    assert len([o for o in g.ops if isinstance(o, Y.PairOp)]) == 2
     # a refusal from the library keeps the convs separate
-    h = Y.pair_bottleneck_convs(Y.fuse_launches(m, pairs=False), takes=lambda a, b: False, min_pixels=0)
+    h = Y.pair_bottleneck_convs(Y.fuse_launches(m, pairs=False), takes=lambda a, b: False)
     assert not any(isinstance(o, Y.PairOp) for o in h.ops)
 
 
