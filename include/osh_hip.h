@@ -131,9 +131,10 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 thread's last osh_dqmm_u8s8 / osh_dqmm_u8s8_noalloc call.
  *   "im2col3x3_variant": -1 (default) = 3x3 stride-1/2 convolutions with
  *                 C % 16 == 0 that neither the NCHWc nor the Winograd gate
- *                 takes run the LDS-patch tiles in the reference's im2col
- *                 order (ConvKernels.cs:554-563), tile picked by first-use
- *                 timing; 0..N-1 forces a tile.  Initial value from
+ *                 takes run in the reference's im2col order
+ *                 (ConvKernels.cs:554-563) on the LDS-patch tiles or the
+ *                 streamed one-block tiles (the last four ids), tile picked
+ *                 by first-use timing; 0..N-1 forces a tile.  Initial value from
  *                 ONNXSHARP_HIP_IM2COL3X3_VARIANT.
  *   "im2col3x3_variants" (get only): N.
  *   "winograd": 1 (default) = 3x3 stride-1 convolutions that pass the

@@ -515,7 +515,7 @@ constexpr int kC3X0 = kC3W0 + kC16wCount;
 constexpr int kC3Count = kC3X0 + kC16sxCount;
 int conv16_variant_count() { return kC3Count; }
 int pointwise_variant_count() { return 1 + kPW16Count; }
-int im2col3x3_variant_count() { return kC16sCount; }
+int im2col3x3_variant_count() { return kC16sCount + kC16wiCount; }
 int group3x3_tile_count() { return 2 * kC16sCount; }  // each tile shared, then one workgroup per CU
 int group_pointwise_tile_count() { return kPW16Count; }
 
@@ -850,7 +850,7 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         return conv16_tuned_launch(p, d_x, w, d_bias, d_res, act, d_y, stream);
     case ALGO_CONV16I:
         return tuned_launch(
-            p, 4, kC16sCount, im2col3x3_variant(), [](int) { return true; },
+            p, 4, kC16sCount + kC16wiCount, im2col3x3_variant(), [](int) { return true; },
             [&](int v) {
                 if (v < 0) {  // cost model
                     const int cus = device_cus();
@@ -860,6 +860,7 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
                         if (v < 0 || c < bc) v = i, bc = c;
                     }
                 }
+                if (v >= kC16sCount) return conv16wi_launch(p, d_x, w, d_bias, d_res, act, d_y, stream, v - kC16sCount);
                 return conv16si_launch(p, d_x, w, d_bias, d_res, act, d_y, stream, v);
             },
             stream);

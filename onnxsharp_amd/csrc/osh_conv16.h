@@ -44,8 +44,13 @@ struct C16Chunk {
 
 // One wave's tile: pixel tile pt (16*BV output pixels), output-channel tile
 // mt (16*TM channels) of image n.  No barriers: any subset of a workgroup's
-// waves may run it.
-template <int TM, int BV, int ACT>
+// waves may run it.  I2C runs the im2col chain instead (bias, then
+// ic -> ky -> kx: ConvKernels.Im2Col / PackedConv, ConvKernels.cs:554-563),
+// with the weights packed in that order (conv16_pack with i2c): step u of a
+// channel block gives lane group g the term 4u + g = 9 ic + tap; with
+// u = 9v + r its channel is 4v + (4r + g) / 9 and its tap (4r + g) % 9, so
+// each lane keeps nine offsets (one per r) and 4v is a scalar offset.
+template <int TM, int BV, int ACT, bool I2C = false>
 __device__ __forceinline__ void conv16_wave(const osh_conv_params &p, const float *__restrict__ x,
                                             const float *__restrict__ wpk, const float *__restrict__ bias,
                                             const float *__restrict__ res, float *__restrict__ y, const int pt,
@@ -59,7 +64,8 @@ __device__ __forceinline__ void conv16_wave(const osh_conv_params &p, const floa
     float *yn = y + (long long)n * M * OHW;
     const float *rn = res ? res + (long long)n * M * OHW : nullptr;
 
-    // per pixel: the nine tap offsets (bytes, lane group g's channel included)
+    // per pixel: the nine tap offsets (bytes, lane group g's channel included;
+    // with I2C offset r holds term 4r + g of a channel block)
     int off[BV][9];
 #pragma unroll
     for (int q = 0; q < BV; q++) {
@@ -68,13 +74,13 @@ __device__ __forceinline__ void conv16_wave(const osh_conv_params &p, const floa
         const int oy = pix / p.ow, ox = pix - oy * p.ow;
         const int iy0 = oy * p.sh - p.pt, ix0 = ox * p.sw - p.pl;
 #pragma unroll
-        for (int ky = 0; ky < 3; ky++)
-#pragma unroll
-            for (int kx = 0; kx < 3; kx++) {
-                const int iy = iy0 + ky, ix = ix0 + kx;
-                const bool ok = (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
-                off[q][ky * 3 + kx] = ok ? (g * HW + iy * p.w + ix) * 4 : (int)C16_OOB;
-            }
+        for (int r = 0; r < 9; r++) {
+            const int term = 4 * r + g;
+            const int tap = I2C ? term % 9 : r, ch = I2C ? term / 9 : g;
+            const int iy = iy0 + tap / 3, ix = ix0 + tap % 3;
+            const bool ok = (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
+            off[q][r] = ok ? (ch * HW + iy * p.w + ix) * 4 : (int)C16_OOB;
+        }
     }
     // packed weights: [mtile16][icb*9 + tap][64 lanes][4 steps]
     const int kgroups = icbs * 9;
@@ -120,9 +126,16 @@ __device__ __forceinline__ void conv16_wave(const osh_conv_params &p, const floa
 #pragma unroll
             for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
-                for (int q = 0; q < BV; q++)
-                    R.b[t][s4][q] = __uint_as_float(
-                        __builtin_amdgcn_raw_buffer_load_b32(rx, off[q][t], (icb * 16 + 4 * s4) * HW * 4, 0));
+                for (int q = 0; q < BV; q++) {
+                    if constexpr (I2C) {
+                        const int u = 4 * t + s4, v = u / 9, r = u - 9 * v;
+                        R.b[t][s4][q] = __uint_as_float(
+                            __builtin_amdgcn_raw_buffer_load_b32(rx, off[q][r], (icb * 16 + 4 * v) * HW * 4, 0));
+                    } else {
+                        R.b[t][s4][q] = __uint_as_float(
+                            __builtin_amdgcn_raw_buffer_load_b32(rx, off[q][t], (icb * 16 + 4 * s4) * HW * 4, 0));
+                    }
+                }
         };
         auto mm = [&](const Blk &R, int t) {
 #pragma unroll
@@ -165,6 +178,7 @@ __device__ __forceinline__ void conv16_wave(const osh_conv_params &p, const floa
             for (int t = 0; t < 9; t++) mm(R0, t);
         }
     } else {
+        static_assert(!I2C, "the im2col order runs on the one-block-per-chunk loop");
         // chunk c = icb * 3 + ky: taps (ky, 0..2) of channel block icb
         auto load = [&](C16Chunk<TM, BV> &R, int c) {
             __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)xn, (short)0, bytes_x, 0x00020000);
@@ -258,7 +272,7 @@ __device__ __forceinline__ void conv16_wave(const osh_conv_params &p, const floa
 // WPB waves per workgroup: 4 packs a workgroup's waves onto one CU's SIMDs;
 // 1 spreads the same waves over as many CUs, which for maps with few tiles
 // and deep K leaves each wave a CU's L1 bandwidth for its operand stream.
-template <int TM, int BV, int ACT, int WPB = 4>
+template <int TM, int BV, int ACT, int WPB = 4, bool I2C = false>
 __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const float *__restrict__ x,
                                                      const float *__restrict__ wpk, const float *__restrict__ bias,
                                                      const float *__restrict__ res, float *__restrict__ y,
@@ -266,7 +280,7 @@ __global__ __launch_bounds__(256) void conv16_kernel(osh_conv_params p, const fl
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pt = blockIdx.x * WPB + wave;  // pixel tile
     if (pt >= tiles_p) return;             // whole wave; no barriers in the tile
-    conv16_wave<TM, BV, ACT>(p, x, wpk, bias, res, y, pt, blockIdx.y, blockIdx.z);
+    conv16_wave<TM, BV, ACT, I2C>(p, x, wpk, bias, res, y, pt, blockIdx.y, blockIdx.z);
 }
 
 // Same chain with the workgroup's weights resident in LDS: the four waves of
@@ -472,7 +486,7 @@ inline osh_status conv16_pack(const osh_conv_params *p, const float *w, void *ou
 // Tile choice: 16*TM output channels x 16*BV pixels per wave.  Prefer the
 // shape whose waves fill the SIMDs in the fewest rounds of the longest chain;
 // larger tiles load fewer operands per MFMA.
-template <int TM, int BV, int WPB = 4>
+template <int TM, int BV, int WPB = 4, bool I2C = false>
 inline osh_status conv16_launch_t(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                                   const float *res, int act, float *y, hipStream_t st) {
     const int ohw = p->oh * p->ow;
@@ -481,7 +495,7 @@ inline osh_status conv16_launch_t(const osh_conv_params *p, const float *x, cons
     const int mtiles = ceil_div(ceil_div(p->m, 16), TM);
     dim3 grid((unsigned)ceil_div(tiles_p, WPB), (unsigned)mtiles, (unsigned)p->n);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16_kernel<TM, BV, ACT, WPB>), grid, dim3(64 * WPB), 0, st, *p, x, w,
+                     hipLaunchKernelGGL((conv16_kernel<TM, BV, ACT, WPB, I2C>), grid, dim3(64 * WPB), 0, st, *p, x, w,
                                         bias, res, y, tiles_p));
     OSH_LAUNCH_CHECK("conv16_kernel");
     return OSH_OK;

@@ -457,6 +457,12 @@ inline osh_status conv16s_launch_s(const osh_conv_params *p, const float *x, con
 // The kC16s tiles in the im2col order (weights packed by conv16_pack with i2c).
 osh_status conv16si_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                            const float *res, int act, float *y, hipStream_t st, int v);
+// Streamed conv16 tiles in the im2col order (same packing): {TM, BV, waves
+// per workgroup} = {1,1,1}, {1,1,4}, {1,2,1}, {2,1,1} -- every wave its own
+// pixel tile, so a conv with 16 or fewer output channels idles no wave.
+constexpr int kC16wiCount = 4;
+osh_status conv16wi_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
+                           const float *res, int act, float *y, hipStream_t st, int v);
 
 osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                           const float *res, int act, float *y, hipStream_t st, int v);
