@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void dw_conv_group_kernel(ConvGroup g) {
 // planes).  One thread per output pixel keeps MM accumulators in registers
 // (output channels MM * blockIdx.y + 0 .. MM-1: smaller maps split M over
 // the grid's y so that more CUs take part); the weight index is the same for
-// every lane, so the weights come through the scalar cache.  Per output
+// every lane, so the weights are read as LDS broadcasts.  Per output
 // channel the chain is bias, then fmaf over ic -> ky -> kx (the panel order of
 // FirstConv.cs:344-362); padding taps add nothing.
 template <int MM, int CC, int ACT>
@@ -221,27 +221,38 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
                                                          const float *__restrict__ w,
                                                          const float *__restrict__ bias,
                                                          const float *__restrict__ res, float *__restrict__ y) {
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    // The workgroup's weights (MM output channels x CC x 9) and biases go to
+    // LDS and are read back as broadcasts: through the scalar cache an output
+    // channel's weights arrived a few words at a time, each batch waited for
+    // before its FMAs (the stem at 640x640: 8.2 us).  Their loads, and with
+    // CC <= 8 the pixel's input taps, are all issued before the barrier.
+    constexpr int NW = MM * CC * 9, NWT = (NW + 255) / 256;
+    __shared__ float lw[NW];
+    __shared__ float lb[MM];
+    const int tid = threadIdx.x;
+    const int oc0 = blockIdx.y * MM;
+    float wr[NWT];
+#pragma unroll
+    for (int i = 0; i < NWT; i++) {
+        const int e = tid + 256 * i;
+        wr[i] = e < NW ? w[(long long)oc0 * CC * 9 + e] : 0.f;
+    }
+    const float br = tid < MM && bias ? bias[oc0 + tid] : 0.f;
+    const long long idx = (long long)blockIdx.x * blockDim.x + tid;
     const long long plane = (long long)p.oh * p.ow;
-    if (idx >= (long long)p.n * plane) return;
-    const int ox = (int)(idx % p.ow);
-    const long long t = idx / p.ow;
+    const bool live = idx < (long long)p.n * plane;
+    const long long id = live ? idx : 0;  // dead lanes address pixel 0 and store nothing
+    const int ox = (int)(id % p.ow);
+    const long long t = id / p.ow;
     const int oy = (int)(t % p.oh);
     const int n = (int)(t / p.oh);
     const int m = p.m;
-    const int oc0 = blockIdx.y * MM;
     const float *xn = x + (long long)n * CC * p.h * p.w;
-    const long long yo = (long long)n * m * plane + (long long)oy * p.ow + ox;
-    float *yp = y + yo;
-    const float *rp = res ? res + yo : nullptr;
-    if constexpr (CC > 8) {
-        // 16 or 32 channels: MM accumulators, input channels in the outer
-        // loop; each output channel still sums bias, then ic -> ky -> kx
-        float acc[MM];
+    // CC <= 8: all CC*9 input taps, independent loads
+    float v[CC <= 8 ? CC : 1][3][3];
+    if constexpr (CC <= 8) {
 #pragma unroll
-        for (int o = 0; o < MM; o++) acc[o] = bias ? bias[oc0 + o] : 0.f;
-        for (int ic = 0; ic < CC; ic++) {
-            float v[3][3];
+        for (int ic = 0; ic < CC; ic++)
 #pragma unroll
             for (int ky = 0; ky < 3; ky++) {
                 const int iy = oy * p.sh - p.pt + ky;
@@ -249,45 +260,66 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
                 for (int kx = 0; kx < 3; kx++) {
                     const int ix = ox * p.sw - p.pl + kx;
                     const bool ok = (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
-                    v[ky][kx] = ok ? xn[((long long)ic * p.h + iy) * p.w + ix] : 0.f;
+                    v[ic][ky][kx] = ok ? xn[((long long)ic * p.h + iy) * p.w + ix] : 0.f;
+                }
+            }
+    }
+    // the residuals too (one round trip, not one per output channel)
+    const long long yo = (long long)n * m * plane + (long long)oy * p.ow + ox;
+    float *yp = y + yo;
+    float rv[MM];
+#pragma unroll
+    for (int o = 0; o < MM; o++) rv[o] = 0.f;
+    if (res) {
+#pragma unroll
+        for (int o = 0; o < MM; o++) rv[o] = res[yo + (oc0 + o) * plane];
+    }
+#pragma unroll
+    for (int i = 0; i < NWT; i++)
+        if (tid + 256 * i < NW) lw[tid + 256 * i] = wr[i];
+    if (tid < MM) lb[tid] = br;
+    __syncthreads();
+    if (!live) return;
+    if constexpr (CC > 8) {
+        // 16 or 32 channels: MM accumulators, input channels in the outer
+        // loop; each output channel still sums bias, then ic -> ky -> kx
+        float acc[MM];
+#pragma unroll
+        for (int o = 0; o < MM; o++) acc[o] = lb[o];
+        for (int ic = 0; ic < CC; ic++) {
+            float vi[3][3];
+#pragma unroll
+            for (int ky = 0; ky < 3; ky++) {
+                const int iy = oy * p.sh - p.pt + ky;
+#pragma unroll
+                for (int kx = 0; kx < 3; kx++) {
+                    const int ix = ox * p.sw - p.pl + kx;
+                    const bool ok = (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
+                    vi[ky][kx] = ok ? xn[((long long)ic * p.h + iy) * p.w + ix] : 0.f;
                 }
             }
 #pragma unroll
             for (int o = 0; o < MM; o++) {
-                const float *wo = w + ((oc0 + o) * CC + ic) * 9;
+                const float *wo = lw + (o * CC + ic) * 9;
 #pragma unroll
                 for (int ky = 0; ky < 3; ky++)
 #pragma unroll
-                    for (int kx = 0; kx < 3; kx++) acc[o] = __builtin_fmaf(wo[ky * 3 + kx], v[ky][kx], acc[o]);
+                    for (int kx = 0; kx < 3; kx++) acc[o] = __builtin_fmaf(wo[ky * 3 + kx], vi[ky][kx], acc[o]);
             }
         }
 #pragma unroll
         for (int o = 0; o < MM; o++) {
             float r = activate<ACT>(acc[o]);
-            if (rp) r += rp[(oc0 + o) * plane];
+            if (res) r += rv[o];
             yp[(oc0 + o) * plane] = r;
         }
         return;
     }
-    // all CC*9 input taps are loaded before the first FMA (independent loads)
-    float v[CC][3][3];
-#pragma unroll
-    for (int ic = 0; ic < CC; ic++)
-#pragma unroll
-        for (int ky = 0; ky < 3; ky++) {
-            const int iy = oy * p.sh - p.pt + ky;
-#pragma unroll
-            for (int kx = 0; kx < 3; kx++) {
-                const int ix = ox * p.sw - p.pl + kx;
-                const bool ok = (unsigned)iy < (unsigned)p.h && (unsigned)ix < (unsigned)p.w;
-                v[ic][ky][kx] = ok ? xn[((long long)ic * p.h + iy) * p.w + ix] : 0.f;
-            }
-        }
-    // 3x3 taps at compile-time offsets: the weights arrive in wide scalar loads
+    // 3x3 taps at compile-time offsets
 #pragma unroll
     for (int oc = oc0; oc < oc0 + MM; oc++) {  // m = MM * gridDim.y (launch)
-        float acc = bias ? bias[oc] : 0.f;
-        const float *wo = w + oc * CC * 9;
+        float acc = lb[oc - oc0];
+        const float *wo = lw + (oc - oc0) * CC * 9;
 #pragma unroll
         for (int ic = 0; ic < CC; ic++)
 #pragma unroll
@@ -295,7 +327,7 @@ __global__ __launch_bounds__(256) void first_conv_kernel(osh_conv_params p, cons
 #pragma unroll
                 for (int kx = 0; kx < 3; kx++) acc = __builtin_fmaf(wo[(ic * 3 + ky) * 3 + kx], v[ic][ky][kx], acc);
         float o = activate<ACT>(acc);
-        if (rp) o += rp[oc * plane];
+        if (res) o += rv[oc - oc0];
         yp[oc * plane] = o;
     }
 }
