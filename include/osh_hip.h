@@ -260,7 +260,7 @@ OSH_API osh_status osh_conv2d_add_f32(const osh_conv_params *p, const float *d_x
                                       const float *d_bias, int act, const float *d_res, float *d_y,
                                       osh_stream s);
 
-/* Up to 4 independent convs in one launch: conv i is ps[i] on d_xs[i] with
+/* Up to 6 independent convs in one launch: conv i is ps[i] on d_xs[i] with
  * packed weights d_ws[i], bias d_biases[i] (d_biases may be NULL), residual
  * d_res[i] (d_res may be NULL), output d_ys[i]; one fused activation for all.
  * No single reference function: it stands for that many ConvLayer.Forward

@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const f
 // i, start[i] <= b < start[i + 1], with conv i's own sizes and pointers.
 // Every conv keeps its own chain, so the outputs are those of separate
 // launches with the same tile.
-constexpr int kConvGroupMax = 4;
+constexpr int kConvGroupMax = 6;
 struct ConvGroup {
     int count;
     int start[kConvGroupMax + 1];

@@ -592,6 +592,33 @@ def group_independent_convs(model: Model, window: int = 12) -> Model:
     return Model(model.size, list(model.bufs), out, model.input, list(model.outputs))
 
 
+def merge_independent_groups(model: Model, window: int = 8, max_members: int = 6) -> Model:
+    """A GroupConvOp and a later one of the same kind that it can move down
+    to -- nothing between them, nor the later group, reads what it writes or
+    writes what it reads or writes, and it reads nothing they write -- run as
+    one group at the later one's place (up to six convs): e.g. the detection
+    head's final box and class 1x1 layers, which end independent branches.
+    Results are unchanged."""
+    ops = list(model.ops)
+    kind = lambda g: {_conv_kind(o) for o in g.ops}
+    i = 0
+    while i < len(ops):
+        a = ops[i]
+        if isinstance(a, GroupConvOp) and len(kind(a)) == 1:
+            for j in range(i + 1, min(len(ops), i + 1 + window)):
+                b = ops[j]
+                if not (_independent(a, b) and _independent(b, a)):
+                    break
+                if (isinstance(b, GroupConvOp) and kind(b) == kind(a) and
+                        len(a.ops) + len(b.ops) <= max_members):
+                    ops[j] = GroupConvOp(a.name + "&" + b.name, a.ops + b.ops)
+                    del ops[i]
+                    i -= 1
+                    break
+        i += 1
+    return Model(model.size, list(model.bufs), ops, model.input, list(model.outputs))
+
+
 def _is_depthwise3x3(op) -> bool:
     return op.k == 3 and op.s == 1 and op.group > 1 and op.group == op.x.c == op.y.c
 
@@ -807,7 +834,7 @@ def pair_supported(a: ConvOp, b: ConvOp) -> bool:
     return N.lib().osh_conv2d_pair_check(C.byref(pa), C.byref(pb), N.ACTIVATIONS[a.act]) == 0
 
 
-def fuse_launches(model: Model, chains: bool = False, pairs: bool = True) -> Model:
+def fuse_launches(model: Model, chains: bool = False, pairs: bool = True, merge: bool = True) -> Model:
     """The launch-saving rewrites of the op list (residual Adds into their
     convs, SPPF's pool chain into one op, the head's three scales per layer
     into one op, other independent convs of one kind into one op, and with
@@ -818,6 +845,8 @@ def fuse_launches(model: Model, chains: bool = False, pairs: bool = True) -> Mod
     MFMA accumulator per wave, while separate launches spread each stage over
     the chip), 0.493 against 0.465 ms per frame."""
     m = group_independent_convs(group_head_convs(fuse_pool_chains(fuse_residual_adds(model))))
+    if merge:
+        m = merge_independent_groups(m)
     if pairs:
         m = pair_bottleneck_convs(m)
     return chain_pointwise_convs(m) if chains else m

@@ -502,6 +502,10 @@ GROUP_CASES = [
     ("head_pointwise_res", [((1, 64, 80, 80), (80, 64, 1, 1), 1), ((1, 80, 40, 40), (80, 80, 1, 1), 1),
                             ((1, 80, 20, 20), (80, 80, 1, 1), 1), ((1, 48, 9, 6), (32, 48, 1, 1), 1)], None, True),
     ("mixed_fallback", [((1, 64, 20, 20), (64, 64, 3, 3), 1), ((1, 32, 20, 20), (32, 1, 3, 3), 32)], "Relu", True),
+    # six members: the head's final box and class 1x1 layers as one launch
+    ("head_final_six", [((1, 64, 80, 80), (64, 64, 1, 1), 1), ((1, 64, 40, 40), (64, 64, 1, 1), 1),
+                        ((1, 64, 20, 20), (64, 64, 1, 1), 1), ((1, 80, 80, 80), (80, 80, 1, 1), 1),
+                        ((1, 80, 40, 40), (80, 80, 1, 1), 1), ((1, 80, 20, 20), (80, 80, 1, 1), 1)], None, False),
     # stride 2, odd maps, a deep member first (the streamed one-wave member of the mixed tiles)
     ("strided_3x3", [((1, 32, 41, 39), (48, 32, 3, 3), 1, 2), ((1, 128, 11, 13), (32, 128, 3, 3), 1, 2)],
      "Silu", True),
@@ -550,7 +554,7 @@ def test_conv_group_equals_separate_launches(cuda, name, convs, act, residual):
     # the 3x3 and pointwise groups: every tile forced in turn (the first-use
     # timing would keep only the last tile's output), then the automatic choice
     key = {"head_3x3_nchwc": b"group3x3_tile", "strided_3x3": b"group3x3_tile",
-           "head_pointwise_res": b"group_pointwise_tile"}.get(name)
+           "head_pointwise_res": b"group_pointwise_tile", "head_final_six": b"group_pointwise_tile"}.get(name)
     tiles = list(range(_group_tiles(key))) if key else []
     try:
         for tile in tiles + [-1]:

@@ -189,6 +189,34 @@ def test_c2f_block_structure():
     assert [(b.c, b.h, b.w) for b in m.outputs] == [(128, 80, 80)]
 
 
+def test_head_branch_ends_share_a_launch():
+    # the head's final box and class 1x1 layers end independent branches:
+    # the box group moves down to the class group's place and the six convs
+    # run as one launch (72 -> 71 launches before the bottleneck pairs)
+    from onnxsharp_amd import yolo11n as Y
+    m = Y.build(640)
+    f = Y.fuse_launches(m, pairs=False)
+    assert len(f.ops) == 71
+    six = [o for o in f.ops if isinstance(o, Y.GroupConvOp) and len(o.ops) == 6]
+    assert len(six) == 1
+    g = six[0]
+    assert [o.name for o in g.ops] == [f"/model.23/cv{b}.{i}/cv{b}.{i}.2/Conv" for b in (2, 3) for i in range(3)]
+    assert len({Y._conv_kind(o) for o in g.ops}) == 1 and all(o.act is None for o in g.ops)
+    # every op still reads only what was written before it, and every conv runs once
+    assert len(f.convs) == len(m.convs)
+    head = lambda mm: sorted(o.name for o in mm.convs if o.name.startswith("/model.23/"))
+    assert head(f) == head(m)
+    written = {id(m.input)}
+    for op in f.ops:
+        reads, writes = Y.op_access(op)
+        assert all(id(r.buf) in written for r in reads), op.name
+        written.update(id(w.buf) for w in writes)
+    # a group never moves past an op that reads its output
+    a = next(o for o in f.ops if isinstance(o, Y.GroupConvOp) and o.name.startswith("/model.23/cv2.#/cv2.#.0"))
+    b = next(o for o in f.ops if isinstance(o, Y.GroupConvOp) and o.name.startswith("/model.23/cv2.#/cv2.#.1"))
+    assert not Y._independent(a, b)
+
+
 def test_pairs_of_the_640_frame():
     # every bottleneck pair the library takes becomes one PairOp (which then
     # times the fused kernel against two launches on first use): all of the
@@ -230,7 +258,7 @@ def test_head_convs_group_by_layer(model):
     # drops from 92 launches to 72 (before the bottleneck pairs and the
     # pointwise chains).
     from onnxsharp_amd import yolo11n as Y
-    fused = Y.fuse_launches(model, chains=False, pairs=False)
+    fused = Y.fuse_launches(model, chains=False, pairs=False, merge=False)
     head = [o for o in fused.ops if isinstance(o, Y.GroupConvOp) and o.name.startswith("/model.23/cv")]
     other = [o for o in fused.ops if isinstance(o, Y.GroupConvOp) and o not in head]
     assert len(head) == 8 and len(other) == 4 and len(fused.ops) == 72
@@ -259,11 +287,11 @@ def test_pointwise_chains_of_the_640_frame(model):
     # and the head's class branch in two launches of three scales: 72
     # launches become 67.  (The C2PSA tail's 576 KB of weights do not fit.)
     from onnxsharp_amd import yolo11n as Y
-    fused = Y.fuse_launches(model, chains=True, pairs=False)
+    fused = Y.fuse_launches(model, chains=True, pairs=False, merge=False)
     chains = [o for o in fused.ops if isinstance(o, Y.ChainOp)]
     assert len(fused.ops) == 67 and len(chains) == 4
-    assert len(Y.fuse_launches(model, pairs=False).ops) == 72  # off by default
-    unchained = Y.fuse_launches(model, chains=False, pairs=False)
+    assert len(Y.fuse_launches(model, pairs=False, merge=False).ops) == 72  # off by default
+    unchained = Y.fuse_launches(model, chains=False, pairs=False, merge=False)
     assert sorted(o.name for o in fused.convs) == sorted(o.name for o in unchained.convs)
     shapes = [[[(o.x.c, o.y.c, o.y.h) for o in ch] for ch in c.chains] for c in chains]
     assert [[(128, 128, 40), (64, 32, 40), (64, 32, 40)]] in shapes  # model.6 cv1 -> C3k cv1, cv2
