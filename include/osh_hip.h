@@ -105,10 +105,11 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 ONNXSHARP_HIP_POINTWISE_VARIANT.
  *   "group3x3_tile": -1 (default) = grouped 3x3 launches
  *                 (osh_conv2d_group_f32) pick their tile by first-use timing
- *                 of the whole group; 0..N-1 forces one of the LDS-patch
- *                 tiles (N/2..N-1: tile i - N/2 with one workgroup per CU,
- *                 which leaves a long member's chain its SIMDs alone); all
- *                 give the same bits.
+ *                 of the whole group; 0..N-1 forces a tile: with T
+ *                 LDS-patch tiles, 0..T-1 those, T..2T-1 the same with one
+ *                 workgroup per CU (a long member's chain keeps its SIMDs),
+ *                 2T..N-1 the streamed one-block tiles; all give the same
+ *                 bits.
  *   "group3x3_tiles" (get only): N.
  *   "group_pointwise_tile", "group_pointwise_tiles": the same for grouped
  *                 pointwise launches (the pointwise LDS tiles that fit every

@@ -548,7 +548,8 @@ constexpr int kC3Count = kC3X0 + kC16sxCount;
 int conv16_variant_count() { return kC3Count; }
 int pointwise_variant_count() { return 1 + kPW16Count; }
 int im2col3x3_variant_count() { return kC16sCount + kC16wiCount; }
-int group3x3_tile_count() { return 2 * kC16sCount; }  // each tile shared, then one workgroup per CU
+// each LDS-patch tile shared, then one workgroup per CU, then the streamed tiles
+int group3x3_tile_count() { return 2 * kC16sCount + kC16gCount; }
 int group_pointwise_tile_count() { return kPW16Count; }
 
 static bool c3_fits(const osh_conv_params *p, int v) {

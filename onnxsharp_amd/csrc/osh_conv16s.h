@@ -421,6 +421,47 @@ inline osh_status conv16s_group_launch_t(ConvGroup g, int act, hipStream_t st, b
     return OSH_OK;
 }
 
+// Grouped 3x3 convs on the streamed one-block tiles (conv16_wave): workgroup
+// b runs WPB waves of conv i = the member whose block-table range holds b,
+// each wave its own 16*BV-pixel, 16*TM-channel tile with no barriers.  On the
+// head's small maps one chain per wave loses less to staging than the
+// LDS-patch tiles' barrier per 16-channel chunk.
+template <int TM, int BV, int ACT, int WPB>
+__global__ __launch_bounds__(256) void conv16_group_kernel(ConvGroup g) {
+    const int b = blockIdx.x;
+    int i = 0;
+    while (i + 1 < g.count && b >= g.start[i + 1]) i++;
+    const int local = b - g.start[i];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int bx = local % g.tiles[i], rest = local / g.tiles[i];
+    const int pt = bx * WPB + wave;
+    if (pt >= g.tiles_w[i]) return;  // tiles_w holds the member's pixel tiles
+    conv16_wave<TM, BV, ACT>(g.p[i], g.x[i], g.w[i], g.bias[i], g.res[i], g.y[i], pt, rest % g.mgroups[i],
+                             rest / g.mgroups[i]);
+}
+
+template <int TM, int BV, int WPB>
+inline osh_status conv16_group_launch_t(ConvGroup g, int act, hipStream_t st) {
+    long long total = 0;
+    for (int i = 0; i < g.count; i++) {
+        const osh_conv_params &p = g.p[i];
+        g.tiles_w[i] = ceil_div(p.oh * p.ow, 16 * BV);  // pixel tiles
+        g.tiles[i] = ceil_div(g.tiles_w[i], WPB);       // workgroups per channel tile
+        g.mgroups[i] = ceil_div(ceil_div(p.m, 16), TM);
+        g.start[i] = (int)total;
+        total += (long long)g.tiles[i] * g.mgroups[i] * p.n;
+    }
+    if (total > 0x7fffffffLL) return fail(OSH_E_UNSUPPORTED, "Conv group: grid too large");
+    g.start[g.count] = (int)total;
+    OSH_DISPATCH_ACT(act, ACT,
+                     hipLaunchKernelGGL((conv16_group_kernel<TM, BV, ACT, WPB>), dim3((unsigned)total),
+                                        dim3(64 * WPB), 0, st, g));
+    OSH_LAUNCH_CHECK("conv16_group_kernel");
+    return OSH_OK;
+}
+// the streamed group tiles {TM, BV, waves per workgroup}
+constexpr int kC16gCount = 4;
+
 struct C16sVariant {
     int tm, bv, twl;
 };

@@ -6,8 +6,17 @@
 
 namespace osh {
 
-// Tiles kC16sCount and up are the same tiles, one workgroup per CU.
+// Tiles kC16sCount .. 2 kC16sCount - 1 are the same tiles, one workgroup per
+// CU; 2 kC16sCount and up the streamed one-block tiles.
 osh_status conv16s_group_launch(ConvGroup g, int act, hipStream_t st, int tile, int s) {
+    if (tile >= 2 * kC16sCount) {
+        switch (tile - 2 * kC16sCount) {
+        case 0: return conv16_group_launch_t<1, 1, 1>(g, act, st);
+        case 1: return conv16_group_launch_t<1, 1, 4>(g, act, st);
+        case 2: return conv16_group_launch_t<1, 2, 1>(g, act, st);
+        default: return conv16_group_launch_t<2, 1, 1>(g, act, st);
+        }
+    }
     const bool ex = tile >= kC16sCount;
     if (ex) tile -= kC16sCount;
 #define OSH_GROUP_TILE(TM, BV, TWL)                                                         \
