@@ -1105,7 +1105,10 @@ constexpr int kPairTuneTag = 30;  // tuning-table tags of the fused pair (+1 wit
 // one 1 x C x H x W map, the second reading the first's output, 16/32/64
 // channels out of each, SiLU, and the single-conv dispatch taking for each
 // the chain the pair computes (NCHWc for 32 and 64 outputs, im2col for 16).
+static const char *first_pair_refusal(const osh_conv_params *pa, const osh_conv_params *pb, int act);
+
 static const char *pair_refusal(const osh_conv_params *pa, const osh_conv_params *pb, int act) {
+    if (pa->c <= 4) return first_pair_refusal(pa, pb, act);
     auto same_map_3x3 = [](const osh_conv_params *p) {
         return p->group == 1 && p->kh == 3 && p->kw == 3 && p->sh == 1 && p->sw == 1 && p->dh == 1 &&
                p->dw == 1 && p->pt == 1 && p->pl == 1 && p->oh == p->h && p->ow == p->w;
@@ -1120,6 +1123,26 @@ static const char *pair_refusal(const osh_conv_params *pa, const osh_conv_params
     if ((long long)pa->c * pa->h * pa->w * 4 >= (1LL << 31)) return "input too large";
     if (select_algo(pa) != (pa->m == 16 ? ALGO_CONV16I : ALGO_CONV16) ||
         select_algo(pb) != (pb->m == 16 ? ALGO_CONV16I : ALGO_CONV16))
+        return "the single-conv dispatch takes another chain for one of the convs";
+    return nullptr;
+}
+
+// The first-layer pair (first_pair_kernel): a 3x3 undilated conv of stride 1
+// or 2 over c <= 4 planes with 16 outputs, which the single-conv dispatch
+// runs as first_conv_kernel, then a 3x3 conv over exactly its output that the
+// dispatch runs in the NCHWc order (32 or 64 outputs, stride 1 or 2, pad 1).
+static const char *first_pair_refusal(const osh_conv_params *pa, const osh_conv_params *pb, int act) {
+    if (pa->group != 1 || pa->kh != 3 || pa->kw != 3 || pa->dh != 1 || pa->dw != 1 || pa->sh != pa->sw ||
+        (pa->sh != 1 && pa->sh != 2))
+        return "a first-layer conv must be 3x3, undilated, stride 1 or 2";
+    if (pa->n != 1 || pb->n != 1) return "batch 1 only";
+    if (pa->m != 16) return "a first-layer conv must have 16 output channels";
+    if (pb->c != 16 || pb->h != pa->oh || pb->w != pa->ow) return "the second conv must read the first one's output";
+    if (pb->m != 32 && pb->m != 64) return "after a first-layer conv the second conv must have 32 or 64 outputs";
+    if (act != OSH_ACT_SILU) return "the fused pair takes SiLU convs";
+    if ((long long)pa->c * pa->h * pa->w * 4 >= (1LL << 31) || (long long)pb->m * pb->oh * pb->ow * 4 >= (1LL << 31))
+        return "tensors too large";
+    if (select_algo(pa) != ALGO_FIRST || !nchwc_gate(pb) || select_algo(pb) != ALGO_CONV16)
         return "the single-conv dispatch takes another chain for one of the convs";
     return nullptr;
 }
@@ -1205,6 +1228,42 @@ OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv
         return fail(OSH_E_INVALID, "Conv pair: the residual overlaps the output");
     if (d_res && d_ya && ranges_overlap(d_res, yb, d_ya, yab))
         return fail(OSH_E_INVALID, "Conv pair: the residual overlaps the intermediate");
+    hipStream_t stream = to_stream(s);
+    if (pa->c <= 4) {
+        // the first-layer pair: its tiles, then (with an intermediate buffer)
+        // the two convs as separate launches; tile 0 before first-use timing
+        FirstPairArgs f{};
+        f.h = pa->h;
+        f.w = pa->w;
+        f.c0 = pa->c;
+        f.pt = pa->pt;
+        f.pl = pa->pl;
+        f.ah = pa->oh;
+        f.aw = pa->ow;
+        f.bh = pb->oh;
+        f.bw = pb->ow;
+        f.x = d_x;
+        f.wa = static_cast<const float *>(d_wa);
+        f.ba = d_bias_a;
+        f.wb = static_cast<const float *>(d_wb);
+        f.bb = d_bias_b;
+        f.res = d_res;
+        f.ya = d_ya;
+        f.y = d_y;
+        const int nft = first_pair_tile_count();
+        const auto key = std::make_tuple(kPairTuneTag + 2 + (d_ya ? 0 : 1), mix_key(conv_key(pa), conv_key(pb)));
+        return tuned_launch_key(
+            key, nft + 1, pair_tile(), [&](int v) { return v < nft || d_ya != nullptr; },
+            [&](int v) {
+                if (v < 0) v = 0;
+                if (v == nft) {
+                    osh_status st = conv2d(pa, d_x, d_wa, d_bias_a, act, nullptr, d_ya, stream);
+                    return st != OSH_OK ? st : conv2d(pb, d_ya, d_wb, d_bias_b, act, d_res, d_y, stream);
+                }
+                return first_pair_launch(f, pa->sh, pb->sh, pb->m / 16, stream, v);
+            },
+            stream);
+    }
     PairArgs a{};
     a.h = pa->h;
     a.w = pa->w;
@@ -1218,7 +1277,6 @@ OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv
     a.ya = d_ya;
     a.y = d_y;
     const int cb1 = pa->m / 16, cb2 = pb->m / 16;
-    hipStream_t stream = to_stream(s);
     // Variants: the pair kernel's tiles, then (when the intermediate has a
     // buffer) the two convs as separate launches -- the pair's ring
     // recompute runs on one CU's four MFMA pipes, which loses to two

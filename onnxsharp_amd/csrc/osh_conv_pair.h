@@ -23,4 +23,27 @@ struct PairArgs {
 osh_status conv_pair_launch(const PairArgs &a, int cb1, int cb2, hipStream_t st, int tile);
 int conv_pair_tile_count();
 
+// A network's first conv (3x3 over c0 <= 4 planes, 16 outputs) and the 3x3
+// pad-1 conv that reads its output (16 -> 32 or 64 channels).
+struct FirstPairArgs {
+    int h, w, c0;  // first conv's input map and planes (1 .. 4)
+    int pt, pl;    // its top and left pads
+    int ah, aw;    // its output map, the second conv's input
+    int bh, bw;    // the second conv's output map
+    int tiles_w;
+    const float *x;   // [c0][h][w]
+    const float *wa;  // [16][c0][3][3] (the first-layer kernel's packing: raw)
+    const float *ba;
+    const float *wb;  // second conv, conv16_pack in the NCHWc order
+    const float *bb;
+    const float *res;  // [m][bh][bw] added after the activation, or null
+    float *ya;         // [16][ah][aw] intermediate, or null
+    float *y;          // [m][bh][bw]
+};
+
+// Launches tile `tile` (0 .. first_pair_tile_count()-1): first conv stride
+// sa, second conv stride sb (1 or 2 each), 16 cb2 outputs (cb2 2 or 4); SiLU.
+osh_status first_pair_launch(const FirstPairArgs &a, int sa, int sb, int cb2, hipStream_t st, int tile);
+int first_pair_tile_count();
+
 }  // namespace osh

@@ -371,4 +371,292 @@ osh_status conv_pair_launch(const PairArgs &a, int cb1, int cb2, hipStream_t st,
 
 int conv_pair_tile_count() { return kPairTileCount; }
 
+// ------------------------------------------------------ first-layer pair
+//
+// A network's first conv (3x3 over c0 <= 4 colour planes, 16 outputs, stride
+// SA: FirstConv.cs) and the 3x3 pad-1 conv that reads it (16 -> 16 CB2
+// channels, stride S2, the NCHWc chain: NchwcConv.cs:533-605) -- YOLO11n's
+// 3 -> 16 -> 32 stem, two stride-2 convs -- in one launch.  The first conv's
+// 16-channel map is the largest tensor of such a network after the image and
+// nothing else reads it; here it never leaves the chip.
+//
+// A workgroup owns a TH x TW tile of the second conv's output.  It stages
+// the image patch under the tile (every plane) in LDS, computes the first
+// conv over the tile's receptive field ((S2 (TH-1) + 3) x (S2 (TW-1) + 3)
+// pixels, zero where that leaves the map: the second conv's padding taps),
+// then the second conv from LDS.
+//
+// Both chains are the single convs' own, on the 16x16x4 MFMA (each step adds
+// its four lane-group products one after another, each rounded like an
+// fmaf):
+//   * first conv: bias, then k = ic*9 + ky*3 + kx ascending -- first_conv_
+//     kernel's ic -> ky -> kx chain.  A step past 9 c0 multiplies a -0 weight
+//     by a +0 input: adding -0 leaves every accumulator as it is;
+//   * second conv: bias, then ky -> kx -> ic16 (one 16-channel block).
+// With S2 = 2 each intermediate row keeps its even columns, then its odd
+// ones, so the stride-2 operand reads of 16 lanes are 16 consecutive words.
+template <int TH, int TW, int SA, int S2>
+struct FirstPairGeom {
+    static constexpr int EH = S2 * (TH - 1) + 3, EW = S2 * (TW - 1) + 3, NE = EH * EW;  // first conv's pixels
+    static constexpr int NBA = (NE + 15) / 16, IA = (NBA + 3) / 4;  // its 16-pixel blocks; per wave
+    static constexpr int PH = SA * (EH - 1) + 3, PW = SA * (EW - 1) + 3;  // its input patch
+    static constexpr int PITCH_X = pair_pitch(PW), PLANE_X = pair_plane(PH, PITCH_X);
+    static constexpr int XE = 4 * PH * PW, NXE = (XE + 255) / 256;  // staging loads per thread (4 planes)
+    static constexpr int HALF = S2 == 2 ? (EW + 1) / 2 : EW;
+    static constexpr int ROW = S2 == 2 ? 2 * HALF : pair_pitch(EW);
+    static constexpr int PLANE_M = (EH * ROW + 47) / 64 * 64 + 16;  // >= EH * ROW, 16 mod 64 words
+    static constexpr int NBB = (TH * TW + 15) / 16;
+    // LDS word of intermediate pixel (ey, ex) within a channel plane
+    static __device__ __forceinline__ int mpos(int ey, int ex) {
+        return S2 == 2 ? ey * ROW + (ex & 1) * HALF + (ex >> 1) : ey * ROW + ex;
+    }
+};
+
+template <int TH, int TW, int SA, int S2, int CB2, int ACT>
+__global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
+    using G = FirstPairGeom<TH, TW, SA, S2>;
+    static_assert(CB2 == 2 || CB2 == 4, "32 or 64 output channels (the NCHWc chain)");
+    static_assert(TW % 16 == 0 || 16 % TW == 0, "16-pixel blocks cover whole rows or whole row sets");
+    __shared__ __align__(16) float lx[4 * G::PLANE_X];
+    __shared__ __align__(16) float lm[16 * G::PLANE_M];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, g = lane >> 4;
+    const int ty = blockIdx.x / a.tiles_w, tx = blockIdx.x - ty * a.tiles_w;
+    const int y0 = ty * TH, x0 = tx * TW;            // the tile, in the second conv's output
+    const int ey0 = S2 * y0 - 1, ex0 = S2 * x0 - 1;  // first-conv pixel at patch (0, 0)
+    const int iy0 = SA * ey0 - a.pt, ix0 = SA * ex0 - a.pl;  // image pixel at input patch (0, 0)
+    const int c0 = a.c0, H = a.h, W = a.w, HW = H * W;
+
+    // ---- the input patch, every plane, in one round trip (outside the
+    // image the load's offset is out of range and returns 0)
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, c0 * HW * 4, 0x00020000);
+    int loff[G::NXE];
+    float sv[G::NXE];
+#pragma unroll
+    for (int i = 0; i < G::NXE; i++) {
+        const int e = tid + 256 * i;
+        const int ch = e / (G::PH * G::PW), rem = e - ch * (G::PH * G::PW);
+        const int r = rem / G::PW, c = rem - r * G::PW;
+        const int iy = iy0 + r, ix = ix0 + c;
+        const bool live = e < G::XE && ch < c0;
+        const bool ok = live && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+        loff[i] = live ? ch * G::PLANE_X + r * G::PITCH_X + c : -1;
+        sv[i] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rx, ok ? (ch * HW + iy * W + ix) * 4 : (int)C16_OOB, 0, 0));
+    }
+
+    // ---- first conv's A operands: lane (j, g) holds w[j][k] for k = 4s + g
+    // (raw OIHW: k = ic*9 + ky*3 + kx), -0 past K = 9 c0; kof[s] is term k's
+    // patch offset (-1 past K)
+    const int K = 9 * c0, ns = (K + 3) / 4;
+    const __amdgpu_buffer_rsrc_t rwa =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.wa, (short)0, 16 * K * 4, 0x00020000);
+    float wa[9];
+    int kof[9];
+#pragma unroll
+    for (int s = 0; s < 9; s++) {
+        const int k = 4 * s + g, ic = k / 9, t = k - 9 * ic;
+        const bool valid = k < K;
+        const float v = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rwa, valid ? (j * K + k) * 4 : (int)C16_OOB, 0, 0));
+        wa[s] = valid ? v : -0.0f;
+        kof[s] = valid ? ic * G::PLANE_X + (t / 3) * G::PITCH_X + t % 3 : -1;
+    }
+    const int cbb = wave % CB2, pb0 = wave / CB2;
+    float biasa[4], biasb[4];
+    {
+        const __amdgpu_buffer_rsrc_t rba =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.ba, (short)0, a.ba ? 64 : 0, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rbb =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.bb, (short)0, a.bb ? 64 * CB2 : 0, 0x00020000);
+        auto va = __builtin_amdgcn_raw_buffer_load_b128(rba, 4 * g * 4, 0, 0);
+        auto vb = __builtin_amdgcn_raw_buffer_load_b128(rbb, (cbb * 16 + 4 * g) * 4, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) biasa[r] = __uint_as_float(va[r]), biasb[r] = __uint_as_float(vb[r]);
+    }
+
+    // ---- first conv: wave -> pixel blocks wave + 4 i (every channel)
+    int basea[G::IA];
+#pragma unroll
+    for (int i = 0; i < G::IA; i++) {
+        int e = (wave + 4 * i) * 16 + j;
+        e = e < G::NE ? e : G::NE - 1;  // lanes past the field compute a duplicate, never stored
+        const int ey = e / G::EW, ex = e - ey * G::EW;
+        basea[i] = SA * (ey * G::PITCH_X + ex);
+    }
+    f32x4 acca[G::IA];
+#pragma unroll
+    for (int i = 0; i < G::IA; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acca[i][r] = biasa[r];
+#pragma unroll
+    for (int i = 0; i < G::NXE; i++)
+        if (loff[i] >= 0) lx[loff[i]] = sv[i];
+    __syncthreads();
+    auto read_a = [&](float (&bv)[G::IA], int s) {
+        const int o = kof[s] < 0 ? 0 : kof[s];
+#pragma unroll
+        for (int i = 0; i < G::IA; i++) {
+            const float v = lx[o + basea[i]];
+            bv[i] = kof[s] < 0 ? 0.0f : v;
+        }
+    };
+    {
+        float bv[2][G::IA];
+        read_a(bv[0], 0);
+#pragma unroll
+        for (int s = 0; s < 9; s++) {
+            if (s < ns) {  // uniform
+                if (s + 1 < ns) read_a(bv[(s + 1) & 1], s + 1);
+                __builtin_amdgcn_sched_barrier(0);  // the next step's reads go out before this step's MFMAs
+#pragma unroll
+                for (int i = 0; i < G::IA; i++)
+                    acca[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], bv[s & 1][i], acca[i], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- second conv's weights (one 16-channel block: nine taps), issued
+    // before the intermediate is written
+    const __amdgpu_buffer_rsrc_t rwb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.wb, (short)0, CB2 * 9 * 1024, 0x00020000);
+    float4 wb[9];
+#pragma unroll
+    for (int t = 0; t < 9; t++) {
+        auto v = __builtin_amdgcn_raw_buffer_load_b128(rwb, (cbb * 9 * 64 + lane) * 16, t * 1024, 0);
+        wb[t] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                            __uint_as_float(v[3]));
+    }
+
+    // ---- the intermediate: activation inside the first conv's map, 0 on
+    // the field outside it
+#pragma unroll
+    for (int i = 0; i < G::IA; i++) {
+        const int e = (wave + 4 * i) * 16 + j;
+        if (wave + 4 * i >= G::NBA || e >= G::NE) continue;
+        const int ey = e / G::EW, ex = e - ey * G::EW;
+        const int yy = ey0 + ey, xx = ex0 + ex;
+        const bool in = (unsigned)yy < (unsigned)a.ah && (unsigned)xx < (unsigned)a.aw;
+        const int pos = G::mpos(ey, ex);
+#pragma unroll
+        for (int r = 0; r < 4; r++) lm[(4 * g + r) * G::PLANE_M + pos] = in ? activate<ACT>(acca[i][r]) : 0.f;
+    }
+    __syncthreads();
+
+    // ---- second conv from LDS: wave -> channel block cbb, pixel blocks
+    // pb0 + i * WB
+    constexpr int WB = 4 / CB2, IB = (G::NBB + WB - 1) / WB;
+    int baseb[IB];
+#pragma unroll
+    for (int i = 0; i < IB; i++) {
+        int o = (pb0 + i * WB) * 16 + j;
+        o = o < TH * TW ? o : TH * TW - 1;
+        const int oy = o / TW, ox = o - oy * TW;
+        baseb[i] = S2 * oy * G::ROW + ox;  // row S2 oy, column S2 ox (with S2 = 2: word ox of the even half)
+    }
+    auto toff = [](int t) {
+        const int ky = t / 3, kx = t % 3;
+        return S2 == 2 ? ky * G::ROW + (kx & 1) * G::HALF + (kx >> 1) : ky * G::ROW + kx;
+    };
+    f32x4 accb[IB];
+#pragma unroll
+    for (int i = 0; i < IB; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) accb[i][r] = biasb[r];
+    auto read_b = [&](float (&bv)[4][IB], int t) {
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int i = 0; i < IB; i++) bv[s][i] = lm[(4 * s + g) * G::PLANE_M + baseb[i] + toff(t)];
+    };
+    {
+        float bv[2][4][IB];
+        read_b(bv[0], 0);
+#pragma unroll
+        for (int t = 0; t < 9; t++) {
+            if (t + 1 < 9) read_b(bv[(t + 1) & 1], t + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                const float w4 = s == 0 ? wb[t].x : s == 1 ? wb[t].y : s == 2 ? wb[t].z : wb[t].w;
+#pragma unroll
+                for (int i = 0; i < IB; i++)
+                    accb[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(w4, bv[t & 1][s][i], accb[i], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- epilogue: activation, residual, store
+    const int HWB = a.bh * a.bw;
+#pragma unroll
+    for (int i = 0; i < IB; i++) {
+        const int o = (pb0 + i * WB) * 16 + j;
+        if (pb0 + i * WB >= G::NBB || o >= TH * TW) continue;
+        const int oy = y0 + o / TW, ox = x0 + o % TW;
+        if (oy >= a.bh || ox >= a.bw) continue;
+        const int pix = oy * a.bw + ox;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int oc = cbb * 16 + 4 * g + r;
+            float v = activate<ACT>(accb[i][r]);
+            if (a.res) v += a.res[oc * HWB + pix];
+            a.y[oc * HWB + pix] = v;
+        }
+    }
+    // ---- the tile's own pixels of the intermediate (S2 TH x S2 TW; the
+    // tiles partition the first conv's map), from LDS
+    if (a.ya) {
+        constexpr int OH = S2 * TH, OW = S2 * TW, OWN = 16 * OH * OW;
+        const int HWA = a.ah * a.aw;
+        for (int e = tid; e < OWN; e += 256) {
+            const int ch = e / (OH * OW), rem = e - ch * (OH * OW);
+            const int ry = rem / OW, rx = rem - ry * OW;
+            const int yy = S2 * y0 + ry, xx = S2 * x0 + rx;
+            if (yy < a.ah && xx < a.aw) a.ya[ch * HWA + yy * a.aw + xx] = lm[ch * G::PLANE_M + G::mpos(ry + 1, rx + 1)];
+        }
+    }
+}
+
+constexpr PairTile kFirstPairTiles[] = {{4, 16}, {8, 16}, {2, 16}};
+constexpr int kFirstPairTileCount = sizeof(kFirstPairTiles) / sizeof(kFirstPairTiles[0]);
+
+template <int TH, int TW, int SA, int S2, int CB2>
+static osh_status first_pair_launch_t(FirstPairArgs a, hipStream_t st) {
+    a.tiles_w = ceil_div(a.bw, TW);
+    const int tiles = a.tiles_w * ceil_div(a.bh, TH);
+    if (exact_silu())
+        hipLaunchKernelGGL((first_pair_kernel<TH, TW, SA, S2, CB2, ACT_SILU_EXACT>), dim3((unsigned)tiles), dim3(256),
+                           0, st, a);
+    else
+        hipLaunchKernelGGL((first_pair_kernel<TH, TW, SA, S2, CB2, OSH_ACT_SILU>), dim3((unsigned)tiles), dim3(256), 0,
+                           st, a);
+    OSH_LAUNCH_CHECK("first_pair_kernel");
+    return OSH_OK;
+}
+
+template <int TH, int TW>
+static osh_status first_pair_launch_tile(const FirstPairArgs &a, int sa, int sb, int cb2, hipStream_t st) {
+#define OSH_FP_CB2(SA, S2) \
+    return cb2 == 2 ? first_pair_launch_t<TH, TW, SA, S2, 2>(a, st) : first_pair_launch_t<TH, TW, SA, S2, 4>(a, st);
+    if (sa == 1) {
+        if (sb == 1) { OSH_FP_CB2(1, 1) }
+        OSH_FP_CB2(1, 2)
+    }
+    if (sb == 1) { OSH_FP_CB2(2, 1) }
+    OSH_FP_CB2(2, 2)
+#undef OSH_FP_CB2
+}
+
+osh_status first_pair_launch(const FirstPairArgs &a, int sa, int sb, int cb2, hipStream_t st, int tile) {
+    switch (tile) {
+    case 0: return first_pair_launch_tile<4, 16>(a, sa, sb, cb2, st);
+    case 1: return first_pair_launch_tile<8, 16>(a, sa, sb, cb2, st);
+    default: return first_pair_launch_tile<2, 16>(a, sa, sb, cb2, st);
+    }
+}
+
+int first_pair_tile_count() { return kFirstPairTileCount; }
+
 }  // namespace osh

@@ -87,7 +87,11 @@ __global__ __launch_bounds__(DQ_THREADS) void dqmm_minmax_kernel(const float *__
                                                                   DqScratch *__restrict__ sc) {
     float lo = 0.f, hi = 0.f;  // 0 is always inside the range (Quantization.cs:115-116)
     long long stride = (long long)gridDim.x * blockDim.x;
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    // XCD-banded block ids: the workgroups of one XCD read one contiguous band
+    // of A, which the fused kernel's workgroups on the same XCD (banded the
+    // same way, row tiles first) then find in that XCD's L2.  Min and max are
+    // exact in any order, so the partials' assignment does not matter.
+    long long i = (long long)xcd_band(blockIdx.x, gridDim.x) * blockDim.x + threadIdx.x;
     // 16-byte loads when the base is aligned (all callers pass tensor bases)
     long long n4 = (reinterpret_cast<uintptr_t>(a) & 15) == 0 ? n / 4 : 0;
     const float4 *a4 = reinterpret_cast<const float4 *>(a);

@@ -124,12 +124,15 @@ class ChainOp:
 
 @dataclass(eq=False)
 class PairOp:
-    """Two chained 3x3 SiLU convs over one map -- a bottleneck's cv1 -> cv2,
-    b reading a's output -- run as one launch (osh_conv2d_pair_f32): a's
-    output stays on chip for b and is still written to a.y."""
+    """Two chained 3x3 SiLU convs, b reading exactly a's output, run as one
+    launch (osh_conv2d_pair_f32): a bottleneck's cv1 -> cv2 over one map, or
+    the network's first conv and the stride-2 conv after it.  a's output
+    stays on chip for b; it is also written to a.y when store_mid is set
+    (which lets first-use timing try the two convs as separate launches)."""
     name: str
     a: ConvOp
     b: ConvOp
+    store_mid: bool = True
 
     @property
     def ops(self):
@@ -777,10 +780,10 @@ def chain_pointwise_convs(model: Model, max_ops: int = 6, min_gain_us: float = 0
 
 def pair_bottleneck_convs(model: Model, takes=None, min_pixels: int = 0) -> Model:
     """Adjacent 3x3 SiLU convs where the second reads exactly the first's
-    output and nothing else touches that buffer (a bottleneck's cv1 -> cv2)
-    become one PairOp, on maps of at least `min_pixels`, where `takes(a, b)`
-    (default: the library's osh_conv2d_pair_check on the resolved params)
-    accepts them.
+    output and nothing else touches that buffer (a bottleneck's cv1 -> cv2;
+    the first conv and the stride-2 conv after it) become one PairOp, on
+    maps of at least `min_pixels`, where `takes(a, b)` (default: the
+    library's osh_conv2d_pair_check on the resolved params) accepts them.
 
     A fused pair saves a launch and the intermediate's round trip, but each
     workgroup also computes the first conv over a one-pixel ring around its
@@ -802,11 +805,13 @@ def pair_bottleneck_convs(model: Model, takes=None, min_pixels: int = 0) -> Mode
         a = ops[i]
         b = ops[i + 1] if i + 1 < len(ops) else None
         if (isinstance(a, ConvOp) and isinstance(b, ConvOp) and a.res is None and
-                all(c.k == 3 and c.s == 1 and c.group == 1 and c.act == "Silu" for c in (a, b)) and
+                all(c.k == 3 and c.group == 1 and c.act == "Silu" for c in (a, b)) and
                 a.y.h * a.y.w >= min_pixels and
                 b.x.buf is a.y.buf and b.x.c0 == a.y.c0 and b.x.c == a.y.c == a.y.buf.c and
                 users.get(id(a.y.buf)) == {id(a), id(b)} and takes(a, b)):
-            out.append(PairOp(a.name.rsplit("/", 3)[0] + "#pair", a, b))
+            # a first-layer pair leaves its 16-channel map unstored: the
+            # fused kernel beats two launches there by far
+            out.append(PairOp(a.name.rsplit("/", 3)[0] + "#pair", a, b, store_mid=a.x.c > 4))
             i += 2
             continue
         out.append(a)
@@ -1005,7 +1010,8 @@ class Frame:
             res = op.b.res.ptr() if op.b.res is not None else None
             return lambda st: N.check(lib.osh_conv2d_pair_f32(
                 C.byref(pa), C.byref(pb), op.a.x.ptr(), C.c_void_p(wa.data_ptr()), C.c_void_p(ba.data_ptr()),
-                C.c_void_p(wb.data_ptr()), C.c_void_p(bb.data_ptr()), act, res, op.a.y.ptr(), op.b.y.ptr(), st))
+                C.c_void_p(wb.data_ptr()), C.c_void_p(bb.data_ptr()), act, res,
+                op.a.y.ptr() if op.store_mid else None, op.b.y.ptr(), st))
         if isinstance(op, ConvOp):
             p, packed, b = self._prepare_conv(op)
             act = N.ACTIVATIONS[op.act]

@@ -670,6 +670,75 @@ def test_conv_pair_equals_two_launches(cuda, name, xs, c1, c2, residual, opts):
             N.call("osh_config_set", k.encode(), v)
 
 
+FIRST_PAIR_CASES = [
+    # (name, x shape, first stride, c2, second stride, residual, options): a
+    # first-layer conv (16 outputs) -> a 3x3 NCHWc conv over its output
+    ("yolo11n_stem_640", (1, 3, 640, 640), 2, 32, 2, False, {}),
+    ("ragged_tiles", (1, 3, 68, 92), 2, 32, 2, True, {}),            # 17 x 23 outputs
+    ("four_planes_64_out", (1, 4, 40, 50), 1, 64, 2, True, {}),
+    ("one_plane_stride_1", (1, 1, 30, 34), 1, 32, 1, True, {}),
+    ("two_planes_exact_silu", (1, 2, 64, 48), 2, 32, 1, False, {"exact_silu": 1}),
+]
+
+
+@pytest.mark.parametrize("name,xs,sa,c2,sb,residual,opts", FIRST_PAIR_CASES, ids=[c[0] for c in FIRST_PAIR_CASES])
+def test_first_layer_pair_equals_two_launches(cuda, name, xs, sa, c2, sb, residual, opts):
+    # The first-layer pair keeps both chains (first_conv_kernel's ic -> ky ->
+    # kx, then the NCHWc chain) with the 16-channel map on chip: outputs and
+    # the stored intermediate equal the two separate launches bit for bit
+    # under every tile, the first-use choice and without the intermediate.
+    import torch
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    print(f"first-layer pair {name}", flush=True)
+    saved = {}
+    for k, v in opts.items():
+        cur = C.c_int(); N.call("osh_config_get", k.encode(), C.byref(cur)); saved[k] = cur.value
+        N.call("osh_config_set", k.encode(), v)
+    try:
+        seed = sum(xs) + 5 * sa + c2 + sb
+        x = _t(synth.uniform(seed, xs), cuda)
+        wa = _t(synth.normal(seed + 1, (16, xs[1], 3, 3), 0, 0.3), cuda)
+        ba = _t(synth.normal(seed + 2, (16,), 0, 0.01), cuda)
+        wb = _t(synth.normal(seed + 3, (c2, 16, 3, 3), 0, 0.05), cuda)
+        bb = _t(synth.normal(seed + 4, (c2,), 0, 0.01), cuda)
+        la = ConvLayer(pads=[1, 1, 1, 1], strides=[sa, sa], fused_activation="Silu")
+        lb = ConvLayer(pads=[1, 1, 1, 1], strides=[sb, sb], fused_activation="Silu")
+        t_ref = la.forward(x, wa, ba)
+        ys = (1, c2, (t_ref.shape[2] - 1) // sb + 1, (t_ref.shape[3] - 1) // sb + 1)
+        r = _t(synth.normal(seed + 5, ys, 0, 1), cuda) if residual else None
+        y_ref = lb.forward(t_ref, wb, bb, residual=r)
+        torch.cuda.synchronize()
+        ts = tuple(t_ref.shape)
+        t_ref, y_ref = t_ref.cpu().numpy(), y_ref.cpu().numpy()
+        _, pa, bufa = la._packed
+        _, pb, bufb = lb._packed
+        st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        N.call("osh_conv2d_pair_check", C.byref(pa), C.byref(pb), N.ACT_SILU)
+        nt = C.c_int(); N.call("osh_config_get", b"pair_tiles", C.byref(nt))
+        ptr = lambda t: C.c_void_p(t.data_ptr()) if t is not None else None
+        try:
+            for tile in list(range(nt.value)) + [-1]:
+                N.call("osh_config_set", b"pair_tile", tile)
+                ya = torch.full(ts, float("nan"), device=cuda)
+                y = torch.full(ys, float("nan"), device=cuda)
+                N.call("osh_conv2d_pair_f32", C.byref(pa), C.byref(pb), ptr(x), ptr(bufa), ptr(ba), ptr(bufb),
+                       ptr(bb), N.ACT_SILU, ptr(r), ptr(ya), ptr(y), st)
+                torch.cuda.synchronize()
+                assert np.array_equal(ya.cpu().numpy(), t_ref), f"{name}: intermediate differs under tile {tile}"
+                assert np.array_equal(y.cpu().numpy(), y_ref), f"{name}: output differs under tile {tile}"
+        finally:
+            N.call("osh_config_set", b"pair_tile", -1)
+        y2 = torch.full(ys, float("nan"), device=cuda)
+        N.call("osh_conv2d_pair_f32", C.byref(pa), C.byref(pb), ptr(x), ptr(bufa), ptr(ba), ptr(bufb), ptr(bb),
+               N.ACT_SILU, ptr(r), None, ptr(y2), st)
+        torch.cuda.synchronize()
+        assert np.array_equal(y2.cpu().numpy(), y_ref)
+    finally:
+        for k, v in saved.items():
+            N.call("osh_config_set", k.encode(), v)
+
+
 def test_conv_pair_refusals(cuda):
     import torch
     from onnxsharp_amd import native as N
@@ -688,6 +757,16 @@ def test_conv_pair_refusals(cuda):
         ("not chained", ok[0], params((1, 16, 40, 40), 32), N.ACT_SILU),
         ("relu", ok[0], ok[1], N.ACT_RELU),
         ("winograd chain", params((1, 32, 40, 40), 16), params((1, 16, 40, 40), 32), N.ACT_SILU),
+        # first-layer pairs
+        ("first-layer 8 outputs", params((1, 3, 64, 64), 8, s=2), params((1, 8, 32, 32), 32, s=2), N.ACT_SILU),
+        ("first-layer then 16 outputs (im2col chain)", params((1, 3, 64, 64), 16, s=2),
+         params((1, 16, 32, 32), 16, s=2), N.ACT_SILU),
+        ("first-layer then 1x1", params((1, 3, 64, 64), 16, s=2),
+         params((1, 16, 32, 32), 32, k=1, pads=(0, 0, 0, 0)), N.ACT_SILU),
+        ("first-layer stride 3", params((1, 3, 64, 64), 16, s=3), params((1, 16, 22, 22), 32), N.ACT_SILU),
+        ("first-layer relu", params((1, 3, 64, 64), 16, s=2), params((1, 16, 32, 32), 32, s=2), N.ACT_RELU),
+        ("first-layer odd map under stride 2", params((1, 3, 66, 66), 16, s=2),
+         params((1, 16, 33, 33), 32, s=2), N.ACT_SILU),
     ]
     for what, pa, pb, act in bad:
         with pytest.raises(N.OshError) as e:

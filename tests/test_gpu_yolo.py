@@ -71,9 +71,11 @@ def test_yolo_per_op_parity(cuda, oracle, exact_silu, size, chains):
             fr.sync()
             for op in members:
                 oin = [np.ascontiguousarray(host[id(s.buf)][:, s.c0:s.c0 + s.c]) for s in YO.op_inputs(op)]
-                got = _host(op.y)
                 ref = YO.run_op(oracle, op, oin)
                 host[id(op.y.buf)][:, op.y.c0:op.y.c0 + op.y.c] = ref
+                if isinstance(launch, Y.PairOp) and op is launch.a and not launch.store_mid:
+                    continue  # the intermediate stayed on chip: its oracle value feeds b
+                got = _host(op.y)
                 what = f"op {i} {type(op).__name__} {op.name}"
                 nbad, dmax = fp32_violations(got, ref)
                 assert_fp32_close(got, ref, what)
