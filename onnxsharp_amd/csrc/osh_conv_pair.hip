@@ -412,12 +412,19 @@ struct FirstPairGeom {
     }
 };
 
-template <int TH, int TW, int SA, int S2, int CB2, int ACT>
+// NS: the first conv's k-steps, 7 for c0 <= 3 (past 9 c0 every term is the
+// -0 x +0 identity) and 9 for c0 = 4; a compile-time count keeps the
+// accumulators in place (a runtime bound had the compiler copy them at every
+// step's join).  Stores of lanes with nothing to store go to dummy words past
+// the input patch, so no store waits behind a branch.
+template <int TH, int TW, int SA, int S2, int CB2, int NS, int ACT>
 __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
     using G = FirstPairGeom<TH, TW, SA, S2>;
     static_assert(CB2 == 2 || CB2 == 4, "32 or 64 output channels (the NCHWc chain)");
     static_assert(TW % 16 == 0 || 16 % TW == 0, "16-pixel blocks cover whole rows or whole row sets");
-    __shared__ __align__(16) float lx[4 * G::PLANE_X];
+    static_assert(NS == 7 || NS == 9, "up to 3 planes in 7 k-steps, 4 in 9");
+    constexpr int XDUMMY = 4 * G::PLANE_X;
+    __shared__ __align__(16) float lx[XDUMMY + 64];  // a dummy word per lane: no bank conflicts
     __shared__ __align__(16) float lm[16 * G::PLANE_M];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -440,29 +447,29 @@ __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
         const int ch = e / (G::PH * G::PW), rem = e - ch * (G::PH * G::PW);
         const int r = rem / G::PW, c = rem - r * G::PW;
         const int iy = iy0 + r, ix = ix0 + c;
-        const bool live = e < G::XE && ch < c0;
-        const bool ok = live && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
-        loff[i] = live ? ch * G::PLANE_X + r * G::PITCH_X + c : -1;
+        // planes c0 .. 3 are staged too, as zeros: the terms past 9 c0 read them
+        const bool ok = e < G::XE && ch < c0 && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+        loff[i] = e < G::XE ? ch * G::PLANE_X + r * G::PITCH_X + c : XDUMMY + lane;
         sv[i] = __uint_as_float(
             __builtin_amdgcn_raw_buffer_load_b32(rx, ok ? (ch * HW + iy * W + ix) * 4 : (int)C16_OOB, 0, 0));
     }
 
     // ---- first conv's A operands: lane (j, g) holds w[j][k] for k = 4s + g
     // (raw OIHW: k = ic*9 + ky*3 + kx), -0 past K = 9 c0; kof[s] is term k's
-    // patch offset (-1 past K)
-    const int K = 9 * c0, ns = (K + 3) / 4;
+    // patch offset (past K: a zero plane, so those terms add -0 x +0)
+    const int K = 9 * c0;
     const __amdgpu_buffer_rsrc_t rwa =
         __builtin_amdgcn_make_buffer_rsrc((void *)a.wa, (short)0, 16 * K * 4, 0x00020000);
-    float wa[9];
-    int kof[9];
+    float wa[NS];
+    int kof[NS];
 #pragma unroll
-    for (int s = 0; s < 9; s++) {
+    for (int s = 0; s < NS; s++) {
         const int k = 4 * s + g, ic = k / 9, t = k - 9 * ic;
         const bool valid = k < K;
         const float v = __uint_as_float(
             __builtin_amdgcn_raw_buffer_load_b32(rwa, valid ? (j * K + k) * 4 : (int)C16_OOB, 0, 0));
         wa[s] = valid ? v : -0.0f;
-        kof[s] = valid ? ic * G::PLANE_X + (t / 3) * G::PITCH_X + t % 3 : -1;
+        kof[s] = ic * G::PLANE_X + (t / 3) * G::PITCH_X + t % 3;  // ic <= 3 (k < 4 NS <= 36)
     }
     const int cbb = wave % CB2, pb0 = wave / CB2;
     float biasa[4], biasb[4];
@@ -477,49 +484,8 @@ __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
         for (int r = 0; r < 4; r++) biasa[r] = __uint_as_float(va[r]), biasb[r] = __uint_as_float(vb[r]);
     }
 
-    // ---- first conv: wave -> pixel blocks wave + 4 i (every channel)
-    int basea[G::IA];
-#pragma unroll
-    for (int i = 0; i < G::IA; i++) {
-        int e = (wave + 4 * i) * 16 + j;
-        e = e < G::NE ? e : G::NE - 1;  // lanes past the field compute a duplicate, never stored
-        const int ey = e / G::EW, ex = e - ey * G::EW;
-        basea[i] = SA * (ey * G::PITCH_X + ex);
-    }
-    f32x4 acca[G::IA];
-#pragma unroll
-    for (int i = 0; i < G::IA; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) acca[i][r] = biasa[r];
-#pragma unroll
-    for (int i = 0; i < G::NXE; i++)
-        if (loff[i] >= 0) lx[loff[i]] = sv[i];
-    __syncthreads();
-    auto read_a = [&](float (&bv)[G::IA], int s) {
-        const int o = kof[s] < 0 ? 0 : kof[s];
-#pragma unroll
-        for (int i = 0; i < G::IA; i++) {
-            const float v = lx[o + basea[i]];
-            bv[i] = kof[s] < 0 ? 0.0f : v;
-        }
-    };
-    {
-        float bv[2][G::IA];
-        read_a(bv[0], 0);
-#pragma unroll
-        for (int s = 0; s < 9; s++) {
-            if (s < ns) {  // uniform
-                if (s + 1 < ns) read_a(bv[(s + 1) & 1], s + 1);
-                __builtin_amdgcn_sched_barrier(0);  // the next step's reads go out before this step's MFMAs
-#pragma unroll
-                for (int i = 0; i < G::IA; i++)
-                    acca[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], bv[s & 1][i], acca[i], 0, 0, 0);
-            }
-        }
-    }
-
     // ---- second conv's weights (one 16-channel block: nine taps), issued
-    // before the intermediate is written
+    // with the first conv's: their latency passes under the first conv
     const __amdgpu_buffer_rsrc_t rwb =
         __builtin_amdgcn_make_buffer_rsrc((void *)a.wb, (short)0, CB2 * 9 * 1024, 0x00020000);
     float4 wb[9];
@@ -530,18 +496,64 @@ __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
                             __uint_as_float(v[3]));
     }
 
-    // ---- the intermediate: activation inside the first conv's map, 0 on
-    // the field outside it
+    // ---- first conv: wave -> pixel blocks wave + 4 i (every channel), one
+    // block after the other: block i's chain (NS dependent MFMAs) runs while
+    // the VALU activates and stores block i - 1, and block i + 1's operands
+    // are read from LDS
 #pragma unroll
-    for (int i = 0; i < G::IA; i++) {
-        const int e = (wave + 4 * i) * 16 + j;
-        if (wave + 4 * i >= G::NBA || e >= G::NE) continue;
-        const int ey = e / G::EW, ex = e - ey * G::EW;
+    for (int i = 0; i < G::NXE; i++) lx[loff[i]] = sv[i];
+    __syncthreads();
+    // block i's pixel: lane j of block wave + 4 i, e = 16 wave + j + 64 i,
+    // stepped from block to block without a division.  Lanes past the field
+    // take its last pixel: they compute and store the same value to the same
+    // word as that pixel's own lane
+    int ey0b, ex0b;
+    {
+        const int e = 16 * wave + j;
+        ey0b = e / G::EW;
+        ex0b = e - ey0b * G::EW;
+    }
+    auto pix = [&](int i, int &ey, int &ex) {
+        ey = ey0b + (64 * i) / G::EW;
+        ex = ex0b + (64 * i) % G::EW;
+        if (ex >= G::EW) ex -= G::EW, ey++;
+        if (16 * wave + j + 64 * i >= G::NE) ey = G::EH - 1, ex = G::EW - 1;
+    };
+    auto read_blk = [&](float (&bv)[NS], int i) {
+        int ey, ex;
+        pix(i, ey, ex);
+        const int base = SA * (ey * G::PITCH_X + ex);
+#pragma unroll
+        for (int s = 0; s < NS; s++) bv[s] = lx[kof[s] + base];
+    };
+    // the intermediate: activation inside the first conv's map, +0 on the
+    // field outside it (the activation's bits masked: no branch)
+    auto store_blk = [&](const f32x4 &acc, int i) {
+        int ey, ex;
+        pix(i, ey, ex);
         const int yy = ey0 + ey, xx = ex0 + ex;
-        const bool in = (unsigned)yy < (unsigned)a.ah && (unsigned)xx < (unsigned)a.aw;
-        const int pos = G::mpos(ey, ex);
+        const int keep = (unsigned)yy < (unsigned)a.ah && (unsigned)xx < (unsigned)a.aw ? -1 : 0;
+        const int pos = 4 * g * G::PLANE_M + G::mpos(ey, ex);
 #pragma unroll
-        for (int r = 0; r < 4; r++) lm[(4 * g + r) * G::PLANE_M + pos] = in ? activate<ACT>(acca[i][r]) : 0.f;
+        for (int r = 0; r < 4; r++)
+            lm[pos + r * G::PLANE_M] = __int_as_float(__float_as_int(activate<ACT>(acc[r])) & keep);
+    };
+    {
+        float bv[2][NS];
+        f32x4 prev;
+        read_blk(bv[0], 0);
+#pragma unroll
+        for (int i = 0; i < G::IA; i++) {
+            if (i + 1 < G::IA) read_blk(bv[(i + 1) & 1], i + 1);
+            f32x4 acc;
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[r] = biasa[r];
+#pragma unroll
+            for (int s = 0; s < NS; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], bv[i & 1][s], acc, 0, 0, 0);
+            if (i > 0) store_blk(prev, i - 1);  // blocks before the last exist for every wave
+            prev = acc;
+        }
+        if (wave + 4 * (G::IA - 1) < G::NBA) store_blk(prev, G::IA - 1);  // uniform
     }
     __syncthreads();
 
@@ -619,19 +631,26 @@ __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
     }
 }
 
-constexpr PairTile kFirstPairTiles[] = {{4, 16}, {8, 16}, {2, 16}};
+constexpr PairTile kFirstPairTiles[] = {{4, 16}, {8, 16}, {2, 16}, {4, 32}, {2, 32}};
 constexpr int kFirstPairTileCount = sizeof(kFirstPairTiles) / sizeof(kFirstPairTiles[0]);
+
+template <int TH, int TW, int SA, int S2, int CB2, int NS>
+static void first_pair_launch_ns(const FirstPairArgs &a, unsigned tiles, hipStream_t st) {
+    if (exact_silu())
+        hipLaunchKernelGGL((first_pair_kernel<TH, TW, SA, S2, CB2, NS, ACT_SILU_EXACT>), dim3(tiles), dim3(256), 0, st,
+                           a);
+    else
+        hipLaunchKernelGGL((first_pair_kernel<TH, TW, SA, S2, CB2, NS, OSH_ACT_SILU>), dim3(tiles), dim3(256), 0, st, a);
+}
 
 template <int TH, int TW, int SA, int S2, int CB2>
 static osh_status first_pair_launch_t(FirstPairArgs a, hipStream_t st) {
     a.tiles_w = ceil_div(a.bw, TW);
-    const int tiles = a.tiles_w * ceil_div(a.bh, TH);
-    if (exact_silu())
-        hipLaunchKernelGGL((first_pair_kernel<TH, TW, SA, S2, CB2, ACT_SILU_EXACT>), dim3((unsigned)tiles), dim3(256),
-                           0, st, a);
+    const unsigned tiles = (unsigned)(a.tiles_w * ceil_div(a.bh, TH));
+    if (a.c0 <= 3)
+        first_pair_launch_ns<TH, TW, SA, S2, CB2, 7>(a, tiles, st);
     else
-        hipLaunchKernelGGL((first_pair_kernel<TH, TW, SA, S2, CB2, OSH_ACT_SILU>), dim3((unsigned)tiles), dim3(256), 0,
-                           st, a);
+        first_pair_launch_ns<TH, TW, SA, S2, CB2, 9>(a, tiles, st);
     OSH_LAUNCH_CHECK("first_pair_kernel");
     return OSH_OK;
 }
@@ -653,7 +672,9 @@ osh_status first_pair_launch(const FirstPairArgs &a, int sa, int sb, int cb2, hi
     switch (tile) {
     case 0: return first_pair_launch_tile<4, 16>(a, sa, sb, cb2, st);
     case 1: return first_pair_launch_tile<8, 16>(a, sa, sb, cb2, st);
-    default: return first_pair_launch_tile<2, 16>(a, sa, sb, cb2, st);
+    case 2: return first_pair_launch_tile<2, 16>(a, sa, sb, cb2, st);
+    case 3: return first_pair_launch_tile<4, 32>(a, sa, sb, cb2, st);
+    default: return first_pair_launch_tile<2, 32>(a, sa, sb, cb2, st);
     }
 }
 
