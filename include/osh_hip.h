@@ -115,7 +115,8 @@ OSH_API osh_status osh_device_synchronize(void);
  *                 pointwise launches (the pointwise LDS tiles that fit every
  *                 member; a forced tile that does not fit takes the default).
  *   "pair_tile", "pair_tiles": the same for osh_conv2d_pair_f32: its
- *                 output tiles (4x4, 4x8, 8x8), then N-1 = the two convs as
+ *                 output tiles (bottleneck pairs 4x4, 4x8, 8x8; first-layer
+ *                 pairs 4x16, 2x32, 2x16), then N-1 = the two convs as
  *                 separate launches (only with an intermediate buffer).
  *   "pointwise_variants" (get only): N.
  *                 The -2 setting of "pointwise_variant" changes the packed
@@ -285,11 +286,17 @@ OSH_API osh_status osh_conv2d_group_f32(int count, const osh_conv_params *ps, co
  * keeps its chain, and the intermediate stays on chip (it is still written to
  * d_ya unless d_ya is NULL).  First-use timing chooses between the fused
  * kernel's tiles and, when d_ya is given, two separate launches, whichever
- * is faster for the shapes.  Takes 3x3 stride-1 pad-1 SiLU convs on one
- * 1 x C x H x W map, C = 16 / 32 / 48 / 64, 16 / 32 / 64 output channels each, in the
- * chain orders the single-conv dispatch takes for them; anything else returns
- * OSH_E_UNSUPPORTED (run the two convs separately).  No output may overlap
- * d_x or the other output, and the residual may not overlap d_y. */
+ * is faster for the shapes.  Takes two kinds of pair of SiLU convs, batch 1,
+ * in the chain orders the single-conv dispatch takes for them:
+ *   - bottleneck pairs: 3x3 stride-1 pad-1 convs on one 1 x C x H x W map,
+ *     C = 16 / 32 / 48 / 64, 16 / 32 / 64 output channels each;
+ *   - first-layer pairs: a 3x3 stride-1 or -2 conv over C <= 4 planes with
+ *     16 outputs (the first_conv chain; a network's first layer, e.g.
+ *     YOLO11n's 3 -> 16 stem, FirstConv.cs), then a 3x3 pad-1 conv of stride
+ *     1 or 2 over its output with 32 or 64 outputs (the NCHWc chain).
+ * Anything else returns OSH_E_UNSUPPORTED (run the two convs separately).
+ * No output may overlap d_x or the other output, and the residual may not
+ * overlap d_y. */
 OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv_params *pb, const float *d_x,
                                        const void *d_wa, const float *d_bias_a, const void *d_wb,
                                        const float *d_bias_b, int act, const float *d_res, float *d_ya, float *d_y,

@@ -631,7 +631,11 @@ __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
     }
 }
 
-constexpr PairTile kFirstPairTiles[] = {{4, 16}, {8, 16}, {2, 16}, {4, 32}, {2, 32}};
+// Measured at YOLO11n's stem (3 -> 16 -> 32, 640 x 640): 4 x 16 10.9 us,
+// 2 x 32 10.8, 2 x 16 11.1; 8 x 16 12.1 and 4 x 32 13.3 (fewer workgroups
+// than CUs) were dropped.  As many tiles as the bottleneck pair's, so that a
+// forced pair_tile means the same for both.
+constexpr PairTile kFirstPairTiles[] = {{4, 16}, {2, 32}, {2, 16}};
 constexpr int kFirstPairTileCount = sizeof(kFirstPairTiles) / sizeof(kFirstPairTiles[0]);
 
 template <int TH, int TW, int SA, int S2, int CB2, int NS>
@@ -671,13 +675,12 @@ static osh_status first_pair_launch_tile(const FirstPairArgs &a, int sa, int sb,
 osh_status first_pair_launch(const FirstPairArgs &a, int sa, int sb, int cb2, hipStream_t st, int tile) {
     switch (tile) {
     case 0: return first_pair_launch_tile<4, 16>(a, sa, sb, cb2, st);
-    case 1: return first_pair_launch_tile<8, 16>(a, sa, sb, cb2, st);
-    case 2: return first_pair_launch_tile<2, 16>(a, sa, sb, cb2, st);
-    case 3: return first_pair_launch_tile<4, 32>(a, sa, sb, cb2, st);
-    default: return first_pair_launch_tile<2, 32>(a, sa, sb, cb2, st);
+    case 1: return first_pair_launch_tile<2, 32>(a, sa, sb, cb2, st);
+    default: return first_pair_launch_tile<2, 16>(a, sa, sb, cb2, st);
     }
 }
 
 int first_pair_tile_count() { return kFirstPairTileCount; }
+static_assert(kFirstPairTileCount == kPairTileCount, "a forced pair_tile indexes both pair families alike");
 
 }  // namespace osh

@@ -176,8 +176,8 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         return OSH_OK;
     }
     if (strcmp(key, "pair_tile") == 0) {
-        if (value < -1 || value > 8)
-            return fail(OSH_E_INVALID, "pair_tile %d out of range [-1, %d]", value, 8);
+        if (value < -1 || value > conv_pair_tile_count())
+            return fail(OSH_E_INVALID, "pair_tile %d out of range [-1, %d]", value, conv_pair_tile_count());
         g_pair_tile = value;
         return OSH_OK;
     }
