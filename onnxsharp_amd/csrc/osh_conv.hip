@@ -1106,9 +1106,11 @@ constexpr int kPairTuneTag = 30;  // tuning-table tags of the fused pair (+1 wit
 // channels out of each, SiLU, and the single-conv dispatch taking for each
 // the chain the pair computes (NCHWc for 32 and 64 outputs, im2col for 16).
 static const char *first_pair_refusal(const osh_conv_params *pa, const osh_conv_params *pb, int act);
+static const char *pair8_refusal(const osh_conv_params *pa, const osh_conv_params *pb, int act);
 
 static const char *pair_refusal(const osh_conv_params *pa, const osh_conv_params *pb, int act) {
     if (pa->c <= 4) return first_pair_refusal(pa, pb, act);
+    if (pa->m == 8) return pair8_refusal(pa, pb, act);
     auto same_map_3x3 = [](const osh_conv_params *p) {
         return p->group == 1 && p->kh == 3 && p->kw == 3 && p->sh == 1 && p->sw == 1 && p->dh == 1 &&
                p->dw == 1 && p->pt == 1 && p->pl == 1 && p->oh == p->h && p->ow == p->w;
@@ -1123,6 +1125,25 @@ static const char *pair_refusal(const osh_conv_params *pa, const osh_conv_params
     if ((long long)pa->c * pa->h * pa->w * 4 >= (1LL << 31)) return "input too large";
     if (select_algo(pa) != (pa->m == 16 ? ALGO_CONV16I : ALGO_CONV16) ||
         select_algo(pb) != (pb->m == 16 ? ALGO_CONV16I : ALGO_CONV16))
+        return "the single-conv dispatch takes another chain for one of the convs";
+    return nullptr;
+}
+
+// The 8-channel pair (conv_pair8_kernel): 16 -> 8 -> 16, both 3x3 stride 1
+// pad 1 on one map, the first in the im2col order and the second in the
+// first-layer chain, as the single-conv dispatch takes them.
+static const char *pair8_refusal(const osh_conv_params *pa, const osh_conv_params *pb, int act) {
+    auto same_map_3x3 = [](const osh_conv_params *p) {
+        return p->group == 1 && p->kh == 3 && p->kw == 3 && p->sh == 1 && p->sw == 1 && p->dh == 1 &&
+               p->dw == 1 && p->pt == 1 && p->pl == 1 && p->oh == p->h && p->ow == p->w;
+    };
+    if (!same_map_3x3(pa) || !same_map_3x3(pb)) return "both convs must be 3x3, stride 1, pad 1 on one map";
+    if (pa->n != 1 || pb->n != 1) return "batch 1 only";
+    if (pb->c != pa->m || pb->h != pa->h || pb->w != pa->w) return "the second conv must read the first one's output";
+    if (pa->c != 16 || pb->m != 16) return "an 8-channel intermediate pairs 16 -> 8 -> 16 only";
+    if (act != OSH_ACT_SILU) return "the fused pair takes SiLU convs";
+    if (16LL * pa->h * pa->w * 4 >= (1LL << 31)) return "input too large";
+    if (select_algo(pa) != ALGO_CONV16I || select_algo(pb) != ALGO_FIRST)
         return "the single-conv dispatch takes another chain for one of the convs";
     return nullptr;
 }
@@ -1277,6 +1298,7 @@ OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv
     a.ya = d_ya;
     a.y = d_y;
     const int cb1 = pa->m / 16, cb2 = pb->m / 16;
+    const bool eight = pa->m == 8;  // conv_pair8_kernel
     // Variants: the pair kernel's tiles, then (when the intermediate has a
     // buffer) the two convs as separate launches -- the pair's ring
     // recompute runs on one CU's four MFMA pipes, which loses to two
@@ -1293,7 +1315,7 @@ OSH_API osh_status osh_conv2d_pair_f32(const osh_conv_params *pa, const osh_conv
                 osh_status st = conv2d(pa, d_x, d_wa, d_bias_a, act, nullptr, d_ya, stream);
                 return st != OSH_OK ? st : conv2d(pb, d_ya, d_wb, d_bias_b, act, d_res, d_y, stream);
             }
-            return conv_pair_launch(a, cb1, cb2, stream, v);
+            return eight ? conv_pair8_launch(a, stream, v) : conv_pair_launch(a, cb1, cb2, stream, v);
         },
         stream);
 }

@@ -23,6 +23,11 @@ struct PairArgs {
 osh_status conv_pair_launch(const PairArgs &a, int cb1, int cb2, hipStream_t st, int tile);
 int conv_pair_tile_count();
 
+// A bottleneck with an 8-channel intermediate: 16 -> 8 (im2col order) ->
+// 16 (the first-layer chain), 3x3 stride 1 pad 1 on one map, SiLU; wa packed
+// by conv16_pack in the im2col order, wb raw OIHW [16][8][3][3].
+osh_status conv_pair8_launch(const PairArgs &a, hipStream_t st, int tile);
+
 // A network's first conv (3x3 over c0 <= 4 planes, 16 outputs) and the 3x3
 // pad-1 conv that reads its output (16 -> 32 or 64 channels).
 struct FirstPairArgs {

@@ -140,6 +140,24 @@ __global__ __launch_bounds__(256) void conv_pair_kernel(PairArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; r++) biasa[r] = __uint_as_float(va[r]), biasb[r] = __uint_as_float(vb[r]);
     }
+    // the residuals of the wave's output pixels, loaded now so that their
+    // latency passes under both convs (out-of-map pixels and a NULL residual
+    // read 0; the add in the epilogue happens only with a residual)
+    float rv[G::IB][4];
+    {
+        const __amdgpu_buffer_rsrc_t rr =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.res, (short)0, a.res ? 16 * CB2 * HW * 4 : 0, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < G::IB; i++) {
+            const int o = (pb0 + i * G::WB) * 16 + j;
+            const int oy = y0 + o / TW, ox = x0 + o % TW;
+            const bool in = pb0 + i * G::WB < G::NBB && o < TH * TW && oy < H && ox < W;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                rv[i][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    rr, in ? ((cbb * 16 + 4 * g + r) * HW + oy * W + ox) * 4 : (int)C16_OOB, 0, 0));
+        }
+    }
     f32x4 acca[G::IA];
 #pragma unroll
     for (int r = 0; r < 4; r++)
@@ -306,7 +324,7 @@ __global__ __launch_bounds__(256) void conv_pair_kernel(PairArgs a) {
         for (int r = 0; r < 4; r++) {
             const int oc = cbb * 16 + 4 * g + r;
             float v = activate<ACT>(accb[i][r]);
-            if (a.res) v += a.res[oc * HW + pix];
+            if (a.res) v += rv[i][r];
             a.y[oc * HW + pix] = v;
         }
     }
@@ -370,6 +388,280 @@ osh_status conv_pair_launch(const PairArgs &a, int cb1, int cb2, hipStream_t st,
 }
 
 int conv_pair_tile_count() { return kPairTileCount; }
+
+// ---------------------------------------------------------- 8-channel pair
+//
+// A bottleneck whose intermediate has 8 channels (YOLO11n's first C3k2 at
+// 160 x 160: 16 -> 8 -> 16, shortcut added after the second conv).  The
+// single-conv dispatch sums the first conv in the im2col order (8 outputs:
+// ConvKernels.cs:554-563) and the second, over 8 input channels, in the
+// first-layer chain ic -> ky -> kx (FirstConv.cs:344-362): both are k =
+// ic*9 + ky*3 + kx ascending from the bias.  Both run on the 16x16x4 MFMA
+// from LDS: the first with the im2col packing of conv16_pack (its rows 8..15
+// are zero weights and a zero bias, so those rows compute zeros, stored to
+// unused planes), the second over the 72 terms of its 8 channels with raw
+// OIHW weights (first_conv_kernel's packing).  The first conv covers the
+// tile and a one-pixel ring, block by block, each block's 36-step chain
+// overlapping the activation and stores of the block before.
+template <int TH, int TW, int ACT>
+__global__ __launch_bounds__(256) void conv_pair8_kernel(PairArgs a) {
+    constexpr int EH = TH + 2, EW = TW + 2, NE = EH * EW;      // first conv's field (tile + ring)
+    constexpr int NBA = (NE + 15) / 16, IA = (NBA + 3) / 4;     // its 16-pixel blocks; per wave
+    constexpr int PH = TH + 4, PW = TW + 4;                     // its input patch (16 channels)
+    constexpr int PITCH_X = pair_pitch(PW), PLANE_X = pair_plane(PH, PITCH_X);
+    constexpr int XE = 16 * PH * PW, NXE = (XE + 255) / 256;
+    constexpr int PITCH_M = pair_pitch(EW), PLANE_M = pair_plane(EH, PITCH_M);
+    constexpr int NBB = TH * TW / 16, IB = (NBB + 3) / 4;       // output blocks; per wave
+    static_assert(TH * TW % 16 == 0, "whole 16-pixel output blocks");
+    constexpr int XDUMMY = 16 * PLANE_X;
+    __shared__ __align__(16) float lx[XDUMMY + 64];  // a dummy word per lane for staging lanes past the patch
+    __shared__ __align__(16) float lm[16 * PLANE_M];  // planes 8..15: the first conv's zero rows
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, g = lane >> 4;
+    const int ty = blockIdx.x / a.tiles_w, tx = blockIdx.x - ty * a.tiles_w;
+    const int y0 = ty * TH, x0 = tx * TW;
+    const int H = a.h, W = a.w, HW = H * W;
+
+    // ---- the first conv's input patch (rows y0-2 .. y0+TH+1, columns
+    // x0-2 .. x0+TW+1, 16 channels) in one round trip; outside the map the
+    // offset is out of range and the load returns 0
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, 16 * HW * 4, 0x00020000);
+    int loff[NXE];
+    float sv[NXE];
+#pragma unroll
+    for (int i = 0; i < NXE; i++) {
+        const int e = tid + 256 * i;
+        const int ch = e / (PH * PW), rem = e - ch * (PH * PW);
+        const int r = rem / PW, c = rem - r * PW;
+        const int iy = y0 - 2 + r, ix = x0 - 2 + c;
+        const bool ok = e < XE && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W;
+        loff[i] = e < XE ? ch * PLANE_X + r * PITCH_X + c : XDUMMY + lane;
+        sv[i] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rx, ok ? (ch * HW + iy * W + ix) * 4 : (int)C16_OOB, 0, 0));
+    }
+    // ---- weights and biases.  First conv: k-group t's float4 holds steps
+    // 4t .. 4t+3 of the lane (im2col packing, one 16-row block).  Second
+    // conv: lane (j, g) step s holds w[j][4s + g] (raw [16][8][3][3]).
+    const __amdgpu_buffer_rsrc_t rwa =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.wa, (short)0, 9 * 1024, 0x00020000);
+    float4 wa[9];
+#pragma unroll
+    for (int t = 0; t < 9; t++) {
+        auto v = __builtin_amdgcn_raw_buffer_load_b128(rwa, lane * 16, t * 1024, 0);
+        wa[t] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                            __uint_as_float(v[3]));
+    }
+    const __amdgpu_buffer_rsrc_t rwb =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.wb, (short)0, 16 * 72 * 4, 0x00020000);
+    float wb[18];
+#pragma unroll
+    for (int s = 0; s < 18; s++)
+        wb[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rwb, (j * 72 + 4 * s + g) * 4, 0, 0));
+    // biases as buffer loads (a NULL bias is a zero-sized buffer: loads
+    // return 0); the first conv's has 8 entries, so lane groups 2 and 3 (its
+    // zero rows) read past it and get 0
+    float biasa[4], biasb[4];
+    {
+        const __amdgpu_buffer_rsrc_t rba =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.ba, (short)0, a.ba ? 32 : 0, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rbb =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.bb, (short)0, a.bb ? 64 : 0, 0x00020000);
+        auto va = __builtin_amdgcn_raw_buffer_load_b128(rba, 16 * g, 0, 0);
+        auto vb = __builtin_amdgcn_raw_buffer_load_b128(rbb, 16 * g, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) biasa[r] = __uint_as_float(va[r]), biasb[r] = __uint_as_float(vb[r]);
+    }
+    // operand offsets.  First conv: step u = 9v + r gives lane group g the
+    // term 4u + g: channel 4v + (4r + g) / 9, tap (4r + g) % 9.  Second conv:
+    // step s gives term 4s + g: channel (4s + g) / 9, tap (4s + g) % 9.
+    int i2ca[9], kofb[18];
+#pragma unroll
+    for (int r = 0; r < 9; r++) {
+        const int term = 4 * r + g, tap = term % 9;
+        i2ca[r] = (term / 9) * PLANE_X + (tap / 3) * PITCH_X + tap % 3;
+    }
+#pragma unroll
+    for (int s = 0; s < 18; s++) {
+        const int term = 4 * s + g, tap = term % 9;
+        kofb[s] = (term / 9) * PLANE_M + (tap / 3) * PITCH_M + tap % 3;
+    }
+
+    // the residuals of the wave's output pixels, loaded now so that their
+    // latency passes under both convs (out-of-map pixels and a NULL residual
+    // read 0; the add below happens only with a residual)
+    float rv[IB][4];
+    {
+        const __amdgpu_buffer_rsrc_t rr =
+            __builtin_amdgcn_make_buffer_rsrc((void *)a.res, (short)0, a.res ? 16 * HW * 4 : 0, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < IB; i++) {
+            const int o = (wave + 4 * i) * 16 + j;
+            const int oy = y0 + o / TW, ox = x0 + o % TW;
+            const bool in = wave + 4 * i < NBB && oy < H && ox < W;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                rv[i][r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    rr, in ? ((4 * g + r) * HW + oy * W + ox) * 4 : (int)C16_OOB, 0, 0));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NXE; i++) lx[loff[i]] = sv[i];
+    __syncthreads();
+
+    // ---- first conv, block by block (pixel e = 16 wave + j + 64 i of the
+    // field, stepped without a division; lanes past the field take its last
+    // pixel and store the same value as that pixel's own lane)
+    int ey0b, ex0b;
+    {
+        const int e = 16 * wave + j;
+        ey0b = e / EW;
+        ex0b = e - ey0b * EW;
+    }
+    auto pix = [&](int i, int &ey, int &ex) {
+        ey = ey0b + (64 * i) / EW;
+        ex = ex0b + (64 * i) % EW;
+        if (ex >= EW) ex -= EW, ey++;
+        if (16 * wave + j + 64 * i >= NE) ey = EH - 1, ex = EW - 1;
+    };
+    auto read_blk = [&](float (&bv)[36], int i) {
+        int ey, ex;
+        pix(i, ey, ex);
+        const int base = ey * PITCH_X + ex;
+#pragma unroll
+        for (int u = 0; u < 36; u++) bv[u] = lx[(u / 9) * 4 * PLANE_X + i2ca[u % 9] + base];
+    };
+    // the intermediate: activation inside the map, +0 on the ring outside it
+    auto store_blk = [&](const f32x4 &acc, int i) {
+        int ey, ex;
+        pix(i, ey, ex);
+        const int yy = y0 - 1 + ey, xx = x0 - 1 + ex;
+        const int keep = (unsigned)yy < (unsigned)H && (unsigned)xx < (unsigned)W ? -1 : 0;
+        const int pos = 4 * g * PLANE_M + ey * PITCH_M + ex;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            lm[pos + r * PLANE_M] = __int_as_float(__float_as_int(activate<ACT>(acc[r])) & keep);
+    };
+    {
+        // One scheduling region per block: its chain, the next block's
+        // operand reads and the block before's stores, the LDS operations
+        // placed one after each MFMA (left to itself the scheduler sank
+        // every read to just before its MFMA, which then waited for it).
+        float bv[2][36];
+        f32x4 prev;
+        read_blk(bv[0], 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < IA; i++) {
+            if (i + 1 < IA) read_blk(bv[(i + 1) & 1], i + 1);
+            f32x4 acc;
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[r] = biasa[r];
+#pragma unroll
+            for (int u = 0; u < 36; u++) {
+                const float4 &w4 = wa[u / 4];
+                const float wv = u % 4 == 0 ? w4.x : u % 4 == 1 ? w4.y : u % 4 == 2 ? w4.z : w4.w;
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wv, bv[i & 1][u], acc, 0, 0, 0);
+            }
+            if (i > 0) store_blk(prev, i - 1);  // blocks before the last exist for every wave
+            prev = acc;
+#pragma unroll
+            for (int u = 0; u < 36; u++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100 | 0x200, 1, 0);  // then one LDS read or write
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (wave + 4 * (IA - 1) < NBA) store_blk(prev, IA - 1);  // uniform
+    }
+    __syncthreads();
+
+    // ---- second conv from LDS: wave -> output blocks wave + 4 i
+    int baseb[IB];
+#pragma unroll
+    for (int i = 0; i < IB; i++) {
+        int o = (wave + 4 * i) * 16 + j;
+        o = o < TH * TW ? o : TH * TW - 1;
+        const int oy = o / TW, ox = o - oy * TW;
+        baseb[i] = oy * PITCH_M + ox;
+    }
+    f32x4 accb[IB];
+#pragma unroll
+    for (int i = 0; i < IB; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) accb[i][r] = biasb[r];
+    {
+        // eight reads ahead, then one read after each MFMA
+        float bv[18][IB];
+#pragma unroll
+        for (int s = 0; s < 18; s++)
+#pragma unroll
+            for (int i = 0; i < IB; i++) bv[s][i] = lm[kofb[s] + baseb[i]];
+#pragma unroll
+        for (int s = 0; s < 18; s++)
+#pragma unroll
+            for (int i = 0; i < IB; i++)
+                accb[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb[s], bv[s][i], accb[i], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int q = 0; q < 18 * IB; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // ---- epilogue: activation, residual, store
+#pragma unroll
+    for (int i = 0; i < IB; i++) {
+        if (wave + 4 * i >= NBB) continue;  // uniform
+        const int o = (wave + 4 * i) * 16 + j;
+        const int oy = y0 + o / TW, ox = x0 + o % TW;
+        if (oy >= H || ox >= W) continue;
+        const int pix_ = oy * W + ox;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int oc = 4 * g + r;
+            float v = activate<ACT>(accb[i][r]);
+            if (a.res) v += rv[i][r];
+            a.y[oc * HW + pix_] = v;
+        }
+    }
+    // ---- the tile's own pixels of the intermediate (8 channels), from LDS
+    if (a.ya) {
+        constexpr int OWN = 8 * TH * TW;
+        for (int e = tid; e < OWN; e += 256) {
+            const int ch = e / (TH * TW), rem = e - ch * (TH * TW);
+            const int oy = rem / TW, ox = rem - oy * TW;
+            if (y0 + oy < H && x0 + ox < W)
+                a.ya[ch * HW + (y0 + oy) * W + x0 + ox] = lm[ch * PLANE_M + (oy + 1) * PITCH_M + ox + 1];
+        }
+    }
+}
+
+constexpr PairTile kPair8Tiles[] = {{4, 16}, {8, 16}, {2, 32}};
+static_assert(sizeof(kPair8Tiles) / sizeof(kPair8Tiles[0]) == kPairTileCount,
+              "a forced pair_tile indexes every pair family alike");
+
+template <int TH, int TW>
+static osh_status pair8_launch_t(PairArgs a, hipStream_t st) {
+    a.tiles_w = ceil_div(a.w, TW);
+    const unsigned tiles = (unsigned)(a.tiles_w * ceil_div(a.h, TH));
+    if (exact_silu())
+        hipLaunchKernelGGL((conv_pair8_kernel<TH, TW, ACT_SILU_EXACT>), dim3(tiles), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((conv_pair8_kernel<TH, TW, OSH_ACT_SILU>), dim3(tiles), dim3(256), 0, st, a);
+    OSH_LAUNCH_CHECK("conv_pair8_kernel");
+    return OSH_OK;
+}
+
+osh_status conv_pair8_launch(const PairArgs &a, hipStream_t st, int tile) {
+    switch (tile) {
+    case 0: return pair8_launch_t<4, 16>(a, st);
+    case 1: return pair8_launch_t<8, 16>(a, st);
+    default: return pair8_launch_t<2, 32>(a, st);
+    }
+}
 
 // ------------------------------------------------------ first-layer pair
 //

@@ -605,6 +605,10 @@ PAIR_CASES = [
     ("odd_map", (1, 32, 13, 11), 16, 32, True, {"winograd": 0}),
     ("deep_ragged", (1, 48, 7, 9), 64, 16, True, {"winograd": 0}),  # 3 input chunks, im2col second conv
     ("exact_silu", (1, 64, 20, 20), 32, 32, False, {"exact_silu": 1}),
+    # an 8-channel intermediate: im2col chain, then the first-layer chain
+    ("c3k2_160_eight", (1, 16, 160, 160), 8, 16, True, {}),
+    ("eight_ragged", (1, 16, 13, 37), 8, 16, False, {"winograd": 0}),
+    ("eight_exact_silu", (1, 16, 40, 24), 8, 16, True, {"winograd": 0, "exact_silu": 1}),
 ]
 
 
