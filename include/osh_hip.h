@@ -289,7 +289,9 @@ OSH_API osh_status osh_conv2d_group_f32(int count, const osh_conv_params *ps, co
  * is faster for the shapes.  Takes two kinds of pair of SiLU convs, batch 1,
  * in the chain orders the single-conv dispatch takes for them:
  *   - bottleneck pairs: 3x3 stride-1 pad-1 convs on one 1 x C x H x W map,
- *     C = 16 / 32 / 48 / 64, 16 / 32 / 64 output channels each;
+ *     C = 16 / 32 / 48 / 64, 16 / 32 / 64 output channels each, or
+ *     16 -> 8 -> 16 (an 8-channel intermediate: the im2col chain, then the
+ *     first-layer chain);
  *   - first-layer pairs: a 3x3 stride-1 or -2 conv over C <= 4 planes with
  *     16 outputs (the first_conv chain; a network's first layer, e.g.
  *     YOLO11n's 3 -> 16 stem, FirstConv.cs), then a 3x3 pad-1 conv of stride
