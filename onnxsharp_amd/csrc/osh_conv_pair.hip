@@ -831,9 +831,13 @@ __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
             lm[pos + r * G::PLANE_M] = __int_as_float(__float_as_int(activate<ACT>(acc[r])) & keep);
     };
     {
+        // one scheduling region per block: its chain, the next block's reads
+        // and the block before's stores, two LDS operations after each MFMA
+        // (left to itself the scheduler sinks each read to its MFMA)
         float bv[2][NS];
         f32x4 prev;
         read_blk(bv[0], 0);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < G::IA; i++) {
             if (i + 1 < G::IA) read_blk(bv[(i + 1) & 1], i + 1);
@@ -844,6 +848,12 @@ __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
             for (int s = 0; s < NS; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[s], bv[i & 1][s], acc, 0, 0, 0);
             if (i > 0) store_blk(prev, i - 1);  // blocks before the last exist for every wave
             prev = acc;
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100 | 0x200, 2, 0);  // then up to two LDS reads / writes
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (wave + 4 * (G::IA - 1) < G::NBA) store_blk(prev, G::IA - 1);  // uniform
     }
