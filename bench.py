@@ -311,8 +311,10 @@ class YoloWorkload(FrameWorkload):
         model = yolo11n.build(640)
         super().__init__(dev, "c4", model, synth.uniform(4000, (1, 3, 640, 640)), "yolo11n frame (HIP graph)")
         nconv = len(self.model.convs)
+        nlaunch = len(self.fr.model.ops)
         self.config = {"workload": "YOLO11n backbone+neck+head, batch 1, 640x640, FP32 NCHW, "
-                                   f"{nconv} conv launches + attention/SPPF/upsample/add glue in one HIP graph",
+                                   f"{nconv} convs + attention/SPPF/upsample glue as {nlaunch} launches "
+                                   "(grouped and paired convs, residual Adds fused) in one HIP graph",
                        "input": "U(0,1) [1,3,640,640], splitmix64 seed 4000",
                        "weights": "N(0,0.05) conv weights, N(0,0.01) biases (BatchNorm folded), seeds 7000+",
                        "conv_gflop": round(sum(o.flops for o in self.model.convs) / 1e9, 4),
