@@ -57,35 +57,83 @@ class ConvLayer:
             raise ValueError(f"Conv '{name}': activation {fused_activation!r} cannot be fused")
         self.name = name
         self.fused_activation = fused_activation
+        lists = [list(kernel_shape), list(strides), list(pads), list(dilations)]
+        for vals, cap in zip(lists, (2, 2, 4, 2)):
+            if len(vals) > cap:
+                raise N.OshUnsupported(N.OSH_E_UNSUPPORTED, f"Conv '{name}': only 1-D and 2-D convolution are implemented")
+        self.attrs = self._make_attrs(group, auto_pad, *lists)
+        # A rank-3 input (ConvLayer.Forward1D, src/OnnxSharp/Ops/DnnOps.cs:235-300,
+        # 422-428) runs as the 2-D conv of [N, C, 1, L] by [M, C/g, 1, K]: the
+        # 1-D attributes on the width axis, kernel 1, stride 1, no pads and
+        # dilation 1 on the height axis (auto_pad then pads only the width).
+        one = lambda v, lead: (lead + v) if len(v) == 1 else v
+        pads1 = [0, pads[0], 0, pads[1]] if len(pads) == 2 else list(pads)
+        self.attrs1d = self._make_attrs(group, auto_pad, one(list(kernel_shape), [1]), one(list(strides), [1]), pads1,
+                                        one(list(dilations), [1]))
+        # 1-D attribute lists: the [N, C, 1, L] view of a rank-3 input takes
+        # the width-axis form too (with no attributes both forms agree)
+        self._attrs_1d = (any(len(v) == 1 for v in (lists[0], lists[1], lists[3])) or len(lists[2]) == 2)
+        self._lists, self._auto_pad = lists, auto_pad
+        self._packed = None  # (key, params, buffer)
+
+    @staticmethod
+    def _make_attrs(group, auto_pad, kernel_shape, strides, pads, dilations) -> N.ConvAttrs:
         a = N.ConvAttrs()
         a.group = int(group)
         a.auto_pad = N.AUTO_PAD[auto_pad]
-        for field, count, vals, cap in (("kernel_shape", "n_kernel_shape", kernel_shape, 2),
-                                        ("strides", "n_strides", strides, 2), ("pads", "n_pads", pads, 4),
-                                        ("dilations", "n_dilations", dilations, 2)):
-            vals = list(vals)
-            if len(vals) > cap:
-                raise N.OshUnsupported(N.OSH_E_UNSUPPORTED, f"Conv '{name}': only 2-D convolution is implemented")
+        for field, count, vals in (("kernel_shape", "n_kernel_shape", kernel_shape), ("strides", "n_strides", strides),
+                                   ("pads", "n_pads", pads), ("dilations", "n_dilations", dilations)):
             setattr(a, count, len(vals))
             arr = getattr(a, field)
             for i, v in enumerate(vals):
                 arr[i] = int(v)
-        self.attrs = a
-        self._packed = None  # (key, params, buffer)
+        return a
+
+    def _shapes2d(self, x_shape: Sequence[int], w_shape: Sequence[int]):
+        """(attrs, x shape, w shape) of the 2-D conv that computes this one."""
+        if len(x_shape) == 3 and len(w_shape) == 3:
+            return self.attrs1d, (x_shape[0], x_shape[1], 1, x_shape[2]), (w_shape[0], w_shape[1], 1, w_shape[2])
+        return (self.attrs1d if self._attrs_1d else self.attrs), tuple(x_shape), tuple(w_shape)
 
     # -- shape logic (C++ side of the library)
+    def _length1d(self, length: int, weight_kernel: int) -> Optional[int]:
+        """Output length of a rank-3 conv with explicit pads (Conv1DShape /
+        Resolve1D, DnnOps.cs:204-227: pads [begin, end], the end pad read when
+        given), or None where the width axis of the 2-D form gives it already
+        (auto_pad, or equal pads: the 2-D shape takes the begin pad twice)."""
+        k, st, pads, dl = self._lists
+        if self._auto_pad != "NOTSET" or len(pads) != 2 or pads[0] == pads[1]:
+            return None
+        kernel = k[0] if k else weight_kernel
+        stride = st[0] if st else 1
+        dilation = dl[0] if dl else 1
+        out = (length + pads[0] + pads[1] - ((kernel - 1) * dilation + 1)) // stride + 1
+        if out <= 0:
+            raise N.OshError(N.OSH_E_INVALID, f"Conv '{self.name}': output length {out}")
+        return out
+
     def get_memory_shapes(self, x_shape: Sequence[int], w_shape: Sequence[int]) -> tuple:
-        if len(x_shape) != 4 or len(w_shape) != 4:
+        if len(x_shape) != len(w_shape) or len(x_shape) not in (3, 4):
             raise N.OshUnsupported(N.OSH_E_UNSUPPORTED,
-                                   f"Conv '{self.name}': only 2D convolution (NCHW) is implemented")
+                                   f"Conv '{self.name}': only 1-D (NCL) and 2-D (NCHW) convolution are implemented")
+        attrs, xs, ws = self._shapes2d(x_shape, w_shape)
         y = N.dims64([0, 0, 0, 0])
-        N.call("osh_conv_infer_shape", C.byref(self.attrs), N.dims64(x_shape), N.dims64(w_shape), y)
-        return tuple(int(v) for v in y)
+        N.call("osh_conv_infer_shape", C.byref(attrs), N.dims64(xs), N.dims64(ws), y)
+        y = tuple(int(v) for v in y)
+        if len(x_shape) == 3:
+            n1 = self._length1d(x_shape[2], w_shape[2])
+            return (y[0], y[1], y[3] if n1 is None else n1)
+        return y
 
     def resolve(self, x_shape: Sequence[int], w_shape: Sequence[int]) -> N.ConvParams:
+        """The launch parameters (for a rank-3 conv: of its 2-D form, h = 1)."""
         self.get_memory_shapes(x_shape, w_shape)
+        attrs, xs, ws = self._shapes2d(x_shape, w_shape)
         p = N.ConvParams()
-        N.call("osh_conv_resolve", C.byref(self.attrs), N.dims64(x_shape), N.dims64(w_shape), C.byref(p))
+        N.call("osh_conv_resolve", C.byref(attrs), N.dims64(xs), N.dims64(ws), C.byref(p))
+        n1 = self._length1d(xs[3], ws[3]) if self._attrs_1d else None
+        if n1 is not None:  # every kernel reads the begin pad and bounds-checks the input
+            p.ow, p.pr = n1, self._lists[2][1]
         return p
 
     # -- one-time weight packing (PrepackWeights)
@@ -117,8 +165,13 @@ class ConvLayer:
     def forward(self, x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """y = act(conv(x) + bias), plus `residual` (the shortcut operand of a
-        following Add, same shape as y) when given: one launch for both."""
+        following Add, same shape as y) when given: one launch for both.  A
+        rank-3 x ([N, C, L], weights [M, C/g, K]) gives a rank-3 y."""
         x = _need_f32("input", x)
+        if x.dim() == 3:
+            out4 = None if out is None else out.unsqueeze(2)
+            res4 = None if residual is None else residual.unsqueeze(2)
+            return self.forward(x.unsqueeze(2), w.unsqueeze(2) if w.dim() == 3 else w, bias, out4, res4).squeeze(2)
         key = (w.data_ptr(), tuple(w.shape), tuple(x.shape), w._version)
         if self._packed is None or self._packed[0] != key:
             self.prepack_weights(tuple(x.shape), w)

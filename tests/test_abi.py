@@ -88,9 +88,11 @@ def test_conv_shape_errors(attrs, x, w, msg):
         ConvLayer(**attrs).get_memory_shapes(x, w)
 
 
-def test_conv_rejects_non_2d():
+def test_conv_rejects_3d():
+    # 1-D (rank-3) and 2-D convs are taken (the rank-3 shapes are pinned by
+    # test_conv1d_shapes_follow_conv1dshape); volumetric ones are refused
     with pytest.raises(N.OshUnsupported):
-        ConvLayer().get_memory_shapes((1, 8, 5), (8, 8, 3))
+        ConvLayer().get_memory_shapes((1, 8, 5, 5, 5), (8, 8, 3, 3, 3))
     with pytest.raises(N.OshUnsupported):
         ConvLayer(strides=[1, 1, 1])
 
@@ -228,3 +230,19 @@ def test_ctypes_structs_match_the_c_header(tmp_path):
         assert int(got[cname]) == C.sizeof(py), cname
         for f, _ in py._fields_:
             assert int(got[f"{cname}.{f}"]) == getattr(py, f).offset, f"{cname}.{f}"
+
+
+def test_conv1d_shapes_follow_conv1dshape():
+    # ConvLayer.Conv1DShape / Resolve1D (src/OnnxSharp/Ops/DnnOps.cs:204-227):
+    # pads [begin, end], the end pad read when given; auto_pad on the one axis
+    from onnxsharp_amd.layers import ConvLayer
+    assert ConvLayer(pads=[1, 1]).get_memory_shapes((2, 16, 100), (32, 16, 3)) == (2, 32, 100)
+    # (77 + 4 + 2 - 9) // 2 + 1 = 38 (the 2-D rule, begin pad twice, would give 39)
+    layer = ConvLayer(strides=[2], pads=[4, 2], dilations=[2])
+    assert layer.get_memory_shapes((1, 8, 77), (12, 8, 5)) == (1, 12, 38)
+    p = layer.resolve((1, 8, 77), (12, 8, 5))
+    assert (p.h, p.w, p.kh, p.kw, p.sh, p.sw, p.dh, p.dw, p.pt, p.pl, p.oh, p.ow) == (1, 77, 1, 5, 1, 2, 1, 2, 0, 4, 1, 38)
+    assert ConvLayer(auto_pad="SAME_UPPER", strides=[3]).get_memory_shapes((1, 6, 33), (5, 6, 4)) == (1, 5, 11)
+    assert ConvLayer(group=4).get_memory_shapes((1, 16, 50), (16, 4, 3)) == (1, 16, 48)
+    with pytest.raises(Exception):
+        ConvLayer().get_memory_shapes((1, 16, 50), (16, 4, 3, 3))  # ranks differ

@@ -787,3 +787,63 @@ def test_conv_pair_refusals(cuda):
     with pytest.raises(N.OshError, match="overlaps"):
         N.call("osh_conv2d_pair_f32", C.byref(pa), C.byref(pb), sl(0), C.c_void_p(bufa.data_ptr()), None,
                C.c_void_p(bufb.data_ptr()), None, N.ACT_SILU, None, None, sl(16), st)
+
+
+# (name, x shape [N, C, L], w shape [M, C/g, K], attrs, act)
+CONV1D_CASES = [
+    ("k3_pad1_batch2", (2, 16, 100), (32, 16, 3), dict(pads=[1, 1]), "Silu"),
+    ("k5_s2_dil2_uneven_pads", (1, 8, 77), (12, 8, 5), dict(strides=[2], pads=[4, 2], dilations=[2]), None),
+    ("grouped_k3", (1, 16, 50), (16, 4, 3), dict(group=4, pads=[1, 1]), "Relu"),
+    ("same_upper_k4_s3", (1, 6, 33), (5, 6, 4), dict(auto_pad="SAME_UPPER", strides=[3]), None),
+    ("k1_residual", (1, 32, 40), (64, 32, 1), dict(), "Silu"),
+]
+
+
+def _conv1d_ref(x, w, b, stride, dilation, pad_begin, out_len, group):
+    """Forward1D (src/OnnxSharp/Ops/DnnOps.cs:235-300) in float64: output t of
+    channel m sums w[m][j][k] * x[j][t*stride - pad_begin + k*dilation] over
+    the group's channels j and taps k, positions outside the input skipped."""
+    n, c, length = x.shape
+    m, cpg, kernel = w.shape
+    opg = m // group
+    y = np.zeros((n, m, out_len))
+    for mm in range(m):
+        base = mm // opg * cpg
+        for k in range(kernel):
+            pos = np.arange(out_len) * stride - pad_begin + k * dilation
+            ok = (pos >= 0) & (pos < length)
+            y[:, mm, ok] += np.einsum("j,njt->nt", w[mm, :, k].astype(np.float64),
+                                      x[:, base:base + cpg, pos[ok]].astype(np.float64))
+    return y + (0 if b is None else b.astype(np.float64)[None, :, None])
+
+
+@pytest.mark.parametrize("name,xs,ws,attrs,act", CONV1D_CASES, ids=[c[0] for c in CONV1D_CASES])
+def test_conv1d_rank3_within_fp32_bar(cuda, oracle, name, xs, ws, attrs, act):
+    # A rank-3 Conv runs as the 2-D conv of [N, C, 1, L] (its im2col chain:
+    # channel -> tap); the reference's Forward1D sums the same terms (channel
+    # -> tap with a multiply and an add each, or per tap with FMAs on its
+    # stride-1 AVX path), so the bar is the FP32 tolerance against the float64
+    # sum, and the output length is Conv1DShape's (the end pad counts).
+    import torch
+    from onnxsharp_amd.layers import ConvLayer
+    print(f"conv1d {name} x={xs} w={ws} {attrs} act={act}", flush=True)
+    seed = sum(xs) * 3 + sum(ws)
+    x = synth.uniform(seed, xs)
+    w = synth.normal(seed + 1, ws, 0, 0.1)
+    b = synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    layer = ConvLayer(fused_activation=act, **attrs)
+    ys = layer.get_memory_shapes(xs, ws)
+    p = layer.resolve(xs, ws)
+    r = synth.normal(seed + 3, ys, 0, 1) if "residual" in name else None
+    y = layer.forward(_t(x, cuda), _t(w, cuda), _t(b, cuda), residual=None if r is None else _t(r, cuda))
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert y.shape == ys
+    ref = _conv1d_ref(x, w, b, p.sw, p.dw, p.pl, ys[2], attrs.get("group", 1))
+    if act == "Silu":
+        ref = ref / (1 + np.exp(-ref))
+    elif act == "Relu":
+        ref = np.maximum(ref, 0)
+    if r is not None:
+        ref = ref + r
+    assert_fp32_close(y, ref, name)
