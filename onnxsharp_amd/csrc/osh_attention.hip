@@ -195,28 +195,38 @@ __global__ __launch_bounds__(256) void attention_kernel(int kd, int hd, int n, f
         // compiler from moving those reads above these writes
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     };
+    // a whole chunk's operands, read one chunk ahead (right after that chunk
+    // is staged) so that the chain of the chunk before hides their latency
+    float a[2][ATT_VC / 4], b[2][ATT_VC / 4];
+    auto read_chunk = [&](int c) {
+        const float *va = vbuf + (c & 1) * 16 * ATT_VP + jl * ATT_VP + g;  // lane: v[16 cb + jl][64 c + 4 t + g]
+        const float *pb = pr + c * ATT_VC;
+#pragma unroll
+        for (int w = 0; w < ATT_VC / 4; w++) {
+            a[c & 1][w] = va[4 * w];
+            b[c & 1][w] = pb[4 * w];
+        }
+    };
     for (int cb = wave; cb < ncb; cb += 4) {
         if (cb != wave) load_v(cb);
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         stage(0);
+        if (n >= ATT_VC) read_chunk(0);
 #pragma unroll
         for (int c = 0; c < ATT_MAX_CH; c++) {
             if (c >= nch) break;
-            if (c + 1 < nch) stage(c + 1);  // the other buffer, read by the chunk before
+            if (c + 1 < nch) {
+                stage(c + 1);  // the other buffer, read by the chunk before
+                if (n - (c + 1) * ATT_VC >= ATT_VC) read_chunk(c + 1);
+            }
             const float *va = vbuf + (c & 1) * 16 * ATT_VP + jl * ATT_VP + g;  // lane: v[16 cb + jl][64 c + 4 t + g]
             const float *pb = pr + c * ATT_VC;
             const int steps = min(ATT_VC, n - c * ATT_VC) / 4;  // a multiple of 4 (n % 16 == 0)
-            if (steps == ATT_VC / 4) {  // a whole chunk: every operand read before the chain starts
-                float a[ATT_VC / 4], b[ATT_VC / 4];
-#pragma unroll
-                for (int w = 0; w < ATT_VC / 4; w++) {
-                    a[w] = va[4 * w];
-                    b[w] = pb[4 * w];
-                }
-                __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the chain
+            if (steps == ATT_VC / 4) {  // a whole chunk: its operands were read a chunk ahead
+                __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's reads ahead of this chain
 #pragma unroll
                 for (int w = 0; w < ATT_VC / 4; w++)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[w], b[w] * inv, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c & 1][w], b[c & 1][w] * inv, acc, 0, 0, 0);
             } else {
                 for (int t = 0; t < steps; t += 4)
 #pragma unroll
