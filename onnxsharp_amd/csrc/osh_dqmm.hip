@@ -645,6 +645,34 @@ __global__ __launch_bounds__(64 * DQF_WAVES) void dqmm_fused_kernel(
     const unsigned alpha = (unsigned)(128 - zp);
     const unsigned colterm = alpha * (unsigned)csum + (unsigned)k * alpha * offj;
     const float comb = scale * ws;  // CombinedScale, QuantizedMatMulOps.cs:203-221
+    if constexpr (FULL) {
+        // Float output only, 16-byte aligned: the wave's 32 x 32 tile goes
+        // through its own 4 KB of lds_a (every wave's A reads ended before
+        // the barrier above) so that each lane stores four 16-byte vectors
+        // -- eight lanes a 128-byte row -- instead of 16 single words.  The
+        // values are the ones the loop below computes.
+        if (out && !acc_out && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {  // uniform
+            float *tl = reinterpret_cast<float *>(lds_a) + wt * 1024;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int il = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                const int v = (int)((unsigned)acc[q] + offj * (unsigned)lds_rs[il] + colterm);
+                float o = __builtin_fmaf((float)v, comb, bj);
+                if (lds_rn[il]) o = __builtin_nanf("");
+                tl[il * 32 + (lane & 31)] = o;
+            }
+            // the lanes of this wave read what the others wrote (LDS accesses
+            // of a wave are in order; this keeps the compiler from moving them)
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+            for (int pass = 0; pass < 4; pass++) {
+                const int rr = pass * 8 + (lane >> 3), c4 = (lane & 7) * 4;
+                const float4 v4 = *reinterpret_cast<const float4 *>(tl + rr * 32 + c4);
+                *reinterpret_cast<float4 *>(out + (long long)(mt * 32 + rr) * n + nt * 32 + c4) = v4;
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int q = 0; q < 16; q++) {
         const int il = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
