@@ -367,13 +367,11 @@ class CopyWorkload(Workload):
 
 def make_workload(name, dev):
     if name == "c2":
-        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "conv16s_kernel (tuned tile)", 1)
+        return ConvWorkload(dev, "c2", (1, 64, 160, 160), (64, 64, 3, 3), 1, "Silu", "", 1)
     if name == "c3a":
-        return ConvWorkload(dev, "c3a", (1, 256, 80, 80), (128, 256, 1, 1), 1, "Silu", "conv16s_kernel (tuned 1x1 tile)",
-                            11)
+        return ConvWorkload(dev, "c3a", (1, 256, 80, 80), (128, 256, 1, 1), 1, "Silu", "", 11)
     if name == "c3b":
-        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "conv16s_kernel (tuned tile)",
-                            21)
+        return ConvWorkload(dev, "c3b", (1, 128, 80, 80), (256, 128, 3, 3), 2, "Silu", "", 21)
     if name == "c1":
         return GemmWorkload(dev)
     if name == "c5":
@@ -387,14 +385,16 @@ def make_workload(name, dev):
     raise SystemExit(f"unknown --config {name}")
 
 
-def time_gpu(wl, steps, warmup, graph=True):
+def time_gpu(wl, steps, warmup, graph=True, marks=False):
     """(device ms over exactly `steps` back-to-back steps, host wall s, eager
     device ms or None).  Single-launch workloads (wl.graphable) are timed as
     one HIP graph holding the `steps` launches, recorded after the warm-up
     (which also runs the first-use tile tuning), so the figure is the device's
     and not the Python launch loop's; the same steps issued one by one are
     timed too and reported beside it.  Frame workloads replay their own graph
-    per step."""
+    per step.  With `marks`, a 1-byte fill kernel runs just before and just
+    after each timed region (outside its events), so that a kernel trace of
+    the run can tell the timed dispatches from the warm-up's."""
     import torch
     from onnxsharp_amd import native as N
     sp = getattr(wl, "stream", None)
@@ -415,13 +415,20 @@ def time_gpu(wl, steps, warmup, graph=True):
     e0, e1 = C.c_void_p(), C.c_void_p()
     N.call("osh_event_create", C.byref(e0))
     N.call("osh_event_create", C.byref(e1))
+    mark_buf = torch.empty(64, dtype=torch.uint8, device="cuda") if marks else None
+
+    def mark():
+        if mark_buf is not None:
+            N.call("osh_memset_d8", C.c_void_p(mark_buf.data_ptr()), 0, 1, sp)
 
     def timed(run):
         N.call("osh_stream_sync", sp)
+        mark()
         t0 = time.perf_counter()
         N.call("osh_event_record", e0, sp)
         run()
         N.call("osh_event_record", e1, sp)
+        mark()
         N.call("osh_stream_sync", sp)
         wall = time.perf_counter() - t0
         ms = C.c_float()
@@ -512,9 +519,25 @@ def read_traffic(name):
         return None
 
 
+def step_kernels(wl):
+    """Names of the kernels one step launches, after the warm-up's first-use
+    tuning has fixed every tile (one extra step issued from the host)."""
+    import torch
+    from onnxsharp_amd import native as N
+    torch.cuda.synchronize()
+    N.kernel_log(reset=True)
+    if hasattr(wl, "fr"):
+        wl.fr.run()
+        wl.fr.sync()
+    else:
+        wl.step(C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return N.kernel_log(reset=True)
+
+
 def measure(wl, args):
     """GPU figures of one workload: step time, rate and roofline."""
-    ms, wall, eager_ms = time_gpu(wl, args.steps, args.warmup, graph=not args.eager)
+    ms, wall, eager_ms = time_gpu(wl, args.steps, args.warmup, graph=not args.eager, marks=args.trace_marks)
     ms_step = ms / args.steps
     rate = wl.flops / (ms_step * 1e-3) / 1e12
     if wl.bound == "hbm":
@@ -525,7 +548,16 @@ def measure(wl, args):
         roof = {"bound": "mfma", "achieved": round(rate, 3), "peak": PEAK["fp32_mfma_tflops"], "unit": "TFLOP/s",
                 "frac": round(rate / PEAK["fp32_mfma_tflops"], 4)}
     roof["traffic"] = read_traffic(wl.name)
-    roof["kernel"] = wl.kernel
+    names = step_kernels(wl)
+    if hasattr(wl, "fr"):
+        from collections import Counter
+        roof["kernel"] = wl.kernel
+        roof["kernels_per_step"] = dict(Counter(names).most_common())
+    else:
+        # the dominant kernel: the only one, or the one the workload names
+        main = [n for n in names if n.startswith(wl.kernel)] or names
+        roof["kernel"] = main[0] if main else wl.kernel
+        roof["kernels_per_step"] = names
     roof["algorithmic_per_launch"] = {"flops": wl.flops, "bytes": wl.bytes}
     out = {"value": round(rate, 3), "unit": "TOP/s" if wl.dtype == "int8" else "TFLOP/s",
            "ms_per_step": round(ms_step, 5), "dtype": wl.dtype, "config": wl.config, "roofline": roof,
@@ -547,6 +579,66 @@ def measure(wl, args):
     return out
 
 
+def launch_table(wl, reps=7, replays=40):
+    """Each launch's share of a frame graph's replay time.  Graphs of the
+    frame's first j launches (j = 1 .. L, the serial order the frame graph
+    records) are replayed `replays` times, `reps` times over; t(j) is the
+    median time per replay, and launch j's share is t(j) - t(j-1), so the
+    shares add up to t(L), the whole frame.  Each share is the time the
+    launch adds where it stands in the frame (its gap to the previous kernel
+    included), measured with HIP events and no tracer."""
+    import torch
+    from onnxsharp_amd import native as N
+    fr = wl.fr
+    ops, calls = fr.model.ops, fr._calls
+    st = fr.stream
+    names = []
+    for c in calls:  # the kernels each launch runs (tiles already tuned)
+        N.kernel_log(reset=True)
+        c(st)
+        N.call("osh_stream_sync", st)
+        names.append(N.kernel_log(reset=True))
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    N.call("osh_event_create", C.byref(e0))
+    N.call("osh_event_create", C.byref(e1))
+    t = [0.0]
+    for j in range(1, len(calls) + 1):
+        g = C.c_void_p()
+        N.call("osh_graph_begin", st)
+        try:
+            for c in calls[:j]:
+                c(st)
+        finally:
+            N.call("osh_graph_end", st, C.byref(g))
+        for _ in range(5):
+            N.call("osh_graph_launch", g, st)
+        samples = []
+        for _ in range(reps):
+            N.call("osh_stream_sync", st)
+            N.call("osh_event_record", e0, st)
+            for _ in range(replays):
+                N.call("osh_graph_launch", g, st)
+            N.call("osh_event_record", e1, st)
+            N.call("osh_stream_sync", st)
+            ms = C.c_float()
+            N.call("osh_event_elapsed_ms", e0, e1, C.byref(ms))
+            samples.append(ms.value * 1e3 / replays)
+        N.call("osh_graph_destroy", g)
+        t.append(float(np.median(samples)))
+    N.call("osh_event_destroy", e0)
+    N.call("osh_event_destroy", e1)
+    rows = []
+    for j, op in enumerate(ops):
+        share = t[j + 1] - t[j]
+        fl = float(getattr(op, "flops", 0.0) or 0.0)
+        rows.append({"launch": j, "op": op.name, "kind": type(op).__name__, "kernels": names[j],
+                     "us": round(share, 3), "gflop": round(fl / 1e9, 4),
+                     "tflops": round(fl / (share * 1e-6) / 1e12, 2) if share > 0 and fl else None})
+    return {"frame_us": round(t[-1], 3), "launches": len(ops), "sum_us": round(sum(r["us"] for r in rows), 3),
+            "method": f"graphs of the first j launches, median of {reps} x {replays} replays each; "
+                      "share(j) = t(j) - t(j-1)", "rows": rows}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -562,6 +654,11 @@ def main():
                     help="c3c/c4: skip the extra timing with PCIe copies")
     ap.add_argument("--eager", action="store_true",
                     help="time the steps issued one by one (default: one HIP graph of the K launches)")
+    ap.add_argument("--trace-marks", action="store_true",
+                    help="run a 1-byte fill kernel just before and after each timed region, so that a "
+                         "kernel trace can pick out the timed dispatches")
+    ap.add_argument("--launch-table", action="store_true",
+                    help="c3c/c4: print each launch's share of the frame graph's time (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU (every box here has one MI355X); "
@@ -584,6 +681,18 @@ def main():
         gbs = wl.bytes / (ms_step * 1e-3) / 1e9
         print(json.dumps({"metric": "device copy GB/s", "value": round(gbs, 1), "unit": "GB/s",
                           "ms_per_step": round(ms_step, 5), "bytes_per_step": wl.bytes}), flush=True)
+        return
+
+    if args.launch_table:
+        if args.config not in ("c3c", "c4"):
+            raise SystemExit("--launch-table needs --config c3c or c4")
+        wl = make_workload(args.config, dev)
+        time_gpu(wl, args.steps, args.warmup)
+        tab = launch_table(wl)
+        tab.update({"config": args.config, "workload": wl.config.get("workload"),
+                    "device": info.name.decode()})
+        print(json.dumps(tab), flush=True)
+        wl.fr.close()
         return
 
     names = CONFIGS if args.config == "all" else (args.config,)

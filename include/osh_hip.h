@@ -71,6 +71,17 @@ OSH_API osh_status osh_init(int dev, osh_device_info *info);
 OSH_API osh_status osh_device_count(int *count);
 OSH_API osh_status osh_device_synchronize(void);
 
+/* Launch log: the kernels the calling thread launched since the last reset,
+ * one "name<template arguments>" per line in launch order (the names
+ * rocprofv3 prints), so a caller can tell which kernel and tile each call ran
+ * after first-use tuning.  *count (may be NULL) receives the number of
+ * launches; buf (may be NULL) receives the names, NUL-terminated
+ * (OSH_E_INVALID if `bytes` is too small); reset != 0 clears the log
+ * afterwards.  Launches recorded into a graph are logged when recorded, not
+ * when replayed.  The per-op kernel names of the reference's profiler
+ * (Net.ProfileAll, src/OnnxSharp/Core/Net.cs:282-332) are its counterpart. */
+OSH_API osh_status osh_kernel_log(int reset, char *buf, size_t bytes, int *count);
+
 /* Backend options (the reference reads its kernel switches from ONNXSHARP_*
  * environment variables, e.g. src/OnnxSharp/Kernels/NchwcConv.cs:39-40).
  *   "exact_silu": 0 (default) = fused SiLU epilogues use exp2/rcp (relative

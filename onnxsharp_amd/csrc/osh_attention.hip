@@ -270,9 +270,16 @@ OSH_API osh_status osh_attention_f32(int heads, int key_dim, int head_dim, int n
     }
     dim3 grid((unsigned)(n / ATT_ROWS), (unsigned)heads);
     const int ks = key_dim / 4;
-    auto kernel = ks <= 4 ? attention_kernel<4> : ks <= 8 ? attention_kernel<8> : attention_kernel<16>;
-    hipLaunchKernelGGL(kernel, grid, dim3(256), lds, to_stream(s), key_dim, head_dim, n, scale, d_qkv,
-                       (long long)head_stride, d_y);
+#define OSH_ATT_LAUNCH(KS) \
+    OSH_LAUNCH(attention_kernel<KS>, grid, dim3(256), lds, to_stream(s), key_dim, head_dim, n, scale, d_qkv, \
+               (long long)head_stride, d_y)
+    if (ks <= 4)
+        OSH_ATT_LAUNCH(4);
+    else if (ks <= 8)
+        OSH_ATT_LAUNCH(8);
+    else
+        OSH_ATT_LAUNCH(16);
+#undef OSH_ATT_LAUNCH
     OSH_LAUNCH_CHECK("attention_kernel");
     return OSH_OK;
 }

@@ -35,6 +35,20 @@ void clear_error();
 
 inline hipStream_t to_stream(osh_stream s) { return reinterpret_cast<hipStream_t>(s); }
 
+// ------------------------------------------------------------- launch log
+
+// Notes one kernel launch of the calling thread (the kernel's host-side
+// handle); osh_kernel_log names them, so a caller can tell which kernel and
+// tile each call ran after first-use tuning.
+void note_launch(const void *kernel);
+
+// Every kernel launch of the library goes through this macro.
+#define OSH_LAUNCH(K, ...)                                                                          \
+    do {                                                                                            \
+        ::osh::note_launch(reinterpret_cast<const void *>(&(K)));                                   \
+        hipLaunchKernelGGL(K, __VA_ARGS__);                                                         \
+    } while (0)
+
 // ------------------------------------------------------------- MFMA types
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));

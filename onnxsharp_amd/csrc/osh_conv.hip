@@ -830,18 +830,18 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         if (dw3_eligible(p)) {
             if (p->sh == 1) {
                 OSH_DISPATCH_ACT(act, ACT,
-                                 hipLaunchKernelGGL((dw3_conv_kernel<ACT, 1>), grid, dim3(256), 0, stream, *p, d_x, w,
+                                 OSH_LAUNCH((dw3_conv_kernel<ACT, 1>), grid, dim3(256), 0, stream, *p, d_x, w,
                                                     d_bias, d_res, d_y));
             } else {
                 OSH_DISPATCH_ACT(act, ACT,
-                                 hipLaunchKernelGGL((dw3_conv_kernel<ACT, 2>), grid, dim3(256), 0, stream, *p, d_x, w,
+                                 OSH_LAUNCH((dw3_conv_kernel<ACT, 2>), grid, dim3(256), 0, stream, *p, d_x, w,
                                                     d_bias, d_res, d_y));
             }
             OSH_LAUNCH_CHECK("dw3_conv_kernel");
             return OSH_OK;
         }
         OSH_DISPATCH_ACT(act, ACT,
-                         hipLaunchKernelGGL(dw_conv_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, w, d_bias, d_res,
+                         OSH_LAUNCH(dw_conv_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, w, d_bias, d_res,
                                             d_y));
         OSH_LAUNCH_CHECK("dw_conv_kernel");
         return OSH_OK;
@@ -856,7 +856,7 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         while (og > 4 && blocks * (p->m / og) < device_cus()) og /= 2;
         dim3 grid((unsigned)blocks, (unsigned)(p->m / og));
 #define OSH_FIRST(MM, CC)                                                                                      \
-    OSH_DISPATCH_ACT(act, ACT, hipLaunchKernelGGL((first_conv_kernel<MM, CC, ACT>), grid, dim3(256), 0, stream, \
+    OSH_DISPATCH_ACT(act, ACT, OSH_LAUNCH((first_conv_kernel<MM, CC, ACT>), grid, dim3(256), 0, stream, \
                                                   *p, d_x, w, d_bias, d_res, d_y))
 #define OSH_FIRST_C(MM)            \
     do {                           \
@@ -903,7 +903,7 @@ static osh_status conv2d(const osh_conv_params *p, const float *d_x, const void 
         if (grid.y > 65535) return fail(OSH_E_UNSUPPORTED, "Conv: Winograd grid too large");
         const float4 *u = reinterpret_cast<const float4 *>(d_wpacked);
         OSH_DISPATCH_ACT(act, ACT,
-                         hipLaunchKernelGGL(wino_f23_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, u, d_bias,
+                         OSH_LAUNCH(wino_f23_kernel<ACT>, grid, dim3(256), 0, stream, *p, d_x, u, d_bias,
                                             d_res, d_y));
         OSH_LAUNCH_CHECK("wino_f23_kernel");
         return OSH_OK;
@@ -988,15 +988,15 @@ static osh_status conv2d_group(int count, const osh_conv_params *ps, const float
             if (!dw3_eligible(&ps[i]) || ps[i].sh != s3) s3 = 0;
         if (s3 == 1) {
             OSH_DISPATCH_ACT(act, ACT,
-                             hipLaunchKernelGGL((dw_conv_group_kernel<ACT, 1>), dim3((unsigned)total), dim3(256), 0, st,
+                             OSH_LAUNCH((dw_conv_group_kernel<ACT, 1>), dim3((unsigned)total), dim3(256), 0, st,
                                                 g));
         } else if (s3 == 2) {
             OSH_DISPATCH_ACT(act, ACT,
-                             hipLaunchKernelGGL((dw_conv_group_kernel<ACT, 2>), dim3((unsigned)total), dim3(256), 0, st,
+                             OSH_LAUNCH((dw_conv_group_kernel<ACT, 2>), dim3((unsigned)total), dim3(256), 0, st,
                                                 g));
         } else {
             OSH_DISPATCH_ACT(act, ACT,
-                             hipLaunchKernelGGL((dw_conv_group_kernel<ACT, 0>), dim3((unsigned)total), dim3(256), 0, st,
+                             OSH_LAUNCH((dw_conv_group_kernel<ACT, 0>), dim3((unsigned)total), dim3(256), 0, st,
                                                 g));
         }
         OSH_LAUNCH_CHECK("dw_conv_group_kernel");

@@ -477,7 +477,7 @@ inline size_t conv16_packed_bytes(const osh_conv_params *p) {
 inline osh_status conv16_pack(const osh_conv_params *p, const float *w, void *out, hipStream_t st,
                               bool i2c = false) {
     const long long total = (long long)conv16_packed_bytes(p) / 4;
-    hipLaunchKernelGGL(conv16_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p->m, p->c,
+    OSH_LAUNCH(conv16_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p->m, p->c,
                        p->kh * p->kw, w, static_cast<float *>(out), i2c && p->kh * p->kw == 9 ? 1 : 0);
     OSH_LAUNCH_CHECK("conv16_pack_kernel");
     return OSH_OK;
@@ -495,7 +495,7 @@ inline osh_status conv16_launch_t(const osh_conv_params *p, const float *x, cons
     const int mtiles = ceil_div(ceil_div(p->m, 16), TM);
     dim3 grid((unsigned)ceil_div(tiles_p, WPB), (unsigned)mtiles, (unsigned)p->n);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16_kernel<TM, BV, ACT, WPB, I2C>), grid, dim3(64 * WPB), 0, st, *p, x, w,
+                     OSH_LAUNCH((conv16_kernel<TM, BV, ACT, WPB, I2C>), grid, dim3(64 * WPB), 0, st, *p, x, w,
                                         bias, res, y, tiles_p));
     OSH_LAUNCH_CHECK("conv16_kernel");
     return OSH_OK;
@@ -513,7 +513,7 @@ inline osh_status conv16l_launch_t(const osh_conv_params *p, const float *x, con
     per = per > ceil_div(tiles_p, 4) ? ceil_div(tiles_p, 4) : per;
     dim3 grid((unsigned)per, (unsigned)mtiles, 1);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16l_kernel<TM, BV, ACT>), grid, dim3(256), 0, st, *p, x, w, bias, res,
+                     OSH_LAUNCH((conv16l_kernel<TM, BV, ACT>), grid, dim3(256), 0, st, *p, x, w, bias, res,
                                         y, tiles_p));
     OSH_LAUNCH_CHECK("conv16l_kernel");
     return OSH_OK;

@@ -414,7 +414,7 @@ inline osh_status conv16s_group_launch_t(ConvGroup g, int act, hipStream_t st, b
     if (total > 0x7fffffffLL) return fail(OSH_E_UNSUPPORTED, "Conv group: grid too large");
     g.start[g.count] = (int)total;
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16s_group_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT>),
+                     OSH_LAUNCH((conv16s_group_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT>),
                                         dim3((unsigned)total), dim3(256), exclusive ? kConvGroupExclusiveLds : 0,
                                         st, g));
     OSH_LAUNCH_CHECK("conv16s_group_kernel");
@@ -454,7 +454,7 @@ inline osh_status conv16_group_launch_t(ConvGroup g, int act, hipStream_t st) {
     if (total > 0x7fffffffLL) return fail(OSH_E_UNSUPPORTED, "Conv group: grid too large");
     g.start[g.count] = (int)total;
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16_group_kernel<TM, BV, ACT, WPB>), dim3((unsigned)total),
+                     OSH_LAUNCH((conv16_group_kernel<TM, BV, ACT, WPB>), dim3((unsigned)total),
                                         dim3(64 * WPB), 0, st, g));
     OSH_LAUNCH_CHECK("conv16_group_kernel");
     return OSH_OK;
@@ -482,7 +482,7 @@ inline osh_status conv16s_launch_t(const osh_conv_params *p, const float *x, con
     const int mgroups = ceil_div(ceil_div(p->m, 16), 4 * TM);
     dim3 grid((unsigned)(tiles_w * tiles_h), (unsigned)mgroups, (unsigned)p->n);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((conv16s_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT, XB, I2C>), grid, dim3(256),
+                     OSH_LAUNCH((conv16s_kernel<TM, BV, TWL, S, KS, CB, VEC, ACT, XB, I2C>), grid, dim3(256),
                                         0, st, *p, x, w, bias, res, y, tiles_w));
     OSH_LAUNCH_CHECK("conv16s_kernel");
     return OSH_OK;

@@ -354,10 +354,10 @@ static osh_status pair_launch_t(PairArgs a, hipStream_t st) {
     a.tiles_w = ceil_div(a.w, TW);
     const int tiles = a.tiles_w * ceil_div(a.h, TH);
     if (exact_silu())
-        hipLaunchKernelGGL((conv_pair_kernel<TH, TW, CB1, CB2, ACT_SILU_EXACT>), dim3((unsigned)tiles), dim3(256), 0,
+        OSH_LAUNCH((conv_pair_kernel<TH, TW, CB1, CB2, ACT_SILU_EXACT>), dim3((unsigned)tiles), dim3(256), 0,
                            st, a);
     else
-        hipLaunchKernelGGL((conv_pair_kernel<TH, TW, CB1, CB2, OSH_ACT_SILU>), dim3((unsigned)tiles), dim3(256), 0,
+        OSH_LAUNCH((conv_pair_kernel<TH, TW, CB1, CB2, OSH_ACT_SILU>), dim3((unsigned)tiles), dim3(256), 0,
                            st, a);
     OSH_LAUNCH_CHECK("conv_pair_kernel");
     return OSH_OK;
@@ -648,9 +648,9 @@ static osh_status pair8_launch_t(PairArgs a, hipStream_t st) {
     a.tiles_w = ceil_div(a.w, TW);
     const unsigned tiles = (unsigned)(a.tiles_w * ceil_div(a.h, TH));
     if (exact_silu())
-        hipLaunchKernelGGL((conv_pair8_kernel<TH, TW, ACT_SILU_EXACT>), dim3(tiles), dim3(256), 0, st, a);
+        OSH_LAUNCH((conv_pair8_kernel<TH, TW, ACT_SILU_EXACT>), dim3(tiles), dim3(256), 0, st, a);
     else
-        hipLaunchKernelGGL((conv_pair8_kernel<TH, TW, OSH_ACT_SILU>), dim3(tiles), dim3(256), 0, st, a);
+        OSH_LAUNCH((conv_pair8_kernel<TH, TW, OSH_ACT_SILU>), dim3(tiles), dim3(256), 0, st, a);
     OSH_LAUNCH_CHECK("conv_pair8_kernel");
     return OSH_OK;
 }
@@ -943,10 +943,10 @@ constexpr int kFirstPairTileCount = sizeof(kFirstPairTiles) / sizeof(kFirstPairT
 template <int TH, int TW, int SA, int S2, int CB2, int NS>
 static void first_pair_launch_ns(const FirstPairArgs &a, unsigned tiles, hipStream_t st) {
     if (exact_silu())
-        hipLaunchKernelGGL((first_pair_kernel<TH, TW, SA, S2, CB2, NS, ACT_SILU_EXACT>), dim3(tiles), dim3(256), 0, st,
+        OSH_LAUNCH((first_pair_kernel<TH, TW, SA, S2, CB2, NS, ACT_SILU_EXACT>), dim3(tiles), dim3(256), 0, st,
                            a);
     else
-        hipLaunchKernelGGL((first_pair_kernel<TH, TW, SA, S2, CB2, NS, OSH_ACT_SILU>), dim3(tiles), dim3(256), 0, st, a);
+        OSH_LAUNCH((first_pair_kernel<TH, TW, SA, S2, CB2, NS, OSH_ACT_SILU>), dim3(tiles), dim3(256), 0, st, a);
 }
 
 template <int TH, int TW, int SA, int S2, int CB2>

@@ -694,7 +694,7 @@ static osh_status run_minmax(const float *a, long long count, DqScratch *sc, int
     long long blocks = (count / 4 + DQ_THREADS - 1) / DQ_THREADS;
     if (blocks < 1) blocks = 1;
     if (blocks > DQ_MINMAX_BLOCKS) blocks = DQ_MINMAX_BLOCKS;
-    hipLaunchKernelGGL(dqmm_minmax_kernel, dim3((unsigned)blocks), dim3(DQ_THREADS), 0, st, a, count, sc);
+    OSH_LAUNCH(dqmm_minmax_kernel, dim3((unsigned)blocks), dim3(DQ_THREADS), 0, st, a, count, sc);
     *nparts = (int)blocks;
     OSH_LAUNCH_CHECK("dqmm_minmax_kernel");
     return OSH_OK;
@@ -721,11 +721,11 @@ static osh_status dqmm_run(int m, int k, int n, const float *d_a, const void *d_
                       (reinterpret_cast<uintptr_t>(d_a) & 15) == 0;
     if (dqmm_variant() == 0 && fblocks <= 0x7fffffffLL) {
         if (full)
-            hipLaunchKernelGGL(dqmm_fused_kernel<true>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k, n,
+            OSH_LAUNCH(dqmm_fused_kernel<true>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k, n,
                                d_a, sc, nparts, (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias, d_out,
                                (int *)d_acc);
         else
-            hipLaunchKernelGGL(dqmm_fused_kernel<false>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k,
+            OSH_LAUNCH(dqmm_fused_kernel<false>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k,
                                n, d_a, sc, nparts, (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias,
                                d_out, (int *)d_acc);
         OSH_LAUNCH_CHECK("dqmm_fused_kernel");
@@ -733,11 +733,11 @@ static osh_status dqmm_run(int m, int k, int n, const float *d_a, const void *d_
         return OSH_OK;
     }
     const int rows_per_block = DQ_THREADS / 64;
-    hipLaunchKernelGGL(dqmm_quantize_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
+    OSH_LAUNCH(dqmm_quantize_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
                        dim3(DQ_THREADS), 0, st, d_a, m, k, sc, nparts, (int *)d_qparams, rowsum, apk);
     OSH_LAUNCH_CHECK("dqmm_quantize_kernel");
     dim3 grid((pad32(n) / 32 + 1) / 2, (pad32(m) / 32 + 1) / 2);
-    hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
+    OSH_LAUNCH(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
                        d_wscale, n_wscale, d_bias, d_out, (int *)d_acc);
     OSH_LAUNCH_CHECK("dqmm_gemm_kernel");
     t_dqmm_launches = 3;
@@ -830,7 +830,7 @@ OSH_API osh_status osh_dqmm_pack_weights(int k, int n, const void *d_w, int w_si
     int8_t *frag = static_cast<int8_t *>(d_packed);
     int *colsum = reinterpret_cast<int *>(frag + (size_t)pad32(n) * pad32(k));
     int *off = colsum + pad32(n);
-    hipLaunchKernelGGL(dqmm_pack_kernel, dim3((pad32(n) + 63) / 64), dim3(64), 0, st, k, n, d_w, w_signed, d_zp,
+    OSH_LAUNCH(dqmm_pack_kernel, dim3((pad32(n) + 63) / 64), dim3(64), 0, st, k, n, d_w, w_signed, d_zp,
                        n_wzp, frag, colsum, off);
     hipError_t le = hipGetLastError();
     hipError_t se = hipStreamSynchronize(st);
@@ -892,7 +892,7 @@ OSH_API osh_status osh_matmul_integer(int m, int k, int n, const void *d_a, int 
     int *rowsum = reinterpret_cast<int *>(sc + 1);
     int8_t *apk = reinterpret_cast<int8_t *>(rowsum + 2 * pad32(m));
     const int rows_per_block = DQ_THREADS / 64;
-    hipLaunchKernelGGL(mmi_pack_a_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
+    OSH_LAUNCH(mmi_pack_a_kernel, dim3((unsigned)((pad32(m) + rows_per_block - 1) / rows_per_block)),
                        dim3(DQ_THREADS), 0, st, static_cast<const uint8_t *>(d_a), m, k, a_signed, a_zp, sc, rowsum,
                        apk);
     OSH_LAUNCH_CHECK("mmi_pack_a_kernel");
@@ -900,7 +900,7 @@ OSH_API osh_status osh_matmul_integer(int m, int k, int n, const void *d_a, int 
     const int *colsum = reinterpret_cast<const int *>(frag + (size_t)pad32(n) * pad32(k));
     const int *off = colsum + pad32(n);
     dim3 grid((pad32(n) / 32 + 1) / 2, (pad32(m) / 32 + 1) / 2);
-    hipLaunchKernelGGL(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
+    OSH_LAUNCH(dqmm_gemm_kernel, grid, dim3(256), 0, st, m, k, n, apk, frag, colsum, off, rowsum, sc,
                        static_cast<const float *>(nullptr), 1, static_cast<const float *>(nullptr),
                        static_cast<float *>(nullptr), (int *)d_c);
     OSH_LAUNCH_CHECK("dqmm_gemm_kernel");
@@ -917,7 +917,7 @@ OSH_API osh_status osh_dynamic_quantize_linear(int64_t n, const float *d_x, uint
     if (r != OSH_OK) return r;
     long long blocks = (n + DQ_THREADS - 1) / DQ_THREADS;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(dql_quantize_kernel, dim3((unsigned)blocks), dim3(DQ_THREADS), 0, st, d_x, n, sc, nparts,
+    OSH_LAUNCH(dql_quantize_kernel, dim3((unsigned)blocks), dim3(DQ_THREADS), 0, st, d_x, n, sc, nparts,
                        (int *)d_qparams, d_q);
     OSH_LAUNCH_CHECK("dql_quantize_kernel");
     return OSH_OK;

@@ -318,11 +318,11 @@ OSH_API osh_status osh_add_f32(int64_t n, const float *d_a, const float *d_b, fl
     const bool vec = n % 4 == 0 && ((reinterpret_cast<uintptr_t>(d_a) | reinterpret_cast<uintptr_t>(d_b) |
                                      reinterpret_cast<uintptr_t>(d_y)) & 15) == 0;
     if (vec) {
-        hipLaunchKernelGGL(add4_kernel, dim3(grid_for(n / 4, 256, 8192)), dim3(256), 0, to_stream(s),
+        OSH_LAUNCH(add4_kernel, dim3(grid_for(n / 4, 256, 8192)), dim3(256), 0, to_stream(s),
                            reinterpret_cast<const float4 *>(d_a), reinterpret_cast<const float4 *>(d_b),
                            reinterpret_cast<float4 *>(d_y), (long long)(n / 4));
     } else {
-        hipLaunchKernelGGL(add_kernel, dim3(grid_for(n, 256, 8192)), dim3(256), 0, to_stream(s), d_a, d_b, d_y,
+        OSH_LAUNCH(add_kernel, dim3(grid_for(n, 256, 8192)), dim3(256), 0, to_stream(s), d_a, d_b, d_y,
                            (long long)n);
     }
     OSH_LAUNCH_CHECK("add_kernel");
@@ -339,7 +339,7 @@ OSH_API osh_status osh_maxpool2d_f32(const osh_pool_params *p, const float *d_x,
         p->kh <= p->pt || p->kw <= p->pl)
         return fail(OSH_E_INVALID, "MaxPool: output window outside the input");
     const long long total = (long long)p->n * p->c * p->oh * p->ow;
-    hipLaunchKernelGGL(maxpool2d_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), *p,
+    OSH_LAUNCH(maxpool2d_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), *p,
                        d_x, d_y, total);
     OSH_LAUNCH_CHECK("maxpool2d_kernel");
     return OSH_OK;
@@ -360,13 +360,13 @@ OSH_API osh_status osh_maxpool_chain3_f32(int n, int c, int h, int w, int k, con
     dim3 grid((unsigned)(tiles_x * tiles_y), (unsigned)(n * c));
     hipStream_t st = to_stream(s);
     if (k == 3)
-        hipLaunchKernelGGL(maxpool_chain3_kernel<3>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
+        OSH_LAUNCH(maxpool_chain3_kernel<3>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
                            d_y1, d_y2, d_y3, (long long)y_batch_stride, tiles_x);
     else if (k == 5)
-        hipLaunchKernelGGL(maxpool_chain3_kernel<5>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
+        OSH_LAUNCH(maxpool_chain3_kernel<5>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
                            d_y1, d_y2, d_y3, (long long)y_batch_stride, tiles_x);
     else
-        hipLaunchKernelGGL(maxpool_chain3_kernel<7>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
+        OSH_LAUNCH(maxpool_chain3_kernel<7>, grid, dim3(256), 0, st, h, w, c, d_x, (long long)x_batch_stride,
                            d_y1, d_y2, d_y3, (long long)y_batch_stride, tiles_x);
     OSH_LAUNCH_CHECK("maxpool_chain3_kernel");
     return OSH_OK;
@@ -381,7 +381,7 @@ OSH_API osh_status osh_dfl_f32(int batches, int sides, int bins, int pixels, con
         return fail(OSH_E_INVALID, "DflSoftmax: batch stride below one image");
     const long long total = (long long)batches * sides * pixels;
     if (total > 0x7fffffffLL * 256) return fail(OSH_E_UNSUPPORTED, "DflSoftmax: too many outputs");
-    hipLaunchKernelGGL(dfl_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), sides, bins,
+    OSH_LAUNCH(dfl_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), sides, bins,
                        pixels, d_x, (long long)x_batch_stride, d_y, (long long)y_batch_stride, total);
     OSH_LAUNCH_CHECK("dfl_kernel");
     return OSH_OK;
@@ -397,12 +397,12 @@ OSH_API osh_status osh_resize_nearest_f32(int n, int c, int h, int w, int fh, in
     const long long pairs = (long long)n * c * h * w / 2;
     if (fh == 2 && fw == 2 && w % 2 == 0 && pairs < (1LL << 31) && y_batch_stride % 4 == 0 &&
         (reinterpret_cast<uintptr_t>(d_x) & 7) == 0 && (reinterpret_cast<uintptr_t>(d_y) & 15) == 0) {
-        hipLaunchKernelGGL(resize2x_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, to_stream(s), c, h,
+        OSH_LAUNCH(resize2x_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, to_stream(s), c, h,
                            w / 2, reinterpret_cast<const float2 *>(d_x), d_y, (long long)y_batch_stride, (int)pairs);
         OSH_LAUNCH_CHECK("resize2x_kernel");
         return OSH_OK;
     }
-    hipLaunchKernelGGL(resize_nearest_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), c,
+    OSH_LAUNCH(resize_nearest_kernel, dim3(grid_for(total, 256, 0x7fffffff)), dim3(256), 0, to_stream(s), c,
                        h, w, fh, fw, d_x, d_y, (long long)y_batch_stride, total);
     OSH_LAUNCH_CHECK("resize_nearest_kernel");
     return OSH_OK;
@@ -416,7 +416,7 @@ OSH_API osh_status osh_transpose_f32(int batch, int rows, int cols, const float 
     if (batch > 65535) return fail(OSH_E_UNSUPPORTED, "Transpose: batch %d exceeds the grid limit", batch);
     dim3 grid(ceil_div(cols, 32), ceil_div(rows, 32), batch);
     if (grid.y > 65535) return fail(OSH_E_UNSUPPORTED, "Transpose: %d rows exceed the grid limit", rows);
-    hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, to_stream(s), rows, cols, d_x, (long long)x_batch_stride,
+    OSH_LAUNCH(transpose_kernel, grid, dim3(256), 0, to_stream(s), rows, cols, d_x, (long long)x_batch_stride,
                        d_y, (long long)y_batch_stride);
     OSH_LAUNCH_CHECK("transpose_kernel");
     return OSH_OK;
@@ -428,10 +428,10 @@ OSH_API osh_status osh_softmax_f32(int64_t rows, int cols, float scale, const fl
     if (!d_x || !d_y) return fail(OSH_E_INVALID, "Softmax: NULL pointer");
     if (d_x == d_y) return fail(OSH_E_INVALID, "Softmax: in-place is not supported");
     if (cols <= SOFTMAX_LDS_COLS)
-        hipLaunchKernelGGL(softmax_kernel<true>, dim3(grid_for(rows, 4, 0x7fffffff)), dim3(256),
+        OSH_LAUNCH(softmax_kernel<true>, dim3(grid_for(rows, 4, 0x7fffffff)), dim3(256),
                            (size_t)4 * cols * sizeof(float), to_stream(s), (long long)rows, cols, scale, d_x, d_y);
     else
-        hipLaunchKernelGGL(softmax_kernel<false>, dim3(grid_for(rows, 4, 0x7fffffff)), dim3(256), 0, to_stream(s),
+        OSH_LAUNCH(softmax_kernel<false>, dim3(grid_for(rows, 4, 0x7fffffff)), dim3(256), 0, to_stream(s),
                            (long long)rows, cols, scale, d_x, d_y);
     OSH_LAUNCH_CHECK("softmax_kernel");
     return OSH_OK;
@@ -447,19 +447,19 @@ OSH_API osh_status osh_activation_f32(int64_t n, const float *d_x, int act, floa
     const int a = act == OSH_ACT_SILU ? ACT_SILU_EXACT : act;
     switch (a) {
     case OSH_ACT_NONE:
-        hipLaunchKernelGGL(activation_kernel<OSH_ACT_NONE>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
+        OSH_LAUNCH(activation_kernel<OSH_ACT_NONE>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
                            d_y, (long long)n);
         break;
     case OSH_ACT_RELU:
-        hipLaunchKernelGGL(activation_kernel<OSH_ACT_RELU>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
+        OSH_LAUNCH(activation_kernel<OSH_ACT_RELU>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
                            d_y, (long long)n);
         break;
     case ACT_SILU_EXACT:
-        hipLaunchKernelGGL(activation_kernel<ACT_SILU_EXACT>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
+        OSH_LAUNCH(activation_kernel<ACT_SILU_EXACT>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), d_x,
                            d_y, (long long)n);
         break;
     case OSH_ACT_SIGMOID:
-        hipLaunchKernelGGL(activation_kernel<OSH_ACT_SIGMOID>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s),
+        OSH_LAUNCH(activation_kernel<OSH_ACT_SIGMOID>, dim3((unsigned)blocks), dim3(256), 0, to_stream(s),
                            d_x, d_y, (long long)n);
         break;
     default:

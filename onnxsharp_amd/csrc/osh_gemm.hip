@@ -75,7 +75,7 @@ static osh_status g16_launch(const IgemmArgs &a, int zcount, int act, hipStream_
     if (blocks > 0x7fffffffLL) return fail(OSH_E_UNSUPPORTED, "GEMM grid too large");
     dim3 grid((unsigned)blocks, zcount);
     OSH_DISPATCH_ACT(act, ACT,
-                     hipLaunchKernelGGL((gemm16_kernel<TM, TN, BV, KC, ACT>), grid, dim3(256), 0, st, a, tiles_m));
+                     OSH_LAUNCH((gemm16_kernel<TM, TN, BV, KC, ACT>), grid, dim3(256), 0, st, a, tiles_m));
     OSH_LAUNCH_CHECK("gemm16_kernel");
     return OSH_OK;
 }
@@ -127,7 +127,7 @@ osh_status launch_igemm(const IgemmArgs &a, int zcount, int bmode, int act, hipS
     do {                                                                                              \
         dim3 grid(ceil_div(a.N, BN), ceil_div(a.M, BM), zcount);                                      \
         OSH_DISPATCH_ACT(act, ACT,                                                                    \
-            hipLaunchKernelGGL((igemm_f32_kernel<BM, BN, WM, WN, BMODE, VA, VB, ACT>), grid, block, 0, \
+            OSH_LAUNCH((igemm_f32_kernel<BM, BN, WM, WN, BMODE, VA, VB, ACT>), grid, block, 0, \
                                st, a));                                                               \
     } while (0)
 #define OSH_IG_SHAPE(BMODE, VA, VB)                                \
@@ -211,7 +211,7 @@ OSH_API osh_status osh_gemm_ex_f32(int trans_a, int trans_b, int m, int n, int k
     const bool bias = beta != 0.0f && d_c && c_len > 0;
     if (!scale && !bias) return OSH_OK;
     const long long total = (long long)m * n;
-    hipLaunchKernelGGL(gemm_ex_epilogue_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, d_y, m, n,
+    OSH_LAUNCH(gemm_ex_epilogue_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, d_y, m, n,
                        alpha, scale ? 1 : 0, beta, bias ? d_c : nullptr, (long long)c_len);
     OSH_LAUNCH_CHECK("gemm_ex_epilogue_kernel");
     return OSH_OK;

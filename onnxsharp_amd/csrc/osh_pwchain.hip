@@ -553,7 +553,7 @@ OSH_API osh_status osh_pw_chain_f32(int count, const osh_pw_chain *chains, osh_s
             return fail(OSH_E_DEVICE, "pointwise chain: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
         }
     }
-    hipLaunchKernelGGL(pw_chain_kernel, dim3((unsigned)total), dim3(PWC_THREADS), lds_bytes, to_stream(s), args);
+    OSH_LAUNCH(pw_chain_kernel, dim3((unsigned)total), dim3(PWC_THREADS), lds_bytes, to_stream(s), args);
     OSH_LAUNCH_CHECK("pw_chain_kernel");
     return OSH_OK;
 }

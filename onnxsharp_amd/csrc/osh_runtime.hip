@@ -2,6 +2,8 @@
 // the C ABI (include/osh_hip.h).  Replaces the Vulkan runtime layer of the
 // reference backend (src/OnnxSharp.Vulkan/VkDevice.cs, VkBufferPool.cs,
 // VkSegment.cs) with plain HIP calls.
+#include <cxxabi.h>
+
 #include <cstdarg>
 #include <cstdlib>
 #include <cstring>
@@ -26,6 +28,43 @@ osh_status fail(osh_status code, const char *fmt, ...) {
 void clear_error() { g_err[0] = 0; }
 
 const char *last_error() { return g_err; }
+
+// Kernels launched by the calling thread since its last osh_kernel_log reset
+// (bounded: launches past the bound are counted, not kept).
+static constexpr size_t kLaunchLogMax = 4096;
+static thread_local std::vector<const void *> t_launch_log;
+static thread_local long long t_launch_count = 0;
+
+void note_launch(const void *kernel) {
+    if (t_launch_log.size() < kLaunchLogMax) t_launch_log.push_back(kernel);
+    ++t_launch_count;
+}
+
+// "name<args>" of a kernel's host handle: its device symbol demangled, without
+// the return type and the parameter list (the form rocprofv3 prints).
+static std::string kernel_name(const void *kernel) {
+    const char *mangled = hipKernelNameRefByPtr(kernel, nullptr);
+    if (!mangled) {
+        (void)hipGetLastError();
+        return "?";
+    }
+    int status = 0;
+    char *dem = abi::__cxa_demangle(mangled, nullptr, nullptr, &status);
+    std::string s = (status == 0 && dem) ? dem : mangled;
+    free(dem);
+    if (s.compare(0, 5, "void ") == 0) s.erase(0, 5);
+    if (s.compare(0, 5, "osh::") == 0) s.erase(0, 5);
+    int depth = 0;
+    for (size_t i = 0; i < s.size(); ++i) {
+        if (s[i] == '<') ++depth;
+        else if (s[i] == '>') --depth;
+        else if (s[i] == '(' && depth == 0) {
+            s.resize(i);
+            break;
+        }
+    }
+    return s;
+}
 
 static int g_exact_silu = -1;  // -1: read ONNXSHARP_HIP_EXACT_SILU on first use
 static int g_gemm_variant = -3;  // -3: read ONNXSHARP_HIP_GEMM_VARIANT on first use
@@ -301,10 +340,13 @@ OSH_API osh_status osh_init(int dev, osh_device_info *info) {
     int n = 0;
     OSH_HIP_CHECK(hipGetDeviceCount(&n));
     if (dev < 0 || dev >= n) return fail(OSH_E_INVALID, "device %d out of range (%d devices)", dev, n);
+    hipDeviceProp_t p;
+    OSH_HIP_CHECK(hipGetDeviceProperties(&p, dev));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(OSH_E_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only", dev,
+                    p.gcnArchName);
     OSH_HIP_CHECK(hipSetDevice(dev));
     if (info) {
-        hipDeviceProp_t p;
-        OSH_HIP_CHECK(hipGetDeviceProperties(&p, dev));
         memset(info, 0, sizeof(*info));
         strncpy(info->name, p.name, sizeof(info->name) - 1);
         strncpy(info->arch, p.gcnArchName, sizeof(info->arch) - 1);
@@ -312,11 +354,32 @@ OSH_API osh_status osh_init(int dev, osh_device_info *info) {
         info->clock_khz = p.clockRate;
         info->total_mem = p.totalGlobalMem;
         info->lds_per_block = p.sharedMemPerBlock;
-        if (strncmp(info->arch, "gfx950", 6) != 0)
-            return fail(OSH_E_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only", dev,
-                        info->arch);
     }
-    return noalloc_scratch_setup(dev);
+    // The no-allocation DQM's scratch address is resolved here when it can be;
+    // if not, osh_dqmm_u8s8_noalloc resolves it (and reports why it cannot) on
+    // its first call, and nothing else depends on it.
+    if (noalloc_scratch_setup(dev) != OSH_OK) clear_error();
+    return OSH_OK;
+}
+
+OSH_API osh_status osh_kernel_log(int reset, char *buf, size_t bytes, int *count) {
+    if (count) *count = (int)t_launch_count;
+    if (buf && bytes) {
+        std::string all;
+        for (const void *k : t_launch_log) {
+            all += kernel_name(k);
+            all += '\n';
+        }
+        if (all.size() + 1 > bytes)
+            return fail(OSH_E_INVALID, "buffer of %zu bytes holds fewer than the %zu the log needs", bytes,
+                        all.size() + 1);
+        memcpy(buf, all.c_str(), all.size() + 1);
+    }
+    if (reset) {
+        t_launch_log.clear();
+        t_launch_count = 0;
+    }
+    return OSH_OK;
 }
 
 OSH_API osh_status osh_device_synchronize(void) {
@@ -388,7 +451,7 @@ OSH_API osh_status osh_memset_d8(void *d_dst, int value, size_t bytes, osh_strea
     if (!d_dst) return fail(OSH_E_INVALID, "d_dst is NULL");
     size_t blocks = (bytes + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(fill_u8_kernel, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), (uint8_t *)d_dst,
+    OSH_LAUNCH(fill_u8_kernel, dim3((unsigned)blocks), dim3(256), 0, to_stream(s), (uint8_t *)d_dst,
                        (uint8_t)value, bytes);
     OSH_LAUNCH_CHECK("fill_u8_kernel");
     return OSH_OK;

@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void wino_f23_kernel(osh_conv_params p, const 
 
 inline osh_status winograd_pack(const osh_conv_params *p, const float *w, void *out, hipStream_t st) {
     const long long total = (long long)((p->m + 15) / 16) * 16 * ((p->c + 15) / 16) * 16;
-    hipLaunchKernelGGL(wino_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p->m, p->c, w,
+    OSH_LAUNCH(wino_pack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, p->m, p->c, w,
                        static_cast<float *>(out));
     OSH_LAUNCH_CHECK("wino_pack_kernel");
     return OSH_OK;

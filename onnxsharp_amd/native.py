@@ -83,6 +83,7 @@ _SIGS = {
     "osh_init": ([_i, C.POINTER(DeviceInfo)], _i),
     "osh_device_count": ([C.POINTER(C.c_int)], _i),
     "osh_device_synchronize": ([], _i),
+    "osh_kernel_log": ([_i, C.c_char_p, _sz, C.POINTER(C.c_int)], _i),
     "osh_config_set": ([C.c_char_p, _i], _i),
     "osh_config_get": ([C.c_char_p, C.POINTER(C.c_int)], _i),
     "osh_malloc": ([C.POINTER(_vp), _sz], _i),
@@ -186,3 +187,14 @@ def dims64(shape) -> "C.Array":
     for i, d in enumerate(shape):
         arr[i] = int(d)
     return arr
+
+
+def kernel_log(reset: bool = True) -> list:
+    """Names ("kernel<template arguments>") of the kernels the calling thread
+    launched since the last reset, in launch order (osh_kernel_log)."""
+    n = C.c_int()
+    call("osh_kernel_log", 0, None, 0, C.byref(n))
+    size = 256 * (min(n.value, 4096) + 1)
+    buf = C.create_string_buffer(size)
+    call("osh_kernel_log", 1 if reset else 0, buf, size, C.byref(n))
+    return [s for s in buf.value.decode().split("\n") if s]
