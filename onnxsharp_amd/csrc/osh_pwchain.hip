@@ -426,7 +426,11 @@ OSH_API osh_status osh_pw_chain_f32(int count, const osh_pw_chain *chains, osh_s
                 T.res = S.res;
                 T.c = S.m;
                 reads[nr++] = Span{S.src[0], (size_t)S.m * hw * sizeof(float), ci, k, true};
-                if (S.res) reads[nr++] = Span{S.res, (size_t)S.m * hw * sizeof(float), ci, k, false};
+                // the depthwise stage reads its residual from memory while other
+                // waves write neighbouring channels of y: y may be the residual
+                // itself (each element read and written by one thread), but it
+                // may not overlap it anywhere else
+                if (S.res) reads[nr++] = Span{S.res, (size_t)S.m * hw * sizeof(float), ci, k, S.res != S.y};
                 writes[nw++] = Span{S.y, (size_t)S.m * hw * sizeof(float), ci, k, false};
                 continue;
             }

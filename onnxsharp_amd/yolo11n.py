@@ -809,9 +809,11 @@ def pair_bottleneck_convs(model: Model, takes=None, min_pixels: int = 0) -> Mode
                 a.y.h * a.y.w >= min_pixels and
                 b.x.buf is a.y.buf and b.x.c0 == a.y.c0 and b.x.c == a.y.c == a.y.buf.c and
                 users.get(id(a.y.buf)) == {id(a), id(b)} and takes(a, b)):
-            # a first-layer pair leaves its 16-channel map unstored: the
-            # fused kernel beats two launches there by far
-            out.append(PairOp(a.name.rsplit("/", 3)[0] + "#pair", a, b, store_mid=a.x.c > 4))
+            # a first-layer pair leaves its 16-channel map unstored (the
+            # fused kernel beats two launches there by far), unless the map is
+            # also a model output
+            is_output = any(a.y.buf is o for o in model.outputs)
+            out.append(PairOp(a.name.rsplit("/", 3)[0] + "#pair", a, b, store_mid=a.x.c > 4 or is_output))
             i += 2
             continue
         out.append(a)

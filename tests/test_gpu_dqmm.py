@@ -297,3 +297,52 @@ def test_dqmm_graph_replays_see_new_inputs(cuda, oracle):
         if g.value:
             N.call("osh_graph_destroy", g)
         N.call("osh_stream_destroy", st)
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 512, 2048), (70, 96, 300)])
+@pytest.mark.parametrize("noalloc", [False, True])
+@pytest.mark.parametrize("offset", [0, 4])
+def test_dqmm_output_without_accumulators(cuda, oracle, m, k, n, noalloc, offset):
+    """With no int32 accumulator output (d_acc NULL, as the benchmark and the
+    C# emitter call it) the full-tile kernel writes its output tiles through
+    LDS as 16-byte vectors when `out` is 16-byte aligned, and element by
+    element otherwise (offset 4).  Both must give the oracle's bits, a NaN row
+    included, from osh_dqmm_u8s8 and from osh_dqmm_u8s8_noalloc."""
+    import ctypes as C
+    import torch
+    from onnxsharp_amd import native as N
+    print(f"dqmm no-acc m={m} k={k} n={n} noalloc={noalloc} offset={offset}", flush=True)
+    a = synth.normal(7 * m + k, (m, k))
+    a[m // 3, k // 2] = np.nan
+    w = synth.randint(7 * n + k, (k, n), -127, 127, np.int8)
+    ws = synth.uniform(7 * k + n, (n,), 0.001, 0.02)
+    bias = synth.normal(7 * m + n, (n,), 0, 0.01)
+    nb = C.c_size_t()
+    N.call("osh_dqmm_packed_weight_bytes", k, n, C.byref(nb))
+    packed = torch.empty(nb.value, dtype=torch.uint8, device=cuda)
+    dw = _t(w, cuda)
+    N.call("osh_dqmm_pack_weights", k, n, C.c_void_p(dw.data_ptr()), 1, None, 0, C.c_void_p(packed.data_ptr()),
+           None)
+    da, dws, db = _t(a, cuda), _t(ws, cuda), _t(bias, cuda)
+    raw = torch.full((m * n + 4,), float("inf"), dtype=torch.float32, device=cuda)
+    out_ptr = C.c_void_p(raw.data_ptr() + offset)
+    ptr = lambda t: C.c_void_p(t.data_ptr())
+    if noalloc:
+        N.call("osh_dqmm_u8s8_noalloc", m, k, n, ptr(da), ptr(packed), ptr(dws), n, ptr(db), out_ptr, None, None,
+               None)
+    else:
+        sb = C.c_size_t()
+        N.call("osh_dqmm_scratch_bytes", m, k, C.byref(sb))
+        scratch = torch.empty(sb.value, dtype=torch.uint8, device=cuda)
+        N.call("osh_dqmm_u8s8", m, k, n, ptr(da), ptr(packed), ptr(dws), n, ptr(db), out_ptr, None, None,
+               ptr(scratch), None)
+    torch.cuda.synchronize()
+    flat = raw.cpu().numpy()
+    got = flat[offset // 4: offset // 4 + m * n].reshape(m, n)
+    # nothing written outside [out, out + m*n)
+    assert np.isinf(np.delete(flat, np.arange(offset // 4, offset // 4 + m * n))).all()
+    eo, _, _, _, _ = oracle.dqmm(a, w, None, ws, bias)
+    good = np.ones(m, bool)
+    good[m // 3] = False
+    assert np.isnan(got[m // 3]).all()
+    assert np.array_equal(got[good].view(np.uint32), eo[good].view(np.uint32))

@@ -219,8 +219,8 @@ def test_head_tails_of_three_scales_in_one_launch(cuda, exact):
 def test_chain_refusals(cuda):
     """An output over a tensor a later stage reads from memory, an output over
     a depthwise stage's input, weights not packed for the stage, a depthwise
-    stage after stage 0, and a chain whose weights do not fit in LDS are
-    refused."""
+    stage after stage 0, a depthwise output that overlaps its residual other
+    than exactly, and a chain whose weights do not fit in LDS are refused."""
     import torch
     from onnxsharp_amd import native as N
     ch, refs, keep = _psa_chain(cuda, (20, 20), 7)
@@ -242,6 +242,14 @@ def test_chain_refusals(cuda):
     bad = N.PwChain.from_buffer_copy(hch)
     bad.stage[1], bad.stage[0] = hch.stage[0], hch.stage[1]
     with pytest.raises(N.OshError):
+        _run([bad])
+    # a depthwise stage whose output overlaps its own residual a plane away
+    hch1, _, hkeep1 = _head_chain(cuda, 80, (20, 20), 11)
+    planes = torch.zeros((1, 81, 20, 20), dtype=torch.float32, device=cuda)
+    bad = N.PwChain.from_buffer_copy(hch1)
+    bad.stage[0].res = planes.data_ptr()
+    bad.stage[0].y = planes[:, 1:].data_ptr()
+    with pytest.raises(N.OshError, match="overlaps"):
         _run([bad])
     big, _, _ = _psa_chain(cuda, (20, 20), 10, c=128)  # 576 KB of weights
     with pytest.raises(N.OshError, match="LDS"):

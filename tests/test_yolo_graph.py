@@ -242,6 +242,13 @@ def test_pairs_of_the_640_frame():
     # a refusal from the library keeps the convs separate
     h = Y.pair_bottleneck_convs(Y.fuse_launches(m, pairs=False), takes=lambda a, b: False)
     assert not any(isinstance(o, Y.PairOp) for o in h.ops)
+    # the stem's map is stored after all when a caller reads it as an output
+    mo = Y.build(640)
+    stem_map = mo.ops[0].y.buf
+    mo.outputs = mo.outputs + [stem_map]
+    fo = Y.fuse_launches(mo)
+    so = [o for o in fo.ops if isinstance(o, Y.PairOp) and o.a.x.c == 3]
+    assert len(so) == 1 and so[0].store_mid and so[0].a.y.buf is stem_map
 
 
 def test_decode_appends_dfl_and_sigmoid_per_scale():
