@@ -316,7 +316,7 @@ class YoloWorkload(FrameWorkload):
                                    f"{nconv} convs + attention/SPPF/upsample glue as {nlaunch} launches "
                                    "(grouped and paired convs, residual Adds fused) in one HIP graph",
                        "input": "U(0,1) [1,3,640,640], splitmix64 seed 4000",
-                       "weights": "N(0,0.05) conv weights, N(0,0.01) biases (BatchNorm folded), seeds 7000+",
+                       "weights": "N(0,0.05) conv weights, N(0,0.01) biases (BatchNorm folded), splitmix64 seeded per layer from its node name and model seed 7000",
                        "conv_gflop": round(sum(o.flops for o in self.model.convs) / 1e9, 4),
                        "outputs": "3 head tensors [1,144,80,80], [1,144,40,40], [1,144,20,20]; "
                                   "DFL/NMS on the host"}
@@ -334,7 +334,7 @@ class C2fWorkload(FrameWorkload):
                                    "+SiLU, split 64/64, bottleneck 3x3 64->64 +SiLU -> 3x3 64->64 +SiLU + residual "
                                    "Add, concat 192, cv2 1x1 192->128 +SiLU",
                        "input": "U(0,1) [1,128,80,80], splitmix64 seed 3300",
-                       "weights": "N(0,0.05) conv weights, N(0,0.01) biases, seeds 9000+",
+                       "weights": "N(0,0.05) conv weights, N(0,0.01) biases, splitmix64 seeded per layer from its node name and model seed 9000",
                        "conv_gflop": round(sum(o.flops for o in self.model.convs) / 1e9, 4),
                        "launches": len(self.fr.model.ops)}
 

@@ -7,6 +7,8 @@ independent streams; every result is rounded once to float32.
 """
 from __future__ import annotations
 
+import zlib
+
 import numpy as np
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
@@ -47,3 +49,10 @@ def randint(seed: int, shape, lo: int, hi: int, dtype=np.int32) -> np.ndarray:
     span = np.uint64(hi - lo + 1)
     r = ((bits(seed, n) >> np.uint64(32)) * span) >> np.uint64(32)
     return (r.astype(np.int64) + lo).astype(dtype).reshape(shape)
+
+
+def layer_seed(model_seed: int, name: str, part: int) -> int:
+    """Seed of tensor `part` (0: weights, 1: bias) of the layer called `name`
+    (its ONNX node name) in a model generated from `model_seed`: a layer's
+    random weights depend on its name only, not on where a builder creates it."""
+    return (int(model_seed) << 40) + (zlib.crc32(name.encode()) << 2) + int(part)

@@ -16,7 +16,8 @@ it once as a HIP graph and replay it per frame.
 
 Weights are random (no checkpoint is available): conv weights N(0, 0.05) and
 biases N(0, 0.01) standing for BatchNorm folded into the conv, from the
-counter-based generator in `synth` with a fixed seed per layer.
+counter-based generator in `synth`, seeded by the model seed and the layer's
+node name (`synth.layer_seed`).
 """
 from __future__ import annotations
 
@@ -257,10 +258,9 @@ class _Builder:
         if y is None:
             y = whole(self.buf(name + "_out", cout, oh, ow))
         assert (y.c, y.h, y.w) == (cout, oh, ow), (name, y.c, y.h, y.w, cout, oh, ow)
-        i = self.nconv
         self.nconv += 1
-        w = synth.normal(self.seed + 2 * i, (cout, x.c // group, k, k), 0.0, 0.05)
-        b = synth.normal(self.seed + 2 * i + 1, (cout,), 0.0, 0.01)
+        w = synth.normal(synth.layer_seed(self.seed, name, 0), (cout, x.c // group, k, k), 0.0, 0.05)
+        b = synth.normal(synth.layer_seed(self.seed, name, 1), (cout,), 0.0, 0.01)
         self.m.ops.append(ConvOp(name, x, y, k, s, group, act, w, b))
         return y
 
@@ -342,15 +342,16 @@ class _Builder:
         self.m.ops.append(op)
         # positional term: depthwise 3x3 over v seen as [1, c, H, W]; the heads'
         # v blocks are not adjacent inside qkv, so the conv runs per head
-        pe = self.buf(f"{q}/attn/pe/conv/Conv", c, x.h, x.w)
+        pe_name = f"{q}/attn/pe/conv/Conv"
+        pe = self.buf(pe_name, c, x.h, x.w)
         rows = 2 * key_dim + head_dim
-        w = synth.normal(self.seed + 2 * self.nconv, (c, 1, 3, 3), 0.0, 0.05)
-        bias = synth.normal(self.seed + 2 * self.nconv + 1, (c,), 0.0, 0.01)
+        w = synth.normal(synth.layer_seed(self.seed, pe_name, 0), (c, 1, 3, 3), 0.0, 0.05)
+        bias = synth.normal(synth.layer_seed(self.seed, pe_name, 1), (c,), 0.0, 0.01)
         self.nconv += 1
         for h in range(heads):
             v = qkv.sub(h * rows + 2 * key_dim, head_dim)
             sl = slice(h * head_dim, (h + 1) * head_dim)
-            self.m.ops.append(ConvOp(f"{q}/attn/pe/conv/Conv" + (f"#head{h}" if heads > 1 else ""), v,
+            self.m.ops.append(ConvOp(pe_name + (f"#head{h}" if heads > 1 else ""), v,
                                      Slice(pe, h * head_dim, head_dim), 3, 1, head_dim, None, w[sl], bias[sl]))
         s1 = self.add(f"{q}/attn/Add", att, whole(pe))
         pr = self.conv(f"{q}/attn/proj/conv/Conv", s1, c, 1, 1, act=None)

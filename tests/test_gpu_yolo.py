@@ -7,8 +7,9 @@ upsampling, concat/split/add glue) against the oracle.
   bit for bit: each kernel sums in the order of the reference's kernel for
   that shape (NCHWc chain, im2col chain, GEMM chain, depthwise, SoftmaxRow's
   lane order, ...).
-* End to end: the frame's three head tensors against the oracle frame run
-  from the same input, bit for bit.
+* End to end: the frame's three head tensors (and, with the decode, the DFL
+  and Sigmoid outputs) against an independent restatement of the network
+  (oracle/yolo11n_net.py) run from the same input, bit for bit.
 * The frame recorded as a HIP graph replays to the eager result, bit for bit,
   with host work and other launches between replays.
 SiLU runs in the exact (reference polynomial) mode throughout."""
@@ -92,7 +93,10 @@ def test_yolo_per_op_parity(cuda, oracle, exact_silu, size, chains):
 
 @pytest.mark.parametrize("size", [320, 640])
 def test_yolo_end_to_end(cuda, oracle, exact_silu, size):
-    from oracle import yolo_frame as YO
+    # against the independent restatement of the network (oracle/yolo11n_net.py,
+    # written without the device package's builder), so the frame's wiring is
+    # checked along with its arithmetic
+    from oracle import yolo11n_net
     model, fr = _frame(cuda, size)
     print(f"end to end at {size}x{size}", flush=True)
     try:
@@ -101,7 +105,7 @@ def test_yolo_end_to_end(cuda, oracle, exact_silu, size):
         fr.run()
         fr.sync()
         got = [t.cpu().numpy() for t in fr.outputs()]
-        ref = YO.Frame(model).run(oracle, x)
+        ref = yolo11n_net.forward(oracle, x)
         for i, (g, r) in enumerate(zip(got, ref)):
             d = np.abs(g.astype(np.float64) - r)
             print(f"head {i} {g.shape}: max|d| {d.max():.3e}, range {np.abs(r).max():.3e}", flush=True)
@@ -113,10 +117,10 @@ def test_yolo_end_to_end(cuda, oracle, exact_silu, size):
 
 def test_yolo_640_graph_default_silu_within_tolerance(cuda, oracle):
     # the benchmarked configuration: the 640 frame replayed as one HIP graph
-    # with the default (fast) SiLU epilogue, against the oracle frame with the
-    # reference polynomial; FP32 bar |d| <= 1e-5 + 1e-4 |ref| on all three
-    # head tensors
-    from oracle import yolo_frame as YO
+    # with the default (fast) SiLU epilogue, against the independent oracle
+    # network with the reference polynomial; FP32 bar |d| <= 1e-5 + 1e-4 |ref|
+    # on all three head tensors
+    from oracle import yolo11n_net
     size = 640
     model, fr = _frame(cuda, size)
     try:
@@ -130,12 +134,32 @@ def test_yolo_640_graph_default_silu_within_tolerance(cuda, oracle):
         fr.launch()
         fr.sync()
         got = [t.cpu().numpy() for t in fr.outputs()]
-        ref = YO.Frame(model).run(oracle, x)
+        ref = yolo11n_net.forward(oracle, x)
         for i, (g, r) in enumerate(zip(got, ref)):
             nbad, dmax = fp32_violations(g, r)
             rel = float((np.abs(g.astype(np.float64) - r) / (1e-5 + np.abs(r))).max())
             print(f"head {i} {g.shape}: max|d| {dmax:.3e}, max |d|/(1e-5+|ref|) {rel:.3e}", flush=True)
             assert_fp32_close(g, r, f"head {i}")
+    finally:
+        fr.close()
+
+
+def test_yolo_decoded_heads_end_to_end(cuda, oracle, exact_silu):
+    # the frame with the head's DFL and class Sigmoid on the device, against
+    # the independent network's decode, bit for bit
+    from oracle import yolo11n_net
+    size = 640
+    model, fr = _frame(cuda, size, decode=True)
+    try:
+        x = synth.uniform(4245, (1, 3, size, size))
+        fr.set_input(x)
+        fr.run()
+        fr.sync()
+        got = [t.cpu().numpy() for t in fr.outputs()]
+        ref = yolo11n_net.forward(oracle, x, decode=True)
+        for i, (g, r) in enumerate(zip(got, ref)):
+            assert g.shape == r.shape == (1, 84, size // (8 << i), size // (8 << i))
+            assert np.array_equal(g, r), f"decoded head {i}: max |d| {np.abs(g - r).max():.3e}"
     finally:
         fr.close()
 
