@@ -138,9 +138,12 @@ OSH_API osh_status osh_kernel_log(int reset, char *buf, size_t bytes, int *count
  *                 appended, so later processes choose the same tiles without
  *                 timing them.
  *   "dqmm_variant": 0 (default) = osh_dqmm_u8s8 runs a min/max launch and
- *                 then one launch that quantizes A and multiplies; 1 = min/max,
- *                 quantize and GEMM as three launches.  Both give identical
- *                 outputs.  Initial value from ONNXSHARP_HIP_DQMM_VARIANT.
+ *                 then one launch that quantizes A and multiplies (on 16x16
+ *                 tiles whose epilogue overlaps the MFMAs where every tile is
+ *                 full); 1 = min/max, quantize and GEMM as three launches;
+ *                 2 = as 0 with 32x32 tiles for full tiles.  All give
+ *                 identical outputs.  Initial value from
+ *                 ONNXSHARP_HIP_DQMM_VARIANT.
  *   "dqmm_launches" (get only): kernel launches (2 or 3) of the calling
  *                 thread's last osh_dqmm_u8s8 / osh_dqmm_u8s8_noalloc call.
  *   "im2col3x3_variant": -1 (default) = 3x3 stride-1/2 convolutions with

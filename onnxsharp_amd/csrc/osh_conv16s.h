@@ -349,6 +349,13 @@ __device__ __forceinline__ void conv16s_tile(const osh_conv_params &p, const flo
     // (otherwise compute_last has stored every block of an active wave)
 }
 
+// XB: workgroups take their tiles XCD-banded (an XCD runs a band of
+// neighbouring pixel tiles of one channel group, whose patches share halo
+// lines in its L2).  Banding with the channel groups of a pixel tile
+// innermost instead (its four workgroups, which stage the same patch, on one
+// XCD) measured slower on every shape tried (3x3 s2 128 -> 256 at 80x80:
+// 16.3 us against 14.7-15.0 in launch order) and the frame's tuner never
+// picked it, so it is not offered.
 template <int TM, int BV, int TWL, int S, int KS, int CB, bool VEC, int ACT, bool XB = false, bool I2C = false>
 __global__ __launch_bounds__(256) void conv16s_kernel(osh_conv_params p, const float *__restrict__ x,
                                                       const float *__restrict__ wpk, const float *__restrict__ bias,
@@ -514,6 +521,7 @@ osh_status conv16s_launch(const osh_conv_params *p, const float *x, const float 
 // seven blocks, instead of 400 with four, two waves on 576 SIMDs).
 constexpr C16sVariant kC16sx[] = {{1, 2, 16}, {1, 4, 16}, {2, 2, 16}, {1, 7, 16}, {1, 8, 16}};
 constexpr int kC16sxCount = sizeof(kC16sx) / sizeof(kC16sx[0]);
+
 
 osh_status conv16sx_launch(const osh_conv_params *p, const float *x, const float *w, const float *bias,
                            const float *res, int act, float *y, hipStream_t st, int v);

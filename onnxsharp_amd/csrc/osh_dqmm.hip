@@ -690,6 +690,181 @@ __global__ __launch_bounds__(64 * DQF_WAVES) void dqmm_fused_kernel(
     }
 }
 
+// The fused kernel on 16 x 16 output tiles (v_mfma_i32_16x16x64_i8), for
+// the full-tile case (m % 32 == 0, n % 128 == 0, k % 512 == 0, A 16-byte
+// aligned).  Same workgroup tile (32 rows x 128 columns), same quantization
+// and arithmetic as dqmm_fused_kernel, so the same bits; what differs is the
+// schedule after the quantization barrier.  A wave's 32 x 32 block is four
+// 16 x 16 tiles, each an 8-step chain over K = 512, run one after another:
+// the integer correction, dequantization and stores of one tile are issued
+// between the next tile's MFMAs, so the epilogue's VALU work and the output
+// writes overlap the matrix core instead of following it.  The row sums and
+// NaN flags are reduced before the barrier, so every tile's epilogue can run
+// as soon as its chain ends.
+//
+// Operands: A (16 rows x 64 k per step) lane l holds row l & 15 and k =
+// 64 s + 16 (l >> 4) + byte.  B is read straight from the 32 x 32 x 32
+// packing: lane l of 16-column subtile c takes packed lane
+// 16 c + (l & 15) + 32 ((l >> 4) & 1) of fragment 2 s + (l >> 5), whose k
+// is the same 64 s + 16 (l >> 4) + byte, so A and B pair matching k.  The
+// output tile's lane l holds column l & 15 and rows 4 (l >> 4) + v,
+// v = 0..3.  ACC: the int32 accumulators are stored too.
+//
+// Tried and slower: the second half of K quantized between the first half's
+// MFMAs, behind one more barrier (7.33 -> 7.65 us per op).
+template <bool ACC>
+__global__ __launch_bounds__(64 * DQF_WAVES) void dqmm_fused16_kernel(
+    int m, int k, int n, const float *a, DqScratch *__restrict__ sc, int nparts, int *__restrict__ qparams,
+    const int8_t *wpk, const int *__restrict__ colsum, const int *__restrict__ off,
+    const float *__restrict__ wscale, int n_wscale, const float *__restrict__ bias, float *__restrict__ out,
+    int *__restrict__ acc_out) {
+    __shared__ __attribute__((aligned(16))) int lds_a[DQF_KS * 256];  // [kstep64 8][row tile 2][64 lanes][16 bytes]
+    __shared__ __attribute__((aligned(16))) int lds_rs[32];
+    __shared__ __attribute__((aligned(16))) int lds_rn[32];
+    const int tid = threadIdx.x, lane = tid & 63, wt = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ks = k / 32;
+    const int ncb = n / 32 / DQF_WAVES, nmt = m / 32;
+    const int id = xcd_band(blockIdx.x, gridDim.x);
+    const int grp = id / (DQF_GM * ncb), gl = id % (DQF_GM * ncb);
+    const int mt0 = grp * DQF_GM;
+    const int gm = nmt - mt0 < DQF_GM ? nmt - mt0 : DQF_GM;
+    const int mt = mt0 + gl % gm;
+    const int nt = (gl / gm) * DQF_WAVES + wt;
+    const int r = tid >> 3, c8 = tid & 7;
+    const float *src = a + (long long)(mt * 32 + r) * k;
+    const int npass = ks / DQF_KS;
+    // B: this lane's 16 bytes of packed lane 16 c + (lane & 15) + 32 ((lane >> 4) & 1)
+    // of fragment (nt, 2 s + (lane >> 5)); subtile c adds 16 lanes (256 bytes)
+    const int8_t *bl = wpk + ((long long)nt * ks + (lane >> 5)) * 1024 + ((lane & 15) + 32 * ((lane >> 4) & 1)) * 16;
+
+    const int pidx = tid < nparts ? tid : 0;
+    const float pmin = sc->partial_min[pidx], pmax = sc->partial_max[pidx];
+    // the epilogue's column operands of both 16-column subtiles
+    int offj_raw[2], csum[2];
+    float ws[2], bj[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int j = nt * 32 + 16 * c + (lane & 15);
+        offj_raw[c] = off[j];
+        csum[c] = colsum[j];
+        ws[c] = n_wscale == 1 ? wscale[0] : wscale[j];
+        bj[c] = bias ? bias[j] : 0.0f;
+    }
+
+    Quad x[DQF_KS];
+    i32x4 b[2][DQF_KS / 2];
+    auto load_pass = [&](int s0) {
+#pragma unroll
+        for (int i = 0; i < DQF_KS; i++) {
+            const float4 v = *reinterpret_cast<const float4 *>(src + (s0 + i) * 32 + 4 * c8);
+            x[i].v[0] = v.x; x[i].v[1] = v.y; x[i].v[2] = v.z; x[i].v[3] = v.w;
+        }
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int s = 0; s < DQF_KS / 2; s++)
+                b[c][s] = *reinterpret_cast<const i32x4 *>(bl + (long long)(s0 + 2 * s) * 1024 + c * 256);
+    };
+    load_pass(0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    float inv, scale;
+    int zp;
+    dq_finish(sc, __builtin_fminf(0.f, pmin), __builtin_fmaxf(0.f, pmax), qparams, blockIdx.x == 0, inv, zp,
+              &scale);
+    const float zpf = (float)zp;
+    const unsigned alpha = (unsigned)(128 - zp);
+
+    int sum = 0;
+    bool nan = false;
+    i32x4 acc[2][2] = {};
+    i32x4 av[2][DQF_KS / 2];
+    // quad i of this thread: k = 32 i + 4 c8 -> step i / 2, lane group 2 (i & 1) + c8 / 4
+    int *dst = lds_a + ((r >> 4) * 64 + (r & 15) + 16 * (c8 >> 2)) * 4 + (c8 & 3);
+    auto quantize_pass = [&]() {
+#pragma unroll
+        for (int i = 0; i < DQF_KS; i++)
+            dst[(i >> 1) * 512 + (i & 1) * 128] = (int)quantize4(x[i], inv, zpf, 0xfu, sum, nan);
+    };
+    auto read_a = [&]() {
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int s = 0; s < DQF_KS / 2; s++)
+                av[rt][s] = *reinterpret_cast<const i32x4 *>(lds_a + ((s * 2 + rt) * 64 + lane) * 4);
+    };
+    auto chain = [&](int t) {
+#pragma unroll
+        for (int s = 0; s < DQF_KS / 2; s++)
+            acc[t >> 1][t & 1] =
+                __builtin_amdgcn_mfma_i32_16x16x64_i8(av[t >> 1][s], b[t & 1][s], acc[t >> 1][t & 1], 0, 0, 0);
+    };
+    for (int ps = 0; ps + 1 < npass; ps++) {  // passes before the last (K > 512)
+        quantize_pass();
+        __syncthreads();
+        read_a();
+#pragma unroll
+        for (int t = 0; t < 4; t++) chain(t);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // every wave has read this pass's a'' before it is rewritten
+        load_pass((ps + 1) * DQF_KS);
+    }
+    quantize_pass();
+    // row sums and NaN flags: a row's 8 threads are consecutive lanes
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+        sum += __shfl_xor(sum, o);
+        const int other = __shfl_xor(nan ? 1 : 0, o);
+        nan = nan || other != 0;
+    }
+    if (c8 == 0) {
+        lds_rs[r] = sum;
+        lds_rn[r] = nan ? 1 : 0;
+    }
+    __syncthreads();
+    read_a();
+    // the lane's row sums and NaN flags (rows 16 rt + 4 (lane >> 4) + v)
+    int4 rs4[2], rn4[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+        rs4[rt] = *reinterpret_cast<const int4 *>(lds_rs + 16 * rt + 4 * (lane >> 4));
+        rn4[rt] = *reinterpret_cast<const int4 *>(lds_rn + 16 * rt + 4 * (lane >> 4));
+    }
+    auto epilogue = [&](int t) {
+        const int rt = t >> 1, c = t & 1;
+        const int j = nt * 32 + 16 * c + (lane & 15);
+        const unsigned offj = (unsigned)offj_raw[c];
+        const unsigned colterm = alpha * (unsigned)csum[c] + (unsigned)k * alpha * offj;
+        const float comb = scale * ws[c];  // CombinedScale, QuantizedMatMulOps.cs:203-221
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int il = 16 * rt + 4 * (lane >> 4) + v;
+            const int rsv = v == 0 ? rs4[rt].x : v == 1 ? rs4[rt].y : v == 2 ? rs4[rt].z : rs4[rt].w;
+            const int rnv = v == 0 ? rn4[rt].x : v == 1 ? rn4[rt].y : v == 2 ? rn4[rt].z : rn4[rt].w;
+            const int val = (int)((unsigned)acc[rt][c][v] + offj * (unsigned)rsv + colterm);
+            const long long o_idx = (long long)(mt * 32 + il) * n + j;
+            if constexpr (ACC) acc_out[o_idx] = val;
+            const float o = __builtin_fmaf((float)val, comb, bj[c]);
+            out[o_idx] = rnv ? __builtin_nanf("") : o;
+        }
+    };
+    // tile t's chain, with tile t - 1's epilogue issued between its MFMAs:
+    // the epilogue's VALU work and stores overlap the matrix core
+    chain(0);
+#pragma unroll
+    for (int t = 1; t < 4; t++) {
+        chain(t);
+        epilogue(t - 1);
+#pragma unroll
+        for (int q = 0; q < DQF_KS / 2; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // five VALU
+            __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);  // one global store
+        }
+    }
+    epilogue(3);
+}
+
 static osh_status run_minmax(const float *a, long long count, DqScratch *sc, int *nparts, hipStream_t st) {
     long long blocks = (count / 4 + DQ_THREADS - 1) / DQ_THREADS;
     if (blocks < 1) blocks = 1;
@@ -719,8 +894,17 @@ static osh_status dqmm_run(int m, int k, int n, const float *d_a, const void *d_
     if (r != OSH_OK) return r;
     const bool full = m % 32 == 0 && n % 128 == 0 && k % (32 * DQF_KS) == 0 &&
                       (reinterpret_cast<uintptr_t>(d_a) & 15) == 0;
-    if (dqmm_variant() == 0 && fblocks <= 0x7fffffffLL) {
-        if (full)
+    const int variant = dqmm_variant();
+    if (variant != 1 && fblocks <= 0x7fffffffLL) {
+        if (full && variant == 0 && d_acc)
+            OSH_LAUNCH(dqmm_fused16_kernel<true>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k, n,
+                       d_a, sc, nparts, (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias, d_out,
+                       (int *)d_acc);
+        else if (full && variant == 0)
+            OSH_LAUNCH(dqmm_fused16_kernel<false>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k, n,
+                       d_a, sc, nparts, (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias, d_out,
+                       (int *)d_acc);
+        else if (full)
             OSH_LAUNCH(dqmm_fused_kernel<true>, dim3((unsigned)fblocks), dim3(64 * DQF_WAVES), 0, st, m, k, n,
                                d_a, sc, nparts, (int *)d_qparams, frag, colsum, off, d_wscale, n_wscale, d_bias, d_out,
                                (int *)d_acc);

@@ -154,7 +154,8 @@ long long winograd_max_pixels() {
 int dqmm_variant() {
     if (g_dqmm_variant == -3) {
         const char *e = getenv("ONNXSHARP_HIP_DQMM_VARIANT");
-        g_dqmm_variant = (e && atoi(e) == 1) ? 1 : 0;
+        const int v = e ? atoi(e) : 0;
+        g_dqmm_variant = (v == 1 || v == 2) ? v : 0;
     }
     return g_dqmm_variant;
 }
@@ -237,7 +238,7 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         return OSH_OK;
     }
     if (strcmp(key, "dqmm_variant") == 0) {
-        if (value != 0 && value != 1) return fail(OSH_E_INVALID, "dqmm_variant %d out of range [0, 2)", value);
+        if (value < 0 || value > 2) return fail(OSH_E_INVALID, "dqmm_variant %d out of range [0, 3)", value);
         g_dqmm_variant = value;
         return OSH_OK;
     }

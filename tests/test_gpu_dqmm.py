@@ -120,9 +120,10 @@ def test_dynamic_quantize_linear_matches_oracle(cuda, oracle):
                                    (64, 1024, 256), (128, 512, 512), (256, 1024, 1024)])
 def test_dqmm_fused_and_three_launch_pipelines_identical(cuda, oracle, m, k, n):
     """dqmm_variant 0 (min/max launch, then quantize inside the GEMM launch, K
-    in chunks of 512; the branch-free kernel where every tile is full) and 1
-    (min/max, quantize and GEMM launches) give the same bits, both equal to
-    the oracle."""
+    in chunks of 512; where every tile is full, the 16 x 16 tile kernel whose
+    epilogue overlaps its MFMAs), 1 (min/max, quantize and GEMM launches) and
+    2 (as 0, with the 32 x 32 tile kernel for full tiles) give the same bits,
+    all equal to the oracle."""
     import ctypes as C
     from onnxsharp_amd import native as N
     print(f"dqmm pipelines m={m} k={k} n={n}", flush=True)
@@ -135,7 +136,7 @@ def test_dqmm_fused_and_three_launch_pipelines_identical(cuda, oracle, m, k, n):
     N.call("osh_config_get", b"dqmm_variant", C.byref(old))
     got, launches = [], []
     try:
-        for v in (0, 1):
+        for v in (0, 1, 2):
             N.call("osh_config_set", b"dqmm_variant", v)
             got.append(run_dqmm(cuda, a, w, None, ws, bias))
             nl = C.c_int()
@@ -143,11 +144,12 @@ def test_dqmm_fused_and_three_launch_pipelines_identical(cuda, oracle, m, k, n):
             launches.append(nl.value)
     finally:
         N.call("osh_config_set", b"dqmm_variant", old.value)
-    assert launches == [2, 3], launches
-    (o0, a0, s0, z0), (o1, a1, s1, z1) = got
-    assert (s0, z0) == (s1, z1)
-    assert np.array_equal(a0, a1)
+    assert launches == [2, 3, 2], launches
+    (o0, a0, s0, z0), (o1, a1, s1, z1), (o2, a2, s2, z2) = got
+    assert (s0, z0) == (s1, z1) == (s2, z2)
+    assert np.array_equal(a0, a1) and np.array_equal(a0, a2)
     assert np.array_equal(o0.view(np.uint32), o1.view(np.uint32))
+    assert np.array_equal(o0.view(np.uint32), o2.view(np.uint32))
     eo, eacc, _, es, ez = oracle.dqmm(a, w, None, ws, bias)
     assert (s0, z0) == (es, ez)
     good = np.ones(m, bool)
@@ -302,16 +304,31 @@ def test_dqmm_graph_replays_see_new_inputs(cuda, oracle):
 @pytest.mark.parametrize("m,k,n", [(512, 512, 2048), (70, 96, 300)])
 @pytest.mark.parametrize("noalloc", [False, True])
 @pytest.mark.parametrize("offset", [0, 4])
-def test_dqmm_output_without_accumulators(cuda, oracle, m, k, n, noalloc, offset):
+@pytest.mark.parametrize("variant", [0, 2])
+def test_dqmm_output_without_accumulators(cuda, oracle, m, k, n, noalloc, offset, variant):
     """With no int32 accumulator output (d_acc NULL, as the benchmark and the
     C# emitter call it) the full-tile kernel writes its output tiles through
     LDS as 16-byte vectors when `out` is 16-byte aligned, and element by
     element otherwise (offset 4).  Both must give the oracle's bits, a NaN row
-    included, from osh_dqmm_u8s8 and from osh_dqmm_u8s8_noalloc."""
+    included, from osh_dqmm_u8s8 and from osh_dqmm_u8s8_noalloc, with the
+    16 x 16 tile kernel (variant 0) and the 32 x 32 one (variant 2)."""
     import ctypes as C
     import torch
     from onnxsharp_amd import native as N
-    print(f"dqmm no-acc m={m} k={k} n={n} noalloc={noalloc} offset={offset}", flush=True)
+    print(f"dqmm no-acc m={m} k={k} n={n} noalloc={noalloc} offset={offset} variant={variant}", flush=True)
+    old = C.c_int()
+    N.call("osh_config_get", b"dqmm_variant", C.byref(old))
+    N.call("osh_config_set", b"dqmm_variant", variant)
+    try:
+        _no_acc_case(cuda, oracle, m, k, n, noalloc, offset)
+    finally:
+        N.call("osh_config_set", b"dqmm_variant", old.value)
+
+
+def _no_acc_case(cuda, oracle, m, k, n, noalloc, offset):
+    import ctypes as C
+    import torch
+    from onnxsharp_amd import native as N
     a = synth.normal(7 * m + k, (m, k))
     a[m // 3, k // 2] = np.nan
     w = synth.randint(7 * n + k, (k, n), -127, 127, np.int8)

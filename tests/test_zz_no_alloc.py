@@ -56,7 +56,7 @@ def _run(cuda, m, k, n, t, noalloc):
     return out.cpu().numpy(), acc.cpu().numpy(), qp.cpu().numpy()
 
 
-@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("variant", [0, 1, 2])
 def test_noalloc_dqmm_matches_the_scratch_entry_point(cuda, variant):
     from onnxsharp_amd import native as N
     old = C.c_int()
