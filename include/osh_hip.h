@@ -160,13 +160,23 @@ OSH_API osh_status osh_kernel_log(int reset, char *buf, size_t bytes, int *count
  *                 gate (NchwcConv.cs:100-126) run Winograd F(2x2,3x3) in the
  *                 reference's arithmetic -- the reference's own choice on an
  *                 AVX-512 host; 2 = Winograd for every shape that passes its
- *                 gate, ahead of the NCHWc kernels (the reference's choice on
- *                 a host without AVX-512); 0 = never (those shapes take the
- *                 im2col chain).  Initial value from ONNXSHARP_HIP_WINOGRAD.
- *                 Changes the packed weight layout: pack again after changing it.
+ *                 gate, ahead of the NCHWc kernels; 0 = never (those shapes
+ *                 take the im2col chain).  Initial value from
+ *                 ONNXSHARP_HIP_WINOGRAD.  Changes the packed weight layout:
+ *                 pack again after changing it.
  *   "winograd_max_pixels": the largest output map (H*W) Winograd takes;
  *                 initial value from the reference's ONNXSHARP_WINO_MAX, else
  *                 4096.  Also changes the packed layout.
+ *   "nchwc": 1 (default) = the reference host runs its NCHWc 3x3 kernel (an
+ *                 AVX-512 host, NchwcConv.Enabled && IsSupported,
+ *                 src/OnnxSharp/Kernels/NchwcConv.cs:38-43), so the shapes its
+ *                 gate takes sum in the NCHWc chain; 0 = it does not (an
+ *                 AVX2-only host, or ONNXSHARP_NCHWC=0): those shapes take
+ *                 what ConvLayer.Forward falls back to (DnnOps.cs:475-482):
+ *                 Winograd where its gate holds, else the panel / im2col
+ *                 chain.  Initial value from the reference's own
+ *                 ONNXSHARP_NCHWC (anything but "0" is on).  Changes the
+ *                 packed weight layout: pack again after changing it.
  *   "tune": 1 (default) = the first launch of a 3x3 conv shape on a stream
  *                 that is not capturing times every conv16 tile (they all give
  *                 identical outputs) and keeps the fastest for that shape;

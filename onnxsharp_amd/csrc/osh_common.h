@@ -187,6 +187,12 @@ int pair_tile();
 int winograd_mode();
 long long winograd_max_pixels();
 
+// Whether the host the backend stands in for runs OnnxSharp's NCHWc 3x3
+// kernel (an AVX-512 host with ONNXSHARP_NCHWC not "0", NchwcConv.cs:38-43).
+// Off, the 3x3 convs the NCHWc gate would take go where the reference then
+// sends them: Winograd, else the panel / im2col chain.
+bool nchwc_enabled();
+
 // DynamicQuantizeMatMul pipeline (0 = min/max launch then one fused
 // quantize + GEMM launch, 1 = min/max, quantize and GEMM as three launches).
 int dqmm_variant();

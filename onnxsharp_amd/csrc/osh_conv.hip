@@ -367,7 +367,7 @@ static ConvAlgo select_algo(const osh_conv_params *p) {
     const bool wino = wm != 0 && winograd_eligible(p, winograd_max_pixels());
     if (p->c <= 4 && first_conv_eligible(p)) return ALGO_FIRST;
     if (wm == 2 && wino) return ALGO_WINOGRAD;
-    if (nchwc_gate(p) && conv16_eligible(p)) return ALGO_CONV16;
+    if (nchwc_enabled() && nchwc_gate(p) && conv16_eligible(p)) return ALGO_CONV16;
     if (wino) return ALGO_WINOGRAD;
     if (conv16s_eligible(p)) return ALGO_CONV16I;  // the LDS-patch tiles in the im2col order
     if (first_conv_eligible(p)) return ALGO_FIRST;
@@ -1163,7 +1163,7 @@ static const char *first_pair_refusal(const osh_conv_params *pa, const osh_conv_
     if (act != OSH_ACT_SILU) return "the fused pair takes SiLU convs";
     if ((long long)pa->c * pa->h * pa->w * 4 >= (1LL << 31) || (long long)pb->m * pb->oh * pb->ow * 4 >= (1LL << 31))
         return "tensors too large";
-    if (select_algo(pa) != ALGO_FIRST || !nchwc_gate(pb) || select_algo(pb) != ALGO_CONV16)
+    if (select_algo(pa) != ALGO_FIRST || !nchwc_enabled() || !nchwc_gate(pb) || select_algo(pb) != ALGO_CONV16)
         return "the single-conv dispatch takes another chain for one of the convs";
     return nullptr;
 }

@@ -73,6 +73,7 @@ static int g_tune = -1;             // -1: read ONNXSHARP_HIP_TUNE on first use
 static int g_pw_variant = -3;       // -3: read ONNXSHARP_HIP_POINTWISE_VARIANT on first use
 static int g_dqmm_variant = -3;     // -3: read ONNXSHARP_HIP_DQMM_VARIANT on first use
 static int g_winograd = -3;         // -3: read ONNXSHARP_HIP_WINOGRAD on first use
+static int g_nchwc = -3;            // -3: read ONNXSHARP_NCHWC on first use
 static int g_i2c_variant = -3;      // -3: read ONNXSHARP_HIP_IM2COL3X3_VARIANT on first use
 static int g_group3x3_tile = -1;    // forced tile of grouped 3x3 launches (-1: first-use timing)
 static int g_group_pw_tile = -1;    // forced tile of grouped pointwise launches (-1: first-use timing)
@@ -138,6 +139,15 @@ int winograd_mode() {
         g_winograd = (v >= 0 && v <= 2) ? v : 1;
     }
     return g_winograd;
+}
+
+bool nchwc_enabled() {
+    if (g_nchwc == -3) {
+        // the reference's own switch (NchwcConv.cs:38-40): anything but "0" keeps it on
+        const char *e = getenv("ONNXSHARP_NCHWC");
+        g_nchwc = (e && strcmp(e, "0") == 0) ? 0 : 1;
+    }
+    return g_nchwc == 1;
 }
 
 long long winograd_max_pixels() {
@@ -237,6 +247,11 @@ OSH_API osh_status osh_config_set(const char *key, int value) {
         g_wino_max = value;
         return OSH_OK;
     }
+    if (strcmp(key, "nchwc") == 0) {
+        if (value != 0 && value != 1) return fail(OSH_E_INVALID, "nchwc %d: 0 or 1", value);
+        g_nchwc = value;
+        return OSH_OK;
+    }
     if (strcmp(key, "dqmm_variant") == 0) {
         if (value < 0 || value > 2) return fail(OSH_E_INVALID, "dqmm_variant %d out of range [0, 3)", value);
         g_dqmm_variant = value;
@@ -297,6 +312,10 @@ OSH_API osh_status osh_config_get(const char *key, int *value) {
     }
     if (strcmp(key, "winograd") == 0) {
         *value = winograd_mode();
+        return OSH_OK;
+    }
+    if (strcmp(key, "nchwc") == 0) {
+        *value = nchwc_enabled() ? 1 : 0;
         return OSH_OK;
     }
     if (strcmp(key, "winograd_max_pixels") == 0) {

@@ -184,7 +184,7 @@ KERNEL_IM2COL = "im2col"
 
 
 def conv_reference_kernel(x_shape, w_shape, strides, pads, dilations, group, out_hw, winograd=1,
-                          wino_max=4096):
+                          wino_max=4096, nchwc=1):
     """The kernel ConvLayer.Forward (src/OnnxSharp/Ops/DnnOps.cs:437-482) runs
     for a 2-D conv on an AVX-512 host, first gate that holds:
     DepthwiseConv.TryConv (group == C == M, one input channel per group,
@@ -193,7 +193,12 @@ def conv_reference_kernel(x_shape, w_shape, strides, pads, dilations, group, out
     (NchwcConv.cs:100-126,166-194); Winograd.TryConv3x3 (Winograd.cs:58-122);
     else PackedConv / Im2Col, both the im2col chain.  winograd = 0 leaves
     Winograd out and 2 puts it ahead of NCHWc, as the backend's option of the
-    same name does.  pads are the begin pads (top, left)."""
+    same name does.  nchwc = 0 is a host that does not run NchwcConv
+    (NchwcConv.Enabled false, ONNXSHARP_NCHWC=0, or no AVX-512:
+    NchwcConv.cs:38-43): its shapes then fall to Winograd or the im2col
+    chain.  Without AVX-512 FirstConv is off too and PackedConv takes its
+    shapes, in the same ic -> ky -> kx order.  pads are the begin pads (top,
+    left)."""
     n, c, h, w = x_shape
     m, cpg, kh, kw = w_shape
     sh, sw = strides
@@ -210,20 +215,20 @@ def conv_reference_kernel(x_shape, w_shape, strides, pads, dilations, group, out
     if winograd == 2 and wino:
         return KERNEL_WINOGRAD
     s2 = sh == 2
-    nchwc = (group == 1 and (kh, kw) == (3, 3) and sh == sw and sh in (1, 2) and (dh, dw) == (1, 1)
-             and (pt, pl) == (1, 1) and (not s2 or (h % 2 == 0 and w % 2 == 0)) and c % 16 == 0
-             and m % 32 == 0 and n == 1 and ((oh * 2, ow * 2) == (h, w) if s2 else (oh, ow) == (h, w)))
-    if nchwc:
+    gate = (nchwc != 0 and group == 1 and (kh, kw) == (3, 3) and sh == sw and sh in (1, 2) and (dh, dw) == (1, 1)
+            and (pt, pl) == (1, 1) and (not s2 or (h % 2 == 0 and w % 2 == 0)) and c % 16 == 0
+            and m % 32 == 0 and n == 1 and ((oh * 2, ow * 2) == (h, w) if s2 else (oh, ow) == (h, w)))
+    if gate:
         return KERNEL_NCHWC
     if wino:
         return KERNEL_WINOGRAD
     return KERNEL_IM2COL
 
 
-def conv_reference(x, w, bias, strides, pads, dilations, group, out_hw, winograd=1, wino_max=4096):
+def conv_reference(x, w, bias, strides, pads, dilations, group, out_hw, winograd=1, wino_max=4096, nchwc=1):
     """Conv output (before the fused activation) of the reference kernel
     conv_reference_kernel picks for the shape."""
-    k = conv_reference_kernel(x.shape, w.shape, strides, pads, dilations, group, out_hw, winograd, wino_max)
+    k = conv_reference_kernel(x.shape, w.shape, strides, pads, dilations, group, out_hw, winograd, wino_max, nchwc)
     if k == KERNEL_DEPTHWISE:
         return conv_dw_f32(x, w, bias, strides, pads, dilations, out_hw)
     if k == KERNEL_WINOGRAD:

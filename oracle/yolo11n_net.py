@@ -13,9 +13,10 @@ between the two.  Tensors are plain numpy arrays; concat and split are
 np.concatenate and slicing.
 
 Arithmetic is the oracle's restatement of the reference's CPU kernels
-(oracle.conv_reference: the kernel ConvLayer.Forward picks per shape,
-src/OnnxSharp/Ops/DnnOps.cs:437-482; silu_ref: VectorMath.Silu; gemm_f32,
-softmax, maxpool2d, resize_nearest, dfl, sigmoid_ref).  Weights come from
+(oracle.conv_reference: the kernel ConvLayer.Forward picks per shape on the
+host that `nchwc` describes, src/OnnxSharp/Ops/DnnOps.cs:437-482;
+silu_ref: VectorMath.Silu; gemm_f32, softmax, maxpool2d, resize_nearest,
+dfl, sigmoid_ref).  Weights come from
 the seeded generator keyed by node name (synth.layer_seed), as the device
 model's do: conv weights N(0, 0.05), biases N(0, 0.01).
 """
@@ -36,10 +37,11 @@ class Net:
     activation).  With dry=True no arithmetic runs: outputs are zeros of the
     right shapes (wiring and shape checks)."""
 
-    def __init__(self, oracle, seed: int = 7000, winograd: int = 1, dry: bool = False):
+    def __init__(self, oracle, seed: int = 7000, winograd: int = 1, dry: bool = False, nchwc: int = 1):
         self.o = oracle
         self.seed = seed
         self.winograd = winograd
+        self.nchwc = nchwc
         self.dry = dry
         self.tensors = {}
         self.convs = []
@@ -64,7 +66,7 @@ class Net:
             y = np.zeros((1, c2, oh, ow), np.float32)
         else:
             y = self.o.conv_reference(np.ascontiguousarray(x), w, b, (s, s), (p, p), (1, 1), g, (oh, ow),
-                                      winograd=self.winograd)
+                                      winograd=self.winograd, nchwc=self.nchwc)
             if act:
                 y = self.o.silu_ref(y)
         return self.keep(name, y)
@@ -233,6 +235,7 @@ class Net:
         return self.decode(heads) if decode else heads
 
 
-def forward(oracle, x, seed=7000, decode=False, winograd=1):
-    """The three head tensors of YOLO11n for input x [1, 3, S, S]."""
-    return Net(oracle, seed, winograd).forward(np.ascontiguousarray(x, np.float32), decode=decode)
+def forward(oracle, x, seed=7000, decode=False, winograd=1, nchwc=1):
+    """The three head tensors of YOLO11n for input x [1, 3, S, S]; nchwc = 0
+    for a reference host that does not run NchwcConv."""
+    return Net(oracle, seed, winograd, nchwc=nchwc).forward(np.ascontiguousarray(x, np.float32), decode=decode)

@@ -13,10 +13,11 @@ attention core uses the GEMM chain for both MatMuls and the oracle softmax.
 import numpy as np
 
 
-def conv(oracle, op, x, res=None, winograd=1):
+def conv(oracle, op, x, res=None, winograd=1, nchwc=1):
     k, s, pad = op.k, op.s, op.k // 2
     out_hw = (op.y.h, op.y.w)
-    y = oracle.conv_reference(x, op.w, op.b, (s, s), (pad, pad), (1, 1), op.group, out_hw, winograd=winograd)
+    y = oracle.conv_reference(x, op.w, op.b, (s, s), (pad, pad), (1, 1), op.group, out_hw, winograd=winograd,
+                              nchwc=nchwc)
     if op.act == "Silu":
         y = oracle.silu_ref(y)
     if res is not None:  # a fused residual Add: one float addition per element
@@ -39,11 +40,12 @@ def attention(oracle, op, qkv):
     return np.concatenate(ys, axis=0).reshape(1, op.y.c, op.y.h, op.y.w)
 
 
-def run_op(oracle, op, inputs):
-    """Output of one op from its input arrays (in the op's own input order)."""
+def run_op(oracle, op, inputs, nchwc=1):
+    """Output of one op from its input arrays (in the op's own input order);
+    nchwc = 0 for a reference host that does not run NchwcConv."""
     from onnxsharp_amd import yolo11n as Y
     if isinstance(op, Y.ConvOp):
-        return conv(oracle, op, inputs[0], inputs[1] if op.res is not None else None)
+        return conv(oracle, op, inputs[0], inputs[1] if op.res is not None else None, nchwc=nchwc)
     if isinstance(op, Y.AddOp):
         return (inputs[0] + inputs[1]).astype(np.float32)
     if isinstance(op, Y.CopyOp):

@@ -246,3 +246,22 @@ def test_conv1d_shapes_follow_conv1dshape():
     assert ConvLayer(group=4).get_memory_shapes((1, 16, 50), (16, 4, 3)) == (1, 16, 48)
     with pytest.raises(Exception):
         ConvLayer().get_memory_shapes((1, 16, 50), (16, 4, 3, 3))  # ranks differ
+
+
+def test_emitter_registry_and_noemit_switch(monkeypatch):
+    # the host side of the emitter registry (VkOpRegistry.CanEmit,
+    # src/OnnxSharp.Vulkan/VkOpRegistry.cs:168-180): fused activations the
+    # launch does not apply are refused, a MatMul's fused bias is taken, and
+    # ONNXSHARP_HIP_NOEMIT drops emitters by name (ONNXSHARP_VK_NOEMIT, :154-161)
+    from onnxsharp_amd import registry as R
+    monkeypatch.delenv("ONNXSHARP_HIP_NOEMIT", raising=False)
+    assert R.can_emit("Conv") and R.can_emit("Conv", "Silu") and R.can_emit("Conv", "Relu")
+    assert not R.can_emit("Conv", "Sigmoid")
+    assert R.can_emit("MatMul", fused_bias=True) and not R.can_emit("MatMul", "Silu")
+    assert not R.can_emit("Gemm", fused_bias=True)
+    assert R.can_emit("DynamicQuantizeMatMul") and not R.can_emit("Resize")
+    monkeypatch.setenv("ONNXSHARP_HIP_NOEMIT", " conv, DQMM ,,")
+    assert R.disabled() == {"conv", "dqmm"}
+    assert not R.can_emit("Conv") and not R.can_emit("DynamicQuantizeMatMul")
+    assert R.can_emit("MatMul") and R.can_emit("MatMulInteger")
+    assert not R.can_emit("MatMul", env="matmul")

@@ -26,13 +26,13 @@ def run_conv(cuda, x, w, b, act=None, **attrs):
     return y.cpu().numpy(), layer.resolve(x.shape, w.shape)
 
 
-def oracle_conv(oracle, x, w, b, p, act, order=None, winograd=1):
+def oracle_conv(oracle, x, w, b, p, act, order=None, winograd=1, nchwc=1):
     """The oracle's conv: with order None the kernel the reference's dispatch
-    picks for the shape (depthwise, NCHWc, Winograd or im2col chain), else the
-    given accumulation order."""
+    picks for the shape (depthwise, NCHWc, Winograd or im2col chain; nchwc = 0
+    on a host without NchwcConv), else the given accumulation order."""
     args = (x, w, b, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), p.group, (p.oh, p.ow))
     if order is None:
-        y = oracle.conv_reference(*args, winograd=winograd)
+        y = oracle.conv_reference(*args, winograd=winograd, nchwc=nchwc)
     else:
         y = oracle.conv2d_f32(*args, order=order)
     if act == "Silu":
@@ -847,3 +847,47 @@ def test_conv1d_rank3_within_fp32_bar(cuda, oracle, name, xs, ws, attrs, act):
     if r is not None:
         ref = ref + r
     assert_fp32_close(y, ref, name)
+
+
+NCHWC_OFF_CASES = [
+    ("c2_3x3s1_64to64_160", (1, 64, 160, 160), (64, 64, 3, 3), 1, "im2col"),
+    ("c3b_3x3s2_128to256_80", (1, 128, 80, 80), (256, 128, 3, 3), 2, "im2col"),
+    ("3x3s1_64to64_20", (1, 64, 20, 20), (64, 64, 3, 3), 1, "winograd"),
+    ("3x3s1_128to128_40", (1, 128, 40, 40), (128, 128, 3, 3), 1, "winograd"),
+]
+
+
+@pytest.mark.parametrize("name,xs,ws,stride,kind", NCHWC_OFF_CASES, ids=[c[0] for c in NCHWC_OFF_CASES])
+def test_conv_without_nchwc_follows_the_avx2_dispatch(cuda, oracle, name, xs, ws, stride, kind):
+    # nchwc = 0 (ONNXSHARP_NCHWC=0, or a host without AVX-512): the shapes
+    # NchwcConv would take go where ConvLayer.Forward then sends them
+    # (DnnOps.cs:475-482) -- Winograd where its gate holds, else PackedConv /
+    # Im2Col, both the ic -> ky -> kx chain -- bit for bit (exact SiLU)
+    from onnxsharp_amd import native as N
+    from onnxsharp_amd.layers import ConvLayer
+    print(f"nchwc=0 {name} x={xs} w={ws} s={stride}", flush=True)
+    seed = sum(xs) * 7 + sum(ws) + stride
+    x = synth.uniform(seed, xs)
+    w = synth.normal(seed + 1, ws, 0, 0.05)
+    b = synth.normal(seed + 2, (ws[0],), 0, 0.01)
+    attrs = dict(strides=[stride, stride], pads=[1, 1, 1, 1])
+    old = C.c_int()
+    N.call("osh_config_get", b"nchwc", C.byref(old))
+    N.call("osh_config_set", b"nchwc", 0)
+    N.call("osh_config_set", b"exact_silu", 1)
+    try:
+        layer = ConvLayer(fused_activation="Silu", **attrs)
+        y = layer.forward(_t(x, cuda), _t(w, cuda), _t(b, cuda)).cpu().numpy()
+        p = layer.resolve(x.shape, w.shape)
+        names = N.kernel_log(reset=True)
+    finally:
+        N.call("osh_config_set", b"nchwc", old.value)
+        N.call("osh_config_set", b"exact_silu", 0)
+    args = (x.shape, w.shape, (p.sh, p.sw), (p.pt, p.pl), (p.dh, p.dw), p.group, (p.oh, p.ow))
+    assert oracle.conv_reference_kernel(*args, nchwc=0) == kind
+    assert oracle.conv_reference_kernel(*args, nchwc=1) == oracle.KERNEL_NCHWC
+    assert any(n.startswith("wino_f23" if kind == "winograd" else "conv16") for n in names), names
+    ref = oracle_conv(oracle, x, w, b, p, "Silu", nchwc=0)
+    assert np.array_equal(y, ref), f"max |d| {np.abs(y - ref).max():.3e} at {np.argwhere(y != ref)[:3]}"
+    # and not the NCHWc chain's bits (the two orders round differently here)
+    assert not np.array_equal(y, oracle_conv(oracle, x, w, b, p, "Silu", nchwc=1))

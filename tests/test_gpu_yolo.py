@@ -144,6 +144,40 @@ def test_yolo_640_graph_default_silu_within_tolerance(cuda, oracle):
         fr.close()
 
 
+def test_yolo_end_to_end_without_nchwc(cuda, oracle, exact_silu):
+    # the 640 frame on a reference host without NchwcConv (nchwc = 0): its 30
+    # NCHWc layers take Winograd (40x40, 20x20) or the im2col chain; pairs and
+    # grouped launches that would sum another chain fall back to single
+    # launches; the heads equal the independent network's, bit for bit
+    from onnxsharp_amd import native as N
+    from oracle import yolo11n_net
+    size = 640
+    old = C.c_int()
+    N.call("osh_config_get", b"nchwc", C.byref(old))
+    N.call("osh_config_set", b"nchwc", 0)
+    try:
+        model, fr = _frame(cuda, size)
+        try:
+            print(f"end to end at {size}x{size} with nchwc=0: {len(fr.model.ops)} launches", flush=True)
+            x = synth.uniform(4247, (1, 3, size, size))
+            fr.set_input(x)
+            N.kernel_log(reset=True)
+            fr.run()
+            fr.sync()
+            names = N.kernel_log(reset=True)
+            got = [t.cpu().numpy() for t in fr.outputs()]
+        finally:
+            fr.close()
+    finally:
+        N.call("osh_config_set", b"nchwc", old.value)
+    assert any(n.startswith("wino_f23") for n in names), names
+    ref = yolo11n_net.forward(oracle, x, nchwc=0)
+    for i, (g, r) in enumerate(zip(got, ref)):
+        assert np.array_equal(g, r), f"head {i}: max |d| {np.abs(g - r).max():.3e}"
+    on = yolo11n_net.forward(oracle, x, nchwc=1)
+    assert not all(np.array_equal(g, r) for g, r in zip(got, on))
+
+
 def test_yolo_decoded_heads_end_to_end(cuda, oracle, exact_silu):
     # the frame with the head's DFL and class Sigmoid on the device, against
     # the independent network's decode, bit for bit

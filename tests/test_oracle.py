@@ -187,7 +187,7 @@ def test_winograd_exact_on_integer_data(oracle):
         assert np.array_equal(oracle.winograd_f23(x, wt, b).astype(np.float64), ref)
 
 
-def _yolo_conv_kernels(oracle, size):
+def _yolo_conv_kernels(oracle, size, nchwc=1, detail=False):
     from onnxsharp_amd import yolo11n
     kinds, seen = [], set()
     for op in yolo11n.build(size).ops:
@@ -195,9 +195,10 @@ def _yolo_conv_kernels(oracle, size):
         if isinstance(op, yolo11n.ConvOp) and op.name.split("#")[0] not in seen:
             seen.add(op.name.split("#")[0])
             pad = op.k // 2
-            kinds.append((oracle.conv_reference_kernel(
+            kind = oracle.conv_reference_kernel(
                 (1, op.x.c, op.x.h, op.x.w), (op.y.c, op.x.c // op.group, op.k, op.k), (op.s, op.s),
-                (pad, pad), (1, 1), op.group, (op.y.h, op.y.w)), op.k))
+                (pad, pad), (1, 1), op.group, (op.y.h, op.y.w), nchwc=nchwc)
+            kinds.append((kind, op.k, op.s, op.group > 1, op.y.h * op.y.w) if detail else (kind, op.k))
     return kinds
 
 
@@ -219,6 +220,32 @@ def test_reference_dispatch_of_the_yolo11n_frame(oracle):
     assert sum(1 for kind, _ in _yolo_conv_kernels(oracle, 128) if kind == oracle.KERNEL_WINOGRAD) >= 4
 
 
+def test_reference_dispatch_of_the_yolo11n_frame_without_nchwc(oracle):
+    # A host that does not run NchwcConv (AVX2 only, or ONNXSHARP_NCHWC=0):
+    # the reference's own family profile of this network on such a host
+    # (bench.md:1747-1755) is 35 3x3 stride-1 layers (Winograd only where the
+    # map is at most 4096 pixels, i.e. 40x40 and 20x20; the 160x160 and
+    # 80x80 ones on im2col), 7 3x3 stride-2 layers (PackedConv: the im2col
+    # order) and 45 1x1 layers (the im2col GEMM).
+    kinds = _yolo_conv_kernels(oracle, 640, nchwc=0, detail=True)
+    assert len(kinds) == 87
+    s1 = [k for k in kinds if k[1] == 3 and k[2] == 1]
+    s2 = [k for k in kinds if k[1] == 3 and k[2] == 2]
+    assert (len(s1), len(s2), sum(1 for k in kinds if k[1] == 1)) == (35, 7, 45)
+    assert not any(k[0] == oracle.KERNEL_NCHWC for k in kinds)
+    assert all(k[0] == oracle.KERNEL_IM2COL for k in s2)  # the stem included (FirstConv needs AVX-512 too)
+    dense_s1 = [k for k in s1 if not k[3]]
+    assert all(k[0] == (oracle.KERNEL_WINOGRAD if k[4] <= 4096 else oracle.KERNEL_IM2COL) for k in dense_s1)
+    # 20 Winograd calls (10 at 40x40, 10 at 20x20) and 8 im2col ones (160x160, 80x80)
+    assert sum(1 for k in dense_s1 if k[0] == oracle.KERNEL_WINOGRAD) == 20
+    assert sum(1 for k in dense_s1 if k[0] == oracle.KERNEL_IM2COL) == 8
+    assert all(k[0] == oracle.KERNEL_DEPTHWISE for k in s1 if k[3])
+    # the 30 NCHWc layers of the AVX-512 host are exactly the ones that move
+    on = _yolo_conv_kernels(oracle, 640, nchwc=1)
+    moved = [a[0] for a, b in zip(on, kinds) if a[0] != b[0]]
+    assert moved == [oracle.KERNEL_NCHWC] * 30
+
+
 def test_reference_dispatch_gates(oracle):
     K = oracle.conv_reference_kernel
     s1, p1, d1 = (1, 1), (1, 1), (1, 1)
@@ -235,6 +262,12 @@ def test_reference_dispatch_gates(oracle):
     assert K((1, 8, 5, 20), (8, 8, 3, 3), s1, p1, d1, 1, (5, 20)) == oracle.KERNEL_IM2COL  # H < 6
     assert K((1, 32, 20, 20), (32, 1, 3, 3), s1, p1, d1, 32, (20, 20)) == oracle.KERNEL_DEPTHWISE
     assert K((1, 3, 64, 64), (16, 3, 3, 3), (2, 2), p1, d1, 1, (32, 32)) == oracle.KERNEL_IM2COL
+    # without NchwcConv: Winograd where its gate holds, else the im2col chain
+    assert K((1, 64, 20, 20), (64, 64, 3, 3), s1, p1, d1, 1, (20, 20), nchwc=0) == oracle.KERNEL_WINOGRAD
+    assert K((1, 64, 160, 160), (64, 64, 3, 3), s1, p1, d1, 1, (160, 160), nchwc=0) == oracle.KERNEL_IM2COL
+    assert K((1, 64, 40, 40), (64, 64, 3, 3), (2, 2), p1, d1, 1, (20, 20), nchwc=0) == oracle.KERNEL_IM2COL
+    assert K((1, 64, 20, 20), (64, 64, 3, 3), s1, p1, d1, 1, (20, 20), winograd=0, nchwc=0) == oracle.KERNEL_IM2COL
+    assert K((1, 32, 20, 20), (32, 1, 3, 3), s1, p1, d1, 32, (20, 20), nchwc=0) == oracle.KERNEL_DEPTHWISE
 
 
 # ----------------------------------------------------------- activations
