@@ -27,8 +27,10 @@ issued one by one; `--eager` makes that the value); `roofline` prices the
 dominant kernel against the MI355X peak, with the HBM bytes per launch the
 committed rocprofv3 counter summaries give; `cpu_baseline` times the CPU
 oracle (a C restatement of the reference's CPU kernels, in the order the
-reference's kernel for that shape uses on an AVX-512 host) on this host at 4
-threads and at all available cores.
+reference's kernel for that shape uses on an AVX-512 host; the NCHWc layers
+through a blocked AVX-512 restatement of NchwcConv) on this host at 4
+threads and at all available cores, beside the reference's own published
+figure where it has one.
 """
 from __future__ import annotations
 
@@ -135,7 +137,9 @@ class ConvWorkload(Workload):
         p = self.p
         k = oracle.conv_reference_kernel(self.x_np.shape, self.w_np.shape, (p.sh, p.sw), (p.pt, p.pl),
                                          (p.dh, p.dw), p.group, (p.oh, p.ow))
-        return {oracle.KERNEL_NCHWC: "NchwcConv chain (ib -> ky -> kx -> lane16, NchwcConv.cs:533-605)",
+        return {oracle.KERNEL_NCHWC: "NchwcConv chain (ib -> ky -> kx -> lane16, NchwcConv.cs:533-605)"
+                                     + (", blocked AVX-512 kernel with its reorders (NchwcConv.cs:247-665)"
+                                        if oracle.nchwc_avx512_ok() else ", scalar loop (no AVX-512 here)"),
                 oracle.KERNEL_WINOGRAD: "Winograd F(2x2,3x3) (Winograd.cs)",
                 oracle.KERNEL_DEPTHWISE: "DepthwiseConv (ky -> kx)"}.get(
             k, "im2col / pointwise GEMM chain (ic -> ky -> kx, ConvKernels.cs:464-563)")
@@ -461,7 +465,16 @@ def time_gpu(wl, steps, warmup, graph=True, marks=False):
 
 
 CPU_LABEL = "C++ restatement of OnnxSharp CPU kernels, not the C# binary"
-CPU_IMPL = "oracle/osh_oracle.c: C, gcc -O3 -mavx2 -mfma -ffp-contract=off, explicit fmaf chains, pthreads"
+CPU_IMPL = ("oracle/osh_oracle.c: C, gcc -O3 -mavx2 -mfma -ffp-contract=off, explicit fmaf chains, pthreads; "
+            "the NCHWc-gate 3x3 layers through the blocked AVX-512 restatement of NchwcConv (input reorder, "
+            "2 output blocks x 8 pixels per step, output reorder) where the host has AVX-512")
+# The reference's own published CPU figures for these workloads (4 threads,
+# its AVX-512 host), printed beside the port's timing.
+REFERENCE_PUBLISHED = {
+    "c2": {"ms_per_step": 4.28, "reorder_ms": 0.24, "threads": 4,
+           "source": "bench.md:1977 (NchwcConv 64->64 160x160, 220.6 GMAC/s; input/output reorder 0.24 ms beside)"},
+    "c4": {"ms_per_frame": 30.4, "threads": 4, "source": "bench.md:3108 (yolo11n 640x640 median, onnxsharp)"},
+}
 # CPU seconds per thread count: the headline gets the longest sample
 CPU_BUDGET = {"c2": 10.0, "c3b": 4.0, "c4": 4.0, "c1": 2.0, "c3a": 2.0, "c3c": 2.0, "c5": 2.0}
 CONFIGS = ("c1", "c2", "c3a", "c3b", "c3c", "c4", "c5")
@@ -498,6 +511,7 @@ def cpu_leg(wl, budget_s, hi):
     v4, n4, el4, t4 = cpu_baseline(wl, 4, budget_s)
     cpu = {"value": round(v4, 5), "unit": unit, "cores": 4, "kind": "port",
            "label": CPU_LABEL, "impl": CPU_IMPL, "order": wl.cpu_order(oracle),
+           "avx512_nchwc": bool(oracle.nchwc_avx512_ok()),
            "ms_per_step_median": round(float(np.median(t4)), 3), "ms_per_step_min": round(min(t4), 3),
            "sample": f"{n4} full steps of the same workload in {el4:.1f} s (4 threads)"}
     allc = int(min(hi.get("affinity_cpus") or 4, hi.get("physical_cores") or 4))
@@ -506,6 +520,8 @@ def cpu_leg(wl, budget_s, hi):
         cpu["all_cores"] = {"value": round(va, 5), "cores": allc,
                             "ms_per_step_median": round(float(np.median(ta)), 3),
                             "ms_per_step_min": round(min(ta), 3), "sample": f"{na} steps in {ela:.1f} s"}
+    if wl.name in REFERENCE_PUBLISHED:
+        cpu["reference_published"] = REFERENCE_PUBLISHED[wl.name]
     return cpu
 
 

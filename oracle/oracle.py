@@ -63,6 +63,10 @@ def lib():
                                _fp, _i32p, _fp, C.c_int, _fp, _ip]
         l.orc_matmul_integer.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, _ip, C.c_int, _i32p]
         l.orc_set_threads.argtypes = [C.c_int]
+        l.orc_nchwc_pack_weights.argtypes = [C.c_int, C.c_int, _fp, _fp]
+        l.orc_nchwc_scratch_floats.argtypes = [C.c_int] * 7 + [C.POINTER(C.c_long)] * 2
+        l.orc_nchwc_conv_avx512.argtypes = [C.c_int] * 7 + [_fp] * 6
+        l.orc_nchwc_conv_avx512.restype = C.c_int
         _lib = l
     return _lib
 
@@ -140,6 +144,61 @@ def conv2d_f32(x, w, bias, strides, pads, dilations, group, out_hw, order=ORDER_
                               dilations[1], pads[0], pads[1], OH, OW, _f(x), _f(w), _f(bias), _f(y))
     if rc != 0:
         raise ValueError("NCHWc order needs C/group % 16 == 0")
+    return y
+
+
+def nchwc_avx512_ok() -> bool:
+    """Whether this host runs the AVX-512 restatement of NchwcConv."""
+    return bool(lib().orc_nchwc_avx512_ok())
+
+
+_nchwc_packs = {}    # id(weights) -> (weakref to the weights, packed copy)
+_nchwc_scratch = {}  # (role, element count) -> reusable blocked buffer
+
+
+def _nchwc_packed(w):
+    """The weights in NchwcConv.PackWeights' layout, packed once per weight
+    array (the reference caches the packing on the weight tensor; weights
+    are not changed in place)."""
+    import weakref
+    hit = _nchwc_packs.get(id(w))
+    if hit is not None and hit[0]() is w:
+        return hit[1]
+    M, Cc = w.shape[:2]
+    wp = np.empty(M * Cc * 9, np.float32)
+    lib().orc_nchwc_pack_weights(Cc, M, _f(_c32(w)), _f(wp))
+    try:
+        _nchwc_packs[id(w)] = (weakref.ref(w), wp)
+    except TypeError:  # an array that takes no weak reference: packed each time
+        pass
+    return wp
+
+
+def _scratch(role, n):
+    """A reusable float buffer of n elements (the reference's temp pool)."""
+    buf = _nchwc_scratch.get((role, n))
+    if buf is None:
+        buf = _nchwc_scratch[(role, n)] = np.empty(max(1, n), np.float32)
+    return buf
+
+
+def conv_nchwc_avx512(x, w, bias, stride, out_hw):
+    """The NCHWc chain through the blocked AVX-512 restatement of NchwcConv
+    (orc_nchwc_conv_avx512): bit-identical to conv2d_f32(order=ORDER_NCHWC)
+    for the shapes the reference's NCHWc gate takes (batch 1, 3x3, pad 1,
+    stride 1 or 2); the input and output reorders run per call, the weight
+    packing once, as in the reference."""
+    x, bias = _c32(x), _c32(bias)
+    _, Cc, H, W = x.shape
+    M = w.shape[0]
+    OH, OW = out_hw
+    nx, ny = C.c_long(), C.c_long()
+    lib().orc_nchwc_scratch_floats(Cc, H, W, M, stride, OH, OW, C.byref(nx), C.byref(ny))
+    y = np.empty((1, M, OH, OW), np.float32)
+    rc = lib().orc_nchwc_conv_avx512(Cc, H, W, M, stride, OH, OW, _f(x), _f(_nchwc_packed(w)), _f(bias), _f(y),
+                                     _f(_scratch("in", nx.value)), _f(_scratch("out", ny.value)))
+    if rc != 0:
+        raise ValueError("NCHWc AVX-512 kernel: shape outside the NCHWc gate, or no AVX-512")
     return y
 
 
@@ -225,10 +284,15 @@ def conv_reference_kernel(x_shape, w_shape, strides, pads, dilations, group, out
     return KERNEL_IM2COL
 
 
-def conv_reference(x, w, bias, strides, pads, dilations, group, out_hw, winograd=1, wino_max=4096, nchwc=1):
+def conv_reference(x, w, bias, strides, pads, dilations, group, out_hw, winograd=1, wino_max=4096, nchwc=1,
+                   fast=True):
     """Conv output (before the fused activation) of the reference kernel
-    conv_reference_kernel picks for the shape."""
+    conv_reference_kernel picks for the shape.  With `fast` the NCHWc shapes
+    run the blocked AVX-512 restatement where the host has AVX-512 (the same
+    bits as the scalar NCHWc-order loop, which fast=False runs)."""
     k = conv_reference_kernel(x.shape, w.shape, strides, pads, dilations, group, out_hw, winograd, wino_max, nchwc)
+    if k == KERNEL_NCHWC and fast and nchwc_avx512_ok():
+        return conv_nchwc_avx512(x, w, bias, strides[0], out_hw)
     if k == KERNEL_DEPTHWISE:
         return conv_dw_f32(x, w, bias, strides, pads, dilations, out_hw)
     if k == KERNEL_WINOGRAD:

@@ -19,6 +19,8 @@
  *                       (ic -> ky -> kx fmaf chain from the bias; also PackedConv.cs:420-440,
  *                       Pointwise ConvKernels.cs:464-514, FirstConv.cs:351-420)
  *                       order ORC_ORDER_NCHWC: NchwcConv.cs:533-605 (icb -> ky -> kx -> lane16)
+ *   orc_nchwc_conv_avx512  NchwcConv.cs:247-665 (blocked layouts, 2 output blocks x 8 pixels
+ *                       per step, AVX-512; the same chain as ORC_ORDER_NCHWC)
  *   orc_conv2d_f64      ConvKernels.cs:656-754 (textbook direct conv, in double)
  *   orc_conv_dw_f32     DepthwiseConv.cs:95-185 (bias, then ky -> kx fmaf)
  *   orc_winograd_f23    Winograd.cs:125-166 (G g G^T), :414-443 (B^T d B), :234-258 (16 GEMMs),
@@ -279,6 +281,173 @@ ORC_API int orc_conv2d_f32(int order, int N, int C, int H, int W, int M, int KH,
     cx.y = y;
     parallel_for((long)N * M * OH, conv_planes, &cx);
     free(xp);
+    return 0;
+}
+
+/* ------------------------------------------------ NCHWc blocked, AVX-512 */
+
+/* The reference's NchwcConv as it runs on an AVX-512 host (NchwcConv.cs:247-665),
+ * restated with AVX-512 intrinsics: the cpu_baseline's fast path for the
+ * shapes the NCHWc gate takes, bit-identical to orc_conv2d_f32's
+ * ORC_ORDER_NCHWC (the same per-element fused multiply-add chain from the
+ * bias, ib -> ky -> kx -> input lane; checked by the CPU tests).
+ *   weights  [M/16][C/16][ky*3 + kx][input lane 16][output lane 16], packed once
+ *            (NchwcConv.PackWeights, :247-274; the reference caches it on the
+ *            weight tensor);
+ *   input    [C/16][H + pad][W + pad][16], pad 2 at stride 1 (a zero ring), 1 at
+ *            stride 2 (top row and left column), repacked per call (PackInput,
+ *            :289-368);
+ *   output   [M/16][OH][OW][16], then back to NCHW (UnpackOutput, :370-412);
+ *   kernel   per (pair of output blocks, output row): groups of 8 pixels x 2
+ *            output blocks = 16 accumulators of 16 lanes, each lane step one
+ *            broadcast input value against a 16-wide weight row (Row, :508-665);
+ *            the last OW % 8 pixels one at a time.
+ * Threads split (block pair, row) tasks as ParallelRange.For does in Conv
+ * (:462-505).  Built only into functions with the avx512f target; callers
+ * check orc_nchwc_avx512_ok() first. */
+#include <immintrin.h>
+
+ORC_API int orc_nchwc_avx512_ok(void)
+{
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f");
+}
+
+/* w: OIHW [M][C][3][3] -> wp [M/16][C/16][9][16][16] */
+ORC_API void orc_nchwc_pack_weights(int C, int M, const float *w, float *wp)
+{
+    const int ib = C / 16;
+    for (int o = 0; o < M; o++)
+        for (int i = 0; i < C; i++)
+            for (int kp = 0; kp < 9; kp++)
+                wp[((((long)(o / 16) * ib + i / 16) * 9 + kp) * 16 + i % 16) * 16 + o % 16] =
+                    w[((long)o * C + i) * 9 + kp];
+}
+
+typedef struct {
+    int C, H, W, M, stride, OH, OW, pad, Hp, Wp;
+    const float *x, *wp, *bias;
+    float *xb, *yb, *y;
+} nchwc_ctx;
+
+/* task = (input block, padded row): NCHW rows into the blocked buffer, halo zero */
+__attribute__((target("avx512f,fma"))) static void nchwc_pack_rows(void *p, long t0, long t1)
+{
+    nchwc_ctx *c = (nchwc_ctx *)p;
+    const long plane = (long)c->H * c->W;
+    for (long t = t0; t < t1; t++) {
+        const int cb = (int)(t / c->Hp), r = (int)(t % c->Hp);
+        float *dst = c->xb + ((long)cb * c->Hp + r) * c->Wp * 16;
+        const int y = r - 1;
+        if (y < 0 || y >= c->H) {
+            memset(dst, 0, sizeof(float) * 16 * c->Wp);
+            continue;
+        }
+        _mm512_storeu_ps(dst, _mm512_setzero_ps());
+        if (c->pad == 2) _mm512_storeu_ps(dst + (long)(c->W + 1) * 16, _mm512_setzero_ps());
+        const float *src = c->x + (long)cb * 16 * plane + (long)y * c->W;
+        for (int xx = 0; xx < c->W; xx++) {
+            float *d = dst + (long)(xx + 1) * 16;
+            for (int lane = 0; lane < 16; lane++) d[lane] = src[lane * plane + xx];
+        }
+    }
+}
+
+/* task = (output block pair, output row) */
+__attribute__((target("avx512f,fma"))) static void nchwc_rows(void *p, long t0, long t1)
+{
+    nchwc_ctx *c = (nchwc_ctx *)p;
+    const int icb = c->C / 16, s = c->stride, OW = c->OW, OH = c->OH;
+    const long wblk = (long)icb * 9 * 256; /* floats of one output block's weights */
+    for (long t = t0; t < t1; t++) {
+        const int row = (int)(t % OH), ob = (int)(t / OH) * 2;
+        const __m512 b0 = c->bias ? _mm512_loadu_ps(c->bias + (long)ob * 16) : _mm512_setzero_ps();
+        const __m512 b1 = c->bias ? _mm512_loadu_ps(c->bias + (long)(ob + 1) * 16) : _mm512_setzero_ps();
+        const float *w0 = c->wp + (long)ob * wblk, *w1 = w0 + wblk;
+        float *o0 = c->yb + ((long)ob * OH + row) * OW * 16, *o1 = o0 + (long)OH * OW * 16;
+        const int groups = OW / 8;
+        for (int g = 0; g < groups; g++) {
+            __m512 a0[8], a1[8];
+            for (int q = 0; q < 8; q++) a0[q] = b0, a1[q] = b1;
+            for (int ib = 0; ib < icb; ib++)
+                for (int ky = 0; ky < 3; ky++) {
+                    const float *rin = c->xb + (((long)ib * c->Hp + (long)row * s + ky) * c->Wp + (long)g * 8 * s) * 16;
+                    for (int kx = 0; kx < 3; kx++) {
+                        const float *wp0 = w0 + (long)(ib * 9 + ky * 3 + kx) * 256;
+                        const float *wp1 = w1 + (long)(ib * 9 + ky * 3 + kx) * 256;
+                        const float *px = rin + kx * 16;
+                        for (int lane = 0; lane < 16; lane++) {
+                            const __m512 wv0 = _mm512_loadu_ps(wp0 + lane * 16);
+                            const __m512 wv1 = _mm512_loadu_ps(wp1 + lane * 16);
+                            for (int q = 0; q < 8; q++) {
+                                const __m512 xv = _mm512_set1_ps(px[(long)q * s * 16 + lane]);
+                                a0[q] = _mm512_fmadd_ps(xv, wv0, a0[q]);
+                                a1[q] = _mm512_fmadd_ps(xv, wv1, a1[q]);
+                            }
+                        }
+                    }
+                }
+            for (int q = 0; q < 8; q++) {
+                _mm512_storeu_ps(o0 + ((long)g * 8 + q) * 16, a0[q]);
+                _mm512_storeu_ps(o1 + ((long)g * 8 + q) * 16, a1[q]);
+            }
+        }
+        for (int col = groups * 8; col < OW; col++) {
+            __m512 a = b0, b = b1;
+            for (int ib = 0; ib < icb; ib++)
+                for (int ky = 0; ky < 3; ky++)
+                    for (int kx = 0; kx < 3; kx++) {
+                        const float *wp0 = w0 + (long)(ib * 9 + ky * 3 + kx) * 256;
+                        const float *wp1 = w1 + (long)(ib * 9 + ky * 3 + kx) * 256;
+                        const float *px =
+                            c->xb + (((long)ib * c->Hp + (long)row * s + ky) * c->Wp + (long)col * s + kx) * 16;
+                        for (int lane = 0; lane < 16; lane++) {
+                            const __m512 xv = _mm512_set1_ps(px[lane]);
+                            a = _mm512_fmadd_ps(xv, _mm512_loadu_ps(wp0 + lane * 16), a);
+                            b = _mm512_fmadd_ps(xv, _mm512_loadu_ps(wp1 + lane * 16), b);
+                        }
+                    }
+            _mm512_storeu_ps(o0 + (long)col * 16, a);
+            _mm512_storeu_ps(o1 + (long)col * 16, b);
+        }
+    }
+}
+
+/* task = (output block, output row): blocked rows back to NCHW */
+static void nchwc_unpack_rows(void *p, long t0, long t1)
+{
+    nchwc_ctx *c = (nchwc_ctx *)p;
+    const long plane = (long)c->OH * c->OW;
+    for (long t = t0; t < t1; t++) {
+        const int ob = (int)(t / c->OH), row = (int)(t % c->OH);
+        const float *src = c->yb + ((long)ob * c->OH + row) * c->OW * 16;
+        float *dst = c->y + (long)ob * 16 * plane + (long)row * c->OW;
+        for (int lane = 0; lane < 16; lane++)
+            for (int col = 0; col < c->OW; col++) dst[lane * plane + col] = src[(long)col * 16 + lane];
+    }
+}
+
+/* Bytes of the blocked input and output buffers the conv needs. */
+ORC_API void orc_nchwc_scratch_floats(int C, int H, int W, int M, int stride, int OH, int OW, long *xb, long *yb)
+{
+    const int pad = stride == 2 ? 1 : 2;
+    *xb = (long)C * (H + pad) * (W + pad);
+    *yb = (long)M * OH * OW;
+}
+
+/* Batch-1 NCHW conv through the blocked kernel.  Returns -1 outside the
+ * reference's NCHWc gate (NchwcConv.Dispatch, :129-143) or without AVX-512. */
+ORC_API int orc_nchwc_conv_avx512(int C, int H, int W, int M, int stride, int OH, int OW, const float *x,
+                                  const float *wp, const float *bias, float *y, float *xb, float *yb)
+{
+    if (!orc_nchwc_avx512_ok() || C % 16 || M % 32 || (stride != 1 && stride != 2)) return -1;
+    if (stride == 2 ? (H % 2 || W % 2 || OH * 2 != H || OW * 2 != W) : (OH != H || OW != W)) return -1;
+    nchwc_ctx c = {C, H, W, M, stride, OH, OW, stride == 2 ? 1 : 2, 0, 0, x, wp, bias, xb, yb, y};
+    c.Hp = H + c.pad;
+    c.Wp = W + c.pad;
+    parallel_for((long)(C / 16) * c.Hp, nchwc_pack_rows, &c);
+    parallel_for((long)(M / 32) * OH, nchwc_rows, &c);
+    parallel_for((long)(M / 16) * OH, nchwc_unpack_rows, &c);
     return 0;
 }
 

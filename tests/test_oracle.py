@@ -626,3 +626,54 @@ def test_attention_matches_float64_and_catches_a_qk_swap(oracle):
     # the planted mistake: q and k exchanged gives attn^T's softmax, far off
     bad = _attention_f64(qkv, heads, key_dim, head_dim, n, op.scale, swap_qk=True)
     assert np.abs(got - bad).max() > 1e-2
+
+
+# ----------------------------------------------------------- the blocked AVX-512 NCHWc restatement
+
+NCHWC_FAST_CASES = [  # (C, H, W, M, stride, bias)
+    (64, 40, 40, 64, 1, True),      # C2's layer at a quarter of the map
+    (128, 40, 40, 256, 2, True),    # C3b's layer at half the map
+    (32, 18, 22, 64, 1, True),      # a row tail (22 = 2 x 8 + 6)
+    (16, 40, 36, 32, 2, False),     # stride 2, tail, no bias
+    (48, 7, 9, 96, 1, True),        # a map narrower than one 8-pixel group on the last row part
+]
+
+
+@pytest.mark.parametrize("case", NCHWC_FAST_CASES, ids=[str(c) for c in NCHWC_FAST_CASES])
+@pytest.mark.parametrize("threads", [1, 3])
+def test_nchwc_avx512_is_the_nchwc_chain(oracle, case, threads):
+    # orc_nchwc_conv_avx512 (blocked input and weights, 2 output blocks x 8
+    # pixels a step, the reference's NchwcConv.Row structure) against the scalar
+    # loop in the same ib -> ky -> kx -> lane order: the same bits
+    if not oracle.nchwc_avx512_ok():
+        pytest.skip("no AVX-512 on this host")
+    cin, h, w_, m, s, with_bias = case
+    x = synth.uniform(31 + cin, (1, cin, h, w_))
+    w = synth.normal(32 + m, (m, cin, 3, 3), 0, 0.05)
+    b = synth.normal(33, (m,), 0, 0.01) if with_bias else None
+    oh, ow = (h, w_) if s == 1 else (h // 2, w_ // 2)
+    old = oracle.lib().orc_get_threads()
+    oracle.set_threads(threads)
+    try:
+        fast = oracle.conv_nchwc_avx512(x, w, b, s, (oh, ow))
+        ref = oracle.conv2d_f32(x, w, b, (s, s), (1, 1), (1, 1), 1, (oh, ow), order=oracle.ORDER_NCHWC)
+        via = oracle.conv_reference(x, w, b, (s, s), (1, 1), (1, 1), 1, (oh, ow))
+    finally:
+        oracle.set_threads(old)
+    assert np.array_equal(fast.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(via.view(np.uint32), ref.view(np.uint32))  # conv_reference takes the fast path
+
+
+@pytest.mark.parametrize("case", range(len(PLANTED)))
+def test_nchwc_avx512_order_pinned_by_planted_magnitudes(oracle, case):
+    # the planted terms on a 3x3 map with pad 1 (the gate's padding): the
+    # centre output pixel of channel 0 sees every tap, so it must give the
+    # hand-derived NCHWc value, not one of the wrong orders'
+    if not oracle.nchwc_avx512_ok():
+        pytest.skip("no AVX-512 on this host")
+    terms, want = PLANTED[case]
+    x, w1 = _planted(terms)
+    w = np.zeros((32, 32, 3, 3), np.float32)
+    w[0] = w1[0]
+    y = oracle.conv_nchwc_avx512(x, w, np.zeros(32, np.float32), 1, (3, 3))
+    assert y[0, 0, 1, 1] == np.float32(want["nchwc"])
