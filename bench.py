@@ -194,7 +194,7 @@ class DqmmWorkload(Workload):
         from onnxsharp_amd import native as N, synth
         from onnxsharp_amd.layers import DynamicQuantizeMatMulLayer
         self.name = "c5"
-        self.kernel = "dqmm_fused_kernel"
+        self.kernel = "dqmm_fused"  # the quantize + GEMM launch (of whichever tile shape)
         self.dtype = "int8"
         self.bound = "hbm"
         m, k, n = 512, 512, 2048

@@ -63,6 +63,8 @@ def lib():
                                _fp, _i32p, _fp, C.c_int, _fp, _ip]
         l.orc_matmul_integer.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, _ip, C.c_int, _i32p]
         l.orc_set_threads.argtypes = [C.c_int]
+        l.orc_gemm_f32_rows.argtypes = l.orc_gemm_f32.argtypes
+        l.orc_unary_scalar.argtypes = [C.c_int, C.c_long, _fp, _fp]
         l.orc_nchwc_pack_weights.argtypes = [C.c_int, C.c_int, _fp, _fp]
         l.orc_nchwc_scratch_floats.argtypes = [C.c_int] * 7 + [C.POINTER(C.c_long)] * 2
         l.orc_nchwc_conv_avx512.argtypes = [C.c_int] * 7 + [_fp] * 6
@@ -96,6 +98,27 @@ def gemm_f32(a, b, row_bias=None, col_bias=None, col_scale=None, fused=True):
     lib().orc_gemm_f32(m, k, n, _f(a), k, _f(b), n, _f(row_bias), _f(col_bias), _f(col_scale), _f(c), n,
                        1 if fused else 0)
     return c
+
+
+def gemm_f32_rows(a, b, row_bias=None, col_bias=None, col_scale=None, fused=True):
+    """gemm_f32 on the scalar row loop only (the blocked AVX-512 path of
+    gemm_f32 gives the same bits; this is its check)."""
+    a, b = _c32(a), _c32(b)
+    row_bias, col_bias, col_scale = _c32(row_bias), _c32(col_bias), _c32(col_scale)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), np.float32)
+    lib().orc_gemm_f32_rows(m, k, n, _f(a), k, _f(b), n, _f(row_bias), _f(col_bias), _f(col_scale), _f(c), n,
+                            1 if fused else 0)
+    return c
+
+
+def unary_scalar(op, x):
+    """exp_ref (op 0), SiLU (1) or sigmoid (2) on the scalar loop only."""
+    x = _c32(x)
+    y = np.empty_like(x)
+    lib().orc_unary_scalar(op, x.size, _f(x), _f(y))
+    return y
 
 
 def gemm_ex(a, b, c=None, alpha=1.0, beta=1.0, trans_a=False, trans_b=False):
@@ -293,6 +316,15 @@ def conv_reference(x, w, bias, strides, pads, dilations, group, out_hw, winograd
     k = conv_reference_kernel(x.shape, w.shape, strides, pads, dilations, group, out_hw, winograd, wino_max, nchwc)
     if k == KERNEL_NCHWC and fast and nchwc_avx512_ok():
         return conv_nchwc_avx512(x, w, bias, strides[0], out_hw)
+    if (k == KERNEL_IM2COL and fast and group == 1 and w.shape[2:] == (1, 1) and tuple(strides) == (1, 1)
+            and tuple(pads) == (0, 0) and tuple(out_hw) == tuple(x.shape[2:])):
+        # a pointwise conv is GemmKernel.Multiply(W[M x C], X[C x HW], rowBias)
+        # (ConvKernels.cs:464-514): the GEMM chain, the same bits as the
+        # im2col loop over input channels
+        n, cin, h, wd = x.shape
+        wm = _c32(w.reshape(w.shape[0], cin))
+        xs = _c32(x).reshape(n, cin, h * wd)
+        return np.stack([gemm_f32(wm, xs[i], row_bias=bias) for i in range(n)]).reshape(n, w.shape[0], h, wd)
     if k == KERNEL_DEPTHWISE:
         return conv_dw_f32(x, w, bias, strides, pads, dilations, out_hw)
     if k == KERNEL_WINOGRAD:

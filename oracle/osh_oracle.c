@@ -43,6 +43,7 @@
  *
  * Build: see oracle/Makefile (gcc, -O3 -ffp-contract=off; fmaf is explicit).
  */
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdint.h>
@@ -64,6 +65,18 @@ ORC_API int orc_cpu_ok(void)
     return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
 }
 
+/* Whether this host runs the AVX-512 paths (the NCHWc kernel, the blocked
+ * GEMM, the vector activations); each is bit-identical to its scalar loop. */
+static int g_avx512 = -1;
+static int have_avx512(void)
+{
+    if (g_avx512 < 0) {
+        __builtin_cpu_init();
+        g_avx512 = __builtin_cpu_supports("avx512f") ? 1 : 0;
+    }
+    return g_avx512;
+}
+
 ORC_API void orc_set_threads(int t) { g_threads = t < 1 ? 1 : t; }
 ORC_API int orc_get_threads(void) { return g_threads; }
 
@@ -75,10 +88,37 @@ typedef struct {
     long begin, end;
 } job_t;
 
-static void *job_main(void *p)
+/* A persistent pool of worker threads (as ParallelRange keeps its workers,
+ * src/OnnxSharp/Threading/ParallelRange.cs:15-373): created on first use,
+ * woken per parallel_for by a generation counter, joined by a countdown.
+ * Creating threads per call cost tens of microseconds each, which the many
+ * small layers of a whole network paid a hundred times per frame. */
+#define POOL_MAX 256
+static pthread_mutex_t pool_mu = PTHREAD_MUTEX_INITIALIZER;
+static pthread_mutex_t pool_call_mu = PTHREAD_MUTEX_INITIALIZER; /* one parallel_for at a time */
+static pthread_cond_t pool_wake = PTHREAD_COND_INITIALIZER;
+static pthread_cond_t pool_done = PTHREAD_COND_INITIALIZER;
+static int pool_started = 0;  /* workers 1 .. pool_started exist */
+static long pool_gen = 0;
+static int pool_active = 0;   /* threads of the current job, the caller included */
+static int pool_pending = 0;  /* workers of the current job not finished */
+static job_t pool_jobs[POOL_MAX];
+
+static void *pool_worker(void *arg)
 {
-    job_t *j = (job_t *)p;
-    j->fn(j->ctx, j->begin, j->end);
+    const int id = (int)(intptr_t)arg;
+    long seen = 0;
+    pthread_mutex_lock(&pool_mu);
+    for (;;) {
+        while (pool_gen == seen) pthread_cond_wait(&pool_wake, &pool_mu);
+        seen = pool_gen;
+        if (id >= pool_active) continue;
+        job_t j = pool_jobs[id];
+        pthread_mutex_unlock(&pool_mu);
+        j.fn(j.ctx, j.begin, j.end);
+        pthread_mutex_lock(&pool_mu);
+        if (--pool_pending == 0) pthread_cond_signal(&pool_done);
+    }
     return NULL;
 }
 
@@ -93,21 +133,36 @@ static void parallel_for(long n, range_fn fn, void *ctx)
         return;
     }
     if (t > n) t = (int)n;
-    pthread_t th[256];
-    job_t jobs[256];
-    if (t > 256) t = 256;
+    if (t > POOL_MAX) t = POOL_MAX;
+    pthread_mutex_lock(&pool_call_mu);
+    pthread_mutex_lock(&pool_mu);
+    while (pool_started < t - 1) {
+        pthread_t th;
+        if (pthread_create(&th, NULL, pool_worker, (void *)(intptr_t)(pool_started + 1)) != 0) break;
+        pthread_detach(th);
+        pool_started++;
+    }
+    if (t > pool_started + 1) t = pool_started + 1;
     long base = n / t, rem = n % t, at = 0;
     for (int i = 0; i < t; i++) {
         long len = base + (i < rem ? 1 : 0);
-        jobs[i].fn = fn;
-        jobs[i].ctx = ctx;
-        jobs[i].begin = at;
-        jobs[i].end = at + len;
+        pool_jobs[i].fn = fn;
+        pool_jobs[i].ctx = ctx;
+        pool_jobs[i].begin = at;
+        pool_jobs[i].end = at + len;
         at += len;
     }
-    for (int i = 1; i < t; i++) pthread_create(&th[i], NULL, job_main, &jobs[i]);
-    job_main(&jobs[0]);
-    for (int i = 1; i < t; i++) pthread_join(th[i], NULL);
+    pool_active = t;
+    pool_pending = t - 1;
+    pool_gen++;
+    pthread_cond_broadcast(&pool_wake);
+    job_t j0 = pool_jobs[0];
+    pthread_mutex_unlock(&pool_mu);
+    j0.fn(j0.ctx, j0.begin, j0.end);
+    pthread_mutex_lock(&pool_mu);
+    while (pool_pending > 0) pthread_cond_wait(&pool_done, &pool_mu);
+    pthread_mutex_unlock(&pool_mu);
+    pthread_mutex_unlock(&pool_call_mu);
 }
 
 /* --------------------------------------------------------------------- GEMM */
@@ -152,12 +207,85 @@ HOT static void gemm_rows(void *p, long r0, long r1)
     }
 }
 
+/* The same chain register-blocked on AVX-512, as the reference's MR12
+ * micro-kernel runs it over packed B panels (GemmKernel.cs:418-526,
+ * 1070-1207): a task is one 32-column block of C; its B columns are copied
+ * into a contiguous [k][32] panel once, then every 8-row block of C runs
+ * against it with 16 accumulators of 16 lanes initialised from the bias --
+ * per k step two 16-wide panel rows against eight broadcast values of A, one
+ * fused multiply-add each.  Every element is the fmaf chain gemm_rows
+ * computes, so the same bits.  Column tails use masked lanes.  No column
+ * scale here. */
+__attribute__((target("avx512f,fma"))) static void gemm_blocks(void *p, long t0, long t1)
+{
+    const gemm_ctx *g = (const gemm_ctx *)p;
+    const int k = g->k;
+    float *panel = (float *)aligned_alloc(64, sizeof(float) * 32 * (size_t)(k > 0 ? k : 1));
+    for (long t = t0; t < t1; t++) {
+        const int j0 = (int)t * 32;
+        const int c0 = g->n - j0 < 16 ? g->n - j0 : 16, c1 = g->n - j0 - 16 < 16 ? g->n - j0 - 16 : 16;
+        const __mmask16 m0 = c0 >= 16 ? 0xFFFF : (__mmask16)((1u << c0) - 1);
+        const __mmask16 m1 = c1 <= 0 ? 0 : c1 >= 16 ? 0xFFFF : (__mmask16)((1u << c1) - 1);
+        for (int kk = 0; kk < k; kk++) {
+            const float *brow = g->b + (long)kk * g->ldb + j0;
+            _mm512_store_ps(panel + (long)kk * 32, _mm512_maskz_loadu_ps(m0, brow));
+            _mm512_store_ps(panel + (long)kk * 32 + 16, _mm512_maskz_loadu_ps(m1, brow + 16));
+        }
+        for (int i0 = 0; i0 < g->m; i0 += 8) {
+            const int rows = g->m - i0 < 8 ? g->m - i0 : 8;
+            __m512 acc0[8], acc1[8];
+            const float *arow[8];
+#pragma GCC unroll 8
+            for (int r = 0; r < 8; r++) {
+                arow[r] = g->a + (long)(i0 + (r < rows ? r : 0)) * g->lda;
+                if (g->col_bias) {
+                    acc0[r] = _mm512_maskz_loadu_ps(m0, g->col_bias + j0);
+                    acc1[r] = _mm512_maskz_loadu_ps(m1, g->col_bias + j0 + 16);
+                } else {
+                    const float rb = (g->row_bias && r < rows) ? g->row_bias[i0 + r] : 0.0f;
+                    acc0[r] = acc1[r] = _mm512_set1_ps(rb);
+                }
+            }
+            for (int kk = 0; kk < k; kk++) {
+                const __m512 b0 = _mm512_load_ps(panel + (long)kk * 32), b1 = _mm512_load_ps(panel + (long)kk * 32 + 16);
+#pragma GCC unroll 8
+                for (int r = 0; r < 8; r++) {
+                    const __m512 av = _mm512_set1_ps(arow[r][kk]);
+                    acc0[r] = _mm512_fmadd_ps(av, b0, acc0[r]);
+                    acc1[r] = _mm512_fmadd_ps(av, b1, acc1[r]);
+                }
+            }
+            for (int r = 0; r < rows; r++) {
+                float *crow = g->c + (long)(i0 + r) * g->ldc + j0;
+                _mm512_mask_storeu_ps(crow, m0, acc0[r]);
+                _mm512_mask_storeu_ps(crow + 16, m1, acc1[r]);
+            }
+        }
+    }
+    free(panel);
+}
+
 /* C[m,n] (ldc) = A[m,k] (lda) * B[k,n] (ldb) with the reference's bias and
  * column-scale epilogue.  fused=1 is the micro-kernel epilogue (one fmaf),
- * fused=0 the ScaleColumns tail (multiply, then add). */
+ * fused=0 the ScaleColumns tail (multiply, then add).  Without a column
+ * scale the register-blocked AVX-512 path runs where the host has AVX-512. */
 ORC_API void orc_gemm_f32(int m, int k, int n, const float *a, int lda, const float *b, int ldb,
                           const float *row_bias, const float *col_bias, const float *col_scale,
                           float *c, int ldc, int fused)
+{
+    gemm_ctx g = {m, k, n, lda, ldb, ldc, fused, a, b, row_bias, col_bias, col_scale, c};
+    if (!col_scale && have_avx512()) {
+        parallel_for((n + 31) / 32, gemm_blocks, &g);
+        return;
+    }
+    parallel_for(m, gemm_rows, &g);
+}
+
+/* The same product on the scalar loop only (gemm_rows), for checking the
+ * blocked path against it. */
+ORC_API void orc_gemm_f32_rows(int m, int k, int n, const float *a, int lda, const float *b, int ldb,
+                               const float *row_bias, const float *col_bias, const float *col_scale,
+                               float *c, int ldc, int fused)
 {
     gemm_ctx g = {m, k, n, lda, ldb, ldc, fused, a, b, row_bias, col_bias, col_scale, c};
     parallel_for(m, gemm_rows, &g);
@@ -305,7 +433,6 @@ ORC_API int orc_conv2d_f32(int order, int N, int C, int H, int W, int M, int KH,
  * Threads split (block pair, row) tasks as ParallelRange.For does in Conv
  * (:462-505).  Built only into functions with the avx512f target; callers
  * check orc_nchwc_avx512_ok() first. */
-#include <immintrin.h>
 
 ORC_API int orc_nchwc_avx512_ok(void)
 {
@@ -482,27 +609,45 @@ ORC_API void orc_conv2d_f64(int N, int C, int H, int W, int M, int KH, int KW, i
 /* Depthwise conv (group == C == M, one input channel per group): the
  * accumulator starts at the bias and runs ky -> kx with fmaf (the reference's
  * vector path; its stride>1 path is unfused, a rounding-only difference). */
+typedef struct {
+    int C, H, W, KH, KW, sh, sw, dh, dw, pt, pl, OH, OW;
+    const float *x, *w, *bias;
+    float *y;
+} dw_ctx;
+
+/* task = (image, channel) plane; per output: bias, then ky -> kx fmaf, taps
+ * off the map skipped */
+static void dw_planes(void *p, long t0, long t1)
+{
+    const dw_ctx *d = (const dw_ctx *)p;
+    for (long t = t0; t < t1; t++) {
+        const int c = (int)(t % d->C);
+        const float *xp = d->x + t * (long)d->H * d->W;
+        const float *wc = d->w + (long)c * d->KH * d->KW;
+        float *yp = d->y + t * (long)d->OH * d->OW;
+        for (int oy = 0; oy < d->OH; oy++)
+            for (int ox = 0; ox < d->OW; ox++) {
+                float acc = d->bias ? d->bias[c] : 0.0f;
+                for (int ky = 0; ky < d->KH; ky++) {
+                    int iy = oy * d->sh - d->pt + ky * d->dh;
+                    if (iy < 0 || iy >= d->H) continue;
+                    for (int kx = 0; kx < d->KW; kx++) {
+                        int ix = ox * d->sw - d->pl + kx * d->dw;
+                        if (ix < 0 || ix >= d->W) continue;
+                        acc = fmaf(wc[ky * d->KW + kx], xp[(long)iy * d->W + ix], acc);
+                    }
+                }
+                yp[(long)oy * d->OW + ox] = acc;
+            }
+    }
+}
+
 ORC_API void orc_conv_dw_f32(int N, int C, int H, int W, int KH, int KW, int sh, int sw, int dh, int dw,
                              int pt, int pl, int OH, int OW, const float *x, const float *w,
                              const float *bias, float *y)
 {
-    for (int n = 0; n < N; n++)
-        for (int c = 0; c < C; c++)
-            for (int oy = 0; oy < OH; oy++)
-                for (int ox = 0; ox < OW; ox++) {
-                    float acc = bias ? bias[c] : 0.0f;
-                    for (int ky = 0; ky < KH; ky++) {
-                        int iy = oy * sh - pt + ky * dh;
-                        if (iy < 0 || iy >= H) continue;
-                        for (int kx = 0; kx < KW; kx++) {
-                            int ix = ox * sw - pl + kx * dw;
-                            if (ix < 0 || ix >= W) continue;
-                            acc = fmaf(w[((long)c * KH + ky) * KW + kx],
-                                       x[(((long)n * C + c) * H + iy) * W + ix], acc);
-                        }
-                    }
-                    y[(((long)n * C + c) * OH + oy) * OW + ox] = acc;
-                }
+    dw_ctx d = {C, H, W, KH, KW, sh, sw, dh, dw, pt, pl, OH, OW, x, w, bias, y};
+    parallel_for((long)N * C, dw_planes, &d);
 }
 
 /* Winograd F(2x2, 3x3), stride 1, pad 1 (Winograd.cs).  Output size == input size. */
@@ -623,20 +768,93 @@ static float exp_ref(float x)
     return p * two_n;
 }
 
-ORC_API void orc_exp_ref(long n, const float *x, float *y)
+/* exp_ref on 16 lanes: the same single IEEE operations (max/min against
+ * the constants return the constant for a NaN lane, as fmaxf/fminf do; the
+ * rounding is round-to-nearest-even; n is integral, so its conversion to int
+ * is exact). */
+__attribute__((target("avx512f,fma"))) static __m512 exp_ref16(__m512 x)
 {
-    for (long i = 0; i < n; i++) y[i] = exp_ref(x[i]);
+    x = _mm512_min_ps(_mm512_max_ps(x, _mm512_set1_ps(-87.3f)), _mm512_set1_ps(88.7f));
+    const __m512 n = _mm512_roundscale_ps(_mm512_mul_ps(x, _mm512_set1_ps(1.4426950408889634f)),
+                                          _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+    __m512 r = _mm512_fmadd_ps(n, _mm512_set1_ps(-0.693145751953125f), x);
+    r = _mm512_fmadd_ps(n, _mm512_set1_ps(-1.4286067653e-6f), r);
+    __m512 p = _mm512_set1_ps(1.0f / 720.0f);
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.0f / 120.0f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.0f / 24.0f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.0f / 6.0f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(0.5f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.0f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.0f));
+    const __m512i bits = _mm512_slli_epi32(_mm512_add_epi32(_mm512_cvtps_epi32(n), _mm512_set1_epi32(127)), 23);
+    return _mm512_mul_ps(p, _mm512_castsi512_ps(bits));
+}
+
+enum { UNARY_EXP = 0, UNARY_SILU = 1, UNARY_SIGMOID = 2 };
+
+typedef struct {
+    int op;
+    const float *x;
+    float *y;
+    long n;
+} unary_ctx;
+
+static float unary1(int op, float v)
+{
+    if (op == UNARY_EXP) return exp_ref(v);
+    const float e = exp_ref(v * -1.0f);
+    return op == UNARY_SILU ? v * (1.0f / (1.0f + e)) : 1.0f / (1.0f + e);
+}
+
+__attribute__((target("avx512f,fma"))) static void unary_avx512(const unary_ctx *u, long i0, long i1)
+{
+    const __m512 one = _mm512_set1_ps(1.0f), neg = _mm512_set1_ps(-1.0f);
+    long i = i0;
+    for (; i + 16 <= i1; i += 16) {
+        const __m512 v = _mm512_loadu_ps(u->x + i);
+        __m512 r;
+        if (u->op == UNARY_EXP) {
+            r = exp_ref16(v);
+        } else {
+            const __m512 q = _mm512_div_ps(one, _mm512_add_ps(one, exp_ref16(_mm512_mul_ps(v, neg))));
+            r = u->op == UNARY_SILU ? _mm512_mul_ps(v, q) : q;
+        }
+        _mm512_storeu_ps(u->y + i, r);
+    }
+    for (; i < i1; i++) u->y[i] = unary1(u->op, u->x[i]);
+}
+
+/* chunk c of 8192 elements (TensorOps.ElementWiseUnary splits large tensors
+ * into parallel chunks, TensorOps.cs:281-298; every element's bits are the
+ * same whichever lane or thread computes it) */
+static void unary_chunks(void *p, long c0, long c1)
+{
+    const unary_ctx *u = (const unary_ctx *)p;
+    const long i0 = c0 * 8192, i1 = c1 * 8192 < u->n ? c1 * 8192 : u->n;
+    if (have_avx512()) {
+        unary_avx512(u, i0, i1);
+        return;
+    }
+    for (long i = i0; i < i1; i++) u->y[i] = unary1(u->op, u->x[i]);
+}
+
+static void unary_run(int op, long n, const float *x, float *y)
+{
+    unary_ctx u = {op, x, y, n};
+    parallel_for((n + 8191) / 8192, unary_chunks, &u);
+}
+
+ORC_API void orc_exp_ref(long n, const float *x, float *y) { unary_run(UNARY_EXP, n, x, y); }
+
+/* The scalar loop alone (op 0 exp, 1 SiLU, 2 sigmoid), for checking the
+ * vector path against it. */
+ORC_API void orc_unary_scalar(int op, long n, const float *x, float *y)
+{
+    for (long i = 0; i < n; i++) y[i] = unary1(op, x[i]);
 }
 
 /* SiLU of the vector path: x * (1 / (1 + exp(x * -1))). */
-ORC_API void orc_silu_ref(long n, const float *x, float *y)
-{
-    for (long i = 0; i < n; i++) {
-        float v = x[i];
-        float e = exp_ref(v * -1.0f);
-        y[i] = v * (1.0f / (1.0f + e));
-    }
-}
+ORC_API void orc_silu_ref(long n, const float *x, float *y) { unary_run(UNARY_SILU, n, x, y); }
 
 /* SiLU of the scalar tail (MathF.Exp; here the C library's expf, whose last
  * bit is not pinned against .NET). */
@@ -655,10 +873,7 @@ static float dotnet_max(float a, float b)
 }
 
 /* Sigmoid of the vector path (VectorMath.cs:64-68): 1 / (1 + exp(x * -1)). */
-ORC_API void orc_sigmoid_ref(long n, const float *x, float *y)
-{
-    for (long i = 0; i < n; i++) y[i] = 1.0f / (1.0f + exp_ref(x[i] * -1.0f));
-}
+ORC_API void orc_sigmoid_ref(long n, const float *x, float *y) { unary_run(UNARY_SIGMOID, n, x, y); }
 
 /* DflSoftmax (DflOps.cs:97-240): x [B][sides*bins][N] -> y [B][sides][N],
  * y = sum_b softmax_b(x[side*bins + b]) * b.  The reference works on blocks of

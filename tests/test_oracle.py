@@ -677,3 +677,37 @@ def test_nchwc_avx512_order_pinned_by_planted_magnitudes(oracle, case):
     w[0] = w1[0]
     y = oracle.conv_nchwc_avx512(x, w, np.zeros(32, np.float32), 1, (3, 3))
     assert y[0, 0, 1, 1] == np.float32(want["nchwc"])
+
+
+# ----------------------------------------------------------- the oracle's vector paths equal its scalar loops
+
+@pytest.mark.parametrize("m,k,n,bias", [(1024, 768, 768, "col"), (37, 100, 53, "row"), (128, 256, 6400, "row"),
+                                        (5, 3, 17, None), (9, 40, 33, "col")])
+def test_blocked_gemm_is_the_gemm_chain(oracle, m, k, n, bias):
+    # the register-blocked AVX-512 GEMM (packed 32-column panels, 8 x 32 blocks)
+    # computes every element's k-ascending fmaf chain from the bias: the same
+    # bits as the row loop
+    a = synth.uniform(m + 1, (m, k), -1, 1)
+    b = synth.uniform(n + 2, (k, n), -1, 1)
+    kw = {} if bias is None else {f"{bias}_bias": synth.uniform(3, (n if bias == "col" else m,), -1, 1)}
+    assert np.array_equal(oracle.gemm_f32(a, b, **kw).view(np.uint32), oracle.gemm_f32_rows(a, b, **kw).view(np.uint32))
+
+
+def test_pointwise_conv_through_the_gemm_is_the_im2col_chain(oracle):
+    x = synth.uniform(41, (2, 48, 9, 13))
+    w = synth.normal(42, (40, 48, 1, 1), 0, 0.05)
+    b = synth.normal(43, (40,), 0, 0.01)
+    args = ((1, 1), (0, 0), (1, 1), 1, (9, 13))
+    fast = oracle.conv_reference(x, w, b, *args)
+    slow = oracle.conv2d_f32(x, w, b, *args, order=oracle.ORDER_IM2COL)
+    assert np.array_equal(fast.view(np.uint32), slow.view(np.uint32))
+
+
+@pytest.mark.parametrize("op", [0, 1, 2])
+def test_vector_activations_are_the_scalar_loop(oracle, op):
+    x = np.concatenate([synth.normal(50 + op, (70001,), 0, 12),
+                        np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 88.7, -87.3, 89, -88, 1e30, -1e30],
+                                 np.float32)]).astype(np.float32)
+    fast = {0: oracle.exp_ref, 1: oracle.silu_ref, 2: oracle.sigmoid_ref}[op](x)
+    slow = oracle.unary_scalar(op, x)
+    assert np.array_equal(fast.view(np.uint32), slow.view(np.uint32))
