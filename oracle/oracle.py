@@ -463,6 +463,42 @@ def dqmm(a, w, w_zp=None, w_scale=None, bias=None, fused=True):
     return out, acc, accf, np.float32(s.value), zz.value
 
 
+_dqmm_widened = {}  # id(weights) -> (weakref, widened weights, zero points)
+
+
+def dqmm_widened_gemm(a, w, w_zp=None, w_scale=None, bias=None):
+    """DynamicQuantizeMatMul as the reference computes it on the CPU
+    (QuantizedMatMulOps.cs:115-201): Quantizer.MinMax and QuantizeAndWiden
+    of A, then the F32 GEMM of the widened operands (weights widened once,
+    w - w_zp, as GetPackedWeights caches them) with the column-scale
+    epilogue fmaf(acc, a_scale * w_scale[j], bias[j]).  The output only; the
+    same bits as dqmm(...)[0] (a CPU test checks), on the blocked GEMM."""
+    import weakref
+    a = _c32(a)
+    m, k = a.shape
+    n = w.shape[1]
+    zps, _ = _zp_arr(w_zp)
+    hit = _dqmm_widened.get(id(w))
+    if hit is not None and hit[0]() is w and ((hit[2] is None and zps is None) or
+                                               (hit[2] is not None and zps is not None and
+                                                np.array_equal(hit[2], zps))):
+        wf = hit[1]
+    else:
+        zcol = np.zeros(n, np.int32) if zps is None else np.broadcast_to(zps.astype(np.int32), (n,))
+        wf = (w.astype(np.int32) - zcol[None, :]).astype(np.float32)
+        try:
+            _dqmm_widened[id(w)] = (weakref.ref(w), wf, zps)
+        except TypeError:
+            pass
+    mn, mx = minmax(a)
+    scale, zp = dql_params(mn, mx)
+    q = quantize_u8(a, scale, zp)
+    af = (q.astype(np.int32) - zp).astype(np.float32)
+    ws = np.ones(n, np.float32) if w_scale is None else np.broadcast_to(np.asarray(w_scale, np.float32), (n,))
+    comb = (np.float32(scale) * ws).astype(np.float32)
+    return gemm_f32(af, wf, col_bias=bias, col_scale=comb, fused=True)
+
+
 def matmul_integer(a, b, a_zp=0, b_zp=None):
     """MatMulInteger (Int8Gemm.MultiplyIntegerScalar; s8 A read as signed): exact int32."""
     a = np.ascontiguousarray(a)

@@ -213,9 +213,9 @@ HOT static void gemm_rows(void *p, long r0, long r1)
  * into a contiguous [k][32] panel once, then every 8-row block of C runs
  * against it with 16 accumulators of 16 lanes initialised from the bias --
  * per k step two 16-wide panel rows against eight broadcast values of A, one
- * fused multiply-add each.  Every element is the fmaf chain gemm_rows
- * computes, so the same bits.  Column tails use masked lanes.  No column
- * scale here. */
+ * fused multiply-add each (from 0 with a column scale, then its epilogue).
+ * Every element is the fmaf chain gemm_rows computes, so the same bits.
+ * Column tails use masked lanes. */
 __attribute__((target("avx512f,fma"))) static void gemm_blocks(void *p, long t0, long t1)
 {
     const gemm_ctx *g = (const gemm_ctx *)p;
@@ -231,6 +231,15 @@ __attribute__((target("avx512f,fma"))) static void gemm_blocks(void *p, long t0,
             _mm512_store_ps(panel + (long)kk * 32, _mm512_maskz_loadu_ps(m0, brow));
             _mm512_store_ps(panel + (long)kk * 32 + 16, _mm512_maskz_loadu_ps(m1, brow + 16));
         }
+        __m512 s0 = _mm512_setzero_ps(), s1 = _mm512_setzero_ps(), cb0 = s0, cb1 = s0;
+        if (g->col_scale) {
+            s0 = _mm512_maskz_loadu_ps(m0, g->col_scale + j0);
+            s1 = _mm512_maskz_loadu_ps(m1, g->col_scale + j0 + 16);
+            if (g->col_bias) {
+                cb0 = _mm512_maskz_loadu_ps(m0, g->col_bias + j0);
+                cb1 = _mm512_maskz_loadu_ps(m1, g->col_bias + j0 + 16);
+            }
+        }
         for (int i0 = 0; i0 < g->m; i0 += 8) {
             const int rows = g->m - i0 < 8 ? g->m - i0 : 8;
             __m512 acc0[8], acc1[8];
@@ -238,7 +247,9 @@ __attribute__((target("avx512f,fma"))) static void gemm_blocks(void *p, long t0,
 #pragma GCC unroll 8
             for (int r = 0; r < 8; r++) {
                 arow[r] = g->a + (long)(i0 + (r < rows ? r : 0)) * g->lda;
-                if (g->col_bias) {
+                if (g->col_scale) {
+                    acc0[r] = acc1[r] = _mm512_setzero_ps();
+                } else if (g->col_bias) {
                     acc0[r] = _mm512_maskz_loadu_ps(m0, g->col_bias + j0);
                     acc1[r] = _mm512_maskz_loadu_ps(m1, g->col_bias + j0 + 16);
                 } else {
@@ -255,6 +266,20 @@ __attribute__((target("avx512f,fma"))) static void gemm_blocks(void *p, long t0,
                     acc1[r] = _mm512_fmadd_ps(av, b1, acc1[r]);
                 }
             }
+            if (g->col_scale)  /* the column-scale epilogue, fused or as the ScaleColumns tail */
+                for (int r = 0; r < rows; r++) {
+                    if (g->fused) {
+                        acc0[r] = _mm512_fmadd_ps(acc0[r], s0, cb0);
+                        acc1[r] = _mm512_fmadd_ps(acc1[r], s1, cb1);
+                    } else {
+                        acc0[r] = _mm512_mul_ps(acc0[r], s0);
+                        acc1[r] = _mm512_mul_ps(acc1[r], s1);
+                        if (g->col_bias) {
+                            acc0[r] = _mm512_add_ps(acc0[r], cb0);
+                            acc1[r] = _mm512_add_ps(acc1[r], cb1);
+                        }
+                    }
+                }
             for (int r = 0; r < rows; r++) {
                 float *crow = g->c + (long)(i0 + r) * g->ldc + j0;
                 _mm512_mask_storeu_ps(crow, m0, acc0[r]);
@@ -267,14 +292,14 @@ __attribute__((target("avx512f,fma"))) static void gemm_blocks(void *p, long t0,
 
 /* C[m,n] (ldc) = A[m,k] (lda) * B[k,n] (ldb) with the reference's bias and
  * column-scale epilogue.  fused=1 is the micro-kernel epilogue (one fmaf),
- * fused=0 the ScaleColumns tail (multiply, then add).  Without a column
- * scale the register-blocked AVX-512 path runs where the host has AVX-512. */
+ * fused=0 the ScaleColumns tail (multiply, then add).  The register-blocked
+ * AVX-512 path runs where the host has AVX-512. */
 ORC_API void orc_gemm_f32(int m, int k, int n, const float *a, int lda, const float *b, int ldb,
                           const float *row_bias, const float *col_bias, const float *col_scale,
                           float *c, int ldc, int fused)
 {
     gemm_ctx g = {m, k, n, lda, ldb, ldc, fused, a, b, row_bias, col_bias, col_scale, c};
-    if (!col_scale && have_avx512()) {
+    if (have_avx512()) {
         parallel_for((n + 31) / 32, gemm_blocks, &g);
         return;
     }

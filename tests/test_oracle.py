@@ -711,3 +711,28 @@ def test_vector_activations_are_the_scalar_loop(oracle, op):
     fast = {0: oracle.exp_ref, 1: oracle.silu_ref, 2: oracle.sigmoid_ref}[op](x)
     slow = oracle.unary_scalar(op, x)
     assert np.array_equal(fast.view(np.uint32), slow.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,n,wdt,zp", [(512, 512, 2048, np.int8, None), (33, 100, 70, np.uint8, "column"),
+                                          (17, 64, 40, np.uint8, "tensor")])
+def test_dqmm_through_the_widened_gemm_is_the_dqmm_chain(oracle, m, k, n, wdt, zp):
+    # QuantizeAndWiden + the blocked F32 GEMM with the fused column-scale
+    # epilogue (the reference's own CPU route, and the cpu_baseline's) gives
+    # dqmm's output bit for bit; the blocked GEMM with a column scale equals
+    # the row loop, fused and unfused
+    a = synth.normal(m + k, (m, k))
+    lo, hi = (-127, 127) if wdt == np.int8 else (0, 255)
+    w = synth.randint(m + n, (k, n), lo, hi, wdt)
+    wzp = None if zp is None else (np.array([131], np.int32) if zp == "tensor"
+                                   else synth.randint(n, (n,), -20, 20, np.int32) + 128)
+    ws = synth.uniform(k + n, (n,), 0.001, 0.02)
+    b = synth.normal(m + k + n, (n,), 0, 0.01)
+    got = oracle.dqmm_widened_gemm(a, w, wzp, ws, b)
+    assert np.array_equal(got.view(np.uint32), oracle.dqmm(a, w, wzp, ws, b, fused=True)[0].view(np.uint32))
+    af = synth.uniform(3, (m, k), -4, 4)
+    wf = synth.uniform(4, (k, n), -4, 4)
+    for fused in (True, False):
+        for cb in (b, None):
+            x = oracle.gemm_f32(af, wf, col_bias=cb, col_scale=ws, fused=fused)
+            y = oracle.gemm_f32_rows(af, wf, col_bias=cb, col_scale=ws, fused=fused)
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
