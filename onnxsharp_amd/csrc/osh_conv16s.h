@@ -341,6 +341,13 @@ __device__ __forceinline__ void conv16s_tile(const osh_conv_params &p, const flo
         stage_store(sv0, 0);
         __syncthreads();
     }
+    // A 3x3 form that stages the whole patch (every channel, up to 256) in
+    // LDS behind a single barrier and then runs the chain with no further
+    // barrier gave the same bits but ran slower (3x3 s2 128 -> 256 at 80x80:
+    // 18.3-19.3 us against 15.1 for this pipeline; the frame's tuner picked
+    // it for no layer): with nothing to multiply until the whole patch has
+    // arrived, the fetch latency is exposed, and the larger LDS footprint
+    // leaves fewer workgroups per CU to hide it.
     if constexpr (BV > 2 || KS != 3) {
         if (!active) return;
 #pragma unroll

@@ -172,6 +172,8 @@ CONV16_CASES = [
     ("pads_0_2_valid_like", (1, 48, 17, 23), (24, 48, 3, 3), dict(pads=[0, 2, 2, 0])),
     ("stride3_16to16_20", (1, 16, 20, 20), (16, 16, 3, 3), dict(strides=[3, 3], pads=[1, 1, 1, 1])),
     ("tall_narrow_32to16_70x9", (1, 32, 70, 9), (16, 32, 3, 3), dict(pads=[1, 1, 1, 1])),
+    ("s2_64to48_batch2_23x29", (2, 64, 23, 29), (48, 64, 3, 3), dict(strides=[2, 2], pads=[1, 1, 1, 1])),
+    ("deep_256to80_s1_13x11", (1, 256, 13, 11), (80, 256, 3, 3), dict(pads=[1, 1, 1, 1])),
 ]
 
 
