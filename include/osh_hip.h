@@ -126,9 +126,9 @@ OSH_API osh_status osh_kernel_log(int reset, char *buf, size_t bytes, int *count
  *                 pointwise launches (the pointwise LDS tiles that fit every
  *                 member; a forced tile that does not fit takes the default).
  *   "pair_tile", "pair_tiles": the same for osh_conv2d_pair_f32: its
- *                 output tiles (bottleneck pairs 4x4, 4x8, 8x8; 8-channel
- *                 pairs 4x16, 8x16, 2x32; first-layer pairs 4x16, 2x32,
- *                 2x16), then N-1 = the two convs as
+ *                 output tiles (bottleneck pairs 4x4, 4x8, 8x8, 2x2;
+ *                 8-channel pairs 4x16, 8x16, 2x32, 2x16; first-layer pairs
+ *                 4x16, 2x32, 2x16, 2x8), then N-1 = the two convs as
  *                 separate launches (only with an intermediate buffer).
  *   "pointwise_variants" (get only): N.
  *                 The -2 setting of "pointwise_variant" changes the packed

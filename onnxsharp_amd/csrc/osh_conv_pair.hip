@@ -344,7 +344,11 @@ __global__ __launch_bounds__(256) void conv_pair_kernel(PairArgs a) {
 struct PairTile {
     int th, tw;
 };
-constexpr PairTile kPairTiles[] = {{4, 4}, {4, 8}, {8, 8}};
+// 2 x 2: one 16-pixel block for each conv (the ring is 4 x 4), so every wave
+// runs a single chain per conv; on small maps with wide intermediates this
+// spreads a pair over four times the CUs of 4 x 4, at the price of computing
+// 16 pixels of each conv per 4 output pixels.
+constexpr PairTile kPairTiles[] = {{4, 4}, {4, 8}, {8, 8}, {2, 2}};
 constexpr int kPairTileCount = sizeof(kPairTiles) / sizeof(kPairTiles[0]);
 
 // The pair takes SiLU convs (the bottlenecks'); exact_silu() selects the
@@ -383,7 +387,8 @@ osh_status conv_pair_launch(const PairArgs &a, int cb1, int cb2, hipStream_t st,
     switch (tile) {
     case 0: return pair_launch_tile<4, 4>(a, cb1, cb2, st);
     case 1: return pair_launch_tile<4, 8>(a, cb1, cb2, st);
-    default: return pair_launch_tile<8, 8>(a, cb1, cb2, st);
+    case 2: return pair_launch_tile<8, 8>(a, cb1, cb2, st);
+    default: return pair_launch_tile<2, 2>(a, cb1, cb2, st);
     }
 }
 
@@ -639,7 +644,7 @@ __global__ __launch_bounds__(256) void conv_pair8_kernel(PairArgs a) {
     }
 }
 
-constexpr PairTile kPair8Tiles[] = {{4, 16}, {8, 16}, {2, 32}};
+constexpr PairTile kPair8Tiles[] = {{4, 16}, {8, 16}, {2, 32}, {2, 16}};
 static_assert(sizeof(kPair8Tiles) / sizeof(kPair8Tiles[0]) == kPairTileCount,
               "a forced pair_tile indexes every pair family alike");
 
@@ -659,7 +664,8 @@ osh_status conv_pair8_launch(const PairArgs &a, hipStream_t st, int tile) {
     switch (tile) {
     case 0: return pair8_launch_t<4, 16>(a, st);
     case 1: return pair8_launch_t<8, 16>(a, st);
-    default: return pair8_launch_t<2, 32>(a, st);
+    case 2: return pair8_launch_t<2, 32>(a, st);
+    default: return pair8_launch_t<2, 16>(a, st);
     }
 }
 
@@ -937,7 +943,7 @@ __global__ __launch_bounds__(256) void first_pair_kernel(FirstPairArgs a) {
 // 2 x 32 10.8, 2 x 16 11.1; 8 x 16 12.1 and 4 x 32 13.3 (fewer workgroups
 // than CUs) were dropped.  As many tiles as the bottleneck pair's, so that a
 // forced pair_tile means the same for both.
-constexpr PairTile kFirstPairTiles[] = {{4, 16}, {2, 32}, {2, 16}};
+constexpr PairTile kFirstPairTiles[] = {{4, 16}, {2, 32}, {2, 16}, {2, 8}};
 constexpr int kFirstPairTileCount = sizeof(kFirstPairTiles) / sizeof(kFirstPairTiles[0]);
 
 template <int TH, int TW, int SA, int S2, int CB2, int NS>
@@ -978,7 +984,8 @@ osh_status first_pair_launch(const FirstPairArgs &a, int sa, int sb, int cb2, hi
     switch (tile) {
     case 0: return first_pair_launch_tile<4, 16>(a, sa, sb, cb2, st);
     case 1: return first_pair_launch_tile<2, 32>(a, sa, sb, cb2, st);
-    default: return first_pair_launch_tile<2, 16>(a, sa, sb, cb2, st);
+    case 2: return first_pair_launch_tile<2, 16>(a, sa, sb, cb2, st);
+    default: return first_pair_launch_tile<2, 8>(a, sa, sb, cb2, st);
     }
 }
 
