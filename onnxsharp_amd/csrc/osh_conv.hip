@@ -418,8 +418,8 @@ constexpr int kGroupTuneTag = 20;  // tuning-table tags of grouped launches (3x3
 
 static std::string tune_db_header() {
     char h[128];
-    snprintf(h, sizeof(h), "onnxsharp-hip tune v1 conv3x3=%d pointwise=%d im2col3x3=%d", conv16_variant_count(),
-             pointwise_variant_count(), im2col3x3_variant_count());
+    snprintf(h, sizeof(h), "onnxsharp-hip tune v1 conv3x3=%d pointwise=%d im2col3x3=%d pair=%d", conv16_variant_count(),
+             pointwise_variant_count(), im2col3x3_variant_count(), conv_pair_tile_count());
     return h;
 }
 
