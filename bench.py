@@ -596,7 +596,45 @@ def measure(wl, args):
         out[f"ms_per_{key}"] = round(ms_step, 4)
         if not args.no_host_copies:
             out[f"ms_per_{key}_with_host_copies"] = round(wl.host_roundtrip_ms(), 4)
+        if getattr(wl, "mode", "") == "graph" and not args.eager and not args.trace_marks:
+            out[f"ms_per_{key}_one_graph"] = round(repeated_graph_ms(wl, min(args.steps, 50)), 5)
     return out
+
+
+def repeated_graph_ms(wl, reps):
+    """ms per step with `reps` steps' launches recorded into one graph (as the
+    one-launch configs are timed) instead of one graph replay per step: the
+    difference is what each replay's own start costs."""
+    from onnxsharp_amd import native as N
+    fr, st = wl.fr, wl.fr.stream
+    g = C.c_void_p()
+    N.call("osh_graph_begin", st)
+    try:
+        for _ in range(reps):
+            for c in fr._calls:
+                c(st)
+    finally:
+        N.call("osh_graph_end", st, C.byref(g))
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    N.call("osh_event_create", C.byref(e0))
+    N.call("osh_event_create", C.byref(e1))
+    try:
+        N.call("osh_graph_launch", g, st)  # one untimed replay
+        best = None
+        for _ in range(3):
+            N.call("osh_stream_sync", st)
+            N.call("osh_event_record", e0, st)
+            N.call("osh_graph_launch", g, st)
+            N.call("osh_event_record", e1, st)
+            N.call("osh_stream_sync", st)
+            ms = C.c_float()
+            N.call("osh_event_elapsed_ms", e0, e1, C.byref(ms))
+            best = ms.value if best is None else min(best, ms.value)
+    finally:
+        N.call("osh_event_destroy", e0)
+        N.call("osh_event_destroy", e1)
+        N.call("osh_graph_destroy", g)
+    return best / reps
 
 
 def launch_table(wl, reps=7, replays=40):
@@ -753,7 +791,8 @@ def main():
         "cpu_baseline": h.get("cpu_baseline"),
     }
     for k in ("timing", "ms_per_step_eager", "wall_s", "ms_per_frame", "ms_per_frame_with_host_copies",
-              "ms_per_block", "ms_per_block_with_host_copies", "frac_of_int8_mfma_peak"):
+              "ms_per_frame_one_graph", "ms_per_block", "ms_per_block_with_host_copies", "ms_per_block_one_graph",
+              "frac_of_int8_mfma_peak"):
         if k in h:
             out[k] = h[k]
     if hi is not None:
